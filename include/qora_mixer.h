@@ -1,0 +1,245 @@
+/*
+ * qora_mixer.h -- C ABI of the MI355X token-mixer library (libqora_mixer.so).
+ *
+ * The library runs the two halves of the QORA-4B token mixer on one
+ * MI355X (gfx950) with hand-written HIP kernels loaded from code objects:
+ *   - Gated DeltaNet: recurrent decode step and chunked prefill;
+ *   - full-attention GQA: decode step over an f16 KV cache and causal
+ *     prefill that writes that cache.
+ * Projections (in_proj_*, q/k/v/o_proj, out_proj), the MLP, lm_head and
+ * sampling stay with the caller.  Each mixer entry replaces the middle of
+ * one reference layer-forward (cited per entry); the surrounding
+ * projection calls are unchanged.
+ *
+ * Conventions
+ *   - Every entry returns int32_t status (QM_OK == 0); qm_status_string()
+ *     names a code and qm_last_error() gives the detail of the last failure
+ *     on that context.  The reference panics on the same conditions
+ *     (gemv.rs:1049, gemv.rs:620-621) and its GPU thread turns panics into
+ *     Err (gpu_inference.rs:950-975); a Rust caller maps non-zero to Err.
+ *   - All pointers named *_dev are device pointers (from qm_alloc or any
+ *     hipMalloc); sizes are element counts unless named *bytes.
+ *   - Kernels are enqueued asynchronously on `stream` (a hipStream_t; NULL
+ *     means the context's own stream).  Nothing synchronises the host
+ *     except qm_sync and the d2h copy.
+ *   - A context is not thread-safe and owns one workspace: enqueue one
+ *     context's mixer calls on one stream at a time (the reference calls
+ *     its layer-forwards from one thread, gpu_inference.rs:946-948).
+ *   - Mixer calls never allocate device memory once qm_reserve() has sized
+ *     the workspace for the largest batch / KV length the caller will use;
+ *     without it the first larger call grows the workspace (not allowed
+ *     while the stream is being captured into a graph: QM_ERR_WORKSPACE).
+ *   - f16 / bf16 values are passed as uint16_t bit patterns.
+ *
+ * Shapes are those of Qor4bConfig::default_4b (config.rs:42-79):
+ *   DeltaNet  num_qk_heads 16, num_v_heads 32, head_dim 128, conv k=4,
+ *             qkv_dim 8192 = [q 2048 | k 2048 | v 4096], v_dim 4096;
+ *   GQA       16 query heads, 4 kv heads, head_dim 256, rope_dim 64.
+ * qm_create() rejects any other qm_config with QM_ERR_SHAPE.
+ */
+#ifndef QORA_MIXER_H
+#define QORA_MIXER_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------- */
+enum {
+    QM_OK = 0,
+    QM_ERR_NO_DEVICE = 1,      /* no HIP device / bad device index        */
+    QM_ERR_CODE_OBJECT = 2,    /* gfx950 code object missing or unusable  */
+    QM_ERR_INVALID_ARG = 3,    /* null pointer, non-positive size, ...    */
+    QM_ERR_SHAPE = 4,          /* dimensions other than the 4B mixer's    */
+    QM_ERR_ROPE_RANGE = 5,     /* position beyond the RoPE table          */
+    QM_ERR_CAPACITY = 6,       /* KV position beyond the cache capacity   */
+    QM_ERR_HIP = 7,            /* HIP runtime error (launch, copy, ...)   */
+    QM_ERR_OUT_OF_MEMORY = 8,
+    QM_ERR_WORKSPACE = 9       /* workspace would have to grow in capture */
+};
+
+typedef struct qm_context qm_context;
+typedef struct qm_graph qm_graph;
+typedef struct qm_event qm_event;
+typedef void* qm_stream;       /* hipStream_t */
+
+/* Mixer dimensions, mirroring Qor4bConfig's mixer fields (config.rs:4-32). */
+typedef struct {
+    int32_t num_qk_heads;      /* 16  */
+    int32_t num_v_heads;       /* 32  */
+    int32_t dn_head_dim;       /* 128 */
+    int32_t conv_kernel;       /* 4   */
+    int32_t num_heads;         /* 16  */
+    int32_t num_kv_heads;      /* 4   */
+    int32_t attn_head_dim;     /* 256 */
+    int32_t rope_dim;          /* 64 = attn_head_dim * partial_rotary_factor */
+} qm_config;
+
+/* ---- context ------------------------------------------------------ */
+/* The default 4B mixer config (config.rs:42-79, rope_dim config.rs:82-85). */
+void        qm_default_config(qm_config* cfg);
+/* Create a context on `device`.  cfg may be NULL (default config).
+ * code_object_dir holds the gfx950 code objects (qm_*.hsaco); NULL means
+ * the directory libqora_mixer.so was loaded from. */
+int32_t     qm_create(qm_context** ctx, const qm_config* cfg,
+                      const char* code_object_dir, int32_t device);
+int32_t     qm_destroy(qm_context* ctx);
+const char* qm_status_string(int32_t status);
+/* Detail of the last failure on ctx (or of the last qm_create failure on
+ * this thread when ctx is NULL).  Valid until the next call on ctx. */
+const char* qm_last_error(const qm_context* ctx);
+int32_t     qm_device_count(int32_t* count);
+/* Size the workspace for batches up to max_batch and KV lengths up to
+ * max_kv_len (and DeltaNet prefill up to max_prefill_tokens) so that later
+ * mixer calls do not allocate (e.g. under graph capture). */
+int32_t     qm_reserve(qm_context* ctx, int32_t max_batch, int32_t max_kv_len,
+                       int32_t max_prefill_tokens);
+/* Launch-shape overrides for tests and tuning (0 = automatic).  Results do
+ * not depend on them beyond fp32 reassociation. */
+enum {
+    QM_OPT_DN_DECODE_SPLITS = 1,   /* row blocks per v-head: 1,2,4,8       */
+    QM_OPT_GQA_DECODE_CHUNK = 2,   /* keys per split-K workgroup (mult. 64)*/
+    QM_OPT_DN_PREFILL_SLICES = 3   /* v-row slices per head in the scan    */
+};
+int32_t     qm_set_option(qm_context* ctx, int32_t option, int64_t value);
+
+/* ---- device memory, streams, events, graphs (caller plumbing) ----- */
+int32_t qm_alloc(qm_context* ctx, uint64_t bytes, void** dev);
+int32_t qm_free(qm_context* ctx, void* dev);
+int32_t qm_memcpy_h2d(qm_context* ctx, void* dst_dev, const void* src_host,
+                      uint64_t bytes, qm_stream stream);
+int32_t qm_memcpy_d2h(qm_context* ctx, void* dst_host, const void* src_dev,
+                      uint64_t bytes, qm_stream stream); /* synchronous */
+int32_t qm_memcpy_d2d(qm_context* ctx, void* dst_dev, const void* src_dev,
+                      uint64_t bytes, qm_stream stream);
+int32_t qm_memset(qm_context* ctx, void* dst_dev, int32_t byte_value,
+                  uint64_t bytes, qm_stream stream);
+int32_t qm_stream_create(qm_context* ctx, qm_stream* stream);
+int32_t qm_stream_destroy(qm_context* ctx, qm_stream stream);
+int32_t qm_sync(qm_context* ctx, qm_stream stream);
+int32_t qm_event_create(qm_context* ctx, qm_event** ev);
+int32_t qm_event_destroy(qm_context* ctx, qm_event* ev);
+int32_t qm_event_record(qm_context* ctx, qm_event* ev, qm_stream stream);
+int32_t qm_event_elapsed_ms(qm_context* ctx, qm_event* start, qm_event* stop,
+                            float* ms);
+/* Capture everything enqueued on `stream` between begin and end into a
+ * replayable graph (amortises launch cost of per-token decode loops). */
+int32_t qm_graph_begin(qm_context* ctx, qm_stream stream);
+int32_t qm_graph_end(qm_context* ctx, qm_stream stream, qm_graph** graph);
+int32_t qm_graph_launch(qm_context* ctx, qm_graph* graph, qm_stream stream);
+int32_t qm_graph_destroy(qm_context* ctx, qm_graph* graph);
+
+/* ---- host helpers --------------------------------------------------- */
+/* RoPE tables [max_pos][rope_dim/2] in host memory, the formula of
+ * convert.rs:161-176 (f32 powf/cosf/sinf); max_pos may exceed the 8192
+ * rows the reference stores. */
+int32_t qm_rope_table(double theta, int32_t rope_dim, int32_t max_pos,
+                      float* cos_host, float* sin_host);
+/* Fill `count` elements with mean + std * N(0,1) from a counter-based
+ * generator (seed, element index); dtype QM_F32 / QM_F16 / QM_BF16.
+ * Synthetic-data plumbing for benchmarks; not a mixer op. */
+enum { QM_F32 = 0, QM_F16 = 1, QM_BF16 = 2 };
+int32_t qm_fill_normal(qm_context* ctx, void* dst_dev, int32_t dtype,
+                       uint64_t count, float mean, float std, uint64_t seed,
+                       qm_stream stream);
+
+/* ---- DeltaNet decode step ------------------------------------------- */
+/* Replaces the mixer slice of forward_deltanet_decode, gemv.rs:744-883
+ * (wgpu twin forward_deltanet_decode_gpu, gpu_inference.rs:149-227), for
+ * `batch` independent sequences:
+ *   [conv1d k=4 + state shift, SiLU] -> split q|k|v -> per-head L2 norm,
+ *   q *= 1/sqrt(128) -> alpha = exp(-exp(A_log) softplus(a + dt_bias)),
+ *   beta = sigmoid(b) -> per v-head vh (q/k head vh/2):
+ *   S = alpha S; S += beta (v - S k) k^T; y = S q -> per-head RMSNorm
+ *   (plain gamma, eps 1e-6) * silu(z).
+ * flags: QM_DN_PREACT  qkv_dev is the raw in_proj_qkv output; conv1d+SiLU
+ *                      run here and conv_buf_dev is shifted (layer mode);
+ *        QM_DN_POSTACT qkv_dev is already activated; conv_buf_dev unused.
+ * qkv_dev      f32 [batch][8192]
+ * conv_buf_dev f32 [batch][8192][3]   (DeltaNetState.conv_buf layout)
+ * conv_w_dev   f32 [8192][4]          (tap 3 multiplies the new token)
+ * a_dev, b_dev f32 [batch][32]; a_log_dev, dt_bias_dev f32 [32]
+ * z_dev        f32 [batch][4096]      (in_proj_z output, pre-silu)
+ * norm_w_dev   f16 [128]              (attn_norm_weight)
+ * state_dev    f32 [batch] x state_stride, each [32][128 v][128 k]
+ *              (DeltaNetState.s layout), updated in place
+ * out_dev      f32 [batch][4096]      (gated output, the out_proj input) */
+enum { QM_DN_POSTACT = 0, QM_DN_PREACT = 1 };
+int32_t qm_deltanet_decode(qm_context* ctx, qm_stream stream, int32_t batch,
+                           int32_t flags, const float* qkv_dev,
+                           float* conv_buf_dev, const float* conv_w_dev,
+                           const float* a_dev, const float* b_dev,
+                           const float* a_log_dev, const float* dt_bias_dev,
+                           const float* z_dev, const uint16_t* norm_w_dev,
+                           float* state_dev, int64_t state_stride,
+                           float* out_dev);
+
+/* ---- DeltaNet chunked prefill --------------------------------------- */
+/* Replaces the sequential mixer loop of prefill_deltanet_layer,
+ * gemv.rs:1119-1219 (wgpu twin prefill_deltanet_layer_gpu's host loop,
+ * gpu_inference.rs:488-588, and its device<->host round trip), for one
+ * sequence of seq_len tokens, computed in chunks of 64 tokens (WY/UT form)
+ * with the same result as seq_len recurrent steps.
+ * qkv_dev   bf16 [seq_len][8192]  raw in_proj_qkv outputs
+ * conv_buf_dev f32 [8192][3] in/out; conv_w_dev f32 [8192][4]
+ * a_dev, b_dev f32 [seq_len][32]; a_log_dev, dt_bias_dev f32 [32]
+ * z_dev     bf16 [seq_len][4096]; norm_w_dev f16 [128]
+ * state_dev f32 [32][128][128] in/out
+ * out_dev   bf16 [seq_len][4096]  gated output */
+int32_t qm_deltanet_prefill(qm_context* ctx, qm_stream stream, int32_t seq_len,
+                            const uint16_t* qkv_dev, float* conv_buf_dev,
+                            const float* conv_w_dev, const float* a_dev,
+                            const float* b_dev, const float* a_log_dev,
+                            const float* dt_bias_dev, const uint16_t* z_dev,
+                            const uint16_t* norm_w_dev, float* state_dev,
+                            uint16_t* out_dev);
+
+/* ---- GQA decode step ------------------------------------------------- */
+/* Replaces the mixer slice of forward_attn_decode, gemv.rs:927-1011
+ * (wgpu twin forward_attn_decode_gpu, gpu_inference.rs:271-349):
+ * split q|gate per head -> per-head RMSNorm (1+gamma) of q and k ->
+ * partial RoPE (dims 0..63, pairs (i, i+32)) at position pos -> append
+ * k, v to the cache at pos (f16) -> softmax(q K^T / 16) V over positions
+ * 0..pos with kv head h/4 -> * sigmoid(gate).
+ * q_gate_dev   f32 [batch][16][512]  interleaved [q_h | gate_h]
+ * k_new_dev, v_new_dev f32 [batch][4][256]
+ * q_norm_dev, k_norm_dev f16 [256]
+ * rope_cos_dev, rope_sin_dev f32 [rope_len][32]
+ * pos_dev      int32 [batch] positions (= cached length before the append)
+ *              or NULL: every sequence is at position max_pos
+ * max_pos      upper bound of the positions; must be < rope_len and
+ *              < cache_capacity (else QM_ERR_ROPE_RANGE / QM_ERR_CAPACITY);
+ *              device positions above it are clamped to it
+ * k_cache_dev, v_cache_dev f16 [batch][4][cache_capacity][256]
+ * out_dev      f32 [batch][16][256]  gated attention (the o_proj input) */
+int32_t qm_gqa_decode(qm_context* ctx, qm_stream stream, int32_t batch,
+                      const float* q_gate_dev, const float* k_new_dev,
+                      const float* v_new_dev, const uint16_t* q_norm_dev,
+                      const uint16_t* k_norm_dev, const float* rope_cos_dev,
+                      const float* rope_sin_dev, int32_t rope_len,
+                      const int32_t* pos_dev, int32_t max_pos,
+                      uint16_t* k_cache_dev, uint16_t* v_cache_dev,
+                      int64_t cache_capacity, float* out_dev);
+
+/* ---- GQA causal prefill ---------------------------------------------- */
+/* Replaces the mixer slice of prefill_attn_layer, gemv.rs:1364-1444
+ * (wgpu twin prefill_attn_layer_gpu, gpu_inference.rs:679-766): per-token
+ * QK RMSNorm + RoPE at positions 0..S-1, the KV cache replaced by the
+ * normed/roped K and V (rows 0..S-1, f16), causal softmax attention, gate.
+ * q_gate_dev bf16 [S][16][512]; k_dev, v_dev bf16 [S][4][256]
+ * k_cache_dev, v_cache_dev f16 [4][cache_capacity][256] (S <= capacity)
+ * out_dev bf16 [S][16][256] */
+int32_t qm_gqa_prefill(qm_context* ctx, qm_stream stream, int32_t seq_len,
+                       const uint16_t* q_gate_dev, const uint16_t* k_dev,
+                       const uint16_t* v_dev, const uint16_t* q_norm_dev,
+                       const uint16_t* k_norm_dev, const float* rope_cos_dev,
+                       const float* rope_sin_dev, int32_t rope_len,
+                       uint16_t* k_cache_dev, uint16_t* v_cache_dev,
+                       int64_t cache_capacity, uint16_t* out_dev);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QORA_MIXER_H */

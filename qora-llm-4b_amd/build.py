@@ -1,0 +1,70 @@
+"""Build recipe for libqora_mixer.so and its gfx950 code objects.
+
+    python qora-llm-4b_amd/build.py          # build into qora-llm-4b_amd/lib/
+
+Each csrc/<name>.hip becomes lib/qm_<name>.hsaco (hipcc --genco for gfx950;
+loaded at run time with hipModuleLoad), and csrc/qm_runtime.cpp becomes
+lib/libqora_mixer.so (host code only, g++ against the HIP runtime).  The
+products are git-ignored and travel with the source tree.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+LIB = PKG / "lib"
+ROOT = PKG.parent
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+ARCH = "gfx950"
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}", "--genco", "-O3", "-std=c++17",
+    # Keep the compiler from emitting packed-fp32 VALU ops.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-parameter",
+]
+
+KERNELS = ["dn_decode", "gqa_decode", "util"]
+
+
+def _run(cmd: list[str]) -> None:
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"build step failed ({r.returncode}): {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+
+
+def hip_cmd(name: str) -> list[str]:
+    return [str(ROCM / "bin" / "hipcc"), *HIPCC_FLAGS, "-I", str(CSRC),
+            str(CSRC / f"{name}.hip"), "-o", str(LIB / f"qm_{name}.hsaco")]
+
+
+def host_cmd() -> list[str]:
+    return ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off",
+            "-Wall", "-Wextra", "-Wno-unused-result", "-D__HIP_PLATFORM_AMD__",
+            "-I", str(ROOT / "include"), "-I", str(CSRC), "-I", str(ROCM / "include"),
+            str(CSRC / "qm_runtime.cpp"), "-o", str(LIB / "libqora_mixer.so"),
+            f"-L{ROCM / 'lib'}", "-lamdhip64", f"-Wl,-rpath,{ROCM / 'lib'}", "-ldl"]
+
+
+def build(jobs: int = 8) -> None:
+    LIB.mkdir(exist_ok=True)
+    cmds = [hip_cmd(k) for k in KERNELS] + [host_cmd()]
+    with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+        for f in [ex.submit(_run, c) for c in cmds]:
+            f.result()
+
+
+def build_oracle() -> None:
+    _run(["make", "-s", "-C", str(ROOT / "oracle")])
+
+
+if __name__ == "__main__":
+    build()
+    if "--no-oracle" not in sys.argv:
+        build_oracle()
+    print("built:", ", ".join(sorted(p.name for p in LIB.iterdir())))

@@ -1,0 +1,178 @@
+// dn_decode.hip -- Gated DeltaNet recurrent decode step for gfx950.
+//
+// Replaces the mixer slice of forward_deltanet_decode (gemv.rs:744-883):
+// conv1d+SiLU (layer mode), per-head L2 norm of q/k, alpha/beta gates, the
+// delta-rule update of the per-v-head 128x128 fp32 state and the gated
+// RMSNorm epilogue.
+//
+// The state update is a pure HBM stream: each state row S[r,:] (512 B) is
+// read once and written once.  One sweep replaces the reference's four
+// passes (decay, retrieve, update, output; simd.rs:304-361):
+//   Sd = alpha*S; p = Sd.k; delta = beta*(v[r]-p); S' = Sd + delta*k;
+//   y[r] = S'.q  (S' is still in registers).
+// Layout: a workgroup owns 128/SPLITS rows of one (sequence, v-head).  A
+// 16-lane DPP row owns one state row at a time; lane l holds columns
+// 4l..4l+3 and 64+4l..64+4l+3, so every dwordx4 load of a wave covers four
+// consecutive rows contiguously.  Row dot products reduce inside the DPP
+// row (4 DPP adds, no LDS).  With SPLITS > 1 the head is split over
+// workgroups (more CUs busy at batch 1) and the last workgroup to finish a
+// head (arrival counter) applies the norm.
+#include "qm_device.h"
+#include "qm_kernel_args.h"
+
+// gemv.rs:744-772 (layer mode): depthwise causal conv with the old buffer,
+// buffer shift, SiLU.  One thread per (sequence, channel), so the in-place
+// buffer update has no readers other than its writer.
+extern "C" __global__ __launch_bounds__(256) void qm_dn_conv_silu(DnConvArgs A) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)A.batch * QM_DN_QKV_DIM) return;
+    const int ch = (int)(idx % QM_DN_QKV_DIM);
+    float* buf = A.conv_buf + idx * 3;
+    const float4 w = ld4(A.conv_w + ch * 4);
+    const float x = A.qkv[idx];
+    const float b0 = buf[0], b1 = buf[1], b2 = buf[2];
+    // Same operation order as the reference, without FMA contraction.
+    float s = 0.0f;
+    s = __fadd_rn(s, __fmul_rn(b0, w.x));
+    s = __fadd_rn(s, __fmul_rn(b1, w.y));
+    s = __fadd_rn(s, __fmul_rn(b2, w.z));
+    s = __fadd_rn(s, __fmul_rn(x, w.w));
+    A.act[idx] = silu_f(s);
+    buf[0] = b1;
+    buf[1] = b2;
+    buf[2] = x;
+}
+
+QM_DEV float dot8(float4 a0, float4 a1, float4 b0, float4 b1) {
+    float s = a0.x * b0.x;
+    s = fmaf(a0.y, b0.y, s); s = fmaf(a0.z, b0.z, s); s = fmaf(a0.w, b0.w, s);
+    s = fmaf(a1.x, b1.x, s); s = fmaf(a1.y, b1.y, s); s = fmaf(a1.z, b1.z, s);
+    s = fmaf(a1.w, b1.w, s);
+    return s;
+}
+
+QM_DEV float4 scale4(float4 a, float s) { return make_float4(a.x * s, a.y * s, a.z * s, a.w * s); }
+
+// gemv.rs:643-649 + :780-785: x /= ||x|| when ||x|| > 1e-12 (per head of 128,
+// the 16 lanes of a DPP row hold the whole head).
+QM_DEV void l2norm_row(float4& x0, float4& x1) {
+    float ss = x0.x * x0.x + x0.y * x0.y + x0.z * x0.z + x0.w * x0.w
+             + x1.x * x1.x + x1.y * x1.y + x1.z * x1.z + x1.w * x1.w;
+    ss = row_sum16(ss);
+    const float norm = sqrtf(ss);
+    if (norm > 1e-12f) {
+        const float inv = 1.0f / norm;
+        x0 = scale4(x0, inv);
+        x1 = scale4(x1, inv);
+    }
+}
+
+template <int SPLITS>
+QM_DEV void dn_decode_body(const DnDecodeArgs& A) {
+    constexpr int ROWS_WG = QM_DN_HD / SPLITS;   // rows of the head per WG
+    constexpr int RPG = ROWS_WG / 16;            // rows per 16-lane group
+    static_assert(RPG >= 1, "split too fine");
+    __shared__ float ys[QM_DN_HD];
+    __shared__ uint32_t is_last;
+
+    const int tid = threadIdx.x;
+    const int g = tid >> 4, l = tid & 15;
+    const int bid = blockIdx.x;
+    const int sp = bid % SPLITS;
+    const int vh = (bid / SPLITS) % QM_DN_V_HEADS;
+    const int b = bid / (SPLITS * QM_DN_V_HEADS);
+    const int qkh = vh >> 1;                      // GVA: vh -> vh/2 (gemv.rs:806)
+    const int r0 = sp * ROWS_WG;
+
+    const float* act = A.act + (size_t)b * QM_DN_QKV_DIM;
+    float* S = A.state + (size_t)b * A.state_stride + (size_t)vh * QM_DN_HEAD_ELEMS;
+
+    // Issue the state loads first: they are the HBM stream.
+    float4 s0[RPG], s1[RPG];
+#pragma unroll
+    for (int i = 0; i < RPG; ++i) {
+        const float* row = S + (size_t)(r0 + g + 16 * i) * QM_DN_HD;
+        s0[i] = ld4(row + 4 * l);
+        s1[i] = ld4(row + 64 + 4 * l);
+    }
+    float vr[RPG];
+#pragma unroll
+    for (int i = 0; i < RPG; ++i) vr[i] = act[2 * 2048 + vh * QM_DN_HD + r0 + g + 16 * i];
+
+    float4 q0 = ld4(act + qkh * QM_DN_HD + 4 * l), q1 = ld4(act + qkh * QM_DN_HD + 64 + 4 * l);
+    float4 k0 = ld4(act + 2048 + qkh * QM_DN_HD + 4 * l), k1 = ld4(act + 2048 + qkh * QM_DN_HD + 64 + 4 * l);
+    l2norm_row(q0, q1);
+    l2norm_row(k0, k1);
+    const float qscale = 1.0f / sqrtf((float)QM_DN_HD);
+    q0 = scale4(q0, qscale);
+    q1 = scale4(q1, qscale);
+
+    // gemv.rs:788-800
+    const float a_exp = expf(A.a_log[vh]);
+    const float spl = softplus_f(A.a[b * QM_DN_V_HEADS + vh] + A.dt_bias[vh]);
+    const float alpha = expf(-a_exp * spl);
+    const float beta = 1.0f / (1.0f + expf(-A.b[b * QM_DN_V_HEADS + vh]));
+
+    float y[RPG];
+#pragma unroll
+    for (int i = 0; i < RPG; ++i) {
+        const float4 d0 = scale4(s0[i], alpha), d1 = scale4(s1[i], alpha);
+        const float p = row_sum16(dot8(d0, d1, k0, k1));
+        const float delta = beta * (vr[i] - p);
+        float4 n0, n1;
+        n0.x = fmaf(delta, k0.x, d0.x); n0.y = fmaf(delta, k0.y, d0.y);
+        n0.z = fmaf(delta, k0.z, d0.z); n0.w = fmaf(delta, k0.w, d0.w);
+        n1.x = fmaf(delta, k1.x, d1.x); n1.y = fmaf(delta, k1.y, d1.y);
+        n1.z = fmaf(delta, k1.z, d1.z); n1.w = fmaf(delta, k1.w, d1.w);
+        float* row = S + (size_t)(r0 + g + 16 * i) * QM_DN_HD;
+        st4(row + 4 * l, n0);
+        st4(row + 64 + 4 * l, n1);
+        y[i] = row_sum16(dot8(n0, n1, q0, q1));
+    }
+
+    float* yo = A.out + (size_t)b * QM_DN_V_DIM + vh * QM_DN_HD;
+    if (SPLITS == 1) {
+        if (l == 0) {
+#pragma unroll
+            for (int i = 0; i < RPG; ++i) ys[g + 16 * i] = y[i];
+        }
+        __syncthreads();
+    } else {
+        // Publish this block's rows, then count arrivals for the head.
+        if (l == 0) {
+#pragma unroll
+            for (int i = 0; i < RPG; ++i) yo[r0 + g + 16 * i] = y[i];
+        }
+        __threadfence();
+        __syncthreads();
+        if (tid == 0) {
+            const uint32_t prev = atomicAdd(&A.counters[b * QM_DN_V_HEADS + vh], 1u);
+            is_last = (prev == SPLITS - 1) ? 1u : 0u;
+        }
+        __syncthreads();
+        if (!is_last) return;
+        __threadfence();
+        if (tid < QM_DN_HD)
+            ys[tid] = __hip_atomic_load(yo + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tid == 0)
+            __hip_atomic_store(&A.counters[b * QM_DN_V_HEADS + vh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+    }
+
+    // gemv.rs:865-883: per-head RMSNorm (plain gamma, eps 1e-6) * silu(z).
+    // The sum of squares runs over rows 0..127 in order, as the reference.
+    if (tid < QM_DN_HD) {
+        float ss = 0.0f;
+#pragma unroll 8
+        for (int r = 0; r < QM_DN_HD; ++r) ss = __fadd_rn(ss, __fmul_rn(ys[r], ys[r]));
+        const float inv_rms = 1.0f / sqrtf(ss / (float)QM_DN_HD + 1e-6f);
+        const float gm = f16_to_f32(A.norm_w[tid]);
+        const float zz = A.z[(size_t)b * QM_DN_V_DIM + vh * QM_DN_HD + tid];
+        yo[tid] = ys[tid] * inv_rms * gm * silu_f(zz);
+    }
+}
+
+extern "C" __global__ __launch_bounds__(256) void qm_dn_decode_s1(DnDecodeArgs A) { dn_decode_body<1>(A); }
+extern "C" __global__ __launch_bounds__(256) void qm_dn_decode_s2(DnDecodeArgs A) { dn_decode_body<2>(A); }
+extern "C" __global__ __launch_bounds__(256) void qm_dn_decode_s4(DnDecodeArgs A) { dn_decode_body<4>(A); }
+extern "C" __global__ __launch_bounds__(256) void qm_dn_decode_s8(DnDecodeArgs A) { dn_decode_body<8>(A); }

@@ -1,0 +1,65 @@
+// qm_device.h -- gfx950 device helpers shared by the mixer kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define QM_DEV __device__ __forceinline__
+
+// ---- cross-lane reductions (wave64; a DPP "row" is 16 lanes) -------------
+// DPP controls: quad_perm[1,0,3,2] = 0xB1, quad_perm[2,3,0,1] = 0x4E,
+// row_half_mirror = 0x141, row_mirror = 0x140.
+template <int CTRL>
+QM_DEV float dpp_f32(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 16 lanes of a DPP row.  The result is bitwise identical in
+// all 16 lanes (each step adds a commutative pair).
+QM_DEV float row_sum16(float x) {
+    x += dpp_f32<0xB1>(x);
+    x += dpp_f32<0x4E>(x);
+    x += dpp_f32<0x141>(x);
+    x += dpp_f32<0x140>(x);
+    return x;
+}
+
+QM_DEV float row_max16(float x) {
+    x = fmaxf(x, dpp_f32<0xB1>(x));
+    x = fmaxf(x, dpp_f32<0x4E>(x));
+    x = fmaxf(x, dpp_f32<0x141>(x));
+    x = fmaxf(x, dpp_f32<0x140>(x));
+    return x;
+}
+
+QM_DEV float readlane_f32(float x, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
+}
+
+// Sum over the whole wave: row sums then the four row results in a fixed
+// order.  Uniform across the wave.
+QM_DEV float wave_sum64(float x) {
+    x = row_sum16(x);
+    float r0 = readlane_f32(x, 0), r1 = readlane_f32(x, 16);
+    float r2 = readlane_f32(x, 32), r3 = readlane_f32(x, 48);
+    return (r0 + r1) + (r2 + r3);
+}
+
+// ---- f16 / bf16 ----------------------------------------------------------
+QM_DEV float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+QM_DEV uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+QM_DEV float bf16_to_f32(uint16_t h) { return __builtin_bit_cast(float, (uint32_t)h << 16); }
+QM_DEV uint16_t f32_to_bf16(float f) {   // round to nearest even
+    uint32_t x = __builtin_bit_cast(uint32_t, f);
+    if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
+    x += 0x7fffu + ((x >> 16) & 1u);
+    return (uint16_t)(x >> 16);
+}
+
+// ---- scalar math (gemv.rs:631-659 semantics) -----------------------------
+QM_DEV float silu_f(float x) { return x / (1.0f + expf(-x)); }
+QM_DEV float softplus_f(float x) { return x > 20.0f ? x : logf(1.0f + expf(x)); }
+QM_DEV float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// ---- memory helpers ------------------------------------------------------
+QM_DEV float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+QM_DEV void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }

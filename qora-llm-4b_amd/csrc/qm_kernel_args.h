@@ -1,0 +1,76 @@
+// qm_kernel_args.h -- argument blocks passed by value to the gfx950 kernels.
+// Shared by the host runtime (g++) and the device code (hipcc --genco), so
+// it uses only fixed-width integer and pointer members.
+#pragma once
+#include <stdint.h>
+
+// Mixer shape (Qor4bConfig::default_4b, config.rs:42-97).
+#define QM_DN_QK_HEADS   16
+#define QM_DN_V_HEADS    32
+#define QM_DN_HD         128
+#define QM_DN_CONV_K     4
+#define QM_DN_QKV_DIM    8192      // 2*16*128 + 32*128
+#define QM_DN_V_DIM      4096
+#define QM_DN_HEAD_ELEMS 16384     // 128*128 state floats per v-head
+#define QM_GQA_HEADS     16
+#define QM_GQA_KV_HEADS  4
+#define QM_GQA_HD        256
+#define QM_GQA_ROT       64
+#define QM_GQA_GROUP     4         // query heads per kv head
+
+// Causal conv1d + SiLU pre-pass of the layer-mode DeltaNet decode step.
+struct DnConvArgs {
+    const float* qkv;        // [B][8192] raw projection
+    float* conv_buf;         // [B][8192][3]
+    const float* conv_w;     // [8192][4]
+    float* act;              // [B][8192] activated output
+    int32_t batch;
+};
+
+// DeltaNet decode step on activated inputs.
+struct DnDecodeArgs {
+    const float* act;        // [B][8192] activated q|k|v (q,k not yet L2-normed)
+    const float* a;          // [B][32]
+    const float* b;          // [B][32]
+    const float* a_log;      // [32]
+    const float* dt_bias;    // [32]
+    const float* z;          // [B][4096]
+    const uint16_t* norm_w;  // [128] f16
+    float* state;            // [B] x state_stride floats
+    int64_t state_stride;
+    float* out;              // [B][4096]
+    uint32_t* counters;      // [B*32] arrival counters (split > 1), zero at rest
+    int32_t batch;
+};
+
+// GQA decode step (fused prep + split-K attention + last-arriver combine).
+struct GqaDecodeArgs {
+    const float* q_gate;     // [B][16][512]
+    const float* k_new;      // [B][4][256]
+    const float* v_new;      // [B][4][256]
+    const uint16_t* q_norm;  // [256] f16
+    const uint16_t* k_norm;  // [256] f16
+    const float* rope_cos;   // [rope_len][32]
+    const float* rope_sin;
+    const int32_t* pos;      // [B] or null
+    uint16_t* k_cache;       // [B][4][cap][256] f16
+    uint16_t* v_cache;
+    float* out;              // [B][16][256]
+    float* partial;          // [B][4][nsplit][4][258]  (m[4], l[4], acc[4][256])
+    uint32_t* counters;      // [B*4]
+    int64_t cap;
+    int32_t max_pos;
+    int32_t chunk;           // keys per split
+    int32_t nsplit;          // splits per (b, kv head)
+    int32_t batch;
+};
+
+// Counter-based normal generator fill.
+struct FillArgs {
+    void* dst;
+    uint64_t count;
+    uint64_t seed;
+    float mean;
+    float stdev;
+    int32_t dtype;
+};

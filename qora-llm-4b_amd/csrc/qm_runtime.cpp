@@ -1,0 +1,563 @@
+// qm_runtime.cpp -- host side of libqora_mixer.so (the C ABI in
+// include/qora_mixer.h).
+//
+// Loads the gfx950 code objects (qm_*.hsaco) with hipModuleLoad, validates
+// every argument before anything is enqueued (so bad shapes, positions and
+// null pointers come back as status codes instead of faults), picks launch
+// shapes and enqueues the kernels with hipModuleLaunchKernel.  Device memory
+// for the mixer's own scratch (split-K partials, arrival counters, the
+// activated qkv of layer-mode decode) lives in a per-context workspace that
+// only grows outside stream capture.
+#include "qora_mixer.h"
+#include "qm_kernel_args.h"
+
+#include <hip/hip_runtime_api.h>
+#include <dlfcn.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+namespace {
+
+thread_local std::string g_create_error;
+
+}  // namespace
+
+struct qm_context {
+    int device = 0;
+    qm_config cfg{};
+    hipStream_t stream = nullptr;
+    std::vector<hipModule_t> modules;
+    hipFunction_t f_conv = nullptr;
+    hipFunction_t f_dn[4] = {nullptr, nullptr, nullptr, nullptr};  // splits 1,2,4,8
+    hipFunction_t f_gqa_decode = nullptr;
+    hipFunction_t f_fill = nullptr;
+    void* ws = nullptr;            // general workspace
+    size_t ws_bytes = 0;
+    uint32_t* counters = nullptr;  // arrival counters, zero at rest
+    size_t counter_slots = 0;
+    std::string err;
+    int64_t opt_dn_splits = 0;
+    int64_t opt_gqa_chunk = 0;
+    int64_t opt_dn_prefill_slices = 0;
+};
+
+struct qm_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+struct qm_event {
+    hipEvent_t ev = nullptr;
+};
+
+namespace {
+
+int32_t fail(qm_context* c, int32_t code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    if (c) c->err = buf; else g_create_error = buf;
+    return code;
+}
+
+#define QM_HIP(c, call)                                                              \
+    do {                                                                             \
+        hipError_t e_ = (call);                                                      \
+        if (e_ != hipSuccess)                                                        \
+            return fail((c), e_ == hipErrorOutOfMemory ? QM_ERR_OUT_OF_MEMORY : QM_ERR_HIP, \
+                        "%s: %s", #call, hipGetErrorString(e_));                     \
+    } while (0)
+
+hipStream_t pick(qm_context* c, qm_stream s) { return s ? static_cast<hipStream_t>(s) : c->stream; }
+
+bool capturing(hipStream_t s) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &st) != hipSuccess) return false;
+    return st != hipStreamCaptureStatusNone;
+}
+
+// Grow the workspace / counter slots.  Growth synchronises the device and is
+// refused while the stream is being captured.
+int32_t ensure(qm_context* c, hipStream_t s, size_t ws_bytes, size_t slots) {
+    if (ws_bytes <= c->ws_bytes && slots <= c->counter_slots) return QM_OK;
+    if (capturing(s))
+        return fail(c, QM_ERR_WORKSPACE,
+                    "workspace must grow to %zu bytes / %zu counters during graph capture; "
+                    "call qm_reserve() before capturing", ws_bytes, slots);
+    QM_HIP(c, hipDeviceSynchronize());
+    if (ws_bytes > c->ws_bytes) {
+        if (c->ws) QM_HIP(c, hipFree(c->ws));
+        c->ws = nullptr;
+        c->ws_bytes = 0;
+        QM_HIP(c, hipMalloc(&c->ws, ws_bytes));
+        c->ws_bytes = ws_bytes;
+    }
+    if (slots > c->counter_slots) {
+        if (c->counters) QM_HIP(c, hipFree(c->counters));
+        c->counters = nullptr;
+        c->counter_slots = 0;
+        QM_HIP(c, hipMalloc(reinterpret_cast<void**>(&c->counters), slots * sizeof(uint32_t)));
+        QM_HIP(c, hipMemset(c->counters, 0, slots * sizeof(uint32_t)));
+        c->counter_slots = slots;
+    }
+    QM_HIP(c, hipDeviceSynchronize());
+    return QM_OK;
+}
+
+template <class Args>
+int32_t launch(qm_context* c, hipFunction_t f, uint32_t grid, uint32_t block, const Args& args,
+               hipStream_t s, const char* what) {
+    Args copy = args;
+    void* params[] = {static_cast<void*>(&copy)};
+    hipError_t e = hipModuleLaunchKernel(f, grid, 1, 1, block, 1, 1, 0, s, params, nullptr);
+    if (e != hipSuccess) return fail(c, QM_ERR_HIP, "launch %s: %s", what, hipGetErrorString(e));
+    return QM_OK;
+}
+
+std::string library_dir() {
+    Dl_info info;
+    if (dladdr(reinterpret_cast<void*>(&qm_create), &info) && info.dli_fname) {
+        std::string p = info.dli_fname;
+        size_t k = p.find_last_of('/');
+        if (k != std::string::npos) return p.substr(0, k);
+    }
+    return ".";
+}
+
+bool same_config(const qm_config& a, const qm_config& b) {
+    return a.num_qk_heads == b.num_qk_heads && a.num_v_heads == b.num_v_heads &&
+           a.dn_head_dim == b.dn_head_dim && a.conv_kernel == b.conv_kernel &&
+           a.num_heads == b.num_heads && a.num_kv_heads == b.num_kv_heads &&
+           a.attn_head_dim == b.attn_head_dim && a.rope_dim == b.rope_dim;
+}
+
+int32_t load_function(qm_context* c, hipModule_t m, const char* name, hipFunction_t* f) {
+    hipError_t e = hipModuleGetFunction(f, m, name);
+    if (e != hipSuccess)
+        return fail(c, QM_ERR_CODE_OBJECT, "kernel %s not found in code object: %s", name,
+                    hipGetErrorString(e));
+    return QM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+void qm_default_config(qm_config* cfg) {
+    if (!cfg) return;
+    cfg->num_qk_heads = QM_DN_QK_HEADS;
+    cfg->num_v_heads = QM_DN_V_HEADS;
+    cfg->dn_head_dim = QM_DN_HD;
+    cfg->conv_kernel = QM_DN_CONV_K;
+    cfg->num_heads = QM_GQA_HEADS;
+    cfg->num_kv_heads = QM_GQA_KV_HEADS;
+    cfg->attn_head_dim = QM_GQA_HD;
+    cfg->rope_dim = QM_GQA_ROT;
+}
+
+const char* qm_status_string(int32_t status) {
+    switch (status) {
+        case QM_OK: return "ok";
+        case QM_ERR_NO_DEVICE: return "no HIP device";
+        case QM_ERR_CODE_OBJECT: return "gfx950 code object missing or unusable";
+        case QM_ERR_INVALID_ARG: return "invalid argument";
+        case QM_ERR_SHAPE: return "unsupported mixer shape";
+        case QM_ERR_ROPE_RANGE: return "position beyond the RoPE table";
+        case QM_ERR_CAPACITY: return "position beyond the KV cache capacity";
+        case QM_ERR_HIP: return "HIP runtime error";
+        case QM_ERR_OUT_OF_MEMORY: return "out of device memory";
+        case QM_ERR_WORKSPACE: return "workspace growth during graph capture";
+        default: return "unknown status";
+    }
+}
+
+const char* qm_last_error(const qm_context* ctx) {
+    return ctx ? ctx->err.c_str() : g_create_error.c_str();
+}
+
+int32_t qm_device_count(int32_t* count) {
+    if (!count) return QM_ERR_INVALID_ARG;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    *count = (e == hipSuccess) ? n : 0;
+    return QM_OK;
+}
+
+int32_t qm_create(qm_context** out, const qm_config* cfg, const char* code_object_dir,
+                  int32_t device) {
+    if (!out) return fail(nullptr, QM_ERR_INVALID_ARG, "qm_create: out is null");
+    *out = nullptr;
+    qm_config want;
+    qm_default_config(&want);
+    if (cfg && !same_config(*cfg, want))
+        return fail(nullptr, QM_ERR_SHAPE,
+                    "kernels are built for the 4B mixer (16/32 heads x 128, conv 4; "
+                    "16q/4kv x 256, rope 64)");
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0)
+        return fail(nullptr, QM_ERR_NO_DEVICE, "no HIP device visible");
+    if (device < 0 || device >= n)
+        return fail(nullptr, QM_ERR_NO_DEVICE, "device %d out of range (%d devices)", device, n);
+    if (hipSetDevice(device) != hipSuccess)
+        return fail(nullptr, QM_ERR_NO_DEVICE, "hipSetDevice(%d) failed", device);
+
+    qm_context* c = new qm_context();
+    c->device = device;
+    c->cfg = want;
+    std::string dir = code_object_dir ? code_object_dir : library_dir();
+    const char* files[] = {"qm_dn_decode.hsaco", "qm_gqa_decode.hsaco", "qm_util.hsaco"};
+    hipModule_t mods[3] = {nullptr, nullptr, nullptr};
+    for (int i = 0; i < 3; ++i) {
+        std::string path = dir + "/" + files[i];
+        hipError_t e = hipModuleLoad(&mods[i], path.c_str());
+        if (e != hipSuccess) {
+            for (int j = 0; j < i; ++j) hipModuleUnload(mods[j]);
+            delete c;
+            return fail(nullptr, QM_ERR_CODE_OBJECT, "cannot load %s: %s", path.c_str(),
+                        hipGetErrorString(e));
+        }
+        c->modules.push_back(mods[i]);
+    }
+    int32_t st = QM_OK;
+    const char* dn_names[4] = {"qm_dn_decode_s1", "qm_dn_decode_s2", "qm_dn_decode_s4", "qm_dn_decode_s8"};
+    if (st == QM_OK) st = load_function(c, mods[0], "qm_dn_conv_silu", &c->f_conv);
+    for (int i = 0; i < 4 && st == QM_OK; ++i) st = load_function(c, mods[0], dn_names[i], &c->f_dn[i]);
+    if (st == QM_OK) st = load_function(c, mods[1], "qm_gqa_decode", &c->f_gqa_decode);
+    if (st == QM_OK) st = load_function(c, mods[2], "qm_fill_normal", &c->f_fill);
+    if (st == QM_OK && hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess)
+        st = fail(c, QM_ERR_HIP, "hipStreamCreate failed");
+    if (st != QM_OK) {
+        g_create_error = c->err;
+        qm_destroy(c);
+        return st;
+    }
+    *out = c;
+    return QM_OK;
+}
+
+int32_t qm_destroy(qm_context* c) {
+    if (!c) return QM_ERR_INVALID_ARG;
+    hipSetDevice(c->device);
+    hipDeviceSynchronize();
+    if (c->ws) hipFree(c->ws);
+    if (c->counters) hipFree(c->counters);
+    if (c->stream) hipStreamDestroy(c->stream);
+    for (hipModule_t m : c->modules) hipModuleUnload(m);
+    delete c;
+    return QM_OK;
+}
+
+int32_t qm_set_option(qm_context* c, int32_t option, int64_t value) {
+    if (!c) return QM_ERR_INVALID_ARG;
+    switch (option) {
+        case QM_OPT_DN_DECODE_SPLITS:
+            if (value != 0 && value != 1 && value != 2 && value != 4 && value != 8)
+                return fail(c, QM_ERR_INVALID_ARG, "DN decode splits must be 0,1,2,4,8");
+            c->opt_dn_splits = value;
+            return QM_OK;
+        case QM_OPT_GQA_DECODE_CHUNK:
+            if (value < 0 || value % 64 != 0 || value > (1 << 20))
+                return fail(c, QM_ERR_INVALID_ARG, "GQA decode chunk must be a multiple of 64");
+            c->opt_gqa_chunk = value;
+            return QM_OK;
+        case QM_OPT_DN_PREFILL_SLICES:
+            if (value != 0 && value != 1 && value != 2 && value != 4 && value != 8)
+                return fail(c, QM_ERR_INVALID_ARG, "DN prefill slices must be 0,1,2,4,8");
+            c->opt_dn_prefill_slices = value;
+            return QM_OK;
+        default:
+            return fail(c, QM_ERR_INVALID_ARG, "unknown option %d", option);
+    }
+}
+
+// ---- plumbing --------------------------------------------------------------
+int32_t qm_alloc(qm_context* c, uint64_t bytes, void** dev) {
+    if (!c || !dev || bytes == 0) return c ? fail(c, QM_ERR_INVALID_ARG, "qm_alloc: bad args") : QM_ERR_INVALID_ARG;
+    *dev = nullptr;
+    QM_HIP(c, hipMalloc(dev, bytes));
+    return QM_OK;
+}
+
+int32_t qm_free(qm_context* c, void* dev) {
+    if (!c) return QM_ERR_INVALID_ARG;
+    if (dev) QM_HIP(c, hipFree(dev));
+    return QM_OK;
+}
+
+int32_t qm_memcpy_h2d(qm_context* c, void* dst, const void* src, uint64_t bytes, qm_stream s) {
+    if (!c || ((!dst || !src) && bytes)) return c ? fail(c, QM_ERR_INVALID_ARG, "qm_memcpy_h2d: null") : QM_ERR_INVALID_ARG;
+    if (!bytes) return QM_OK;
+    QM_HIP(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, pick(c, s)));
+    QM_HIP(c, hipStreamSynchronize(pick(c, s)));   // src may be pageable / temporary
+    return QM_OK;
+}
+
+int32_t qm_memcpy_d2h(qm_context* c, void* dst, const void* src, uint64_t bytes, qm_stream s) {
+    if (!c || ((!dst || !src) && bytes)) return c ? fail(c, QM_ERR_INVALID_ARG, "qm_memcpy_d2h: null") : QM_ERR_INVALID_ARG;
+    if (!bytes) return QM_OK;
+    QM_HIP(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, pick(c, s)));
+    QM_HIP(c, hipStreamSynchronize(pick(c, s)));
+    return QM_OK;
+}
+
+int32_t qm_memcpy_d2d(qm_context* c, void* dst, const void* src, uint64_t bytes, qm_stream s) {
+    if (!c || ((!dst || !src) && bytes)) return c ? fail(c, QM_ERR_INVALID_ARG, "qm_memcpy_d2d: null") : QM_ERR_INVALID_ARG;
+    if (!bytes) return QM_OK;
+    QM_HIP(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, pick(c, s)));
+    return QM_OK;
+}
+
+int32_t qm_memset(qm_context* c, void* dst, int32_t v, uint64_t bytes, qm_stream s) {
+    if (!c || (!dst && bytes)) return c ? fail(c, QM_ERR_INVALID_ARG, "qm_memset: null") : QM_ERR_INVALID_ARG;
+    if (!bytes) return QM_OK;
+    QM_HIP(c, hipMemsetAsync(dst, v, bytes, pick(c, s)));
+    return QM_OK;
+}
+
+int32_t qm_stream_create(qm_context* c, qm_stream* s) {
+    if (!c || !s) return QM_ERR_INVALID_ARG;
+    hipStream_t h = nullptr;
+    QM_HIP(c, hipStreamCreateWithFlags(&h, hipStreamNonBlocking));
+    *s = h;
+    return QM_OK;
+}
+
+int32_t qm_stream_destroy(qm_context* c, qm_stream s) {
+    if (!c || !s) return QM_ERR_INVALID_ARG;
+    QM_HIP(c, hipStreamDestroy(static_cast<hipStream_t>(s)));
+    return QM_OK;
+}
+
+int32_t qm_sync(qm_context* c, qm_stream s) {
+    if (!c) return QM_ERR_INVALID_ARG;
+    QM_HIP(c, hipStreamSynchronize(pick(c, s)));
+    return QM_OK;
+}
+
+int32_t qm_event_create(qm_context* c, qm_event** ev) {
+    if (!c || !ev) return QM_ERR_INVALID_ARG;
+    qm_event* e = new qm_event();
+    hipError_t r = hipEventCreate(&e->ev);
+    if (r != hipSuccess) { delete e; return fail(c, QM_ERR_HIP, "hipEventCreate: %s", hipGetErrorString(r)); }
+    *ev = e;
+    return QM_OK;
+}
+
+int32_t qm_event_destroy(qm_context* c, qm_event* ev) {
+    if (!c || !ev) return QM_ERR_INVALID_ARG;
+    hipEventDestroy(ev->ev);
+    delete ev;
+    return QM_OK;
+}
+
+int32_t qm_event_record(qm_context* c, qm_event* ev, qm_stream s) {
+    if (!c || !ev) return QM_ERR_INVALID_ARG;
+    QM_HIP(c, hipEventRecord(ev->ev, pick(c, s)));
+    return QM_OK;
+}
+
+int32_t qm_event_elapsed_ms(qm_context* c, qm_event* a, qm_event* b, float* ms) {
+    if (!c || !a || !b || !ms) return QM_ERR_INVALID_ARG;
+    QM_HIP(c, hipEventSynchronize(b->ev));
+    QM_HIP(c, hipEventElapsedTime(ms, a->ev, b->ev));
+    return QM_OK;
+}
+
+int32_t qm_graph_begin(qm_context* c, qm_stream s) {
+    if (!c) return QM_ERR_INVALID_ARG;
+    QM_HIP(c, hipStreamBeginCapture(pick(c, s), hipStreamCaptureModeThreadLocal));
+    return QM_OK;
+}
+
+int32_t qm_graph_end(qm_context* c, qm_stream s, qm_graph** out) {
+    if (!c || !out) return QM_ERR_INVALID_ARG;
+    qm_graph* g = new qm_graph();
+    hipError_t e = hipStreamEndCapture(pick(c, s), &g->graph);
+    if (e != hipSuccess) { delete g; return fail(c, QM_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(e)); }
+    e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        hipGraphDestroy(g->graph);
+        delete g;
+        return fail(c, QM_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
+    }
+    *out = g;
+    return QM_OK;
+}
+
+int32_t qm_graph_launch(qm_context* c, qm_graph* g, qm_stream s) {
+    if (!c || !g) return QM_ERR_INVALID_ARG;
+    QM_HIP(c, hipGraphLaunch(g->exec, pick(c, s)));
+    return QM_OK;
+}
+
+int32_t qm_graph_destroy(qm_context* c, qm_graph* g) {
+    if (!c || !g) return QM_ERR_INVALID_ARG;
+    if (g->exec) hipGraphExecDestroy(g->exec);
+    if (g->graph) hipGraphDestroy(g->graph);
+    delete g;
+    return QM_OK;
+}
+
+// ---- host helpers ------------------------------------------------------------
+// convert.rs:161-176 (built with -ffp-contract=off: plain f32 rounding).
+int32_t qm_rope_table(double theta, int32_t rope_dim, int32_t max_pos, float* cos_host,
+                      float* sin_host) {
+    if (!cos_host || !sin_host || rope_dim <= 0 || rope_dim % 2 || max_pos <= 0 || !(theta > 0.0))
+        return QM_ERR_INVALID_ARG;
+    const int32_t half = rope_dim / 2;
+    const float th = static_cast<float>(theta);
+    for (int32_t i = 0; i < half; ++i) {
+        const float freq = 1.0f / powf(th, 2.0f * static_cast<float>(i) / static_cast<float>(rope_dim));
+        for (int32_t pos = 0; pos < max_pos; ++pos) {
+            const float angle = static_cast<float>(pos) * freq;
+            cos_host[static_cast<size_t>(pos) * half + i] = cosf(angle);
+            sin_host[static_cast<size_t>(pos) * half + i] = sinf(angle);
+        }
+    }
+    return QM_OK;
+}
+
+int32_t qm_fill_normal(qm_context* c, void* dst, int32_t dtype, uint64_t count, float mean,
+                       float stdev, uint64_t seed, qm_stream s) {
+    if (!c) return QM_ERR_INVALID_ARG;
+    if (!dst || count == 0 || dtype < QM_F32 || dtype > QM_BF16)
+        return fail(c, QM_ERR_INVALID_ARG, "qm_fill_normal: bad args");
+    FillArgs a{dst, count, seed, mean, stdev, dtype};
+    uint64_t blocks = (count + 255) / 256;
+    uint32_t grid = static_cast<uint32_t>(std::min<uint64_t>(blocks, 1u << 16));
+    return launch(c, c->f_fill, grid, 256, a, pick(c, s), "qm_fill_normal");
+}
+
+// ---- DeltaNet decode ---------------------------------------------------------------
+static int dn_auto_splits(int32_t batch) {
+    const int64_t heads = static_cast<int64_t>(batch) * QM_DN_V_HEADS;
+    if (heads >= 1024) return 1;
+    if (heads >= 512) return 2;
+    if (heads >= 256) return 4;
+    return 8;
+}
+
+int32_t qm_deltanet_decode(qm_context* c, qm_stream stream, int32_t batch, int32_t flags,
+                           const float* qkv, float* conv_buf, const float* conv_w,
+                           const float* a, const float* b, const float* a_log,
+                           const float* dt_bias, const float* z, const uint16_t* norm_w,
+                           float* state, int64_t state_stride, float* out) {
+    if (!c) return QM_ERR_INVALID_ARG;
+    if (batch <= 0) return fail(c, QM_ERR_INVALID_ARG, "qm_deltanet_decode: batch %d", batch);
+    if (flags != QM_DN_PREACT && flags != QM_DN_POSTACT)
+        return fail(c, QM_ERR_INVALID_ARG, "qm_deltanet_decode: flags %d", flags);
+    if (!qkv || !a || !b || !a_log || !dt_bias || !z || !norm_w || !state || !out)
+        return fail(c, QM_ERR_INVALID_ARG, "qm_deltanet_decode: null pointer");
+    if (flags == QM_DN_PREACT && (!conv_buf || !conv_w))
+        return fail(c, QM_ERR_INVALID_ARG, "qm_deltanet_decode: layer mode needs conv_buf and conv_w");
+    if (state_stride < static_cast<int64_t>(QM_DN_V_HEADS) * QM_DN_HEAD_ELEMS || state_stride % 4)
+        return fail(c, QM_ERR_INVALID_ARG, "qm_deltanet_decode: state_stride %lld",
+                    static_cast<long long>(state_stride));
+    hipStream_t s = pick(c, stream);
+    const int splits = c->opt_dn_splits ? static_cast<int>(c->opt_dn_splits) : dn_auto_splits(batch);
+    const size_t act_bytes = flags == QM_DN_PREACT ? static_cast<size_t>(batch) * QM_DN_QKV_DIM * 4 : 0;
+    const size_t slots = splits > 1 ? static_cast<size_t>(batch) * QM_DN_V_HEADS : 0;
+    int32_t st = ensure(c, s, act_bytes, slots);
+    if (st != QM_OK) return st;
+    const float* act = qkv;
+    if (flags == QM_DN_PREACT) {
+        DnConvArgs ca{qkv, conv_buf, conv_w, static_cast<float*>(c->ws), batch};
+        const uint64_t n = static_cast<uint64_t>(batch) * QM_DN_QKV_DIM;
+        st = launch(c, c->f_conv, static_cast<uint32_t>((n + 255) / 256), 256, ca, s, "qm_dn_conv_silu");
+        if (st != QM_OK) return st;
+        act = static_cast<const float*>(c->ws);
+    }
+    DnDecodeArgs da{act, a, b, a_log, dt_bias, z, norm_w, state, state_stride, out, c->counters, batch};
+    const int fi = splits == 1 ? 0 : splits == 2 ? 1 : splits == 4 ? 2 : 3;
+    const uint64_t grid = static_cast<uint64_t>(batch) * QM_DN_V_HEADS * splits;
+    if (grid > 0x7fffffffull) return fail(c, QM_ERR_INVALID_ARG, "qm_deltanet_decode: batch too large");
+    return launch(c, c->f_dn[fi], static_cast<uint32_t>(grid), 256, da, s, "qm_dn_decode");
+}
+
+// ---- GQA decode --------------------------------------------------------------------
+static int64_t gqa_auto_chunk(int64_t len, int32_t batch) {
+    // Aim for ~2048 workgroups (8 per CU) with at least 64 keys each.
+    int64_t want = (len * batch * QM_GQA_KV_HEADS + 2047) / 2048;
+    int64_t ch = ((want + 63) / 64) * 64;
+    return std::max<int64_t>(64, std::min<int64_t>(ch, 2048));
+}
+
+int32_t qm_gqa_decode(qm_context* c, qm_stream stream, int32_t batch, const float* q_gate,
+                      const float* k_new, const float* v_new, const uint16_t* q_norm,
+                      const uint16_t* k_norm, const float* rope_cos, const float* rope_sin,
+                      int32_t rope_len, const int32_t* pos, int32_t max_pos, uint16_t* k_cache,
+                      uint16_t* v_cache, int64_t cap, float* out) {
+    if (!c) return QM_ERR_INVALID_ARG;
+    if (batch <= 0) return fail(c, QM_ERR_INVALID_ARG, "qm_gqa_decode: batch %d", batch);
+    if (!q_gate || !k_new || !v_new || !q_norm || !k_norm || !rope_cos || !rope_sin || !k_cache ||
+        !v_cache || !out)
+        return fail(c, QM_ERR_INVALID_ARG, "qm_gqa_decode: null pointer");
+    if (max_pos < 0) return fail(c, QM_ERR_INVALID_ARG, "qm_gqa_decode: max_pos %d", max_pos);
+    if (max_pos >= rope_len)
+        return fail(c, QM_ERR_ROPE_RANGE, "position %d beyond RoPE table of %d rows", max_pos, rope_len);
+    if (cap <= 0 || max_pos >= cap)
+        return fail(c, QM_ERR_CAPACITY, "position %d beyond cache capacity %lld", max_pos,
+                    static_cast<long long>(cap));
+    hipStream_t s = pick(c, stream);
+    const int64_t len = static_cast<int64_t>(max_pos) + 1;
+    const int64_t chunk = c->opt_gqa_chunk ? c->opt_gqa_chunk : gqa_auto_chunk(len, batch);
+    const int64_t nsplit = (len + chunk - 1) / chunk;
+    const uint64_t grid = static_cast<uint64_t>(batch) * QM_GQA_KV_HEADS * nsplit;
+    if (grid > 0x7fffffffull) return fail(c, QM_ERR_INVALID_ARG, "qm_gqa_decode: grid too large");
+    const size_t part_bytes = static_cast<size_t>(grid) * 4 * 260 * sizeof(float);
+    const size_t slots = static_cast<size_t>(batch) * QM_GQA_KV_HEADS;
+    int32_t st = ensure(c, s, part_bytes, slots);
+    if (st != QM_OK) return st;
+    GqaDecodeArgs ga{q_gate, k_new, v_new, q_norm, k_norm, rope_cos, rope_sin, pos, k_cache, v_cache,
+                     out, static_cast<float*>(c->ws), c->counters, cap, max_pos,
+                     static_cast<int32_t>(chunk), static_cast<int32_t>(nsplit), batch};
+    return launch(c, c->f_gqa_decode, static_cast<uint32_t>(grid), 256, ga, s, "qm_gqa_decode");
+}
+
+int32_t qm_reserve(qm_context* c, int32_t max_batch, int32_t max_kv_len, int32_t max_prefill_tokens) {
+    if (!c || max_batch <= 0 || max_kv_len < 0 || max_prefill_tokens < 0)
+        return c ? fail(c, QM_ERR_INVALID_ARG, "qm_reserve: bad args") : QM_ERR_INVALID_ARG;
+    size_t ws = static_cast<size_t>(max_batch) * QM_DN_QKV_DIM * 4;
+    if (max_kv_len > 0) {
+        // Bound on batch * nsplit over every batch <= max_batch and length
+        // <= max_kv_len.  Automatic chunks: below the 2048 cap a chunk holds
+        // at least len*batch/512 keys, so nsplit <= ceil(512/batch); at the
+        // cap nsplit = ceil(len/2048); and always nsplit <= ceil(len/64).
+        const int64_t L = max_kv_len, B = max_batch;
+        int64_t bn;
+        if (c->opt_gqa_chunk) {
+            bn = B * ((L + c->opt_gqa_chunk - 1) / c->opt_gqa_chunk);
+        } else {
+            bn = std::min<int64_t>(B * ((L + 63) / 64), std::max<int64_t>(512 + B, B * ((L + 2047) / 2048)));
+        }
+        ws = std::max(ws, static_cast<size_t>(bn) * QM_GQA_KV_HEADS * 4 * 260 * sizeof(float));
+    }
+    (void)max_prefill_tokens;
+    const size_t slots = static_cast<size_t>(max_batch) * QM_DN_V_HEADS;
+    return ensure(c, c->stream, ws, slots);
+}
+
+// ---- prefill entries (kernels land in qm_dn_prefill / qm_gqa_prefill) ------
+int32_t qm_deltanet_prefill(qm_context* c, qm_stream, int32_t, const uint16_t*, float*,
+                            const float*, const float*, const float*, const float*,
+                            const float*, const uint16_t*, const uint16_t*, float*, uint16_t*) {
+    if (!c) return QM_ERR_INVALID_ARG;
+    return fail(c, QM_ERR_CODE_OBJECT, "qm_deltanet_prefill: kernel not built yet");
+}
+
+int32_t qm_gqa_prefill(qm_context* c, qm_stream, int32_t, const uint16_t*, const uint16_t*,
+                       const uint16_t*, const uint16_t*, const uint16_t*, const float*,
+                       const float*, int32_t, uint16_t*, uint16_t*, int64_t, uint16_t*) {
+    if (!c) return QM_ERR_INVALID_ARG;
+    return fail(c, QM_ERR_CODE_OBJECT, "qm_gqa_prefill: kernel not built yet");
+}
+
+}  // extern "C"

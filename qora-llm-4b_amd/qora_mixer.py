@@ -1,0 +1,327 @@
+"""ctypes binding of libqora_mixer.so (the C ABI in include/qora_mixer.h).
+
+This is the Python-side caller of the MI355X mixer library, used by the
+tests and the benchmark.  It is a thin, typed mirror of the C entry points:
+device buffers are plain integer addresses owned by `DeviceBuffer`, arrays
+cross the boundary as numpy arrays, and every non-zero status raises
+`MixerError` carrying the library's status code and message.  There is no
+fallback path: if the library or its code objects are missing, creating a
+`Context` fails loudly.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+import numpy as np
+
+PKG_DIR = Path(__file__).resolve().parent
+LIB_DIR = PKG_DIR / "lib"
+LIB_PATH = LIB_DIR / "libqora_mixer.so"
+
+QM_OK = 0
+STATUS_NAMES = {
+    0: "QM_OK", 1: "QM_ERR_NO_DEVICE", 2: "QM_ERR_CODE_OBJECT", 3: "QM_ERR_INVALID_ARG",
+    4: "QM_ERR_SHAPE", 5: "QM_ERR_ROPE_RANGE", 6: "QM_ERR_CAPACITY", 7: "QM_ERR_HIP",
+    8: "QM_ERR_OUT_OF_MEMORY", 9: "QM_ERR_WORKSPACE",
+}
+QM_DN_POSTACT, QM_DN_PREACT = 0, 1
+QM_F32, QM_F16, QM_BF16 = 0, 1, 2
+QM_OPT_DN_DECODE_SPLITS, QM_OPT_GQA_DECODE_CHUNK, QM_OPT_DN_PREFILL_SLICES = 1, 2, 3
+
+# Mixer shape (config.rs:42-97).
+DN_QK_HEADS, DN_V_HEADS, DN_HD, DN_CONV_K = 16, 32, 128, 4
+DN_QKV_DIM, DN_V_DIM = 8192, 4096
+GQA_HEADS, GQA_KV_HEADS, GQA_HD, GQA_ROT = 16, 4, 256, 64
+ROPE_THETA = 10_000_000.0
+
+
+class QmConfig(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in (
+        "num_qk_heads", "num_v_heads", "dn_head_dim", "conv_kernel",
+        "num_heads", "num_kv_heads", "attn_head_dim", "rope_dim")]
+
+
+class MixerError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"{STATUS_NAMES.get(code, code)}: {message}")
+        self.code = code
+        self.message = message
+
+
+_P, _I32, _I64, _U64 = C.c_void_p, C.c_int32, C.c_int64, C.c_uint64
+
+# name -> argtypes (restype is int32 unless listed in _RESTYPES)
+_SIGNATURES = {
+    "qm_default_config": [C.POINTER(QmConfig)],
+    "qm_create": [C.POINTER(_P), C.POINTER(QmConfig), C.c_char_p, _I32],
+    "qm_destroy": [_P],
+    "qm_status_string": [_I32],
+    "qm_last_error": [_P],
+    "qm_device_count": [C.POINTER(_I32)],
+    "qm_reserve": [_P, _I32, _I32, _I32],
+    "qm_set_option": [_P, _I32, _I64],
+    "qm_alloc": [_P, _U64, C.POINTER(_P)],
+    "qm_free": [_P, _P],
+    "qm_memcpy_h2d": [_P, _P, _P, _U64, _P],
+    "qm_memcpy_d2h": [_P, _P, _P, _U64, _P],
+    "qm_memcpy_d2d": [_P, _P, _P, _U64, _P],
+    "qm_memset": [_P, _P, _I32, _U64, _P],
+    "qm_stream_create": [_P, C.POINTER(_P)],
+    "qm_stream_destroy": [_P, _P],
+    "qm_sync": [_P, _P],
+    "qm_event_create": [_P, C.POINTER(_P)],
+    "qm_event_destroy": [_P, _P],
+    "qm_event_record": [_P, _P, _P],
+    "qm_event_elapsed_ms": [_P, _P, _P, C.POINTER(C.c_float)],
+    "qm_graph_begin": [_P, _P],
+    "qm_graph_end": [_P, _P, C.POINTER(_P)],
+    "qm_graph_launch": [_P, _P, _P],
+    "qm_graph_destroy": [_P, _P],
+    "qm_rope_table": [C.c_double, _I32, _I32, _P, _P],
+    "qm_fill_normal": [_P, _P, _I32, _U64, C.c_float, C.c_float, _U64, _P],
+    "qm_deltanet_decode": [_P, _P, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P],
+    "qm_deltanet_prefill": [_P, _P, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P],
+    "qm_gqa_decode": [_P, _P, _I32, _P, _P, _P, _P, _P, _P, _P, _I32, _P, _I32, _P, _P, _I64, _P],
+    "qm_gqa_prefill": [_P, _P, _I32, _P, _P, _P, _P, _P, _P, _P, _I32, _P, _P, _I64, _P],
+}
+_RESTYPES = {"qm_default_config": None, "qm_status_string": C.c_char_p, "qm_last_error": C.c_char_p}
+
+_lib = None
+
+
+def load_library(path: str | os.PathLike | None = None) -> C.CDLL:
+    """Load libqora_mixer.so and declare every exported entry point."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise FileNotFoundError(f"{p} is not built; run `python qora-llm-4b_amd/build.py`")
+    lib = C.CDLL(str(p))
+    for name, argtypes in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = _RESTYPES.get(name, _I32)
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def default_config() -> QmConfig:
+    cfg = QmConfig()
+    load_library().qm_default_config(C.byref(cfg))
+    return cfg
+
+
+def rope_table(max_pos: int, theta: float = ROPE_THETA, rope_dim: int = GQA_ROT):
+    """convert.rs:161-176 tables, shape [max_pos, rope_dim/2] float32."""
+    cos = np.empty((max_pos, rope_dim // 2), np.float32)
+    sin = np.empty_like(cos)
+    st = load_library().qm_rope_table(theta, rope_dim, max_pos, cos.ctypes.data, sin.ctypes.data)
+    if st != QM_OK:
+        raise MixerError(st, "qm_rope_table")
+    return cos, sin
+
+
+def device_count() -> int:
+    n = _I32(0)
+    load_library().qm_device_count(C.byref(n))
+    return int(n.value)
+
+
+def _addr(x) -> int | None:
+    if x is None:
+        return None
+    if isinstance(x, DeviceBuffer):
+        return x.ptr
+    return int(x)
+
+
+class DeviceBuffer:
+    """A device allocation made through qm_alloc; freed on close()/GC."""
+
+    def __init__(self, ctx: "Context", nbytes: int):
+        self.ctx = ctx
+        self.nbytes = int(nbytes)
+        p = _P(0)
+        ctx._check(ctx.lib.qm_alloc(ctx.h, self.nbytes, C.byref(p)))
+        self.ptr = int(p.value)
+
+    def offset(self, nbytes: int) -> int:
+        if not 0 <= nbytes <= self.nbytes:
+            raise ValueError("offset outside the buffer")
+        return self.ptr + int(nbytes)
+
+    def close(self):
+        if self.ptr and self.ctx.h:
+            self.ctx.lib.qm_free(self.ctx.h, self.ptr)
+        self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Context:
+    """One qm_context on one device (not thread-safe, one stream at a time)."""
+
+    def __init__(self, device: int = 0, code_object_dir: str | None = None):
+        self.lib = load_library()
+        h = _P(0)
+        cdir = str(code_object_dir).encode() if code_object_dir else None
+        st = self.lib.qm_create(C.byref(h), None, cdir, device)
+        if st != QM_OK:
+            raise MixerError(st, self.lib.qm_last_error(None).decode())
+        self.h = h.value
+        self.stream = None  # the context's own stream
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.qm_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, st: int):
+        if st != QM_OK:
+            raise MixerError(st, self.lib.qm_last_error(self.h).decode())
+
+    def last_error(self) -> str:
+        return self.lib.qm_last_error(self.h).decode()
+
+    # ---- plumbing -------------------------------------------------------
+    def alloc(self, nbytes: int) -> DeviceBuffer:
+        return DeviceBuffer(self, nbytes)
+
+    def upload(self, arr: np.ndarray, buf: DeviceBuffer | None = None) -> DeviceBuffer:
+        arr = np.ascontiguousarray(arr)
+        if buf is None:
+            buf = self.alloc(max(arr.nbytes, 1))
+        elif buf.nbytes < arr.nbytes:
+            raise ValueError("buffer too small")
+        self._check(self.lib.qm_memcpy_h2d(self.h, buf.ptr, arr.ctypes.data, arr.nbytes, self.stream))
+        return buf
+
+    def upload_to(self, addr: int, arr: np.ndarray):
+        arr = np.ascontiguousarray(arr)
+        self._check(self.lib.qm_memcpy_h2d(self.h, int(addr), arr.ctypes.data, arr.nbytes, self.stream))
+
+    def download(self, src, shape, dtype) -> np.ndarray:
+        out = np.empty(shape, dtype)
+        self._check(self.lib.qm_memcpy_d2h(self.h, out.ctypes.data, _addr(src), out.nbytes, self.stream))
+        return out
+
+    def copy(self, dst, src, nbytes: int):
+        self._check(self.lib.qm_memcpy_d2d(self.h, _addr(dst), _addr(src), int(nbytes), self.stream))
+
+    def memset(self, dst, value: int, nbytes: int):
+        self._check(self.lib.qm_memset(self.h, _addr(dst), value, int(nbytes), self.stream))
+
+    def fill_normal(self, dst, dtype: int, count: int, mean: float, std: float, seed: int):
+        self._check(self.lib.qm_fill_normal(self.h, _addr(dst), dtype, int(count), mean, std, int(seed), self.stream))
+
+    def sync(self):
+        self._check(self.lib.qm_sync(self.h, self.stream))
+
+    def reserve(self, max_batch: int, max_kv_len: int = 0, max_prefill_tokens: int = 0):
+        self._check(self.lib.qm_reserve(self.h, max_batch, max_kv_len, max_prefill_tokens))
+
+    def set_option(self, option: int, value: int):
+        self._check(self.lib.qm_set_option(self.h, option, int(value)))
+
+    def event(self) -> "Event":
+        return Event(self)
+
+    def graph_begin(self):
+        self._check(self.lib.qm_graph_begin(self.h, self.stream))
+
+    def graph_end(self) -> "Graph":
+        g = _P(0)
+        self._check(self.lib.qm_graph_end(self.h, self.stream, C.byref(g)))
+        return Graph(self, g.value)
+
+    # ---- mixer ops --------------------------------------------------------
+    def deltanet_decode(self, batch, flags, qkv, conv_buf, conv_w, a, b, a_log, dt_bias, z,
+                        norm_w, state, out, state_stride=DN_V_HEADS * DN_HD * DN_HD):
+        self._check(self.lib.qm_deltanet_decode(
+            self.h, self.stream, batch, flags, _addr(qkv), _addr(conv_buf), _addr(conv_w),
+            _addr(a), _addr(b), _addr(a_log), _addr(dt_bias), _addr(z), _addr(norm_w),
+            _addr(state), state_stride, _addr(out)))
+
+    def deltanet_prefill(self, seq_len, qkv, conv_buf, conv_w, a, b, a_log, dt_bias, z, norm_w,
+                         state, out):
+        self._check(self.lib.qm_deltanet_prefill(
+            self.h, self.stream, seq_len, _addr(qkv), _addr(conv_buf), _addr(conv_w), _addr(a),
+            _addr(b), _addr(a_log), _addr(dt_bias), _addr(z), _addr(norm_w), _addr(state),
+            _addr(out)))
+
+    def gqa_decode(self, batch, q_gate, k_new, v_new, q_norm, k_norm, rope_cos, rope_sin,
+                   rope_len, pos, max_pos, k_cache, v_cache, cap, out):
+        self._check(self.lib.qm_gqa_decode(
+            self.h, self.stream, batch, _addr(q_gate), _addr(k_new), _addr(v_new), _addr(q_norm),
+            _addr(k_norm), _addr(rope_cos), _addr(rope_sin), rope_len, _addr(pos), max_pos,
+            _addr(k_cache), _addr(v_cache), cap, _addr(out)))
+
+    def gqa_prefill(self, seq_len, q_gate, k, v, q_norm, k_norm, rope_cos, rope_sin, rope_len,
+                    k_cache, v_cache, cap, out):
+        self._check(self.lib.qm_gqa_prefill(
+            self.h, self.stream, seq_len, _addr(q_gate), _addr(k), _addr(v), _addr(q_norm),
+            _addr(k_norm), _addr(rope_cos), _addr(rope_sin), rope_len, _addr(k_cache),
+            _addr(v_cache), cap, _addr(out)))
+
+
+class Event:
+    def __init__(self, ctx: Context):
+        self.ctx = ctx
+        e = _P(0)
+        ctx._check(ctx.lib.qm_event_create(ctx.h, C.byref(e)))
+        self.h = e.value
+
+    def record(self):
+        self.ctx._check(self.ctx.lib.qm_event_record(self.ctx.h, self.h, self.ctx.stream))
+
+    def elapsed_ms(self, later: "Event") -> float:
+        ms = C.c_float(0)
+        self.ctx._check(self.ctx.lib.qm_event_elapsed_ms(self.ctx.h, self.h, later.h, C.byref(ms)))
+        return float(ms.value)
+
+    def __del__(self):
+        try:
+            if self.h and self.ctx.h:
+                self.ctx.lib.qm_event_destroy(self.ctx.h, self.h)
+        except Exception:
+            pass
+
+
+class Graph:
+    def __init__(self, ctx: Context, h: int):
+        self.ctx = ctx
+        self.h = h
+
+    def launch(self):
+        self.ctx._check(self.ctx.lib.qm_graph_launch(self.ctx.h, self.h, self.ctx.stream))
+
+    def close(self):
+        if self.h and self.ctx.h:
+            self.ctx.lib.qm_graph_destroy(self.ctx.h, self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

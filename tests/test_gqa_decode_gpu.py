@@ -1,0 +1,107 @@
+"""GPU parity: GQA decode step (qm_gqa_decode) vs the CPU oracle.
+
+The oracle restates gemv.rs:927-1011 on an f32 cache in the reference's
+[seq][kv_head][dim] layout, filled with the f16 cache values (exact), with
+the appended row rounded to f16 as the MI355X cache stores it.  Bar:
+max-abs <= 1e-3 on the gated output.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import load_mixer, load_oracle, load_workloads
+
+pytestmark = pytest.mark.gpu
+
+M = load_mixer()
+O = load_oracle()
+W = load_workloads()
+TOL = 1e-3
+
+
+def run_gpu(ctx, w, positions, rope_rows, chunk=0):
+    B = w["q_gate"].shape[0]
+    cos, sin = M.rope_table(rope_rows)
+    d = {k: ctx.upload(w[k]) for k in ["q_gate", "k_new", "v_new", "q_norm", "k_norm", "k_cache", "v_cache"]}
+    rc, rs = ctx.upload(cos), ctx.upload(sin)
+    pos_dev = ctx.upload(np.asarray(positions, np.int32))
+    out = ctx.alloc(B * 16 * 256 * 4)
+    ctx.set_option(M.QM_OPT_GQA_DECODE_CHUNK, chunk)
+    try:
+        ctx.gqa_decode(B, d["q_gate"], d["k_new"], d["v_new"], d["q_norm"], d["k_norm"], rc, rs,
+                       rope_rows, pos_dev, int(max(positions)), d["k_cache"], d["v_cache"], w["cap"], out)
+    finally:
+        ctx.set_option(M.QM_OPT_GQA_DECODE_CHUNK, 0)
+    o = ctx.download(out, (B, 16, 256), np.float32)
+    kc = ctx.download(d["k_cache"], w["k_cache"].shape, np.uint16)
+    vc = ctx.download(d["v_cache"], w["v_cache"].shape, np.uint16)
+    return o, kc, vc
+
+
+def run_oracle(w, positions, rope_rows):
+    cfg = O.config()
+    cos, sin = O.rope_table(rope_rows)
+    B = w["q_gate"].shape[0]
+    outs, krows, vrows = [], [], []
+    for b in range(B):
+        p = positions[b]
+        K = np.ascontiguousarray(np.transpose(W.f16_value(w["k_cache"][b, :, :p + 1]), (1, 0, 2)))
+        V = np.ascontiguousarray(np.transpose(W.f16_value(w["v_cache"][b, :, :p + 1]), (1, 0, 2)))
+        o = O.attn_decode_step(cfg, w["q_gate"][b].ravel(), w["k_new"][b].ravel(), w["v_new"][b].ravel(),
+                               w["q_norm"], w["k_norm"], cos, sin, K, V, p, round_kv_f16=True, nthreads=8)
+        outs.append(o.reshape(16, 256))
+        krows.append(K[p])
+        vrows.append(V[p])
+    return np.stack(outs), krows, vrows
+
+
+def test_decode_pos4096_batch1(ctx):
+    """One step at position 4096 (4097 keys), f16 cache."""
+    w = W.gqa_decode_workload(4096, 1, seed=1)
+    print("case: gqa decode B=1 pos=4096", flush=True)
+    got, kc, vc = run_gpu(ctx, w, [4096], 4097)
+    ref, krows, vrows = run_oracle(w, [4096], 4097)
+    err = np.abs(got - ref).max()
+    print(f"max|dout|={err:.3e}")
+    assert err <= TOL
+    # appended rows: f16 of the normed+roped k (within one f16 step) and of v (exact)
+    kgot = W.f16_value(kc[0, :, 4096])
+    assert np.all(np.abs(kgot - krows[0]) <= np.abs(krows[0]) * 2 ** -10 + 1e-7)
+    assert np.array_equal(W.f16_value(vc[0, :, 4096]), vrows[0])
+
+
+def test_decode_ragged_positions(ctx):
+    """Sequences at different positions in one batch (pos_dev)."""
+    positions = [0, 100, 2049, 777]
+    w = W.gqa_decode_workload(2049, 4, cap=2100, seed=2)
+    print("case: gqa decode ragged", positions, flush=True)
+    got, _, _ = run_gpu(ctx, w, positions, 4096)
+    ref, _, _ = run_oracle(w, positions, 4096)
+    print(f"max|dout|={np.abs(got - ref).max():.3e}")
+    assert np.abs(got - ref).max() <= TOL
+
+
+@pytest.mark.parametrize("chunk", [64, 192, 1024, 4160])
+def test_decode_chunk_invariance(ctx, chunk):
+    w = W.gqa_decode_workload(3000, 2, seed=3)
+    print(f"case: gqa decode chunk={chunk}", flush=True)
+    got, _, _ = run_gpu(ctx, w, [3000, 3000], 3001, chunk=chunk)
+    ref, _, _ = run_oracle(w, [3000, 3000], 3001)
+    assert np.abs(got - ref).max() <= TOL
+
+
+def test_decode_range_errors(ctx):
+    w = W.gqa_decode_workload(16, 1, cap=17, seed=4)
+    cos, sin = M.rope_table(16)
+    d = {k: ctx.upload(w[k]) for k in ["q_gate", "k_new", "v_new", "q_norm", "k_norm", "k_cache", "v_cache"]}
+    rc, rs = ctx.upload(cos), ctx.upload(sin)
+    out = ctx.alloc(16 * 256 * 4)
+    with pytest.raises(M.MixerError) as e:      # position 16 with a 16-row table
+        ctx.gqa_decode(1, d["q_gate"], d["k_new"], d["v_new"], d["q_norm"], d["k_norm"], rc, rs, 16,
+                       None, 16, d["k_cache"], d["v_cache"], 17, out)
+    assert e.value.code == 5
+    with pytest.raises(M.MixerError) as e:      # position 17 with capacity 17
+        ctx.gqa_decode(1, d["q_gate"], d["k_new"], d["v_new"], d["q_norm"], d["k_norm"], rc, rs, 64,
+                       None, 17, d["k_cache"], d["v_cache"], 17, out)
+    assert e.value.code == 6
