@@ -1,0 +1,410 @@
+#!/usr/bin/env python3
+"""Token-mixer benchmark on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--workload NAME]
+
+Workloads (synthetic, seeded; inputs resident in HBM before timing):
+  stack       32-layer hybrid mixer stack (3x DeltaNet + 1x GQA, x8) in batched
+              decode: 64 sequences at context 32768, one step = one token per
+              sequence through all 32 mixers.  Default; the headline line.
+  dn_decode   one DeltaNet layer, batch 1, one step = one token.
+  gqa_decode  one GQA layer, batch 1, one step at position 4096.
+Prints one JSON line with throughput, the dominant kernel's roofline
+position (average launch time from HIP events on the launch stream) and the
+CPU oracle timed on this host on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+HBM_PEAK = 8.0e12          # MI355X HBM3E, bytes/s
+N_DN, N_GQA = 24, 8        # 3x DeltaNet + 1x GQA, repeated 8 times (config.rs:44-50)
+
+
+def _load(name, path):
+    spec = importlib.util.spec_from_file_location(name, path)
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+M = _load("qora_mixer", ROOT / "qora-llm-4b_amd" / "qora_mixer.py")
+W = _load("qora_workloads", ROOT / "qora-llm-4b_amd" / "workloads.py")
+
+
+def host_cores() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+# ----------------------------------------------------------------------------
+# algorithmic bytes
+def dn_decode_bytes(batch: int) -> int:
+    """State read + write plus the per-token vectors, per launch."""
+    state = 2 * 32 * 128 * 128 * 4
+    vec = (8192 + 32 + 32 + 4096 + 4096) * 4          # act q|k|v, a, b, z, out
+    params = (32 + 32) * 4 + 128 * 2                   # A_log, dt_bias, norm weight
+    return batch * (state + vec) + params
+
+
+def gqa_decode_bytes(batch: int, length: int) -> int:
+    """K and V rows 0..len-1 read, new row written, per-token vectors."""
+    kv = 2 * 4 * length * 256 * 2
+    vec = (16 * 512 + 2 * 4 * 256 + 16 * 256) * 4
+    rope = 2 * 32 * 4
+    return batch * (kv + vec + rope) + 2 * 256 * 2
+
+
+# ----------------------------------------------------------------------------
+class Timer:
+    """HIP events on the launch stream around every launch of one kernel."""
+
+    def __init__(self, ctx):
+        self.ctx = ctx
+        self.pairs = []
+
+    def wrap(self, fn):
+        a, b = self.ctx.event(), self.ctx.event()
+        a.record()
+        fn()
+        b.record()
+        self.pairs.append((a, b))
+
+    def mean_ms(self):
+        return float(np.mean([a.elapsed_ms(b) for a, b in self.pairs])) if self.pairs else float("nan")
+
+
+def run_stack(args, ctx):
+    B, ctx0 = 64, 32768
+    K, Wm = args.steps, args.warmup
+    total_steps = K + Wm
+    cap = ctx0 + total_steps
+    rope_rows = cap + 1
+    rng = np.random.default_rng(4)
+    seed = [1000]
+
+    def fill(buf, dtype, count, std, mean=0.0):
+        seed[0] += 1
+        ctx.fill_normal(buf, dtype, count, mean, std, seed[0])
+
+    # per-layer parameters (host generated, tiny)
+    dn_par = []
+    for _ in range(N_DN):
+        p = W.dn_params(rng)
+        dn_par.append({k: ctx.upload(p[k]) for k in ["a_log", "dt_bias", "norm_w"]})
+    gqa_par = []
+    for _ in range(N_GQA):
+        gqa_par.append({
+            "q_norm": ctx.upload(W.f16_bits(0.1 * rng.standard_normal(256, dtype=np.float32))),
+            "k_norm": ctx.upload(W.f16_bits(0.1 * rng.standard_normal(256, dtype=np.float32))),
+        })
+    cos, sin = M.rope_table(rope_rows)
+    rc, rs = ctx.upload(cos), ctx.upload(sin)
+
+    # state, caches, per-step inputs: all in HBM
+    S_LAYER = B * 32 * 128 * 128
+    states = [ctx.alloc(S_LAYER * 4) for _ in range(N_DN)]
+    for s in states:
+        fill(s, M.QM_F32, S_LAYER, 0.02)
+    KV_LAYER = B * 4 * cap * 256
+    kcs = [ctx.alloc(KV_LAYER * 2) for _ in range(N_GQA)]
+    vcs = [ctx.alloc(KV_LAYER * 2) for _ in range(N_GQA)]
+    for buf in kcs + vcs:
+        fill(buf, M.QM_F16, KV_LAYER, 1.0)
+    DN_IN = B * (8192 + 32 + 32 + 4096)
+    dn_in = ctx.alloc(total_steps * N_DN * DN_IN * 4)
+    fill(dn_in, M.QM_F32, total_steps * N_DN * DN_IN, 1.0)
+    GQA_IN = B * (16 * 512 + 2 * 4 * 256)
+    gqa_in = ctx.alloc(total_steps * N_GQA * GQA_IN * 4)
+    fill(gqa_in, M.QM_F32, total_steps * N_GQA * GQA_IN, 1.0)
+    dn_out = ctx.alloc(B * 4096 * 4)
+    gqa_out = ctx.alloc(B * 16 * 256 * 4)
+    ctx.reserve(max_batch=B, max_kv_len=cap)
+    ctx.sync()
+
+    dn_timer, gqa_timer = Timer(ctx), Timer(ctx)
+
+    def step(s, timed):
+        pos = ctx0 + s
+        li_dn = li_gqa = 0
+        for layer in range(32):
+            if layer % 4 != 3:
+                base = dn_in.offset(((s * N_DN + li_dn) * DN_IN) * 4)
+                qkv = base
+                a = base + B * 8192 * 4
+                b = a + B * 32 * 4
+                z = b + B * 32 * 4
+                p = dn_par[li_dn]
+                call = lambda: ctx.deltanet_decode(B, M.QM_DN_POSTACT, qkv, None, None, a, b,
+                                                   p["a_log"], p["dt_bias"], z, p["norm_w"],
+                                                   states[li_dn], dn_out)
+                dn_timer.wrap(call) if timed else call()
+                li_dn += 1
+            else:
+                base = gqa_in.offset(((s * N_GQA + li_gqa) * GQA_IN) * 4)
+                qg = base
+                kn = qg + B * 16 * 512 * 4
+                vn = kn + B * 4 * 256 * 4
+                p = gqa_par[li_gqa]
+                call = lambda: ctx.gqa_decode(B, qg, kn, vn, p["q_norm"], p["k_norm"], rc, rs,
+                                              rope_rows, None, pos, kcs[li_gqa], vcs[li_gqa], cap,
+                                              gqa_out)
+                gqa_timer.wrap(call) if timed else call()
+                li_gqa += 1
+
+    for s in range(Wm):
+        step(s, False)
+    ctx.sync()
+    t0 = ctx.event()
+    t1 = ctx.event()
+    wall0 = time.perf_counter()
+    t0.record()
+    for s in range(Wm, Wm + K):
+        step(s, True)
+    t1.record()
+    ctx.sync()
+    wall = time.perf_counter() - wall0
+    total_ms = t0.elapsed_ms(t1)
+
+    # GQA kernel: average length over the timed steps
+    mean_len = ctx0 + Wm + (K - 1) / 2.0 + 1
+    gqa_ms = gqa_timer.mean_ms()
+    dn_ms = dn_timer.mean_ms()
+    gqa_bytes = gqa_decode_bytes(B, int(round(mean_len)))
+    dn_bytes = dn_decode_bytes(B)
+    step_bytes = N_DN * dn_bytes + N_GQA * gqa_bytes
+    res = {
+        "tokens": B * K, "total_ms": total_ms, "wall_s": wall,
+        "dominant": "qm_gqa_decode_split+merge",
+        "roofline": {"bound": "hbm", "achieved": gqa_bytes / (gqa_ms * 1e-3), "peak": HBM_PEAK,
+                     "unit": "GB/s", "kernel_ms": gqa_ms, "bytes_per_launch": gqa_bytes},
+        "kernels": {
+            "qm_gqa_decode_split+merge": {"avg_ms": gqa_ms, "bytes": gqa_bytes,
+                              "GB_s": gqa_bytes / gqa_ms / 1e6, "frac_hbm": gqa_bytes / (gqa_ms * 1e-3) / HBM_PEAK},
+            "qm_dn_decode_t256": {"avg_ms": dn_ms, "bytes": dn_bytes,
+                                "GB_s": dn_bytes / dn_ms / 1e6, "frac_hbm": dn_bytes / (dn_ms * 1e-3) / HBM_PEAK},
+        },
+        "step_frac_hbm": step_bytes * K / (total_ms * 1e-3) / HBM_PEAK,
+        "config": {"workload": "hybrid mixer stack decode: 32 layers (24 DeltaNet + 8 GQA), "
+                               "64 sequences, context 32768, f16 KV, fp32 state",
+                   "batch": B, "context": ctx0, "layers": 32, "seq_len": ctx0, "global_batch": B,
+                   "parallelism": "single GPU"},
+    }
+    return res
+
+
+def run_dn_decode(args, ctx):
+    K, Wm = args.steps, args.warmup
+    w = W.dn_decode_workload(K + Wm, 1, seed=0)
+    up = ctx.upload
+    qkv, a, b, z = up(w["qkv"]), up(w["a"]), up(w["b"]), up(w["z"])
+    a_log, dt_bias, norm_w = up(w["a_log"]), up(w["dt_bias"]), up(w["norm_w"])
+    state = up(w["state0"])
+    out = ctx.alloc((K + Wm) * 4096 * 4)
+    ctx.reserve(max_batch=1)
+
+    def step(t):
+        ctx.deltanet_decode(1, M.QM_DN_POSTACT, qkv.offset(t * 8192 * 4), None, None,
+                            a.offset(t * 32 * 4), b.offset(t * 32 * 4), a_log, dt_bias,
+                            z.offset(t * 4096 * 4), norm_w, state, out.offset(t * 4096 * 4))
+
+    for t in range(Wm):
+        step(t)
+    # the timed steps run from one captured graph (one launch per step inside)
+    ctx.graph_begin()
+    for t in range(Wm, Wm + K):
+        step(t)
+    g = ctx.graph_end()
+    ctx.sync()
+    t0, t1 = ctx.event(), ctx.event()
+    wall0 = time.perf_counter()
+    t0.record()
+    g.launch()
+    t1.record()
+    ctx.sync()
+    wall = time.perf_counter() - wall0
+    total_ms = t0.elapsed_ms(t1)
+    # per-launch time, eager, events around each launch
+    tm = Timer(ctx)
+    for t in range(min(K, 64)):
+        tm.wrap(lambda: step(Wm + t))
+    ctx.sync()
+    k_ms = tm.mean_ms()
+    nbytes = dn_decode_bytes(1)
+    return {
+        "tokens": K, "total_ms": total_ms, "wall_s": wall, "dominant": "qm_dn_decode_t1024",
+        "roofline": {"bound": "hbm", "achieved": nbytes / (k_ms * 1e-3), "peak": HBM_PEAK,
+                     "unit": "GB/s", "kernel_ms": k_ms, "bytes_per_launch": nbytes},
+        "graph_ms_per_step": total_ms / K,
+        "config": {"workload": "DeltaNet decode, 1 layer, batch 1, 16 qk / 32 v heads x 128, fp32 state",
+                   "batch": 1, "seq_len": K, "global_batch": 1, "parallelism": "single GPU"},
+    }
+
+
+def run_gqa_decode(args, ctx):
+    K, Wm = args.steps, args.warmup
+    pos = 4096
+    w = W.gqa_decode_workload(pos, 1, seed=1)
+    cos, sin = M.rope_table(pos + 1)
+    d = {k: ctx.upload(w[k]) for k in ["q_gate", "k_new", "v_new", "q_norm", "k_norm", "k_cache", "v_cache"]}
+    rc, rs = ctx.upload(cos), ctx.upload(sin)
+    out = ctx.alloc(16 * 256 * 4)
+    ctx.reserve(max_batch=1, max_kv_len=pos + 1)
+
+    def step():
+        ctx.gqa_decode(1, d["q_gate"], d["k_new"], d["v_new"], d["q_norm"], d["k_norm"], rc, rs,
+                       pos + 1, None, pos, d["k_cache"], d["v_cache"], w["cap"], out)
+
+    for _ in range(Wm):
+        step()
+    ctx.sync()
+    tm = Timer(ctx)
+    t0, t1 = ctx.event(), ctx.event()
+    wall0 = time.perf_counter()
+    t0.record()
+    for _ in range(K):
+        tm.wrap(step)
+    t1.record()
+    ctx.sync()
+    wall = time.perf_counter() - wall0
+    total_ms = t0.elapsed_ms(t1)
+    k_ms = tm.mean_ms()
+    nbytes = gqa_decode_bytes(1, pos + 1)
+    return {
+        "tokens": K, "total_ms": total_ms, "wall_s": wall, "dominant": "qm_gqa_decode_split+merge",
+        "roofline": {"bound": "hbm", "achieved": nbytes / (k_ms * 1e-3), "peak": HBM_PEAK,
+                     "unit": "GB/s", "kernel_ms": k_ms, "bytes_per_launch": nbytes},
+        "config": {"workload": "GQA decode, 1 layer, batch 1, 16q/4kv x 256, position 4096, f16 KV",
+                   "batch": 1, "seq_len": pos + 1, "global_batch": 1, "parallelism": "single GPU"},
+    }
+
+
+# ----------------------------------------------------------------------------
+# CPU baseline: the oracle (C restatement of the reference CPU path) on this host
+def cpu_baseline(workload: str) -> dict:
+    O = _load("qora_oracle_py", ROOT / "oracle" / "oracle.py")
+    cores = host_cores()
+    att_threads = min(16, cores)
+    cfg = O.config()
+    if workload == "dn_decode":
+        steps = 256
+        w = W.dn_decode_workload(steps, 1, seed=0)
+        S = w["state0"][0].copy()
+        t0 = time.perf_counter()
+        for t in range(steps):
+            O.deltanet_decode_step(cfg, w["qkv"][t, 0], w["a"][t, 0], w["b"][t, 0], w["z"][t, 0],
+                                   w["conv_w"], w["a_log"], w["dt_bias"], w["norm_w"], S)
+        dt = time.perf_counter() - t0
+        return {"value": steps / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
+                "sample": f"256 decode steps, batch 1, {'AVX-512' if O.has_avx512() else 'scalar'} head update, 1 thread"}
+    if workload == "gqa_decode":
+        pos = 4096
+        w = W.gqa_decode_workload(pos, 1, seed=1)
+        cos, sin = O.rope_table(pos + 1)
+        K = np.ascontiguousarray(np.transpose(W.f16_value(w["k_cache"][0]), (1, 0, 2)))
+        V = np.ascontiguousarray(np.transpose(W.f16_value(w["v_cache"][0]), (1, 0, 2)))
+        reps = 20
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            O.attn_decode_step(cfg, w["q_gate"][0].ravel(), w["k_new"][0].ravel(), w["v_new"][0].ravel(),
+                               w["q_norm"], w["k_norm"], cos, sin, K, V, pos, nthreads=att_threads)
+        dt = time.perf_counter() - t0
+        return {"value": reps / dt, "unit": "tokens/s", "cores": att_threads, "kind": "port",
+                "sample": f"{reps} decode steps at position 4096, f32 KV, heads over {att_threads} threads"}
+    # stack: one sequence, a few decode steps through all 32 layers at context 32768
+    steps, ctx0 = 2, 32768
+    rng = np.random.default_rng(7)
+    cos, sin = O.rope_table(ctx0 + steps + 1)
+    dn_w = [W.dn_params(rng) for _ in range(N_DN)]
+    dn_S = [(0.02 * rng.standard_normal((32, 128, 128), dtype=np.float32)) for _ in range(N_DN)]
+    caches = []
+    for _ in range(N_GQA):
+        Kc = np.empty((ctx0 + steps, 4, 256), np.float32)
+        Vc = np.empty_like(Kc)
+        Kc[:ctx0] = W.f16_value(W.f16_bits(rng.standard_normal((ctx0, 4, 256), dtype=np.float32)))
+        Vc[:ctx0] = W.f16_value(W.f16_bits(rng.standard_normal((ctx0, 4, 256), dtype=np.float32)))
+        caches.append((Kc, Vc))
+    qn = W.f16_bits(0.1 * rng.standard_normal(256, dtype=np.float32))
+    dn_in = rng.standard_normal((steps, N_DN, 8192 + 32 + 32 + 4096), dtype=np.float32)
+    g_in = rng.standard_normal((steps, N_GQA, 16 * 512 + 2 * 1024), dtype=np.float32)
+    t0 = time.perf_counter()
+    for s in range(steps):
+        li_dn = li_g = 0
+        for layer in range(32):
+            if layer % 4 != 3:
+                p, x = dn_w[li_dn], dn_in[s, li_dn]
+                O.deltanet_decode_step(cfg, x[:8192], x[8192:8224], x[8224:8256], x[8256:],
+                                       p["conv_w"], p["a_log"], p["dt_bias"], p["norm_w"], dn_S[li_dn])
+                li_dn += 1
+            else:
+                Kc, Vc = caches[li_g]
+                x = g_in[s, li_g]
+                O.attn_decode_step(cfg, x[:8192], x[8192:9216], x[9216:], qn, qn, cos, sin,
+                                   Kc, Vc, ctx0 + s, nthreads=att_threads)
+                li_g += 1
+    dt = time.perf_counter() - t0
+    return {"value": steps / dt, "unit": "tokens/s", "cores": att_threads, "kind": "port",
+            "sample": f"1 sequence x {steps} decode steps through 32 layers at context {ctx0}; "
+                      f"f32 KV (the reference's storage), attention heads over {att_threads} threads, "
+                      f"DeltaNet heads serial (AVX-512 update: {O.has_avx512()})"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--workload", default="stack", choices=["stack", "dn_decode", "gqa_decode"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: the mixer path here is a single-GPU build "
+              "(sharding is a design note, not a launched path); run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    defaults = {"stack": (32, 4), "dn_decode": (256, 16), "gqa_decode": (200, 20)}[args.workload]
+    args.steps = args.steps or defaults[0]
+    args.warmup = defaults[1] if args.warmup is None else args.warmup
+
+    ctx = M.Context(0)
+    run = {"stack": run_stack, "dn_decode": run_dn_decode, "gqa_decode": run_gqa_decode}[args.workload]
+    r = run(args, ctx)
+    ctx.sync()
+    ctx.close()
+
+    value = r["tokens"] / (r["total_ms"] * 1e-3)
+    roof = r["roofline"]
+    line = {
+        "metric": "mixer tokens/s (decode) on 1x MI355X" if args.workload != "stack"
+        else "mixer tokens/s (decode, 32-layer hybrid stack) on 1x MI355X",
+        "value": value, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": r["total_ms"] / args.steps,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded normal inputs, random-init state and f16 KV cache)",
+        "config": r["config"],
+        "roofline": {"bound": roof["bound"], "achieved": roof["achieved"] / 1e9, "peak": roof["peak"] / 1e9,
+                     "unit": "GB/s", "frac": roof["achieved"] / roof["peak"], "traffic": None,
+                     "kernel": r["dominant"], "kernel_avg_ms": roof["kernel_ms"],
+                     "bytes_per_launch": roof["bytes_per_launch"]},
+    }
+    for k in ("kernels", "step_frac_hbm", "graph_ms_per_step"):
+        if k in r:
+            line[k] = r[k]
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(args.workload)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

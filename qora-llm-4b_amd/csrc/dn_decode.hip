@@ -10,13 +10,13 @@
 // passes (decay, retrieve, update, output; simd.rs:304-361):
 //   Sd = alpha*S; p = Sd.k; delta = beta*(v[r]-p); S' = Sd + delta*k;
 //   y[r] = S'.q  (S' is still in registers).
-// Layout: a workgroup owns 128/SPLITS rows of one (sequence, v-head).  A
-// 16-lane DPP row owns one state row at a time; lane l holds columns
-// 4l..4l+3 and 64+4l..64+4l+3, so every dwordx4 load of a wave covers four
-// consecutive rows contiguously.  Row dot products reduce inside the DPP
-// row (4 DPP adds, no LDS).  With SPLITS > 1 the head is split over
-// workgroups (more CUs busy at batch 1) and the last workgroup to finish a
-// head (arrival counter) applies the norm.
+// Layout: a workgroup owns one (sequence, v-head), all 128 rows.  A 16-lane
+// DPP row owns one state row at a time; lane l holds columns 4l..4l+3 and
+// 64+4l..64+4l+3, so every dwordx4 load of a wave covers four consecutive
+// rows contiguously.  Row dot products reduce inside the DPP row (4 DPP
+// adds, no LDS).  The head never spans workgroups: publishing rows to
+// another workgroup needs an agent-scope fence, i.e. an L2 writeback and
+// invalidate, which measured 4-50x slower than the whole update.
 #include "qm_device.h"
 #include "qm_kernel_args.h"
 
@@ -67,37 +67,34 @@ QM_DEV void l2norm_row(float4& x0, float4& x1) {
     }
 }
 
-template <int SPLITS>
+template <int RPG>
 QM_DEV void dn_decode_body(const DnDecodeArgs& A) {
-    constexpr int ROWS_WG = QM_DN_HD / SPLITS;   // rows of the head per WG
-    constexpr int RPG = ROWS_WG / 16;            // rows per 16-lane group
-    static_assert(RPG >= 1, "split too fine");
+    constexpr int GROUPS = QM_DN_HD / RPG;       // 16-lane groups per workgroup
     __shared__ float ys[QM_DN_HD];
-    __shared__ uint32_t is_last;
 
     const int tid = threadIdx.x;
     const int g = tid >> 4, l = tid & 15;
     const int bid = blockIdx.x;
-    const int sp = bid % SPLITS;
-    const int vh = (bid / SPLITS) % QM_DN_V_HEADS;
-    const int b = bid / (SPLITS * QM_DN_V_HEADS);
+    const int vh = bid % QM_DN_V_HEADS;
+    const int b = bid / QM_DN_V_HEADS;
     const int qkh = vh >> 1;                      // GVA: vh -> vh/2 (gemv.rs:806)
-    const int r0 = sp * ROWS_WG;
 
     const float* act = A.act + (size_t)b * QM_DN_QKV_DIM;
     float* S = A.state + (size_t)b * A.state_stride + (size_t)vh * QM_DN_HEAD_ELEMS;
 
-    // Issue the state loads first: they are the HBM stream.
+    // Issue the state loads first: they are the HBM stream.  Group g owns
+    // rows g, g + GROUPS, ...; at each i the groups of a wave cover
+    // consecutive rows, so every wave instruction reads contiguous 2 KB.
     float4 s0[RPG], s1[RPG];
 #pragma unroll
     for (int i = 0; i < RPG; ++i) {
-        const float* row = S + (size_t)(r0 + g + 16 * i) * QM_DN_HD;
+        const float* row = S + (size_t)(g + GROUPS * i) * QM_DN_HD;
         s0[i] = ld4(row + 4 * l);
         s1[i] = ld4(row + 64 + 4 * l);
     }
     float vr[RPG];
 #pragma unroll
-    for (int i = 0; i < RPG; ++i) vr[i] = act[2 * 2048 + vh * QM_DN_HD + r0 + g + 16 * i];
+    for (int i = 0; i < RPG; ++i) vr[i] = act[2 * 2048 + vh * QM_DN_HD + g + GROUPS * i];
 
     float4 q0 = ld4(act + qkh * QM_DN_HD + 4 * l), q1 = ld4(act + qkh * QM_DN_HD + 64 + 4 * l);
     float4 k0 = ld4(act + 2048 + qkh * QM_DN_HD + 4 * l), k1 = ld4(act + 2048 + qkh * QM_DN_HD + 64 + 4 * l);
@@ -113,7 +110,6 @@ QM_DEV void dn_decode_body(const DnDecodeArgs& A) {
     const float alpha = expf(-a_exp * spl);
     const float beta = 1.0f / (1.0f + expf(-A.b[b * QM_DN_V_HEADS + vh]));
 
-    float y[RPG];
 #pragma unroll
     for (int i = 0; i < RPG; ++i) {
         const float4 d0 = scale4(s0[i], alpha), d1 = scale4(s1[i], alpha);
@@ -124,40 +120,13 @@ QM_DEV void dn_decode_body(const DnDecodeArgs& A) {
         n0.z = fmaf(delta, k0.z, d0.z); n0.w = fmaf(delta, k0.w, d0.w);
         n1.x = fmaf(delta, k1.x, d1.x); n1.y = fmaf(delta, k1.y, d1.y);
         n1.z = fmaf(delta, k1.z, d1.z); n1.w = fmaf(delta, k1.w, d1.w);
-        float* row = S + (size_t)(r0 + g + 16 * i) * QM_DN_HD;
+        float* row = S + (size_t)(g + GROUPS * i) * QM_DN_HD;
         st4(row + 4 * l, n0);
         st4(row + 64 + 4 * l, n1);
-        y[i] = row_sum16(dot8(n0, n1, q0, q1));
+        const float y = row_sum16(dot8(n0, n1, q0, q1));
+        if (l == 0) ys[g + GROUPS * i] = y;
     }
-
-    float* yo = A.out + (size_t)b * QM_DN_V_DIM + vh * QM_DN_HD;
-    if (SPLITS == 1) {
-        if (l == 0) {
-#pragma unroll
-            for (int i = 0; i < RPG; ++i) ys[g + 16 * i] = y[i];
-        }
-        __syncthreads();
-    } else {
-        // Publish this block's rows, then count arrivals for the head.
-        if (l == 0) {
-#pragma unroll
-            for (int i = 0; i < RPG; ++i) yo[r0 + g + 16 * i] = y[i];
-        }
-        __threadfence();
-        __syncthreads();
-        if (tid == 0) {
-            const uint32_t prev = atomicAdd(&A.counters[b * QM_DN_V_HEADS + vh], 1u);
-            is_last = (prev == SPLITS - 1) ? 1u : 0u;
-        }
-        __syncthreads();
-        if (!is_last) return;
-        __threadfence();
-        if (tid < QM_DN_HD)
-            ys[tid] = __hip_atomic_load(yo + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (tid == 0)
-            __hip_atomic_store(&A.counters[b * QM_DN_V_HEADS + vh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __syncthreads();
-    }
+    __syncthreads();
 
     // gemv.rs:865-883: per-head RMSNorm (plain gamma, eps 1e-6) * silu(z).
     // The sum of squares runs over rows 0..127 in order, as the reference.
@@ -168,11 +137,13 @@ QM_DEV void dn_decode_body(const DnDecodeArgs& A) {
         const float inv_rms = 1.0f / sqrtf(ss / (float)QM_DN_HD + 1e-6f);
         const float gm = f16_to_f32(A.norm_w[tid]);
         const float zz = A.z[(size_t)b * QM_DN_V_DIM + vh * QM_DN_HD + tid];
-        yo[tid] = ys[tid] * inv_rms * gm * silu_f(zz);
+        A.out[(size_t)b * QM_DN_V_DIM + vh * QM_DN_HD + tid] = ys[tid] * inv_rms * gm * silu_f(zz);
     }
 }
 
-extern "C" __global__ __launch_bounds__(256) void qm_dn_decode_s1(DnDecodeArgs A) { dn_decode_body<1>(A); }
-extern "C" __global__ __launch_bounds__(256) void qm_dn_decode_s2(DnDecodeArgs A) { dn_decode_body<2>(A); }
-extern "C" __global__ __launch_bounds__(256) void qm_dn_decode_s4(DnDecodeArgs A) { dn_decode_body<4>(A); }
-extern "C" __global__ __launch_bounds__(256) void qm_dn_decode_s8(DnDecodeArgs A) { dn_decode_body<8>(A); }
+// One workgroup per (sequence, v-head) holds the whole head, so the norm
+// needs no cross-workgroup exchange.  Variants differ only in threads per
+// workgroup (rows per 16-lane group 8 / 4 / 2 -> 256 / 512 / 1024 threads).
+extern "C" __global__ __launch_bounds__(256) void qm_dn_decode_t256(DnDecodeArgs A) { dn_decode_body<8>(A); }
+extern "C" __global__ __launch_bounds__(512) void qm_dn_decode_t512(DnDecodeArgs A) { dn_decode_body<4>(A); }
+extern "C" __global__ __launch_bounds__(1024) void qm_dn_decode_t1024(DnDecodeArgs A) { dn_decode_body<2>(A); }

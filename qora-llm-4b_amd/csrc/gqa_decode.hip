@@ -5,17 +5,26 @@
 // 0..63 at position pos, KV append (f16 cache), softmax attention over
 // positions 0..pos with kv head h/4, sigmoid output gate.
 //
-// One launch per step: split-K flash decode.  Workgroup (b, g, split) owns
+// Split-K flash decode.  Workgroup (b, g, split) of qm_gqa_decode_split owns
 // `chunk` cache positions of kv head g and all four query heads of g, so
 // each K/V byte is read from HBM once per step (the reference re-reads the
-// cache once per query head, gemv.rs:963-986).  The last workgroup of a
-// (b, g) to arrive merges the split partials and applies the gate.
+// cache once per query head, gemv.rs:963-986).  qm_gqa_decode_merge then
+// merges the split partials of each (b, g) and applies the gate; with a
+// single split the first kernel finishes the job itself.  The two-kernel
+// form is deliberate: handing partials to a last-arriving workgroup inside
+// one kernel needs agent-scope fences (an L2 writeback per workgroup), which
+// measured ~1.8 us of serialized L2 time per workgroup.
 //
-// QK^T runs on MFMA (v_mfma_f32_16x16x32_f16).  q is fp32 in the reference,
-// so it enters as an exact two-term f16 split q = q_hi + q_lo (rows 0..3 hi,
-// rows 4..7 lo of the A operand); K comes straight from the f16 cache as the
-// B operand and every product is exact in the fp32 accumulator.  PV stays on
-// VALU: each lane owns 4 of the 256 dims of all four heads.
+// The kernel is an HBM stream.  Each wave walks 16-key rounds; the K and V
+// rows of round r+1 are issued into a second register set before round r is
+// computed (a scheduling barrier keeps the compiler from sinking them), so
+// 16-32 KB per wave stay in flight.
+//   QK^T: MFMA v_mfma_f32_16x16x32_f16.  q is fp32 in the reference, so it
+//         enters as an exact two-term f16 split q = q_hi + q_lo (A rows 0..3
+//         hi, rows 4..7 lo); K comes straight from the f16 cache as the B
+//         operand; products are exact in the fp32 accumulator.
+//   PV:   VALU; each lane owns 4 of the 256 dims of all four heads; the 64
+//         probabilities of a round are broadcast through LDS.
 #include "qm_device.h"
 #include "qm_kernel_args.h"
 
@@ -23,10 +32,6 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 #define GQA_PART_STRIDE 260   // acc[256], m, l, pad[2]
-
-QM_DEV float ld_coherent(const float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // Per-head RMSNorm (1+gamma, eps 1e-6; gemv.rs:586-597) and split-half RoPE
 // (gemv.rs:604-627) of one 256-wide head held by a wave: lane owns dims
@@ -61,11 +66,100 @@ QM_DEV float4 norm_rope_head(float4 x, const uint16_t* gamma, const float* cos_r
     return x;
 }
 
-extern "C" __global__ __launch_bounds__(256) void qm_gqa_decode(GqaDecodeArgs A) {
+struct RoundBuf {
+    half8 k[8];     // B operand: key (lane & 15), dims 64*(lane>>4) + 8*s .. +7
+    uint2 v[16];    // V rows of the 16 keys, dims 4*lane .. 4*lane+3
+};
+
+// Issue the loads of one 16-key round (keys t0..t0+15, clamped to t_last so
+// every address is inside the cache; clamped keys are masked later).
+QM_DEV void load_round(RoundBuf& rb, const uint16_t* kbase, const uint16_t* vbase, int t0,
+                       int t_last, int arow, int aq, int lane) {
+    const int tk = min(t0 + arow, t_last);
+    const uint16_t* krow = kbase + (size_t)tk * QM_GQA_HD + 64 * aq;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) rb.k[s] = *reinterpret_cast<const half8*>(krow + 8 * s);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int tv = min(t0 + j, t_last);
+        rb.v[j] = *reinterpret_cast<const uint2*>(vbase + (size_t)tv * QM_GQA_HD + 4 * lane);
+    }
+}
+
+struct WaveState {
+    float m[4], l[4], acc[4][4];
+};
+
+// One 16-key round: scores on MFMA, online softmax, PV on VALU.
+QM_DEV void compute_round(WaveState& st, const RoundBuf& rb, const half8 (&afr)[8], int t0,
+                          int t_end, int lane, float4* pw /* LDS [16] of this wave */) {
+    floatx4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) c = __builtin_amdgcn_mfma_f32_16x16x32_f16(afr[s], rb.k[s], c, 0, 0, 0);
+    // D[i][j] sits in lane j + 16*(i/4), element i%4: lanes 0..15 carry the
+    // hi rows, lanes 16..31 the lo rows of key j = lane & 15.
+    const bool valid = (lane < 16) && (t0 + (lane & 15) < t_end);
+    const float scale = 1.0f / sqrtf((float)QM_GQA_HD);
+    float p[4], corr[4];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+        const float sc = (c[h] + __shfl_xor(c[h], 16)) * scale;
+        const float x = valid ? sc : -INFINITY;
+        const float mt = readlane_f32(row_max16(x), 0);
+        const float m_new = fmaxf(st.m[h], mt);
+        corr[h] = (st.m[h] == -INFINITY) ? 0.0f : expf(st.m[h] - m_new);
+        p[h] = valid ? expf(sc - m_new) : 0.0f;
+        const float ps = readlane_f32(row_sum16(p[h]), 0);
+        st.l[h] = st.l[h] * corr[h] + ps;
+        st.m[h] = m_new;
+    }
+    if (lane < 16) pw[lane] = make_float4(p[0], p[1], p[2], p[3]);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) st.acc[h][e] *= corr[h];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const float4 pj = pw[j];
+        const float v0 = f16_to_f32((uint16_t)(rb.v[j].x & 0xffffu));
+        const float v1 = f16_to_f32((uint16_t)(rb.v[j].x >> 16));
+        const float v2 = f16_to_f32((uint16_t)(rb.v[j].y & 0xffffu));
+        const float v3 = f16_to_f32((uint16_t)(rb.v[j].y >> 16));
+        const float ph[4] = {pj.x, pj.y, pj.z, pj.w};
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            st.acc[h][0] = fmaf(ph[h], v0, st.acc[h][0]);
+            st.acc[h][1] = fmaf(ph[h], v1, st.acc[h][1]);
+            st.acc[h][2] = fmaf(ph[h], v2, st.acc[h][2]);
+            st.acc[h][3] = fmaf(ph[h], v3, st.acc[h][3]);
+        }
+    }
+    // pw is rewritten next round: order those writes after these reads.
+    __builtin_amdgcn_wave_barrier();
+}
+
+// Gate and store one head's output: out = (acc / l) * sigmoid(gate).
+QM_DEV void gqa_store_out(const GqaDecodeArgs& A, int b, int qh, int lane, float o0, float o1,
+                          float o2, float o3, float Ls) {
+    const float inv = 1.0f / Ls;
+    const float* gate = A.q_gate + ((size_t)b * QM_GQA_HEADS + qh) * (2 * QM_GQA_HD) + QM_GQA_HD + 4 * lane;
+    const float4 gv = ld4(gate);
+    float4 r;
+    r.x = (o0 * inv) * sigmoid_f(gv.x);
+    r.y = (o1 * inv) * sigmoid_f(gv.y);
+    r.z = (o2 * inv) * sigmoid_f(gv.z);
+    r.w = (o3 * inv) * sigmoid_f(gv.w);
+    st4(A.out + ((size_t)b * QM_GQA_HEADS + qh) * QM_GQA_HD + 4 * lane, r);
+}
+
+extern "C" __global__ __launch_bounds__(256) void qm_gqa_decode_split(GqaDecodeArgs A) {
     __shared__ float qs[4][QM_GQA_HD];          // normed+roped q, heads 4g..4g+3
     __shared__ float wacc[4][4][QM_GQA_HD];     // per-wave partial PV
+    __shared__ float4 pbuf[4][16];              // per-wave probabilities of a round
     __shared__ float wm[4][4], wl[4][4];
-    __shared__ uint32_t is_last;
 
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int bid = blockIdx.x;
@@ -82,6 +176,19 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_decode(GqaDecodeArgs A)
     const float* cos_row = A.rope_cos + (size_t)pos * (QM_GQA_ROT / 2);
     const float* sin_row = A.rope_sin + (size_t)pos * (QM_GQA_ROT / 2);
     const size_t kv_base = ((size_t)b * QM_GQA_KV_HEADS + g) * (size_t)A.cap * QM_GQA_HD;
+    const uint16_t* kbase = A.k_cache + kv_base;
+    const uint16_t* vbase = A.v_cache + kv_base;
+
+    // 4a. Wave w takes rounds t_begin + 64*r + 16*w (r = 0 .. nr-1).  A
+    //     split that does not append issues its first round now, so the
+    //     loads overlap the q preparation.
+    const bool appends = (t_begin <= pos && pos < t_end);
+    const int span = t_end - t_begin - 16 * w;
+    const int nr = __builtin_amdgcn_readfirstlane(span > 0 ? (span + 63) / 64 : 0);
+    const int t_last = t_end - 1;
+    const int arow = lane & 15, aq = lane >> 4;
+    RoundBuf ra, rb;
+    if (!appends && nr > 0) load_round(ra, kbase, vbase, t_begin + 16 * w, t_last, arow, aq, lane);
 
     // 1. q prep: wave w handles query head 4g+w (gemv.rs:927-949).
     {
@@ -90,7 +197,7 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_decode(GqaDecodeArgs A)
         *reinterpret_cast<float4*>(&qs[w][4 * lane]) = x;
     }
     // 2. The split that holds position pos appends the new k, v (gemv.rs:946-956).
-    if (t_begin <= pos && pos < t_end) {
+    if (appends) {
         if (w == 0) {
             const float* kn = A.k_new + ((size_t)b * QM_GQA_KV_HEADS + g) * QM_GQA_HD;
             float4 x = norm_rope_head(ld4(kn + 4 * lane), A.k_norm, cos_row, sin_row, lane);
@@ -106,17 +213,20 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_decode(GqaDecodeArgs A)
             o.y = (uint32_t)f32_to_f16(x.z) | ((uint32_t)f32_to_f16(x.w) << 16);
             *reinterpret_cast<uint2*>(A.v_cache + kv_base + (size_t)pos * QM_GQA_HD + 4 * lane) = o;
         }
-        __threadfence();
+        // Make the appended row visible to the other waves' loads below.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     }
     __syncthreads();
-    __threadfence();
+    if (appends) {
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        if (nr > 0) load_round(ra, kbase, vbase, t_begin + 16 * w, t_last, arow, aq, lane);
+    }
 
     // 3. A operand: row i (= lane & 15) is q_hi of head i (i < 4), q_lo of
     //    head i-4 (4 <= i < 8), zero otherwise.  K-step s, lane group
     //    aq = lane >> 4 and element e map to head dim 64*aq + 8*s + e; the B
     //    operand uses the same map, so lane group aq streams a contiguous
     //    128-byte quarter of each key row.
-    const int arow = lane & 15, aq = lane >> 4;
     half8 afr[8];
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
@@ -129,76 +239,36 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_decode(GqaDecodeArgs A)
         }
     }
 
-    float m_run[4], l_run[4], acc[4][4];
+    WaveState st;
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
-        m_run[h] = -INFINITY; l_run[h] = 0.0f;
+        st.m[h] = -INFINITY; st.l[h] = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[h][e] = 0.0f;
+        for (int e = 0; e < 4; ++e) st.acc[h][e] = 0.0f;
     }
-    const float scale = 1.0f / sqrtf((float)QM_GQA_HD);
 
-    // 4. Keys in rounds of 64: wave w takes keys base+16w .. base+16w+15.
-    for (int base = t_begin; base < t_end; base += 64) {
-        const int t0 = base + 16 * w;
-        if (t0 >= t_end) break;
-        const int tk = min(t0 + arow, t_end - 1);            // clamped: in bounds
-        const uint16_t* krow = A.k_cache + kv_base + (size_t)tk * QM_GQA_HD + 64 * aq;
-        half8 kf[8];
-#pragma unroll
-        for (int s = 0; s < 8; ++s) kf[s] = *reinterpret_cast<const half8*>(krow + 8 * s);
-        uint2 vr[16];
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const int tv = min(t0 + j, t_end - 1);
-            vr[j] = *reinterpret_cast<const uint2*>(A.v_cache + kv_base + (size_t)tv * QM_GQA_HD + 4 * lane);
-        }
-        floatx4 c = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int s = 0; s < 8; ++s) c = __builtin_amdgcn_mfma_f32_16x16x32_f16(afr[s], kf[s], c, 0, 0, 0);
-        // D[i][j] sits in lane j + 16*(i/4), element i%4: lanes 0..15 carry
-        // the hi rows, lanes 16..31 the lo rows of key j = lane & 15.
-        const bool valid = (lane < 16) && (t0 + arow < t_end);
-        float p[4];
-#pragma unroll
-        for (int h = 0; h < 4; ++h) {
-            const float sc = (c[h] + __shfl_xor(c[h], 16)) * scale;
-            const float x = valid ? sc : -INFINITY;
-            const float mt = readlane_f32(row_max16(x), 0);
-            const float m_new = fmaxf(m_run[h], mt);
-            const float corr = (m_run[h] == -INFINITY) ? 0.0f : expf(m_run[h] - m_new);
-            p[h] = valid ? expf(sc - m_new) : 0.0f;
-            const float ps = readlane_f32(row_sum16(p[h]), 0);
-            l_run[h] = l_run[h] * corr + ps;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[h][e] *= corr;
-            m_run[h] = m_new;
-        }
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const float v0 = f16_to_f32((uint16_t)(vr[j].x & 0xffffu));
-            const float v1 = f16_to_f32((uint16_t)(vr[j].x >> 16));
-            const float v2 = f16_to_f32((uint16_t)(vr[j].y & 0xffffu));
-            const float v3 = f16_to_f32((uint16_t)(vr[j].y >> 16));
-#pragma unroll
-            for (int h = 0; h < 4; ++h) {
-                const float ph = readlane_f32(p[h], j);
-                acc[h][0] = fmaf(ph, v0, acc[h][0]);
-                acc[h][1] = fmaf(ph, v1, acc[h][1]);
-                acc[h][2] = fmaf(ph, v2, acc[h][2]);
-                acc[h][3] = fmaf(ph, v3, acc[h][3]);
-            }
-        }
+    // 4b. Stream the rounds, next round's loads in flight during compute.
+    float4* pw = pbuf[w];
+    for (int r = 0; r < nr; r += 2) {
+        const int t0 = t_begin + 64 * r + 16 * w;
+        if (r + 1 < nr) load_round(rb, kbase, vbase, t0 + 64, t_last, arow, aq, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        compute_round(st, ra, afr, t0, t_end, lane, pw);
+        if (r + 1 >= nr) break;
+        if (r + 2 < nr) load_round(ra, kbase, vbase, t0 + 128, t_last, arow, aq, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        compute_round(st, rb, afr, t0 + 64, t_end, lane, pw);
     }
 
     // 5. Merge the four waves, write this split's partial.
     if (lane == 0) {
 #pragma unroll
-        for (int h = 0; h < 4; ++h) { wm[w][h] = m_run[h]; wl[w][h] = l_run[h]; }
+        for (int h = 0; h < 4; ++h) { wm[w][h] = st.m[h]; wl[w][h] = st.l[h]; }
     }
 #pragma unroll
     for (int h = 0; h < 4; ++h)
-        *reinterpret_cast<float4*>(&wacc[w][h][4 * lane]) = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+        *reinterpret_cast<float4*>(&wacc[w][h][4 * lane]) =
+            make_float4(st.acc[h][0], st.acc[h][1], st.acc[h][2], st.acc[h][3]);
     __syncthreads();
     {
         const int h = w;                      // thread (h, lane): dims 4*lane..+3
@@ -214,51 +284,45 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_decode(GqaDecodeArgs A)
             const float4 a = *reinterpret_cast<const float4*>(&wacc[ww][h][4 * lane]);
             o.x += a.x * f; o.y += a.y * f; o.z += a.z * f; o.w += a.w * f;
         }
-        float* P = A.partial + ((((size_t)b * QM_GQA_KV_HEADS + g) * A.nsplit + split) * 4 + h) * GQA_PART_STRIDE;
-        st4(P + 4 * lane, o);
-        if (lane == 0) { P[256] = M; P[257] = Ls; }
-    }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t prev = atomicAdd(&A.counters[b * QM_GQA_KV_HEADS + g], 1u);
-        is_last = (prev == (uint32_t)A.nsplit - 1u) ? 1u : 0u;
-    }
-    __syncthreads();
-    if (!is_last) return;
-    __threadfence();
-
-    // 6. Last arrival: merge splits in split order, gate, store.
-    {
-        const int h = w;
-        float M = -INFINITY, Ls = 0.0f;
-        float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f;
-        for (int s = 0; s < A.nsplit; ++s) {
-            const float* P = A.partial + ((((size_t)b * QM_GQA_KV_HEADS + g) * A.nsplit + s) * 4 + h) * GQA_PART_STRIDE;
-            const float ms = ld_coherent(P + 256);
-            if (ms == -INFINITY) continue;
-            const float ls = ld_coherent(P + 257);
-            const float Mn = fmaxf(M, ms);
-            const float fo = (M == -INFINITY) ? 0.0f : expf(M - Mn);
-            const float fs = expf(ms - Mn);
-            Ls = Ls * fo + ls * fs;
-            o0 = o0 * fo + ld_coherent(P + 4 * lane + 0) * fs;
-            o1 = o1 * fo + ld_coherent(P + 4 * lane + 1) * fs;
-            o2 = o2 * fo + ld_coherent(P + 4 * lane + 2) * fs;
-            o3 = o3 * fo + ld_coherent(P + 4 * lane + 3) * fs;
-            M = Mn;
+        if (A.nsplit == 1) {
+            gqa_store_out(A, b, 4 * g + h, lane, o.x, o.y, o.z, o.w, Ls);
+        } else {
+            float* P = A.partial + ((((size_t)b * QM_GQA_KV_HEADS + g) * A.nsplit + split) * 4 + h) * GQA_PART_STRIDE;
+            st4(P + 4 * lane, o);
+            if (lane == 0) { P[256] = M; P[257] = Ls; }
         }
-        const float inv = 1.0f / Ls;
-        const int qh = 4 * g + h;
-        const float* gate = A.q_gate + ((size_t)b * QM_GQA_HEADS + qh) * (2 * QM_GQA_HD) + QM_GQA_HD + 4 * lane;
-        const float4 gv = ld4(gate);
-        float4 r;
-        r.x = (o0 * inv) * sigmoid_f(gv.x);
-        r.y = (o1 * inv) * sigmoid_f(gv.y);
-        r.z = (o2 * inv) * sigmoid_f(gv.z);
-        r.w = (o3 * inv) * sigmoid_f(gv.w);
-        st4(A.out + ((size_t)b * QM_GQA_HEADS + qh) * QM_GQA_HD + 4 * lane, r);
-        if (tid == 0)
-            __hip_atomic_store(&A.counters[b * QM_GQA_KV_HEADS + g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+}
+
+// Merge the split partials of (b, g) in split order and apply the gate.
+// Thread (h = tid / 64, lane) owns dims 4*lane..4*lane+3 of query head 4g+h.
+// Two passes with loads independent of the running sums (the global max
+// first, then the weighted sums), so the loads of many splits are in flight
+// together instead of one dependent round trip per split.
+extern "C" __global__ __launch_bounds__(256) void qm_gqa_decode_merge(GqaDecodeArgs A) {
+    const int tid = threadIdx.x, h = tid >> 6, lane = tid & 63;
+    const int g = blockIdx.x % QM_GQA_KV_HEADS;
+    const int b = blockIdx.x / QM_GQA_KV_HEADS;
+    const float* P0 = A.partial + (((size_t)b * QM_GQA_KV_HEADS + g) * A.nsplit * 4 + h) * GQA_PART_STRIDE;
+    const size_t step = 4 * GQA_PART_STRIDE;
+    float M = -INFINITY;
+#pragma unroll 8
+    for (int s = 0; s < A.nsplit; ++s) M = fmaxf(M, P0[s * step + 256]);
+    float Ls = 0.0f;
+    float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f;
+#pragma unroll 8
+    for (int s = 0; s < A.nsplit; ++s) {
+        const float* P = P0 + s * step;
+        const float ms = P[256];
+        const float ls = P[257];
+        const float4 a = ld4(P + 4 * lane);
+        // empty splits (sequence shorter than max_pos) carry m = -inf
+        const float f = (ms == -INFINITY) ? 0.0f : expf(ms - M);
+        Ls = fmaf(ls, f, Ls);
+        o0 = fmaf(a.x, f, o0);
+        o1 = fmaf(a.y, f, o1);
+        o2 = fmaf(a.z, f, o2);
+        o3 = fmaf(a.w, f, o3);
+    }
+    gqa_store_out(A, b, 4 * g + h, lane, o0, o1, o2, o3, Ls);
 }

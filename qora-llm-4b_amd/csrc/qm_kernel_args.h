@@ -39,11 +39,10 @@ struct DnDecodeArgs {
     float* state;            // [B] x state_stride floats
     int64_t state_stride;
     float* out;              // [B][4096]
-    uint32_t* counters;      // [B*32] arrival counters (split > 1), zero at rest
     int32_t batch;
 };
 
-// GQA decode step (fused prep + split-K attention + last-arriver combine).
+// GQA decode step (split-K attention with fused q/k prep, then merge).
 struct GqaDecodeArgs {
     const float* q_gate;     // [B][16][512]
     const float* k_new;      // [B][4][256]
@@ -56,8 +55,7 @@ struct GqaDecodeArgs {
     uint16_t* k_cache;       // [B][4][cap][256] f16
     uint16_t* v_cache;
     float* out;              // [B][16][256]
-    float* partial;          // [B][4][nsplit][4][258]  (m[4], l[4], acc[4][256])
-    uint32_t* counters;      // [B*4]
+    float* partial;          // [B][4][nsplit][4 heads][260]: acc[256], m, l, pad
     int64_t cap;
     int32_t max_pos;
     int32_t chunk;           // keys per split

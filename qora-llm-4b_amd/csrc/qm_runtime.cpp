@@ -5,9 +5,9 @@
 // every argument before anything is enqueued (so bad shapes, positions and
 // null pointers come back as status codes instead of faults), picks launch
 // shapes and enqueues the kernels with hipModuleLaunchKernel.  Device memory
-// for the mixer's own scratch (split-K partials, arrival counters, the
-// activated qkv of layer-mode decode) lives in a per-context workspace that
-// only grows outside stream capture.
+// for the mixer's own scratch (split-K partials, the activated qkv of
+// layer-mode decode) lives in a per-context workspace that only grows
+// outside stream capture.
 #include "qora_mixer.h"
 #include "qm_kernel_args.h"
 
@@ -34,15 +34,14 @@ struct qm_context {
     hipStream_t stream = nullptr;
     std::vector<hipModule_t> modules;
     hipFunction_t f_conv = nullptr;
-    hipFunction_t f_dn[4] = {nullptr, nullptr, nullptr, nullptr};  // splits 1,2,4,8
-    hipFunction_t f_gqa_decode = nullptr;
+    hipFunction_t f_dn[3] = {nullptr, nullptr, nullptr};  // 256, 512, 1024 threads
+    hipFunction_t f_gqa_split = nullptr;
+    hipFunction_t f_gqa_merge = nullptr;
     hipFunction_t f_fill = nullptr;
     void* ws = nullptr;            // general workspace
     size_t ws_bytes = 0;
-    uint32_t* counters = nullptr;  // arrival counters, zero at rest
-    size_t counter_slots = 0;
     std::string err;
-    int64_t opt_dn_splits = 0;
+    int64_t opt_dn_threads = 0;
     int64_t opt_gqa_chunk = 0;
     int64_t opt_dn_prefill_slices = 0;
 };
@@ -84,31 +83,20 @@ bool capturing(hipStream_t s) {
     return st != hipStreamCaptureStatusNone;
 }
 
-// Grow the workspace / counter slots.  Growth synchronises the device and is
-// refused while the stream is being captured.
-int32_t ensure(qm_context* c, hipStream_t s, size_t ws_bytes, size_t slots) {
-    if (ws_bytes <= c->ws_bytes && slots <= c->counter_slots) return QM_OK;
+// Grow the workspace.  Growth synchronises the device and is refused while
+// the stream is being captured.
+int32_t ensure(qm_context* c, hipStream_t s, size_t ws_bytes) {
+    if (ws_bytes <= c->ws_bytes) return QM_OK;
     if (capturing(s))
         return fail(c, QM_ERR_WORKSPACE,
-                    "workspace must grow to %zu bytes / %zu counters during graph capture; "
-                    "call qm_reserve() before capturing", ws_bytes, slots);
+                    "workspace must grow to %zu bytes during graph capture; "
+                    "call qm_reserve() before capturing", ws_bytes);
     QM_HIP(c, hipDeviceSynchronize());
-    if (ws_bytes > c->ws_bytes) {
-        if (c->ws) QM_HIP(c, hipFree(c->ws));
-        c->ws = nullptr;
-        c->ws_bytes = 0;
-        QM_HIP(c, hipMalloc(&c->ws, ws_bytes));
-        c->ws_bytes = ws_bytes;
-    }
-    if (slots > c->counter_slots) {
-        if (c->counters) QM_HIP(c, hipFree(c->counters));
-        c->counters = nullptr;
-        c->counter_slots = 0;
-        QM_HIP(c, hipMalloc(reinterpret_cast<void**>(&c->counters), slots * sizeof(uint32_t)));
-        QM_HIP(c, hipMemset(c->counters, 0, slots * sizeof(uint32_t)));
-        c->counter_slots = slots;
-    }
-    QM_HIP(c, hipDeviceSynchronize());
+    if (c->ws) QM_HIP(c, hipFree(c->ws));
+    c->ws = nullptr;
+    c->ws_bytes = 0;
+    QM_HIP(c, hipMalloc(&c->ws, ws_bytes));
+    c->ws_bytes = ws_bytes;
     return QM_OK;
 }
 
@@ -227,10 +215,11 @@ int32_t qm_create(qm_context** out, const qm_config* cfg, const char* code_objec
         c->modules.push_back(mods[i]);
     }
     int32_t st = QM_OK;
-    const char* dn_names[4] = {"qm_dn_decode_s1", "qm_dn_decode_s2", "qm_dn_decode_s4", "qm_dn_decode_s8"};
+    const char* dn_names[3] = {"qm_dn_decode_t256", "qm_dn_decode_t512", "qm_dn_decode_t1024"};
     if (st == QM_OK) st = load_function(c, mods[0], "qm_dn_conv_silu", &c->f_conv);
-    for (int i = 0; i < 4 && st == QM_OK; ++i) st = load_function(c, mods[0], dn_names[i], &c->f_dn[i]);
-    if (st == QM_OK) st = load_function(c, mods[1], "qm_gqa_decode", &c->f_gqa_decode);
+    for (int i = 0; i < 3 && st == QM_OK; ++i) st = load_function(c, mods[0], dn_names[i], &c->f_dn[i]);
+    if (st == QM_OK) st = load_function(c, mods[1], "qm_gqa_decode_split", &c->f_gqa_split);
+    if (st == QM_OK) st = load_function(c, mods[1], "qm_gqa_decode_merge", &c->f_gqa_merge);
     if (st == QM_OK) st = load_function(c, mods[2], "qm_fill_normal", &c->f_fill);
     if (st == QM_OK && hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess)
         st = fail(c, QM_ERR_HIP, "hipStreamCreate failed");
@@ -248,7 +237,6 @@ int32_t qm_destroy(qm_context* c) {
     hipSetDevice(c->device);
     hipDeviceSynchronize();
     if (c->ws) hipFree(c->ws);
-    if (c->counters) hipFree(c->counters);
     if (c->stream) hipStreamDestroy(c->stream);
     for (hipModule_t m : c->modules) hipModuleUnload(m);
     delete c;
@@ -258,10 +246,10 @@ int32_t qm_destroy(qm_context* c) {
 int32_t qm_set_option(qm_context* c, int32_t option, int64_t value) {
     if (!c) return QM_ERR_INVALID_ARG;
     switch (option) {
-        case QM_OPT_DN_DECODE_SPLITS:
-            if (value != 0 && value != 1 && value != 2 && value != 4 && value != 8)
-                return fail(c, QM_ERR_INVALID_ARG, "DN decode splits must be 0,1,2,4,8");
-            c->opt_dn_splits = value;
+        case QM_OPT_DN_DECODE_THREADS:
+            if (value != 0 && value != 256 && value != 512 && value != 1024)
+                return fail(c, QM_ERR_INVALID_ARG, "DN decode threads must be 0, 256, 512 or 1024");
+            c->opt_dn_threads = value;
             return QM_OK;
         case QM_OPT_GQA_DECODE_CHUNK:
             if (value < 0 || value % 64 != 0 || value > (1 << 20))
@@ -437,12 +425,13 @@ int32_t qm_fill_normal(qm_context* c, void* dst, int32_t dtype, uint64_t count, 
 }
 
 // ---- DeltaNet decode ---------------------------------------------------------------
-static int dn_auto_splits(int32_t batch) {
+// Threads per (sequence, v-head) workgroup.  Small batches leave most CUs idle,
+// so they take wider workgroups (more loads in flight per head).
+static int dn_auto_threads(int32_t batch) {
     const int64_t heads = static_cast<int64_t>(batch) * QM_DN_V_HEADS;
-    if (heads >= 1024) return 1;
-    if (heads >= 512) return 2;
-    if (heads >= 256) return 4;
-    return 8;
+    if (heads >= 512) return 256;
+    if (heads >= 128) return 512;
+    return 1024;
 }
 
 int32_t qm_deltanet_decode(qm_context* c, qm_stream stream, int32_t batch, int32_t flags,
@@ -461,11 +450,12 @@ int32_t qm_deltanet_decode(qm_context* c, qm_stream stream, int32_t batch, int32
     if (state_stride < static_cast<int64_t>(QM_DN_V_HEADS) * QM_DN_HEAD_ELEMS || state_stride % 4)
         return fail(c, QM_ERR_INVALID_ARG, "qm_deltanet_decode: state_stride %lld",
                     static_cast<long long>(state_stride));
+    const uint64_t grid = static_cast<uint64_t>(batch) * QM_DN_V_HEADS;
+    if (grid > 0x7fffffffull) return fail(c, QM_ERR_INVALID_ARG, "qm_deltanet_decode: batch too large");
     hipStream_t s = pick(c, stream);
-    const int splits = c->opt_dn_splits ? static_cast<int>(c->opt_dn_splits) : dn_auto_splits(batch);
+    const int threads = c->opt_dn_threads ? static_cast<int>(c->opt_dn_threads) : dn_auto_threads(batch);
     const size_t act_bytes = flags == QM_DN_PREACT ? static_cast<size_t>(batch) * QM_DN_QKV_DIM * 4 : 0;
-    const size_t slots = splits > 1 ? static_cast<size_t>(batch) * QM_DN_V_HEADS : 0;
-    int32_t st = ensure(c, s, act_bytes, slots);
+    int32_t st = ensure(c, s, act_bytes);
     if (st != QM_OK) return st;
     const float* act = qkv;
     if (flags == QM_DN_PREACT) {
@@ -475,19 +465,18 @@ int32_t qm_deltanet_decode(qm_context* c, qm_stream stream, int32_t batch, int32
         if (st != QM_OK) return st;
         act = static_cast<const float*>(c->ws);
     }
-    DnDecodeArgs da{act, a, b, a_log, dt_bias, z, norm_w, state, state_stride, out, c->counters, batch};
-    const int fi = splits == 1 ? 0 : splits == 2 ? 1 : splits == 4 ? 2 : 3;
-    const uint64_t grid = static_cast<uint64_t>(batch) * QM_DN_V_HEADS * splits;
-    if (grid > 0x7fffffffull) return fail(c, QM_ERR_INVALID_ARG, "qm_deltanet_decode: batch too large");
-    return launch(c, c->f_dn[fi], static_cast<uint32_t>(grid), 256, da, s, "qm_dn_decode");
+    DnDecodeArgs da{act, a, b, a_log, dt_bias, z, norm_w, state, state_stride, out, batch};
+    const int fi = threads == 256 ? 0 : threads == 512 ? 1 : 2;
+    return launch(c, c->f_dn[fi], static_cast<uint32_t>(grid), threads, da, s, "qm_dn_decode");
 }
 
 // ---- GQA decode --------------------------------------------------------------------
+// Keys per split workgroup: about 2048 workgroups per launch (8 per CU) with
+// at least 256 keys each, at most 2048.
 static int64_t gqa_auto_chunk(int64_t len, int32_t batch) {
-    // Aim for ~2048 workgroups (8 per CU) with at least 64 keys each.
     int64_t want = (len * batch * QM_GQA_KV_HEADS + 2047) / 2048;
     int64_t ch = ((want + 63) / 64) * 64;
-    return std::max<int64_t>(64, std::min<int64_t>(ch, 2048));
+    return std::max<int64_t>(256, std::min<int64_t>(ch, 2048));
 }
 
 int32_t qm_gqa_decode(qm_context* c, qm_stream stream, int32_t batch, const float* q_gate,
@@ -512,14 +501,16 @@ int32_t qm_gqa_decode(qm_context* c, qm_stream stream, int32_t batch, const floa
     const int64_t nsplit = (len + chunk - 1) / chunk;
     const uint64_t grid = static_cast<uint64_t>(batch) * QM_GQA_KV_HEADS * nsplit;
     if (grid > 0x7fffffffull) return fail(c, QM_ERR_INVALID_ARG, "qm_gqa_decode: grid too large");
-    const size_t part_bytes = static_cast<size_t>(grid) * 4 * 260 * sizeof(float);
-    const size_t slots = static_cast<size_t>(batch) * QM_GQA_KV_HEADS;
-    int32_t st = ensure(c, s, part_bytes, slots);
+    const size_t part_bytes = nsplit > 1 ? static_cast<size_t>(grid) * 4 * 260 * sizeof(float) : 0;
+    int32_t st = ensure(c, s, part_bytes);
     if (st != QM_OK) return st;
     GqaDecodeArgs ga{q_gate, k_new, v_new, q_norm, k_norm, rope_cos, rope_sin, pos, k_cache, v_cache,
-                     out, static_cast<float*>(c->ws), c->counters, cap, max_pos,
+                     out, static_cast<float*>(c->ws), cap, max_pos,
                      static_cast<int32_t>(chunk), static_cast<int32_t>(nsplit), batch};
-    return launch(c, c->f_gqa_decode, static_cast<uint32_t>(grid), 256, ga, s, "qm_gqa_decode");
+    st = launch(c, c->f_gqa_split, static_cast<uint32_t>(grid), 256, ga, s, "qm_gqa_decode_split");
+    if (st != QM_OK || nsplit == 1) return st;
+    return launch(c, c->f_gqa_merge, static_cast<uint32_t>(batch) * QM_GQA_KV_HEADS, 256, ga, s,
+                  "qm_gqa_decode_merge");
 }
 
 int32_t qm_reserve(qm_context* c, int32_t max_batch, int32_t max_kv_len, int32_t max_prefill_tokens) {
@@ -536,13 +527,12 @@ int32_t qm_reserve(qm_context* c, int32_t max_batch, int32_t max_kv_len, int32_t
         if (c->opt_gqa_chunk) {
             bn = B * ((L + c->opt_gqa_chunk - 1) / c->opt_gqa_chunk);
         } else {
-            bn = std::min<int64_t>(B * ((L + 63) / 64), std::max<int64_t>(512 + B, B * ((L + 2047) / 2048)));
+            bn = std::min<int64_t>(B * ((L + 255) / 256), std::max<int64_t>(512 + B, B * ((L + 2047) / 2048)));
         }
         ws = std::max(ws, static_cast<size_t>(bn) * QM_GQA_KV_HEADS * 4 * 260 * sizeof(float));
     }
     (void)max_prefill_tokens;
-    const size_t slots = static_cast<size_t>(max_batch) * QM_DN_V_HEADS;
-    return ensure(c, c->stream, ws, slots);
+    return ensure(c, c->stream, ws);
 }
 
 // ---- prefill entries (kernels land in qm_dn_prefill / qm_gqa_prefill) ------

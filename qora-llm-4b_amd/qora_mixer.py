@@ -28,7 +28,7 @@ STATUS_NAMES = {
 }
 QM_DN_POSTACT, QM_DN_PREACT = 0, 1
 QM_F32, QM_F16, QM_BF16 = 0, 1, 2
-QM_OPT_DN_DECODE_SPLITS, QM_OPT_GQA_DECODE_CHUNK, QM_OPT_DN_PREFILL_SLICES = 1, 2, 3
+QM_OPT_DN_DECODE_THREADS, QM_OPT_GQA_DECODE_CHUNK, QM_OPT_DN_PREFILL_SLICES = 1, 2, 3
 
 # Mixer shape (config.rs:42-97).
 DN_QK_HEADS, DN_V_HEADS, DN_HD, DN_CONV_K = 16, 32, 128, 4
@@ -170,7 +170,11 @@ class Context:
     """One qm_context on one device (not thread-safe, one stream at a time)."""
 
     def __init__(self, device: int = 0, code_object_dir: str | None = None):
+        """code_object_dir: directory of the qm_*.hsaco files; default is the
+        QORA_MIXER_CODE_OBJECTS environment variable, else the library's own
+        directory."""
         self.lib = load_library()
+        code_object_dir = code_object_dir or os.environ.get("QORA_MIXER_CODE_OBJECTS") or None
         h = _P(0)
         cdir = str(code_object_dir).encode() if code_object_dir else None
         st = self.lib.qm_create(C.byref(h), None, cdir, device)

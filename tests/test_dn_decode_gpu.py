@@ -112,19 +112,19 @@ def test_decode_batched_sequences_independent(ctx):
 
 
 @pytest.mark.parametrize("batch", [1, 3])
-def test_decode_split_invariance_and_determinism(ctx, batch):
-    """Row-block splits (1,2,4,8 workgroups per head) give bit-identical results."""
+def test_decode_block_size_invariance_and_determinism(ctx, batch):
+    """256/512/1024-thread workgroups give bit-identical results, run after run."""
     steps = 3
     w = W.dn_decode_workload(steps, batch, seed=21)
     results = []
-    for splits in [1, 2, 4, 8, 8]:
-        print(f"case: dn decode split={splits} B={batch}", flush=True)
-        ctx.set_option(M.QM_OPT_DN_DECODE_SPLITS, splits)
+    for threads in [256, 512, 1024, 1024]:
+        print(f"case: dn decode threads={threads} B={batch}", flush=True)
+        ctx.set_option(M.QM_OPT_DN_DECODE_THREADS, threads)
         dev = DnDevice(ctx, w, steps, batch)
         for t in range(steps):
             dev.step(t)
         results.append((dev.outputs(), dev.final_state()))
-    ctx.set_option(M.QM_OPT_DN_DECODE_SPLITS, 0)
+    ctx.set_option(M.QM_OPT_DN_DECODE_THREADS, 0)
     for o, s in results[1:]:
         assert np.array_equal(o, results[0][0]) and np.array_equal(s, results[0][1])
 

@@ -82,7 +82,7 @@ def test_decode_ragged_positions(ctx):
     assert np.abs(got - ref).max() <= TOL
 
 
-@pytest.mark.parametrize("chunk", [64, 192, 1024, 4160])
+@pytest.mark.parametrize("chunk", [64, 192, 1024, 4160])  # 4160: one split, no merge kernel
 def test_decode_chunk_invariance(ctx, chunk):
     w = W.gqa_decode_workload(3000, 2, seed=3)
     print(f"case: gqa decode chunk={chunk}", flush=True)
