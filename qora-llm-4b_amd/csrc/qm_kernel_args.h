@@ -63,6 +63,44 @@ struct GqaDecodeArgs {
     int32_t batch;
 };
 
+// DeltaNet chunked prefill (chunk 64).  Workspace tensors, T_pad = 64 * nc:
+//   qh, kh  f16 [T_pad][16][128]   L2-normed q (times 1/sqrt(128)) and k
+//   vv      f16 [T_pad][32][128]   activated v
+//   G, beta f32 [32][T_pad]        within-chunk cumulative log decay, beta
+//   Wn, Qt  f16 [32][nc][64][128]  -W = -T diag(beta*gamma) K and
+//                                   Q~ = diag(gamma) Q - P W, token-major
+//   Ut, Y0t f16 [32][nc][128][64]  U~ = T diag(beta) V and Y0 = P U~,
+//                                   transposed (v-row-major)
+//   Ktt     f16 [32][nc][128][64]  K~^T = (diag(gamma_C / gamma) K)^T
+//   gC      f32 [32][nc]           gamma_C = prod of the chunk's decays
+#define QM_DN_CHUNK 64
+struct DnPrefillArgs {
+    const uint16_t* qkv;     // bf16 [T][8192]
+    float* conv_buf;         // [8192][3]
+    const float* conv_w;     // [8192][4]
+    const float* a;          // [T][32]
+    const float* b;          // [T][32]
+    const float* a_log;      // [32]
+    const float* dt_bias;    // [32]
+    const uint16_t* z;       // bf16 [T][4096]
+    const uint16_t* norm_w;  // f16 [128]
+    float* state;            // [32][128][128]
+    uint16_t* out;           // bf16 [T][4096]
+    uint16_t* qh;
+    uint16_t* kh;
+    uint16_t* vv;
+    float* G;
+    float* beta;
+    uint16_t* Wn;
+    uint16_t* Qt;
+    uint16_t* Ut;
+    uint16_t* Y0t;
+    uint16_t* Ktt;
+    float* gC;
+    int32_t T;
+    int32_t nc;
+};
+
 // Counter-based normal generator fill.
 struct FillArgs {
     void* dst;

@@ -38,6 +38,9 @@ struct qm_context {
     hipFunction_t f_gqa_split = nullptr;
     hipFunction_t f_gqa_merge = nullptr;
     hipFunction_t f_fill = nullptr;
+    hipFunction_t f_dnp_prep = nullptr;
+    hipFunction_t f_dnp_chunk = nullptr;
+    hipFunction_t f_dnp_scan = nullptr;
     void* ws = nullptr;            // general workspace
     size_t ws_bytes = 0;
     std::string err;
@@ -137,6 +140,33 @@ int32_t load_function(qm_context* c, hipModule_t m, const char* name, hipFunctio
 
 }  // namespace
 
+namespace {
+struct DnPrefillLayout {
+    size_t qh, kh, vv, G, beta, Wn, Qt, Ut, Y0t, Ktt, gC, total;
+};
+
+DnPrefillLayout dn_prefill_layout(int64_t T) {
+    const int64_t nc = (T + QM_DN_CHUNK - 1) / QM_DN_CHUNK, tpad = nc * QM_DN_CHUNK;
+    auto al = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
+    DnPrefillLayout L{};
+    size_t o = 0;
+    L.qh = o; o += al(static_cast<size_t>(tpad) * QM_DN_QK_HEADS * QM_DN_HD * 2);
+    L.kh = o; o += al(static_cast<size_t>(tpad) * QM_DN_QK_HEADS * QM_DN_HD * 2);
+    L.vv = o; o += al(static_cast<size_t>(tpad) * QM_DN_V_HEADS * QM_DN_HD * 2);
+    L.G = o; o += al(static_cast<size_t>(tpad) * QM_DN_V_HEADS * 4);
+    L.beta = o; o += al(static_cast<size_t>(tpad) * QM_DN_V_HEADS * 4);
+    const size_t blk = static_cast<size_t>(QM_DN_V_HEADS) * nc * QM_DN_CHUNK * QM_DN_HD * 2;
+    L.Wn = o; o += al(blk);
+    L.Qt = o; o += al(blk);
+    L.Ut = o; o += al(blk);
+    L.Y0t = o; o += al(blk);
+    L.Ktt = o; o += al(blk);
+    L.gC = o; o += al(static_cast<size_t>(QM_DN_V_HEADS) * nc * 4);
+    L.total = o;
+    return L;
+}
+}  // namespace
+
 extern "C" {
 
 void qm_default_config(qm_config* cfg) {
@@ -201,9 +231,11 @@ int32_t qm_create(qm_context** out, const qm_config* cfg, const char* code_objec
     c->device = device;
     c->cfg = want;
     std::string dir = code_object_dir ? code_object_dir : library_dir();
-    const char* files[] = {"qm_dn_decode.hsaco", "qm_gqa_decode.hsaco", "qm_util.hsaco"};
-    hipModule_t mods[3] = {nullptr, nullptr, nullptr};
-    for (int i = 0; i < 3; ++i) {
+    const char* files[] = {"qm_dn_decode.hsaco", "qm_gqa_decode.hsaco", "qm_util.hsaco",
+                           "qm_dn_prefill.hsaco"};
+    constexpr int kModules = 4;
+    hipModule_t mods[kModules] = {nullptr, nullptr, nullptr, nullptr};
+    for (int i = 0; i < kModules; ++i) {
         std::string path = dir + "/" + files[i];
         hipError_t e = hipModuleLoad(&mods[i], path.c_str());
         if (e != hipSuccess) {
@@ -221,6 +253,9 @@ int32_t qm_create(qm_context** out, const qm_config* cfg, const char* code_objec
     if (st == QM_OK) st = load_function(c, mods[1], "qm_gqa_decode_split", &c->f_gqa_split);
     if (st == QM_OK) st = load_function(c, mods[1], "qm_gqa_decode_merge", &c->f_gqa_merge);
     if (st == QM_OK) st = load_function(c, mods[2], "qm_fill_normal", &c->f_fill);
+    if (st == QM_OK) st = load_function(c, mods[3], "qm_dn_prefill_prep", &c->f_dnp_prep);
+    if (st == QM_OK) st = load_function(c, mods[3], "qm_dn_prefill_chunk", &c->f_dnp_chunk);
+    if (st == QM_OK) st = load_function(c, mods[3], "qm_dn_prefill_scan", &c->f_dnp_scan);
     if (st == QM_OK && hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess)
         st = fail(c, QM_ERR_HIP, "hipStreamCreate failed");
     if (st != QM_OK) {
@@ -531,16 +566,38 @@ int32_t qm_reserve(qm_context* c, int32_t max_batch, int32_t max_kv_len, int32_t
         }
         ws = std::max(ws, static_cast<size_t>(bn) * QM_GQA_KV_HEADS * 4 * 260 * sizeof(float));
     }
-    (void)max_prefill_tokens;
+    if (max_prefill_tokens > 0) ws = std::max(ws, dn_prefill_layout(max_prefill_tokens).total);
     return ensure(c, c->stream, ws);
 }
 
-// ---- prefill entries (kernels land in qm_dn_prefill / qm_gqa_prefill) ------
-int32_t qm_deltanet_prefill(qm_context* c, qm_stream, int32_t, const uint16_t*, float*,
-                            const float*, const float*, const float*, const float*,
-                            const float*, const uint16_t*, const uint16_t*, float*, uint16_t*) {
+// ---- DeltaNet chunked prefill --------------------------------------------------------
+
+int32_t qm_deltanet_prefill(qm_context* c, qm_stream stream, int32_t seq_len, const uint16_t* qkv,
+                            float* conv_buf, const float* conv_w, const float* a, const float* b,
+                            const float* a_log, const float* dt_bias, const uint16_t* z,
+                            const uint16_t* norm_w, float* state, uint16_t* out) {
     if (!c) return QM_ERR_INVALID_ARG;
-    return fail(c, QM_ERR_CODE_OBJECT, "qm_deltanet_prefill: kernel not built yet");
+    if (seq_len <= 0) return fail(c, QM_ERR_INVALID_ARG, "qm_deltanet_prefill: seq_len %d", seq_len);
+    if (!qkv || !conv_buf || !conv_w || !a || !b || !a_log || !dt_bias || !z || !norm_w || !state || !out)
+        return fail(c, QM_ERR_INVALID_ARG, "qm_deltanet_prefill: null pointer");
+    hipStream_t s = pick(c, stream);
+    const DnPrefillLayout L = dn_prefill_layout(seq_len);
+    int32_t st = ensure(c, s, L.total);
+    if (st != QM_OK) return st;
+    char* ws = static_cast<char*>(c->ws);
+    const int32_t nc = (seq_len + QM_DN_CHUNK - 1) / QM_DN_CHUNK;
+    DnPrefillArgs pa{qkv, conv_buf, conv_w, a, b, a_log, dt_bias, z, norm_w, state, out,
+                     reinterpret_cast<uint16_t*>(ws + L.qh), reinterpret_cast<uint16_t*>(ws + L.kh),
+                     reinterpret_cast<uint16_t*>(ws + L.vv), reinterpret_cast<float*>(ws + L.G),
+                     reinterpret_cast<float*>(ws + L.beta), reinterpret_cast<uint16_t*>(ws + L.Wn),
+                     reinterpret_cast<uint16_t*>(ws + L.Qt), reinterpret_cast<uint16_t*>(ws + L.Ut),
+                     reinterpret_cast<uint16_t*>(ws + L.Y0t), reinterpret_cast<uint16_t*>(ws + L.Ktt),
+                     reinterpret_cast<float*>(ws + L.gC), seq_len, nc};
+    st = launch(c, c->f_dnp_prep, static_cast<uint32_t>(nc) * 64, 256, pa, s, "qm_dn_prefill_prep");
+    if (st != QM_OK) return st;
+    st = launch(c, c->f_dnp_chunk, static_cast<uint32_t>(nc) * QM_DN_V_HEADS, 256, pa, s, "qm_dn_prefill_chunk");
+    if (st != QM_OK) return st;
+    return launch(c, c->f_dnp_scan, QM_DN_V_HEADS, 512, pa, s, "qm_dn_prefill_scan");
 }
 
 int32_t qm_gqa_prefill(qm_context* c, qm_stream, int32_t, const uint16_t*, const uint16_t*,

@@ -1,0 +1,98 @@
+"""GPU parity: DeltaNet chunked prefill (qm_deltanet_prefill).
+
+Checked against (a) the oracle's sequential prefill (gemv.rs:1119-1219) on
+the same bf16-rounded inputs and (b) seq_len recurrent steps of the GPU
+decode kernel in layer mode (conv1d + SiLU in-kernel), the chunked form's
+own criterion.  Bar (bf16 path): ||d||_inf / ||ref||_inf <= 2e-2 for the
+outputs and the final state; the conv buffer is exact.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import load_mixer, load_oracle, load_workloads
+
+pytestmark = pytest.mark.gpu
+
+M = load_mixer()
+O = load_oracle()
+W = load_workloads()
+RTOL = 2e-2
+
+
+def rel(got, ref):
+    return float(np.abs(got.astype(np.float64) - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def run_prefill(ctx, w, T):
+    up = ctx.upload
+    d = {k: up(w[k]) for k in ["qkv", "conv_w", "a", "b", "a_log", "dt_bias", "z", "norm_w"]}
+    state = up(w["state0"])
+    buf = up(w["conv_buf0"])
+    out = ctx.alloc(T * 4096 * 2)
+    ctx.deltanet_prefill(T, d["qkv"], buf, d["conv_w"], d["a"], d["b"], d["a_log"], d["dt_bias"],
+                         d["z"], d["norm_w"], state, out)
+    o = W.bf16_value(ctx.download(out, (T, 4096), np.uint16))
+    S = ctx.download(state, (32, 128, 128), np.float32)
+    cb = ctx.download(buf, (8192, 3), np.float32)
+    return o, S, cb
+
+
+def run_oracle(w, T):
+    cfg = O.config()
+    S = w["state0"].copy()
+    buf = w["conv_buf0"].copy()
+    out = O.deltanet_prefill(cfg, W.bf16_value(w["qkv"]), w["a"], w["b"], W.bf16_value(w["z"]),
+                             w["conv_w"], w["a_log"], w["dt_bias"], w["norm_w"], S, buf)
+    return out, S, buf
+
+
+@pytest.mark.parametrize("T,warm", [(256, False), (100, True), (1, True), (65, True)])
+def test_prefill_vs_oracle(ctx, T, warm):
+    w = W.dn_prefill_workload(T, seed=2 + T)
+    if warm:   # nonzero entering state and conv history
+        r = np.random.default_rng(T)
+        w["state0"] = (0.02 * r.standard_normal((32, 128, 128))).astype(np.float32)
+        w["conv_buf0"] = r.standard_normal((8192, 3)).astype(np.float32)
+    print(f"case: dn prefill T={T} warm={warm}", flush=True)
+    o, S, cb = run_prefill(ctx, w, T)
+    ro, rS, rcb = run_oracle(w, T)
+    eo, es = rel(o, ro), rel(S, rS)
+    print(f"rel out {eo:.3e} rel state {es:.3e}")
+    assert eo <= RTOL and es <= RTOL
+    assert np.array_equal(cb, rcb)
+
+
+def test_prefill_4096_vs_oracle_and_recurrent_decode(ctx):
+    """seq 4096, zero initial state: chunked == 4096 recurrent steps."""
+    T = 4096
+    w = W.dn_prefill_workload(T, seed=2)
+    print("case: dn prefill T=4096 vs oracle", flush=True)
+    o, S, cb = run_prefill(ctx, w, T)
+    ro, rS, rcb = run_oracle(w, T)
+    eo, es = rel(o, ro), rel(S, rS)
+    print(f"vs oracle: rel out {eo:.3e} rel state {es:.3e}")
+    assert eo <= RTOL and es <= RTOL
+    assert np.array_equal(cb, rcb)
+
+    # the decode kernel, one launch per token, layer mode
+    print("case: dn decode x4096 (layer mode)", flush=True)
+    up = ctx.upload
+    qkv = up(W.bf16_value(w["qkv"]))
+    z = up(W.bf16_value(w["z"]))
+    a, b = up(w["a"]), up(w["b"])
+    conv_w, a_log, dt_bias, norm_w = up(w["conv_w"]), up(w["a_log"]), up(w["dt_bias"]), up(w["norm_w"])
+    state = up(w["state0"])
+    buf = up(w["conv_buf0"])
+    out = ctx.alloc(T * 4096 * 4)
+    for t in range(T):
+        ctx.deltanet_decode(1, M.QM_DN_PREACT, qkv.offset(t * 8192 * 4), buf, conv_w, a.offset(t * 32 * 4),
+                            b.offset(t * 32 * 4), a_log, dt_bias, z.offset(t * 4096 * 4), norm_w, state,
+                            out.offset(t * 4096 * 4))
+    od = ctx.download(out, (T, 4096), np.float32)
+    Sd = ctx.download(state, (32, 128, 128), np.float32)
+    e1, e2 = rel(o, od), rel(S, Sd)
+    print(f"vs recurrent decode: rel out {e1:.3e} rel state {e2:.3e}")
+    assert e1 <= RTOL and e2 <= RTOL
+    assert np.array_equal(ctx.download(buf, (8192, 3), np.float32), cb)
