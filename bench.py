@@ -9,6 +9,8 @@ Workloads (synthetic, seeded; inputs resident in HBM before timing):
               sequence through all 32 mixers.  Default; the headline line.
   dn_decode   one DeltaNet layer, batch 1, one step = one token.
   gqa_decode  one GQA layer, batch 1, one step at position 4096.
+  dn_prefill  one DeltaNet layer, chunked prefill of 4096 tokens (bf16 in,
+              fp32 state), one step = one prefill call.
 Prints one JSON line with throughput, the dominant kernel's roofline
 position (average launch time from HIP events on the launch stream) and the
 CPU oracle timed on this host on a bounded sample of the same workload.
@@ -27,6 +29,7 @@ import numpy as np
 
 ROOT = Path(__file__).resolve().parent
 HBM_PEAK = 8.0e12          # MI355X HBM3E, bytes/s
+MFMA_BF16_PEAK = 2.5e15    # MI355X dense bf16/f16 MFMA, flop/s
 N_DN, N_GQA = 24, 8        # 3x DeltaNet + 1x GQA, repeated 8 times (config.rs:44-50)
 
 
@@ -65,6 +68,15 @@ def gqa_decode_bytes(batch: int, length: int) -> int:
     vec = (16 * 512 + 2 * 4 * 256 + 16 * 256) * 4
     rope = 2 * 32 * 4
     return batch * (kv + vec + rope) + 2 * 256 * 2
+
+
+def dn_prefill_flops(T: int, C: int = 64) -> int:
+    """Chunked-form flops per layer: per head and chunk 5 C x C x d products
+    (KK^T, QK^T, W, U~, P U~) and 3 C x d x d products (W S^T, Q~ S^T,
+    U^T K~); the triangular solve is not counted."""
+    d, H = 128, 32
+    nc = -(-T // C)
+    return H * nc * (5 * 2 * C * C * d + 3 * 2 * C * d * d)
 
 
 # ----------------------------------------------------------------------------
@@ -291,6 +303,46 @@ def run_gqa_decode(args, ctx):
     }
 
 
+def run_dn_prefill(args, ctx):
+    K, Wm = args.steps, args.warmup
+    T = 4096
+    w = W.dn_prefill_workload(T, seed=2)
+    up = ctx.upload
+    d = {k: up(w[k]) for k in ["qkv", "conv_w", "a", "b", "a_log", "dt_bias", "z", "norm_w"]}
+    state, buf = up(w["state0"]), up(w["conv_buf0"])
+    out = ctx.alloc(T * 4096 * 2)
+    ctx.reserve(max_batch=1, max_prefill_tokens=T)
+
+    def step():
+        ctx.deltanet_prefill(T, d["qkv"], buf, d["conv_w"], d["a"], d["b"], d["a_log"], d["dt_bias"],
+                             d["z"], d["norm_w"], state, out)
+
+    for _ in range(Wm):
+        step()
+    ctx.sync()
+    tm = Timer(ctx)
+    t0, t1 = ctx.event(), ctx.event()
+    wall0 = time.perf_counter()
+    t0.record()
+    for _ in range(K):
+        tm.wrap(step)
+    t1.record()
+    ctx.sync()
+    wall = time.perf_counter() - wall0
+    total_ms = t0.elapsed_ms(t1)
+    k_ms = tm.mean_ms()
+    flops = dn_prefill_flops(T)
+    return {
+        "tokens": K * T, "total_ms": total_ms, "wall_s": wall,
+        "dominant": "qm_deltanet_prefill (prep+chunk+scan)",
+        "roofline": {"bound": "mfma", "achieved": flops / (k_ms * 1e-3), "peak": MFMA_BF16_PEAK,
+                     "unit": "TFLOP/s", "kernel_ms": k_ms, "flops_per_launch": flops},
+        "config": {"workload": "DeltaNet chunked prefill, 1 layer, batch 1, seq 4096, chunk 64, "
+                               "bf16 in, fp32 state", "batch": 1, "seq_len": T, "global_batch": 1,
+                   "parallelism": "single GPU"},
+    }
+
+
 # ----------------------------------------------------------------------------
 # CPU baseline: the oracle (C restatement of the reference CPU path) on this host
 def cpu_baseline(workload: str) -> dict:
@@ -309,6 +361,18 @@ def cpu_baseline(workload: str) -> dict:
         dt = time.perf_counter() - t0
         return {"value": steps / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
                 "sample": f"256 decode steps, batch 1, {'AVX-512' if O.has_avx512() else 'scalar'} head update, 1 thread"}
+    if workload == "dn_prefill":
+        T = 1024
+        w = W.dn_prefill_workload(T, seed=2)
+        S, buf = w["state0"].copy(), w["conv_buf0"].copy()
+        qkv, z = W.bf16_value(w["qkv"]), W.bf16_value(w["z"])
+        t0 = time.perf_counter()
+        O.deltanet_prefill(cfg, qkv, w["a"], w["b"], z, w["conv_w"], w["a_log"], w["dt_bias"],
+                           w["norm_w"], S, buf)
+        dt = time.perf_counter() - t0
+        return {"value": T / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
+                "sample": f"sequential prefill of the first {T} of 4096 tokens (gemv.rs:1119-1219 "
+                          "scalar loop, 1 thread); per-token cost is independent of position"}
     if workload == "gqa_decode":
         pos = 4096
         w = W.gqa_decode_workload(pos, 1, seed=1)
@@ -366,37 +430,49 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="stack", choices=["stack", "dn_decode", "gqa_decode"])
+    ap.add_argument("--workload", default="stack",
+                    choices=["stack", "dn_decode", "gqa_decode", "dn_prefill"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the mixer path here is a single-GPU build "
               "(sharding is a design note, not a launched path); run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
-    defaults = {"stack": (32, 4), "dn_decode": (256, 16), "gqa_decode": (200, 20)}[args.workload]
+    defaults = {"stack": (32, 4), "dn_decode": (256, 16), "gqa_decode": (200, 20),
+                "dn_prefill": (20, 3)}[args.workload]
     args.steps = args.steps or defaults[0]
     args.warmup = defaults[1] if args.warmup is None else args.warmup
 
     ctx = M.Context(0)
-    run = {"stack": run_stack, "dn_decode": run_dn_decode, "gqa_decode": run_gqa_decode}[args.workload]
+    run = {"stack": run_stack, "dn_decode": run_dn_decode, "gqa_decode": run_gqa_decode,
+           "dn_prefill": run_dn_prefill}[args.workload]
     r = run(args, ctx)
     ctx.sync()
     ctx.close()
 
     value = r["tokens"] / (r["total_ms"] * 1e-3)
     roof = r["roofline"]
+    if roof["bound"] == "mfma":
+        rl = {"bound": "mfma", "achieved": roof["achieved"] / 1e12, "peak": roof["peak"] / 1e12,
+              "unit": "TFLOP/s", "frac": roof["achieved"] / roof["peak"], "traffic": None,
+              "kernel": r["dominant"], "kernel_avg_ms": roof["kernel_ms"],
+              "flops_per_launch": roof["flops_per_launch"]}
+    else:
+        rl = {"bound": roof["bound"], "achieved": roof["achieved"] / 1e9, "peak": roof["peak"] / 1e9,
+              "unit": "GB/s", "frac": roof["achieved"] / roof["peak"], "traffic": None,
+              "kernel": r["dominant"], "kernel_avg_ms": roof["kernel_ms"],
+              "bytes_per_launch": roof["bytes_per_launch"]}
     line = {
-        "metric": "mixer tokens/s (decode) on 1x MI355X" if args.workload != "stack"
-        else "mixer tokens/s (decode, 32-layer hybrid stack) on 1x MI355X",
+        "metric": {"stack": "mixer tokens/s (decode, 32-layer hybrid stack) on 1x MI355X",
+                   "dn_prefill": "mixer tokens/s (prefill) on 1x MI355X"}.get(
+                       args.workload, "mixer tokens/s (decode) on 1x MI355X"),
         "value": value, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": r["total_ms"] / args.steps,
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16" if args.workload == "dn_prefill" else "f32",
         "data": "synthetic (seeded normal inputs, random-init state and f16 KV cache)",
         "config": r["config"],
-        "roofline": {"bound": roof["bound"], "achieved": roof["achieved"] / 1e9, "peak": roof["peak"] / 1e9,
-                     "unit": "GB/s", "frac": roof["achieved"] / roof["peak"], "traffic": None,
-                     "kernel": r["dominant"], "kernel_avg_ms": roof["kernel_ms"],
-                     "bytes_per_launch": roof["bytes_per_launch"]},
+        "roofline": rl,
     }
     for k in ("kernels", "step_frac_hbm", "graph_ms_per_step"):
         if k in r:

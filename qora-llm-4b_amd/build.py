@@ -29,7 +29,7 @@ HIPCC_FLAGS = [
     "-Wall", "-Wno-unused-parameter",
 ]
 
-KERNELS = ["dn_decode", "gqa_decode", "util", "dn_prefill"]
+KERNELS = ["dn_decode", "gqa_decode", "util", "dn_prefill", "gqa_prefill"]
 
 
 def _run(cmd: list[str]) -> None:

@@ -27,44 +27,12 @@
 //         probabilities of a round are broadcast through LDS.
 #include "qm_device.h"
 #include "qm_kernel_args.h"
+#include "qm_gqa_common.h"
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 #define GQA_PART_STRIDE 260   // acc[256], m, l, pad[2]
-
-// Per-head RMSNorm (1+gamma, eps 1e-6; gemv.rs:586-597) and split-half RoPE
-// (gemv.rs:604-627) of one 256-wide head held by a wave: lane owns dims
-// 4*lane..4*lane+3.  Lanes 0..7 hold dims 0..31, lanes 8..15 dims 32..63,
-// so rotation partners are 8 lanes apart inside DPP row 0 (row_ror:8).
-QM_DEV float4 norm_rope_head(float4 x, const uint16_t* gamma, const float* cos_row,
-                             const float* sin_row, int lane) {
-    float ss = x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
-    ss = wave_sum64(ss);
-    const float inv = 1.0f / sqrtf(ss / (float)QM_GQA_HD + 1e-6f);
-    const uint2 gw = *reinterpret_cast<const uint2*>(gamma + 4 * lane);
-    x.x = x.x * inv * (1.0f + f16_to_f32((uint16_t)(gw.x & 0xffffu)));
-    x.y = x.y * inv * (1.0f + f16_to_f32((uint16_t)(gw.x >> 16)));
-    x.z = x.z * inv * (1.0f + f16_to_f32((uint16_t)(gw.y & 0xffffu)));
-    x.w = x.w * inv * (1.0f + f16_to_f32((uint16_t)(gw.y >> 16)));
-    float4 pr;
-    pr.x = dpp_f32<0x128>(x.x);
-    pr.y = dpp_f32<0x128>(x.y);
-    pr.z = dpp_f32<0x128>(x.z);
-    pr.w = dpp_f32<0x128>(x.w);
-    if (lane < 16) {
-        const int i0 = (lane & 7) * 4;
-        const float4 c = ld4(cos_row + i0), s = ld4(sin_row + i0);
-        if (lane < 8) {          // x1 = own, x2 = partner: x1 c - x2 s
-            x.x = x.x * c.x - pr.x * s.x; x.y = x.y * c.y - pr.y * s.y;
-            x.z = x.z * c.z - pr.z * s.z; x.w = x.w * c.w - pr.w * s.w;
-        } else {                 // x2 = own, x1 = partner: x2 c + x1 s
-            x.x = x.x * c.x + pr.x * s.x; x.y = x.y * c.y + pr.y * s.y;
-            x.z = x.z * c.z + pr.z * s.z; x.w = x.w * c.w + pr.w * s.w;
-        }
-    }
-    return x;
-}
 
 struct RoundBuf {
     half8 k[8];     // B operand: key (lane & 15), dims 64*(lane>>4) + 8*s .. +7

@@ -101,6 +101,26 @@ struct DnPrefillArgs {
     int32_t nc;
 };
 
+// GQA causal prefill.  vt is a workspace copy of V transposed per kv head,
+// f16 [4][256][s_pad] (s_pad = S rounded up to 64, zero padded), so the PV
+// product can read consecutive keys per lane.
+struct GqaPrefillArgs {
+    const uint16_t* q_gate;  // bf16 [S][16][512]
+    const uint16_t* k;       // bf16 [S][4][256]
+    const uint16_t* v;       // bf16 [S][4][256]
+    const uint16_t* q_norm;  // f16 [256]
+    const uint16_t* k_norm;  // f16 [256]
+    const float* rope_cos;   // [rope_len][32]
+    const float* rope_sin;
+    uint16_t* k_cache;       // f16 [4][cap][256]
+    uint16_t* v_cache;
+    uint16_t* vt;            // f16 [4][256][s_pad]
+    uint16_t* out;           // bf16 [S][16][256]
+    int64_t cap;
+    int32_t S;
+    int32_t s_pad;
+};
+
 // Counter-based normal generator fill.
 struct FillArgs {
     void* dst;

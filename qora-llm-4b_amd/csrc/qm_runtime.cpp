@@ -41,6 +41,8 @@ struct qm_context {
     hipFunction_t f_dnp_prep = nullptr;
     hipFunction_t f_dnp_chunk = nullptr;
     hipFunction_t f_dnp_scan = nullptr;
+    hipFunction_t f_gqp_kv = nullptr;
+    hipFunction_t f_gqp_attn = nullptr;
     void* ws = nullptr;            // general workspace
     size_t ws_bytes = 0;
     std::string err;
@@ -232,9 +234,9 @@ int32_t qm_create(qm_context** out, const qm_config* cfg, const char* code_objec
     c->cfg = want;
     std::string dir = code_object_dir ? code_object_dir : library_dir();
     const char* files[] = {"qm_dn_decode.hsaco", "qm_gqa_decode.hsaco", "qm_util.hsaco",
-                           "qm_dn_prefill.hsaco"};
-    constexpr int kModules = 4;
-    hipModule_t mods[kModules] = {nullptr, nullptr, nullptr, nullptr};
+                           "qm_dn_prefill.hsaco", "qm_gqa_prefill.hsaco"};
+    constexpr int kModules = 5;
+    hipModule_t mods[kModules] = {nullptr, nullptr, nullptr, nullptr, nullptr};
     for (int i = 0; i < kModules; ++i) {
         std::string path = dir + "/" + files[i];
         hipError_t e = hipModuleLoad(&mods[i], path.c_str());
@@ -256,6 +258,8 @@ int32_t qm_create(qm_context** out, const qm_config* cfg, const char* code_objec
     if (st == QM_OK) st = load_function(c, mods[3], "qm_dn_prefill_prep", &c->f_dnp_prep);
     if (st == QM_OK) st = load_function(c, mods[3], "qm_dn_prefill_chunk", &c->f_dnp_chunk);
     if (st == QM_OK) st = load_function(c, mods[3], "qm_dn_prefill_scan", &c->f_dnp_scan);
+    if (st == QM_OK) st = load_function(c, mods[4], "qm_gqa_prefill_kv", &c->f_gqp_kv);
+    if (st == QM_OK) st = load_function(c, mods[4], "qm_gqa_prefill_attn", &c->f_gqp_attn);
     if (st == QM_OK && hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess)
         st = fail(c, QM_ERR_HIP, "hipStreamCreate failed");
     if (st != QM_OK) {
@@ -566,7 +570,11 @@ int32_t qm_reserve(qm_context* c, int32_t max_batch, int32_t max_kv_len, int32_t
         }
         ws = std::max(ws, static_cast<size_t>(bn) * QM_GQA_KV_HEADS * 4 * 260 * sizeof(float));
     }
-    if (max_prefill_tokens > 0) ws = std::max(ws, dn_prefill_layout(max_prefill_tokens).total);
+    if (max_prefill_tokens > 0) {
+        ws = std::max(ws, dn_prefill_layout(max_prefill_tokens).total);
+        const size_t s_pad = (static_cast<size_t>(max_prefill_tokens) + 63) / 64 * 64;
+        ws = std::max(ws, static_cast<size_t>(QM_GQA_KV_HEADS) * QM_GQA_HD * s_pad * 2);
+    }
     return ensure(c, c->stream, ws);
 }
 
@@ -600,11 +608,32 @@ int32_t qm_deltanet_prefill(qm_context* c, qm_stream stream, int32_t seq_len, co
     return launch(c, c->f_dnp_scan, QM_DN_V_HEADS, 512, pa, s, "qm_dn_prefill_scan");
 }
 
-int32_t qm_gqa_prefill(qm_context* c, qm_stream, int32_t, const uint16_t*, const uint16_t*,
-                       const uint16_t*, const uint16_t*, const uint16_t*, const float*,
-                       const float*, int32_t, uint16_t*, uint16_t*, int64_t, uint16_t*) {
+// ---- GQA causal prefill ------------------------------------------------------------
+int32_t qm_gqa_prefill(qm_context* c, qm_stream stream, int32_t seq_len, const uint16_t* q_gate,
+                       const uint16_t* k, const uint16_t* v, const uint16_t* q_norm,
+                       const uint16_t* k_norm, const float* rope_cos, const float* rope_sin,
+                       int32_t rope_len, uint16_t* k_cache, uint16_t* v_cache, int64_t cap,
+                       uint16_t* out) {
     if (!c) return QM_ERR_INVALID_ARG;
-    return fail(c, QM_ERR_CODE_OBJECT, "qm_gqa_prefill: kernel not built yet");
+    if (seq_len <= 0) return fail(c, QM_ERR_INVALID_ARG, "qm_gqa_prefill: seq_len %d", seq_len);
+    if (!q_gate || !k || !v || !q_norm || !k_norm || !rope_cos || !rope_sin || !k_cache || !v_cache || !out)
+        return fail(c, QM_ERR_INVALID_ARG, "qm_gqa_prefill: null pointer");
+    if (seq_len > rope_len)
+        return fail(c, QM_ERR_ROPE_RANGE, "positions 0..%d beyond RoPE table of %d rows", seq_len - 1, rope_len);
+    if (seq_len > cap)
+        return fail(c, QM_ERR_CAPACITY, "%d tokens beyond cache capacity %lld", seq_len,
+                    static_cast<long long>(cap));
+    hipStream_t s = pick(c, stream);
+    const int32_t s_pad = (seq_len + 63) / 64 * 64;
+    int32_t st = ensure(c, s, static_cast<size_t>(QM_GQA_KV_HEADS) * QM_GQA_HD * s_pad * 2);
+    if (st != QM_OK) return st;
+    GqaPrefillArgs ga{q_gate, k, v, q_norm, k_norm, rope_cos, rope_sin, k_cache, v_cache,
+                      static_cast<uint16_t*>(c->ws), out, cap, seq_len, s_pad};
+    st = launch(c, c->f_gqp_kv, static_cast<uint32_t>(s_pad / 64) * QM_GQA_KV_HEADS, 256, ga, s,
+                "qm_gqa_prefill_kv");
+    if (st != QM_OK) return st;
+    return launch(c, c->f_gqp_attn, static_cast<uint32_t>(s_pad / 32) * QM_GQA_KV_HEADS, 256, ga, s,
+                  "qm_gqa_prefill_attn");
 }
 
 }  // extern "C"
