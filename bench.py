@@ -11,6 +11,8 @@ Workloads (synthetic, seeded; inputs resident in HBM before timing):
   gqa_decode  one GQA layer, batch 1, one step at position 4096.
   dn_prefill  one DeltaNet layer, chunked prefill of 4096 tokens (bf16 in,
               fp32 state), one step = one prefill call.
+  gqa_prefill one GQA layer, causal prefill of 8192 tokens (bf16 in, f16 KV
+              cache written), one step = one prefill call.
 Prints one JSON line with throughput, the dominant kernel's roofline
 position (average launch time from HIP events on the launch stream) and the
 CPU oracle timed on this host on a bounded sample of the same workload.
@@ -77,6 +79,11 @@ def dn_prefill_flops(T: int, C: int = 64) -> int:
     d, H = 128, 32
     nc = -(-T // C)
     return H * nc * (5 * 2 * C * C * d + 3 * 2 * C * d * d)
+
+
+def gqa_prefill_flops(S: int) -> int:
+    """QK^T and PV over the causal triangle: 2 products x 2 flop x D x H x S(S+1)/2."""
+    return 2 * 2 * 256 * 16 * S * (S + 1) // 2
 
 
 # ----------------------------------------------------------------------------
@@ -343,6 +350,46 @@ def run_dn_prefill(args, ctx):
     }
 
 
+def run_gqa_prefill(args, ctx):
+    K, Wm = args.steps, args.warmup
+    S = 8192
+    w = W.gqa_prefill_workload(S, seed=3)
+    cos, sin = M.rope_table(S)
+    d = {k: ctx.upload(w[k]) for k in ["q_gate", "k", "v", "q_norm", "k_norm"]}
+    rc, rs = ctx.upload(cos), ctx.upload(sin)
+    kc, vc = ctx.alloc(4 * S * 256 * 2), ctx.alloc(4 * S * 256 * 2)
+    out = ctx.alloc(S * 16 * 256 * 2)
+    ctx.reserve(max_batch=1, max_prefill_tokens=S)
+
+    def step():
+        ctx.gqa_prefill(S, d["q_gate"], d["k"], d["v"], d["q_norm"], d["k_norm"], rc, rs, S, kc, vc, S, out)
+
+    for _ in range(Wm):
+        step()
+    ctx.sync()
+    tm = Timer(ctx)
+    t0, t1 = ctx.event(), ctx.event()
+    wall0 = time.perf_counter()
+    t0.record()
+    for _ in range(K):
+        tm.wrap(step)
+    t1.record()
+    ctx.sync()
+    wall = time.perf_counter() - wall0
+    total_ms = t0.elapsed_ms(t1)
+    k_ms = tm.mean_ms()
+    flops = gqa_prefill_flops(S)
+    return {
+        "tokens": K * S, "total_ms": total_ms, "wall_s": wall,
+        "dominant": "qm_gqa_prefill (kv+attn)",
+        "roofline": {"bound": "mfma", "achieved": flops / (k_ms * 1e-3), "peak": MFMA_BF16_PEAK,
+                     "unit": "TFLOP/s", "kernel_ms": k_ms, "flops_per_launch": flops},
+        "config": {"workload": "GQA causal prefill, 1 layer, batch 1, seq 8192, 16q/4kv x 256, "
+                               "bf16 in, f16 KV cache out", "batch": 1, "seq_len": S,
+                   "global_batch": 1, "parallelism": "single GPU"},
+    }
+
+
 # ----------------------------------------------------------------------------
 # CPU baseline: the oracle (C restatement of the reference CPU path) on this host
 def cpu_baseline(workload: str) -> dict:
@@ -373,6 +420,24 @@ def cpu_baseline(workload: str) -> dict:
         return {"value": T / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
                 "sample": f"sequential prefill of the first {T} of 4096 tokens (gemv.rs:1119-1219 "
                           "scalar loop, 1 thread); per-token cost is independent of position"}
+    if workload == "gqa_prefill":
+        S = 8192
+        w = W.gqa_prefill_workload(S, seed=3)
+        cos, sin = O.rope_table(S)
+        rows = np.arange(S - 16, S)          # the 16 most expensive rows
+        t0 = time.perf_counter()
+        O.attn_prefill(cfg, W.bf16_value(w["q_gate"]).reshape(S, -1), W.bf16_value(w["k"]).reshape(S, -1),
+                       W.bf16_value(w["v"]).reshape(S, -1), w["q_norm"], w["k_norm"], cos, sin,
+                       rows=rows, nthreads=att_threads)
+        dt = time.perf_counter() - t0
+        # scale by work: the 16 sampled rows attend to ~S keys each; a full
+        # prefill does S(S+1)/2 row-key pairs
+        work_sample = float(np.sum(rows + 1))
+        work_full = S * (S + 1) / 2.0
+        return {"value": S / (dt * work_full / work_sample), "unit": "tokens/s", "cores": att_threads,
+                "kind": "port",
+                "sample": f"rows {S - 16}..{S - 1} of the 8192-token causal prefill (gemv.rs:1402-1444), "
+                          f"heads over {att_threads} threads, extrapolated linearly in row-key pairs"}
     if workload == "gqa_decode":
         pos = 4096
         w = W.gqa_decode_workload(pos, 1, seed=1)
@@ -431,21 +496,31 @@ def main():
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="stack",
-                    choices=["stack", "dn_decode", "gqa_decode", "dn_prefill"])
+                    choices=["stack", "dn_decode", "gqa_decode", "dn_prefill", "gqa_prefill"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="before timing, copy 1 GiB device-to-device once (a dispatch of known "
+                         "traffic for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the mixer path here is a single-GPU build "
               "(sharding is a design note, not a launched path); run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     defaults = {"stack": (32, 4), "dn_decode": (256, 16), "gqa_decode": (200, 20),
-                "dn_prefill": (20, 3)}[args.workload]
+                "dn_prefill": (20, 3), "gqa_prefill": (10, 2)}[args.workload]
     args.steps = args.steps or defaults[0]
     args.warmup = defaults[1] if args.warmup is None else args.warmup
 
     ctx = M.Context(0)
+    if args.calibrate_copy:
+        src, dst = ctx.alloc(1 << 30), ctx.alloc(1 << 30)
+        ctx.fill_normal(src, M.QM_F32, (1 << 30) // 4, 0.0, 1.0, 7)
+        ctx.copy(dst, src, 1 << 30)
+        ctx.sync()
+        src.close()
+        dst.close()
     run = {"stack": run_stack, "dn_decode": run_dn_decode, "gqa_decode": run_gqa_decode,
-           "dn_prefill": run_dn_prefill}[args.workload]
+           "dn_prefill": run_dn_prefill, "gqa_prefill": run_gqa_prefill}[args.workload]
     r = run(args, ctx)
     ctx.sync()
     ctx.close()
@@ -464,12 +539,13 @@ def main():
               "bytes_per_launch": roof["bytes_per_launch"]}
     line = {
         "metric": {"stack": "mixer tokens/s (decode, 32-layer hybrid stack) on 1x MI355X",
-                   "dn_prefill": "mixer tokens/s (prefill) on 1x MI355X"}.get(
+                   "dn_prefill": "mixer tokens/s (prefill) on 1x MI355X",
+                   "gqa_prefill": "mixer tokens/s (prefill) on 1x MI355X"}.get(
                        args.workload, "mixer tokens/s (decode) on 1x MI355X"),
         "value": value, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": r["total_ms"] / args.steps,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16" if args.workload == "dn_prefill" else "f32",
+        "dtype": "bf16" if args.workload in ("dn_prefill", "gqa_prefill") else "f32",
         "data": "synthetic (seeded normal inputs, random-init state and f16 KV cache)",
         "config": r["config"],
         "roofline": rl,

@@ -63,8 +63,19 @@ def build_oracle() -> None:
     _run(["make", "-s", "-C", str(ROOT / "oracle")])
 
 
+def build_host_test() -> None:
+    """tests/cpp/host_mirror_test.cpp: the C++ mirror driven against the oracle
+    (test infrastructure; needs the library and the oracle built)."""
+    _run(["g++", "-O2", "-std=c++17", "-Wall", "-Wextra", "-I", str(ROOT / "include"),
+          "-I", str(PKG / "host"), "-I", str(ROOT / "oracle"),
+          str(ROOT / "tests" / "cpp" / "host_mirror_test.cpp"), "-o", str(LIB / "host_mirror_test"),
+          f"-L{LIB}", "-lqora_mixer", f"-L{ROOT / 'oracle'}", "-loracle",
+          "-Wl,-rpath,$ORIGIN", "-Wl,-rpath,$ORIGIN/../../oracle"])
+
+
 if __name__ == "__main__":
     build()
     if "--no-oracle" not in sys.argv:
         build_oracle()
+        build_host_test()
     print("built:", ", ".join(sorted(p.name for p in LIB.iterdir())))

@@ -1,0 +1,226 @@
+// host_mirror_test.cpp -- runs the reference's layer flow through the C++
+// mirror (qor4b_mixer.hpp): a DeltaNet layer and a GQA layer each prefill a
+// prompt and then decode tokens, carrying state / conv buffer / KV cache
+// from prefill into decode as generate.rs does (prefill at :243, decode
+// loop at :126).  Every output is checked against the CPU oracle
+// (test infrastructure, linked only here).  Exit status 0 = all checks pass.
+#include "qor4b_mixer.hpp"
+#include "qora_oracle.h"
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+using namespace qor4b;
+
+namespace {
+
+struct Rng {
+    uint64_t s;
+    explicit Rng(uint64_t seed) : s(seed) {}
+    uint64_t next() {
+        uint64_t z = (s += 0x9E3779B97F4A7C15ull);
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+        return z ^ (z >> 31);
+    }
+    double uniform() { return ((next() >> 11) + 0.5) * (1.0 / 9007199254740992.0); }
+    float normal() { return static_cast<float>(std::sqrt(-2.0 * std::log(uniform())) * std::cos(6.283185307179586 * uniform())); }
+};
+
+std::vector<float> normals(Rng& r, std::size_t n, float std = 1.0f) {
+    std::vector<float> v(n);
+    for (auto& x : v) x = std * r.normal();
+    return v;
+}
+std::vector<uint16_t> to_bf16(const std::vector<float>& v) {
+    std::vector<uint16_t> o(v.size());
+    for (std::size_t i = 0; i < v.size(); ++i) o[i] = or_f32_to_bf16(v[i]);
+    return o;
+}
+std::vector<float> from_bf16(const std::vector<uint16_t>& v) {
+    std::vector<float> o(v.size());
+    for (std::size_t i = 0; i < v.size(); ++i) o[i] = or_bf16_to_f32(v[i]);
+    return o;
+}
+std::vector<uint16_t> to_f16(const std::vector<float>& v) {
+    std::vector<uint16_t> o(v.size());
+    for (std::size_t i = 0; i < v.size(); ++i) o[i] = or_f32_to_f16(v[i]);
+    return o;
+}
+template <class T>
+DeviceBuffer upload(Context& ctx, const std::vector<T>& v) {
+    DeviceBuffer b(ctx, v.size() * sizeof(T));
+    b.upload(v.data(), v.size() * sizeof(T));
+    return b;
+}
+double rel_err(const float* got, const float* ref, std::size_t n) {
+    double e = 0, m = 0;
+    for (std::size_t i = 0; i < n; ++i) {
+        e = std::fmax(e, std::fabs((double)got[i] - ref[i]));
+        m = std::fmax(m, std::fabs((double)ref[i]));
+    }
+    return m > 0 ? e / m : e;
+}
+double abs_err(const float* got, const float* ref, std::size_t n) {
+    double e = 0;
+    for (std::size_t i = 0; i < n; ++i) e = std::fmax(e, std::fabs((double)got[i] - ref[i]));
+    return e;
+}
+
+int failures = 0;
+void expect(bool ok, const char* what, double v, double bar) {
+    std::printf("%-52s %.3e (bar %.0e) %s\n", what, v, bar, ok ? "ok" : "FAIL");
+    if (!ok) ++failures;
+}
+
+or_config oracle_cfg(const Qor4bConfig& c) {
+    or_config o;
+    o.num_qk_heads = (int32_t)c.num_qk_heads; o.num_v_heads = (int32_t)c.num_v_heads;
+    o.dn_head_dim = (int32_t)c.deltanet_head_dim; o.conv_kernel = (int32_t)c.conv_kernel_size;
+    o.num_heads = (int32_t)c.num_attn_heads; o.num_kv_heads = (int32_t)c.num_kv_heads;
+    o.attn_head_dim = (int32_t)c.attn_head_dim; o.rope_dim = (int32_t)c.rope_dim();
+    return o;
+}
+
+void deltanet_flow(Context& ctx, const Qor4bConfig& cfg) {
+    const std::size_t T = 100, steps = 4;
+    const std::size_t qkv_dim = cfg.deltanet_qkv_dim(), v_dim = cfg.deltanet_v_dim(), nv = cfg.num_v_heads;
+    Rng r(11);
+    std::vector<float> conv_w = normals(r, qkv_dim * 4, 0.5f);
+    std::vector<float> a_log(nv), dt_bias(nv, 0.0f);
+    for (auto& x : a_log) x = std::log(0.01f + 0.09f * (float)r.uniform());
+    std::vector<float> gamma = normals(r, cfg.deltanet_head_dim, 0.1f);
+    for (auto& x : gamma) x += 1.0f;
+    std::vector<uint16_t> norm_w = to_f16(gamma);
+
+    GpuDeltaNetLayer layer{upload(ctx, conv_w), upload(ctx, a_log), upload(ctx, dt_bias), upload(ctx, norm_w)};
+    GpuDeltaNetState state = GpuDeltaNetState::zeros(ctx, cfg);
+
+    // prefill (bf16 projections)
+    std::vector<uint16_t> qkv_p = to_bf16(normals(r, T * qkv_dim)), z_p = to_bf16(normals(r, T * v_dim));
+    std::vector<float> a_p = normals(r, T * nv), b_p = normals(r, T * nv);
+    DeviceBuffer d_qkv = upload(ctx, qkv_p), d_z = upload(ctx, z_p), d_a = upload(ctx, a_p), d_b = upload(ctx, b_p);
+    DeviceBuffer d_out(ctx, T * v_dim * 2);
+    prefill_deltanet_layer_gpu(ctx, T, d_qkv.as<uint16_t>(), d_a.as<float>(), d_b.as<float>(), d_z.as<uint16_t>(),
+                               layer, state, cfg, d_out.as<uint16_t>());
+    std::vector<uint16_t> out_p(T * v_dim);
+    d_out.download(out_p.data(), out_p.size() * 2);
+
+    const or_config oc = oracle_cfg(cfg);
+    std::vector<float> S(nv * cfg.deltanet_head_dim * cfg.deltanet_head_dim, 0.0f), buf(qkv_dim * 3, 0.0f);
+    std::vector<float> ref_p(T * v_dim);
+    std::vector<float> qkv_pf = from_bf16(qkv_p), z_pf = from_bf16(z_p);
+    or_deltanet_prefill(&oc, (int32_t)T, qkv_pf.data(), a_p.data(), b_p.data(), z_pf.data(), buf.data(),
+                        conv_w.data(), a_log.data(), dt_bias.data(), norm_w.data(), S.data(), ref_p.data());
+    std::vector<float> got_p = from_bf16(out_p);
+    const double ep = rel_err(got_p.data(), ref_p.data(), got_p.size());
+    expect(ep <= 2e-2, "deltanet prefill T=100: rel out", ep, 2e-2);
+
+    // decode steps continue from the prefilled state and conv buffer
+    double ed = 0;
+    for (std::size_t s = 0; s < steps; ++s) {
+        std::vector<float> qkv = normals(r, qkv_dim), a = normals(r, nv), b = normals(r, nv), z = normals(r, v_dim);
+        DeviceBuffer dq = upload(ctx, qkv), da = upload(ctx, a), db = upload(ctx, b), dz = upload(ctx, z);
+        DeviceBuffer dout(ctx, v_dim * 4);
+        forward_deltanet_decode_gpu(ctx, dq.as<float>(), da.as<float>(), db.as<float>(), dz.as<float>(), layer,
+                                    state, cfg, dout.as<float>());
+        std::vector<float> got(v_dim), ref(v_dim);
+        dout.download(got.data(), got.size() * 4);
+        or_deltanet_decode_step(&oc, qkv.data(), 1, buf.data(), conv_w.data(), a.data(), b.data(), a_log.data(),
+                                dt_bias.data(), z.data(), norm_w.data(), S.data(), ref.data(), OR_UPDATE_AUTO);
+        ed = std::fmax(ed, rel_err(got.data(), ref.data(), v_dim));
+    }
+    expect(ed <= 2e-2, "deltanet decode x4 after prefill: rel out", ed, 2e-2);
+    std::vector<float> Sg(S.size()), bufg(buf.size());
+    state.s.download(Sg.data(), Sg.size() * 4);
+    state.conv_buf.download(bufg.data(), bufg.size() * 4);
+    expect(rel_err(Sg.data(), S.data(), S.size()) <= 2e-2, "deltanet state after prefill+decode: rel",
+           rel_err(Sg.data(), S.data(), S.size()), 2e-2);
+    expect(std::memcmp(bufg.data(), buf.data(), buf.size() * 4) == 0, "deltanet conv buffer exact (mismatch = 1)",
+           std::memcmp(bufg.data(), buf.data(), buf.size() * 4) != 0, 0.5);
+    expect(state.conv_pos == T + steps, "deltanet conv_pos advanced (error = |diff|)",
+           std::fabs((double)state.conv_pos - (double)(T + steps)), 0.5);
+}
+
+void attention_flow(Context& ctx, const Qor4bConfig& cfg) {
+    const std::size_t S = 50, steps = 3, cap = 64;
+    const std::size_t H = cfg.num_attn_heads, KV = cfg.num_kv_heads, D = cfg.attn_head_dim;
+    Rng r(12);
+    const int32_t rope_len = 128;
+    std::vector<float> cos_t(rope_len * cfg.rope_dim() / 2), sin_t(cos_t.size());
+    ctx.check(qm_rope_table(cfg.rope_theta, (int32_t)cfg.rope_dim(), rope_len, cos_t.data(), sin_t.data()));
+    DeviceBuffer d_cos = upload(ctx, cos_t), d_sin = upload(ctx, sin_t);
+    std::vector<uint16_t> qn = to_f16(normals(r, D, 0.1f)), kn = to_f16(normals(r, D, 0.1f));
+    GpuFullAttnLayer layer{upload(ctx, qn), upload(ctx, kn)};
+    GpuKvCacheEntry kv = GpuKvCacheEntry::with_capacity(ctx, cfg, cap);
+
+    std::vector<uint16_t> qg = to_bf16(normals(r, S * H * 2 * D)), k = to_bf16(normals(r, S * KV * D)),
+                          v = to_bf16(normals(r, S * KV * D));
+    DeviceBuffer d_qg = upload(ctx, qg), d_k = upload(ctx, k), d_v = upload(ctx, v);
+    DeviceBuffer d_out(ctx, S * H * D * 2);
+    prefill_attn_layer_gpu(ctx, S, d_qg.as<uint16_t>(), d_k.as<uint16_t>(), d_v.as<uint16_t>(), layer, kv, cfg,
+                           d_cos.as<float>(), d_sin.as<float>(), rope_len, d_out.as<uint16_t>());
+    std::vector<uint16_t> out_b(S * H * D);
+    d_out.download(out_b.data(), out_b.size() * 2);
+
+    const or_config oc = oracle_cfg(cfg);
+    std::vector<float> qgf = from_bf16(qg), kf = from_bf16(k), vf = from_bf16(v);
+    std::vector<float> Kc(cap * KV * D, 0.0f), Vc(cap * KV * D, 0.0f), ref(S * H * D);
+    or_attn_prefill(&oc, (int32_t)S, qgf.data(), kf.data(), vf.data(), qn.data(), kn.data(), cos_t.data(),
+                    sin_t.data(), rope_len, Kc.data(), Vc.data(), ref.data(), nullptr, 0, 4);
+    std::vector<float> got = from_bf16(out_b);
+    const double ep = rel_err(got.data(), ref.data(), got.size());
+    expect(ep <= 2e-2, "gqa prefill S=50: rel out", ep, 2e-2);
+    // the MI355X cache holds f16: decode in the oracle reads the same rounding
+    for (std::size_t i = 0; i < S * KV * D; ++i) {
+        Kc[i] = or_f16_to_f32(or_f32_to_f16(Kc[i]));
+        Vc[i] = or_f16_to_f32(or_f32_to_f16(Vc[i]));
+    }
+    double ed = 0;
+    for (std::size_t s = 0; s < steps; ++s) {
+        std::vector<float> q_gate = normals(r, H * 2 * D), k_new = normals(r, KV * D), v_new = normals(r, KV * D);
+        DeviceBuffer dq = upload(ctx, q_gate), dk = upload(ctx, k_new), dv = upload(ctx, v_new);
+        DeviceBuffer dout(ctx, H * D * 4);
+        const std::size_t pos = kv.seq_len;
+        forward_attn_decode_gpu(ctx, dq.as<float>(), dk.as<float>(), dv.as<float>(), layer, kv, cfg,
+                                d_cos.as<float>(), d_sin.as<float>(), rope_len, dout.as<float>());
+        std::vector<float> g(H * D), rf(H * D);
+        dout.download(g.data(), g.size() * 4);
+        or_attn_decode_step(&oc, q_gate.data(), k_new.data(), v_new.data(), qn.data(), kn.data(), cos_t.data(),
+                            sin_t.data(), rope_len, Kc.data(), Vc.data(), (int32_t)pos, 1, rf.data(), 4);
+        ed = std::fmax(ed, abs_err(g.data(), rf.data(), g.size()));
+    }
+    expect(ed <= 1e-3, "gqa decode x3 after prefill: max-abs out", ed, 1e-3);
+    expect(kv.seq_len == S + steps, "gqa kv seq_len advanced (error = |diff|)",
+           std::fabs((double)kv.seq_len - (double)(S + steps)), 0.5);
+    // a position past the RoPE table is an error, not a fault (gemv.rs:620-621 panics)
+    bool raised = false;
+    try {
+        kv.seq_len = rope_len;
+        std::vector<float> z(H * 2 * D, 0.0f);
+        DeviceBuffer dz = upload(ctx, z);
+        forward_attn_decode_gpu(ctx, dz.as<float>(), dz.as<float>(), dz.as<float>(), layer, kv, cfg,
+                                d_cos.as<float>(), d_sin.as<float>(), rope_len, dz.as<float>());
+    } catch (const MixerError& e) {
+        raised = e.code() == QM_ERR_ROPE_RANGE;
+    }
+    expect(raised, "gqa decode past the RoPE table raises (missing = 1)", raised ? 0 : 1, 0.5);
+}
+
+}  // namespace
+
+int main() {
+    try {
+        const Qor4bConfig cfg = Qor4bConfig::default_4b();
+        Context ctx(cfg);
+        deltanet_flow(ctx, cfg);
+        attention_flow(ctx, cfg);
+    } catch (const std::exception& e) {
+        std::printf("exception: %s\n", e.what());
+        return 2;
+    }
+    std::printf("%s\n", failures ? "FAILED" : "all checks passed");
+    return failures ? 1 : 0;
+}
