@@ -392,84 +392,107 @@ def run_gqa_prefill(args, ctx):
 
 # ----------------------------------------------------------------------------
 # CPU baseline: the oracle (C restatement of the reference CPU path) on this host
+CPU_SAMPLE_S = 10.0        # minimum seconds of CPU work per baseline sample
+
+
+def _repeat_for(fn, min_s=CPU_SAMPLE_S, max_iters=10 ** 6):
+    """Call fn() until min_s seconds have elapsed; returns (calls, seconds)."""
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_s or n >= max_iters:
+            return n, dt
+
+
 def cpu_baseline(workload: str) -> dict:
     O = _load("qora_oracle_py", ROOT / "oracle" / "oracle.py")
     cores = host_cores()
     att_threads = min(16, cores)
     cfg = O.config()
+    avx = "AVX-512" if O.has_avx512() else "scalar"
     if workload == "dn_decode":
         steps = 256
         w = W.dn_decode_workload(steps, 1, seed=0)
         S = w["state0"][0].copy()
-        t0 = time.perf_counter()
-        for t in range(steps):
-            O.deltanet_decode_step(cfg, w["qkv"][t, 0], w["a"][t, 0], w["b"][t, 0], w["z"][t, 0],
-                                   w["conv_w"], w["a_log"], w["dt_bias"], w["norm_w"], S)
-        dt = time.perf_counter() - t0
-        return {"value": steps / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
-                "sample": f"256 decode steps, batch 1, {'AVX-512' if O.has_avx512() else 'scalar'} head update, 1 thread"}
+
+        def sample():
+            for t in range(steps):
+                O.deltanet_decode_step(cfg, w["qkv"][t, 0], w["a"][t, 0], w["b"][t, 0], w["z"][t, 0],
+                                       w["conv_w"], w["a_log"], w["dt_bias"], w["norm_w"], S)
+        n, dt = _repeat_for(sample)
+        return {"value": n * steps / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
+                "sample": f"{n} x 256 decode steps, batch 1, {avx} head update, 1 thread ({dt:.1f} s)"}
     if workload == "dn_prefill":
         T = 1024
         w = W.dn_prefill_workload(T, seed=2)
         S, buf = w["state0"].copy(), w["conv_buf0"].copy()
         qkv, z = W.bf16_value(w["qkv"]), W.bf16_value(w["z"])
-        t0 = time.perf_counter()
-        O.deltanet_prefill(cfg, qkv, w["a"], w["b"], z, w["conv_w"], w["a_log"], w["dt_bias"],
-                           w["norm_w"], S, buf)
-        dt = time.perf_counter() - t0
-        return {"value": T / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
-                "sample": f"sequential prefill of the first {T} of 4096 tokens (gemv.rs:1119-1219 "
-                          "scalar loop, 1 thread); per-token cost is independent of position"}
+
+        def sample():
+            O.deltanet_prefill(cfg, qkv, w["a"], w["b"], z, w["conv_w"], w["a_log"], w["dt_bias"],
+                               w["norm_w"], S, buf)
+        n, dt = _repeat_for(sample)
+        return {"value": n * T / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
+                "sample": f"{n} x sequential prefill of 1024 tokens (gemv.rs:1119-1219 scalar loop, "
+                          f"1 thread; per-token cost is independent of position) ({dt:.1f} s)"}
     if workload == "gqa_prefill":
         S = 8192
         w = W.gqa_prefill_workload(S, seed=3)
         cos, sin = O.rope_table(S)
-        rows = np.arange(S - 16, S)          # the 16 most expensive rows
-        t0 = time.perf_counter()
-        O.attn_prefill(cfg, W.bf16_value(w["q_gate"]).reshape(S, -1), W.bf16_value(w["k"]).reshape(S, -1),
-                       W.bf16_value(w["v"]).reshape(S, -1), w["q_norm"], w["k_norm"], cos, sin,
-                       rows=rows, nthreads=att_threads)
-        dt = time.perf_counter() - t0
-        # scale by work: the 16 sampled rows attend to ~S keys each; a full
-        # prefill does S(S+1)/2 row-key pairs
-        work_sample = float(np.sum(rows + 1))
-        work_full = S * (S + 1) / 2.0
-        return {"value": S / (dt * work_full / work_sample), "unit": "tokens/s", "cores": att_threads,
+        qg = W.bf16_value(w["q_gate"]).reshape(S, -1)
+        kk = W.bf16_value(w["k"]).reshape(S, -1)
+        vv = W.bf16_value(w["v"]).reshape(S, -1)
+        done = {"rows": 0.0, "pairs": 0.0}
+
+        def sample():
+            hi = S - 16 * int(done["rows"] // 16)
+            rows = np.arange(max(hi - 16, 0), hi)
+            O.attn_prefill(cfg, qg, kk, vv, w["q_norm"], w["k_norm"], cos, sin, rows=rows,
+                           nthreads=att_threads)
+            done["rows"] += len(rows)
+            done["pairs"] += float(np.sum(rows + 1))
+        n, dt = _repeat_for(sample, max_iters=S // 16)
+        full = S * (S + 1) / 2.0
+        return {"value": S / (dt * full / done["pairs"]), "unit": "tokens/s", "cores": att_threads,
                 "kind": "port",
-                "sample": f"rows {S - 16}..{S - 1} of the 8192-token causal prefill (gemv.rs:1402-1444), "
-                          f"heads over {att_threads} threads, extrapolated linearly in row-key pairs"}
+                "sample": f"{int(done['rows'])} of the last rows of the 8192-token causal prefill "
+                          f"(gemv.rs:1402-1444), heads over {att_threads} threads, extrapolated "
+                          f"linearly in row-key pairs ({dt:.1f} s)"}
     if workload == "gqa_decode":
         pos = 4096
         w = W.gqa_decode_workload(pos, 1, seed=1)
         cos, sin = O.rope_table(pos + 1)
         K = np.ascontiguousarray(np.transpose(W.f16_value(w["k_cache"][0]), (1, 0, 2)))
         V = np.ascontiguousarray(np.transpose(W.f16_value(w["v_cache"][0]), (1, 0, 2)))
-        reps = 20
-        t0 = time.perf_counter()
-        for _ in range(reps):
+
+        def sample():
             O.attn_decode_step(cfg, w["q_gate"][0].ravel(), w["k_new"][0].ravel(), w["v_new"][0].ravel(),
                                w["q_norm"], w["k_norm"], cos, sin, K, V, pos, nthreads=att_threads)
-        dt = time.perf_counter() - t0
-        return {"value": reps / dt, "unit": "tokens/s", "cores": att_threads, "kind": "port",
-                "sample": f"{reps} decode steps at position 4096, f32 KV, heads over {att_threads} threads"}
-    # stack: one sequence, a few decode steps through all 32 layers at context 32768
-    steps, ctx0 = 2, 32768
+        n, dt = _repeat_for(sample)
+        return {"value": n / dt, "unit": "tokens/s", "cores": att_threads, "kind": "port",
+                "sample": f"{n} decode steps at position 4096, f32 KV, heads over {att_threads} threads ({dt:.1f} s)"}
+    # stack: one sequence decoding through all 32 layers at context 32768
+    max_steps, ctx0 = 64, 32768
     rng = np.random.default_rng(7)
-    cos, sin = O.rope_table(ctx0 + steps + 1)
+    cos, sin = O.rope_table(ctx0 + max_steps + 1)
     dn_w = [W.dn_params(rng) for _ in range(N_DN)]
     dn_S = [(0.02 * rng.standard_normal((32, 128, 128), dtype=np.float32)) for _ in range(N_DN)]
     caches = []
     for _ in range(N_GQA):
-        Kc = np.empty((ctx0 + steps, 4, 256), np.float32)
+        Kc = np.empty((ctx0 + max_steps, 4, 256), np.float32)
         Vc = np.empty_like(Kc)
         Kc[:ctx0] = W.f16_value(W.f16_bits(rng.standard_normal((ctx0, 4, 256), dtype=np.float32)))
         Vc[:ctx0] = W.f16_value(W.f16_bits(rng.standard_normal((ctx0, 4, 256), dtype=np.float32)))
         caches.append((Kc, Vc))
     qn = W.f16_bits(0.1 * rng.standard_normal(256, dtype=np.float32))
-    dn_in = rng.standard_normal((steps, N_DN, 8192 + 32 + 32 + 4096), dtype=np.float32)
-    g_in = rng.standard_normal((steps, N_GQA, 16 * 512 + 2 * 1024), dtype=np.float32)
-    t0 = time.perf_counter()
-    for s in range(steps):
+    dn_in = rng.standard_normal((max_steps, N_DN, 8192 + 32 + 32 + 4096), dtype=np.float32)
+    g_in = rng.standard_normal((max_steps, N_GQA, 16 * 512 + 2 * 1024), dtype=np.float32)
+    state = {"s": 0}
+
+    def sample():
+        s = state["s"]
         li_dn = li_g = 0
         for layer in range(32):
             if layer % 4 != 3:
@@ -483,11 +506,12 @@ def cpu_baseline(workload: str) -> dict:
                 O.attn_decode_step(cfg, x[:8192], x[8192:9216], x[9216:], qn, qn, cos, sin,
                                    Kc, Vc, ctx0 + s, nthreads=att_threads)
                 li_g += 1
-    dt = time.perf_counter() - t0
-    return {"value": steps / dt, "unit": "tokens/s", "cores": att_threads, "kind": "port",
-            "sample": f"1 sequence x {steps} decode steps through 32 layers at context {ctx0}; "
+        state["s"] += 1
+    n, dt = _repeat_for(sample, max_iters=max_steps)
+    return {"value": n / dt, "unit": "tokens/s", "cores": att_threads, "kind": "port",
+            "sample": f"1 sequence x {n} decode steps through 32 layers at context {ctx0}; "
                       f"f32 KV (the reference's storage), attention heads over {att_threads} threads, "
-                      f"DeltaNet heads serial (AVX-512 update: {O.has_avx512()})"}
+                      f"DeltaNet heads serial ({avx} update) ({dt:.1f} s)"}
 
 
 def main():
@@ -550,6 +574,10 @@ def main():
         "config": r["config"],
         "roofline": rl,
     }
+    if args.workload == "stack":
+        tf = ROOT / "profiles" / "traffic_stack_gqa_decode.json"
+        if tf.exists():   # measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (see the profile summary)
+            line["roofline"]["traffic"] = json.loads(tf.read_text())["traffic_bytes_per_launch"]
     for k in ("kernels", "step_frac_hbm", "graph_ms_per_step"):
         if k in r:
             line[k] = r[k]
