@@ -18,13 +18,14 @@
 //                        workgroup per (chunk, 128-channel head);
 //   qm_dn_prefill_chunk  everything that does not depend on S0, fully
 //                        parallel over (chunk, v-head): KK^T / QK^T on MFMA,
-//                        T by blocked inversion in fp32 (16x16 diagonal
-//                        blocks by substitution, off-diagonal blocks with
-//                        fp32 MFMA), W, U~, Q~ = diag(gamma)Q - PW, Y0 = PU~
-//                        on f16 MFMA;
-//   qm_dn_prefill_scan   the sequential part, one workgroup per v-head with
-//                        the 128x128 fp32 state in registers: three f16
-//                        MFMA GEMMs per chunk plus the fused gated RMSNorm.
+//                        [W | U~] by block forward substitution (16x16
+//                        diagonal inverses by substitution in fp32, the
+//                        off-diagonal corrections on MFMA), Q~ = diag(gamma)Q
+//                        - PW and Y0 = PU~, all products on f16 MFMA;
+//   qm_dn_prefill_scan   the sequential part: one wave per (v-head, 16 state
+//                        rows) with its rows of the fp32 state in registers,
+//                        three f16 MFMA GEMMs per chunk, Y out in fp32;
+//   qm_dn_prefill_norm   gated RMSNorm of Y and the conv buffer update.
 // The scan uses v_mfma_f32_16x16x16_f16 throughout because its fragment
 // layouts chain without lane shuffles: the state's C fragment (4 consecutive
 // k-cols per lane) is the B operand of U and Y, and U's C fragment (4
@@ -37,6 +38,10 @@ typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 #define CHK QM_DN_CHUNK
+
+QM_DEV half8 cat8(half4 a, half4 b) {
+    return half8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
 
 QM_DEV half4 to_half4(floatx4 v) {
     half4 r;
@@ -54,56 +59,86 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_prep(DnPrefillAr
     const int c = blockIdx.x / 64, gi = blockIdx.x % 64;     // 64 heads of 128 channels
     const int t0 = c * CHK;
     const int tpad = A.nc * CHK;
-    const int chl = tid & 127, half = tid >> 7;
-    const int ch = gi * 128 + chl;
-    const float4 w = ld4(A.conv_w + ch * 4);
-    const int tf = t0 + 32 * half;
-    auto raw = [&](int t) -> float {
-        if (t < 0) return A.conv_buf[(size_t)ch * 3 + 3 + t];   // buffer: x_{-3}, x_{-2}, x_{-1}
-        if (t >= A.T) return 0.0f;
-        return bf16_to_f32(A.qkv[(size_t)t * QM_DN_QKV_DIM + ch]);
-    };
-    float x3 = raw(tf - 3), x2 = raw(tf - 2), x1 = raw(tf - 1);
-    for (int j = 0; j < 32; ++j) {
-        const int t = tf + j;
-        const float x0 = raw(t);
-        float s = 0.0f;
-        s = __fadd_rn(s, __fmul_rn(x3, w.x));
-        s = __fadd_rn(s, __fmul_rn(x2, w.y));
-        s = __fadd_rn(s, __fmul_rn(x1, w.z));
-        s = __fadd_rn(s, __fmul_rn(x0, w.w));
-        act[32 * half + j][chl] = (t < A.T) ? silu_f(s) : 0.0f;
-        x3 = x2; x2 = x1; x1 = x0;
+    {
+        // thread: 8 channels (one 16-byte load per row) x 4 tokens; the 7 raw
+        // rows it needs are all loaded before any arithmetic
+        const int cg = tid & 15, tg = tid >> 4;
+        const int ch0 = gi * 128 + 8 * cg;
+        float x[7][8];
+#pragma unroll
+        for (int r = 0; r < 7; ++r) {
+            const int t = t0 + 4 * tg - 3 + r;
+            if (t >= 0 && t < A.T) {
+                const uint4 u = *reinterpret_cast<const uint4*>(A.qkv + (size_t)t * QM_DN_QKV_DIM + ch0);
+                const uint32_t wv[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    x[r][2 * e] = bf16_to_f32((uint16_t)(wv[e] & 0xffffu));
+                    x[r][2 * e + 1] = bf16_to_f32((uint16_t)(wv[e] >> 16));
+                }
+            } else if (t < 0) {                                  // x_{-3..-1} from the conv buffer
+#pragma unroll
+                for (int e = 0; e < 8; ++e) x[r][e] = A.conv_buf[(size_t)(ch0 + e) * 3 + 3 + t];
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) x[r][e] = 0.0f;
+            }
+        }
+        float4 w[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) w[e] = ld4(A.conv_w + (size_t)(ch0 + e) * 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int tok = 4 * tg + j;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                // gemv.rs:1134-1139 order: buffer taps oldest first, then the new token
+                float s = 0.0f;
+                s = __fadd_rn(s, __fmul_rn(x[j][e], w[e].x));
+                s = __fadd_rn(s, __fmul_rn(x[j + 1][e], w[e].y));
+                s = __fadd_rn(s, __fmul_rn(x[j + 2][e], w[e].z));
+                s = __fadd_rn(s, __fmul_rn(x[j + 3][e], w[e].w));
+                act[tok][8 * cg + e] = (t0 + tok < A.T) ? silu_f(s) : 0.0f;
+            }
+        }
     }
     __syncthreads();
 
-    const int tok = tid >> 2, part = tid & 3;                // 4 threads per token
-    float v[32];
+    // 16 lanes per token, 8 channels each: a store instruction writes four
+    // whole 256-byte rows
+    {
+        const int w = tid >> 6, lane = tid & 63, l16 = lane & 15;
+        float scale = 1.0f;
+        uint16_t* base;
+        if (gi < 32) {
+            scale = gi < 16 ? 1.0f / sqrtf((float)QM_DN_HD) : 1.0f;
+            base = (gi < 16 ? A.qh : A.kh) + (size_t)(gi & 15) * QM_DN_HD;
+        } else {
+            base = A.vv + (size_t)(gi - 32) * QM_DN_HD;
+        }
+        const int rows = gi < 32 ? QM_DN_QK_HEADS : QM_DN_V_HEADS;
 #pragma unroll
-    for (int e = 0; e < 32; ++e) v[e] = act[tok][32 * part + e];
-    uint16_t* dst;
-    if (gi < 32) {
-        // q (gi < 16) or k head: x /= ||x|| when ||x|| > 1e-12, q *= 1/sqrt(128)
-        float ss = 0.0f;
+        for (int q = 0; q < 4; ++q) {
+            const int tok = 16 * w + 4 * q + (lane >> 4);
+            float v[8];
 #pragma unroll
-        for (int e = 0; e < 32; ++e) ss = fmaf(v[e], v[e], ss);
-        ss += dpp_f32<0xB1>(ss);
-        ss += dpp_f32<0x4E>(ss);
-        const float norm = sqrtf(ss);
-        const float inv = norm > 1e-12f ? 1.0f / norm : 1.0f;
-        const float scale = gi < 16 ? 1.0f / sqrtf((float)QM_DN_HD) : 1.0f;
+            for (int e = 0; e < 8; ++e) v[e] = act[tok][8 * l16 + e];
+            if (gi < 32) {
+                // x /= ||x|| when ||x|| > 1e-12, q *= 1/sqrt(128)
+                float ss = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 32; ++e) v[e] = (v[e] * inv) * scale;
-        dst = (gi < 16 ? A.qh : A.kh) + ((size_t)(t0 + tok) * QM_DN_QK_HEADS + (gi & 15)) * QM_DN_HD + 32 * part;
-    } else {
-        dst = A.vv + ((size_t)(t0 + tok) * QM_DN_V_HEADS + (gi - 32)) * QM_DN_HD + 32 * part;
-    }
+                for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
+                ss = row_sum16(ss);
+                const float norm = sqrtf(ss);
+                const float inv = norm > 1e-12f ? 1.0f / norm : 1.0f;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        half8 h;
+                for (int e = 0; e < 8; ++e) v[e] = (v[e] * inv) * scale;
+            }
+            half8 hv;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) h[e] = (_Float16)v[8 * q + e];
-        *reinterpret_cast<half8*>(dst + 8 * q) = h;
+            for (int e = 0; e < 8; ++e) hv[e] = (_Float16)v[e];
+            *reinterpret_cast<half8*>(base + (size_t)(t0 + tok) * rows * QM_DN_HD + 8 * l16) = hv;
+        }
     }
 
     if (gi >= 32 && tid < 64) {
@@ -131,33 +166,24 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_prep(DnPrefillAr
 // ============================================================================
 // 2. chunk: per (chunk, v-head), everything independent of the entering state
 // ============================================================================
-QM_DEV floatx4 mm16_f32(floatx4 c, const float (*X)[68], int xr, int xc, const float (*Y)[68], int yr,
-                        int yc, int lane) {
-    // c += X[xr:xr+16, xc:xc+16] * Y[yr:yr+16, yc:yc+16], fp32 MFMA 16x16x4
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-        const float a = X[xr + (lane & 15)][xc + 4 * ks + (lane >> 4)];
-        const float b = Y[yr + 4 * ks + (lane >> 4)][yc + (lane & 15)];
-        c = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-    }
-    return c;
-}
-
-QM_DEV void store_c16(float (*D)[68], int r0, int c0, floatx4 c, float sgn, int lane) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) D[r0 + 4 * (lane >> 4) + e][c0 + (lane & 15)] = sgn * c[e];
-}
-
+// [W | U~] = (I + A)^-1 [diag(beta gamma) K | diag(beta) V] is solved by block
+// forward substitution over the four 16-token blocks b:
+//   R_b = B_b - sum_{k<b} A_bk X_k,  X_b = T_bb R_b,  T_bb = (I + A_bb)^-1,
+// with the 16x16 diagonal inverses by substitution in fp32 and the products on
+// v_mfma_f32_16x16x16_f16.  Each wave owns 4 of the 16 column tiles (k-col
+// tiles 2w, 2w+1 of W and v-col tiles 2w, 2w+1 of U~) for every block, and
+// an X_k fragment (4 consecutive tokens of one column per lane) is already
+// the B operand of the next block's correction, so the solve needs no
+// workgroup barrier.
 extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillArgs A) {
-    __shared__ _Float16 Ks[CHK][136];
-    __shared__ _Float16 Qs[CHK][136];
-    __shared__ _Float16 Kt[QM_DN_HD][72];
-    __shared__ _Float16 Vt[QM_DN_HD][72];
-    __shared__ _Float16 Pm[CHK][72];
-    __shared__ float Af[CHK][68];
-    __shared__ float Tf[CHK][68];
-    __shared__ float scr[4][16][68];
+    __shared__ _Float16 Ks[CHK][136];              // K row-major; later -W staging
+    __shared__ _Float16 Kt[QM_DN_HD][72];          // K^T
+    __shared__ _Float16 Vt[QM_DN_HD][72];          // V^T; later Q~ staging
+    __shared__ _Float16 Pm[CHK][72];               // P (lower, incl. diagonal)
+    __shared__ _Float16 Am[CHK][72];               // A (strictly lower)
+    __shared__ _Float16 Td[4][16][24];             // (I + A_bb)^-1
     __shared__ float Gs[CHK], Bs[CHK], Eg[CHK], BG[CHK], Kd[CHK];
+    _Float16 (*Qstage)[136] = reinterpret_cast<_Float16 (*)[136]>(&Vt[0][0]);
 
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int c = blockIdx.x / QM_DN_V_HEADS, h = blockIdx.x % QM_DN_V_HEADS;
@@ -166,156 +192,124 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
     const int tpad = A.nc * CHK;
     const size_t hc = (size_t)h * A.nc + c;
     const int lr = lane & 15, lq = lane >> 4;
+    const uint16_t* qbase = A.qh + ((size_t)t0 * QM_DN_QK_HEADS + qkh) * QM_DN_HD;   // row stride 16*128
 
-    // ---- 0. load K, Q (row-major and K, V transposed) and the gates
+    // ---- 0. K (row-major and transposed), V (transposed), gates
     {
         const int i = tid >> 2, p = tid & 3;
         const uint16_t* kr = A.kh + ((size_t)(t0 + i) * QM_DN_QK_HEADS + qkh) * QM_DN_HD + 32 * p;
-        const uint16_t* qr = A.qh + ((size_t)(t0 + i) * QM_DN_QK_HEADS + qkh) * QM_DN_HD + 32 * p;
         const uint16_t* vr = A.vv + ((size_t)(t0 + i) * QM_DN_V_HEADS + h) * QM_DN_HD + 32 * p;
+        half8 kv[4], vv[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const half8 kv = *reinterpret_cast<const half8*>(kr + 8 * q);
-            const half8 qv = *reinterpret_cast<const half8*>(qr + 8 * q);
-            const half8 vv = *reinterpret_cast<const half8*>(vr + 8 * q);
-            *reinterpret_cast<half8*>(&Ks[i][32 * p + 8 * q]) = kv;
-            *reinterpret_cast<half8*>(&Qs[i][32 * p + 8 * q]) = qv;
+            kv[q] = *reinterpret_cast<const half8*>(kr + 8 * q);
+            vv[q] = *reinterpret_cast<const half8*>(vr + 8 * q);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            *reinterpret_cast<half8*>(&Ks[i][32 * p + 8 * q]) = kv[q];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                Kt[32 * p + 8 * q + e][i] = kv[e];
-                Vt[32 * p + 8 * q + e][i] = vv[e];
+                Kt[32 * p + 8 * q + e][i] = kv[q][e];
+                Vt[32 * p + 8 * q + e][i] = vv[q][e];
             }
         }
         if (tid < CHK) {
-            Gs[tid] = A.G[(size_t)h * tpad + t0 + tid];
-            Bs[tid] = A.beta[(size_t)h * tpad + t0 + tid];
-        }
-        // T: zero the blocks above the block diagonal
-        for (int idx = tid; idx < 6 * 256; idx += 256) {
-            const int blk = idx >> 8, e = idx & 255;
-            const int rb = blk < 3 ? 0 : (blk < 5 ? 1 : 2);
-            const int cb = blk < 3 ? blk + 1 : (blk < 5 ? blk - 1 : 3);
-            Tf[16 * rb + (e >> 4)][16 * cb + (e & 15)] = 0.0f;
+            const float gg = A.G[(size_t)h * tpad + t0 + tid];
+            const float bb = A.beta[(size_t)h * tpad + t0 + tid];
+            Gs[tid] = gg;
+            Bs[tid] = bb;
+            Eg[tid] = expf(gg);                  // gamma_i
+            BG[tid] = bb * expf(gg);             // beta_i gamma_i
         }
     }
     __syncthreads();
-    if (tid < CHK) {
-        Eg[tid] = expf(Gs[tid]);                  // gamma_i
-        BG[tid] = Bs[tid] * Eg[tid];              // beta_i gamma_i
-        Kd[tid] = expf(Gs[CHK - 1] - Gs[tid]);    // gamma_C / gamma_i
-    }
+    if (tid < CHK) Kd[tid] = expf(Gs[CHK - 1] - Gs[tid]);     // gamma_C / gamma_i
 
-    // ---- 1. KK^T and QK^T (16x16x32 f16), masked and decayed
+    // ---- 1. KK^T and QK^T (16x16x32 f16), masked and decayed -> A, P (f16)
     {
         const int i0 = 16 * w;
-        for (int j = 0; j <= w; ++j) {
+        half8 aq[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            aq[s] = *reinterpret_cast<const half8*>(qbase + (size_t)(i0 + lr) * QM_DN_QK_HEADS * QM_DN_HD + 32 * s + 8 * lq);
+        for (int j = 0; j < 4; ++j) {
+            if (j > w) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    Pm[i0 + 4 * lq + e][16 * j + lr] = (_Float16)0.0f;
+                    Am[i0 + 4 * lq + e][16 * j + lr] = (_Float16)0.0f;
+                }
+                continue;
+            }
             floatx4 ckk = {0.0f, 0.0f, 0.0f, 0.0f}, cqk = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
                 const int kk = 32 * s + 8 * lq;
                 const half8 ak = *reinterpret_cast<const half8*>(&Ks[i0 + lr][kk]);
-                const half8 aq = *reinterpret_cast<const half8*>(&Qs[i0 + lr][kk]);
                 const half8 bk = *reinterpret_cast<const half8*>(&Ks[16 * j + lr][kk]);
                 ckk = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak, bk, ckk, 0, 0, 0);
-                cqk = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq, bk, cqk, 0, 0, 0);
+                cqk = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq[s], bk, cqk, 0, 0, 0);
             }
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int i = i0 + 4 * lq + e, jj = 16 * j + lr;
                 const float dec = jj <= i ? expf(Gs[i] - Gs[jj]) : 0.0f;
-                Af[i][jj] = jj < i ? Bs[i] * dec * ckk[e] : 0.0f;
+                Am[i][jj] = (_Float16)(jj < i ? Bs[i] * dec * ckk[e] : 0.0f);
                 Pm[i][jj] = (_Float16)(jj <= i ? dec * cqk[e] : 0.0f);
             }
-        }
-        for (int j = w + 1; j < 4; ++j) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) Pm[i0 + 4 * lq + e][16 * j + lr] = (_Float16)0.0f;
         }
     }
     __syncthreads();
 
-    // ---- 2. T = (I + A)^-1
-    // 2a. diagonal 16x16 blocks by forward substitution (lane m owns column m)
+    // ---- 2. diagonal blocks T_bb = (I + A_bb)^-1 by substitution (lane m owns column m)
     if (lane < 16) {
         const int b0 = 16 * w, m = lane;
         float t[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
+            const half8 r0 = *reinterpret_cast<const half8*>(&Am[b0 + i][b0]);
+            const half8 r1 = *reinterpret_cast<const half8*>(&Am[b0 + i][b0 + 8]);
             float v = (i == m) ? 1.0f : 0.0f;
 #pragma unroll
-            for (int j = 0; j < i; ++j) v -= Af[b0 + i][b0 + j] * t[j];
+            for (int j = 0; j < i; ++j) v -= (float)(j < 8 ? r0[j] : r1[j - 8]) * t[j];
             t[i] = v;
         }
 #pragma unroll
-        for (int i = 0; i < 16; ++i) Tf[b0 + i][b0 + m] = t[i];
-    }
-    __syncthreads();
-    // 2b. T_{2p+1,2p} = -T_{2p+1,2p+1} A_{2p+1,2p} T_{2p,2p}
-    if (w < 2) {
-        const int r = 16 * (2 * w + 1), cb = 16 * (2 * w);
-        floatx4 m = {0.0f, 0.0f, 0.0f, 0.0f};
-        m = mm16_f32(m, Af, r, cb, Tf, cb, cb, lane);
-        store_c16(scr[w], 0, 0, m, 1.0f, lane);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        floatx4 t = {0.0f, 0.0f, 0.0f, 0.0f};
-        t = mm16_f32(t, Tf, r, r, scr[w], 0, 0, lane);
-        store_c16(Tf, r, cb, t, -1.0f, lane);
-    }
-    __syncthreads();
-    // 2c. lower-left 32x32 quadrant: T21 = -T22 (A21 T11) with 2x2 blocks
-    {
-        const int rb = 2 + (w >> 1), cb = w & 1;
-        floatx4 m = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int kb = cb; kb < 2; ++kb) m = mm16_f32(m, Af, 16 * rb, 16 * kb, Tf, 16 * kb, 16 * cb, lane);
-        store_c16(scr[w], 0, 0, m, 1.0f, lane);
-    }
-    __syncthreads();
-    {
-        const int rb = 2 + (w >> 1), cb = w & 1;
-        floatx4 t = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int kb = 2; kb <= rb; ++kb) t = mm16_f32(t, Tf, 16 * rb, 16 * kb, scr[(kb - 2) * 2 + cb], 0, 0, lane);
-        __syncthreads();   // every wave has read T_{3,2} (rb == 3) before any block is written
-        store_c16(Tf, 16 * rb, 16 * cb, t, -1.0f, lane);
+        for (int i = 0; i < 16; ++i) Td[w][i][m] = (_Float16)t[i];
     }
     __syncthreads();
 
-    // ---- 3. W = T diag(beta gamma) K and U~ = T diag(beta) V (16x16x32 f16)
-    //      wave w owns k-col tiles 2w, 2w+1 of W and v-col tiles 2w, 2w+1 of U~
+    // ---- 3. [W | U~] by block forward substitution (16x16x16 f16)
+    //      tiles: cc = 0,1 -> W k-col tiles 2w+cc; cc = 2,3 -> U~ v-col tiles 2w+cc-2
     floatx4 cw[4][2], cu[4][2];
+    half4 xh[4][4];                                   // X_b fragments as f16 B operands
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int b = 0; b < 4; ++b) {
+        const half4 tb = *reinterpret_cast<const half4*>(&Td[b][lr][4 * lq]);
 #pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
-            cw[i][cc] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-            cu[i][cc] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-        }
+        for (int cc = 0; cc < 4; ++cc) {
+            const int col = 16 * (2 * w + (cc & 1)) + lr;
+            floatx4 r;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int s = 0; s <= (i >> 1); ++s) {
-            const int row = 16 * i + lr, k0 = 32 * s + 8 * lq;
-            half8 a1, a2;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float tv = Tf[row][k0 + e];
-                a1[e] = (_Float16)(tv * BG[k0 + e]);
-                a2[e] = (_Float16)(tv * Bs[k0 + e]);
+            for (int e = 0; e < 4; ++e) {
+                const int tk = 16 * b + 4 * lq + e;
+                r[e] = cc < 2 ? BG[tk] * (float)Kt[col][tk] : Bs[tk] * (float)Vt[col][tk];
             }
 #pragma unroll
-            for (int cc = 0; cc < 2; ++cc) {
-                const int col = 16 * (2 * w + cc) + lr;
-                const half8 bk = *reinterpret_cast<const half8*>(&Kt[col][k0]);
-                const half8 bv = *reinterpret_cast<const half8*>(&Vt[col][k0]);
-                cw[i][cc] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bk, cw[i][cc], 0, 0, 0);
-                cu[i][cc] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, bv, cu[i][cc], 0, 0, 0);
+            for (int k = 0; k < b; ++k) {
+                const half4 an = -*reinterpret_cast<const half4*>(&Am[16 * b + lr][16 * k + 4 * lq]);
+                r = __builtin_amdgcn_mfma_f32_16x16x16f16(an, xh[k][cc], r, 0, 0, 0);
             }
+            floatx4 x = {0.0f, 0.0f, 0.0f, 0.0f};
+            x = __builtin_amdgcn_mfma_f32_16x16x16f16(tb, to_half4(r), x, 0, 0, 0);
+            xh[b][cc] = to_half4(x);
+            if (cc < 2) cw[b][cc] = x; else cu[b][cc - 2] = x;
         }
     }
 
     // ---- 4. Q~ = diag(gamma) Q - P W and Y0 = P U~ (16x16x16 f16; the W / U~
-    //      C fragments are the B operands as they stand)
+    //      fragments are the B operands as they stand)
     floatx4 cq[4][2], cy[4][2];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -325,7 +319,8 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int tk = 16 * i + 4 * lq + e;
-                cq[i][cc][e] = Eg[tk] * (float)Qs[tk][col];
+                const uint16_t qb = qbase[(size_t)tk * QM_DN_QK_HEADS * QM_DN_HD + col];
+                cq[i][cc][e] = Eg[tk] * f16_to_f32(qb);
             }
             cy[i][cc] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
         }
@@ -337,40 +332,48 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
             const half4 an = -ap;
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc) {
-                cq[i][cc] = __builtin_amdgcn_mfma_f32_16x16x16f16(an, to_half4(cw[kt][cc]), cq[i][cc], 0, 0, 0);
-                cy[i][cc] = __builtin_amdgcn_mfma_f32_16x16x16f16(ap, to_half4(cu[kt][cc]), cy[i][cc], 0, 0, 0);
+                cq[i][cc] = __builtin_amdgcn_mfma_f32_16x16x16f16(an, xh[kt][cc], cq[i][cc], 0, 0, 0);
+                cy[i][cc] = __builtin_amdgcn_mfma_f32_16x16x16f16(ap, xh[kt][cc + 2], cy[i][cc], 0, 0, 0);
             }
         }
     }
 
-    // ---- 5. outputs
-    // U~^T and Y0^T: lane holds 4 consecutive tokens of one v-row -> 8-byte stores
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
+    // ---- 5. outputs, all in the scan's fragment order (16-byte pieces; see
+    //      the scan kernel for the piece layouts)
+    // U~ and Y0: this wave's C fragments are the scan's fragments as they stand
+    {
+        const size_t base = hc * CHK * QM_DN_HD;
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
-            const int row = 16 * (2 * w + cc) + lr;
-            const size_t o = (hc * QM_DN_HD + row) * CHK + 16 * i + 4 * lq;
-            *reinterpret_cast<half4*>(A.Ut + o) = to_half4(cu[i][cc]);
-            *reinterpret_cast<half4*>(A.Y0t + o) = to_half4(cy[i][cc]);
+            const int vt = 2 * w + cc;
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                const size_t o = base + (size_t)((vt * 2 + p) * 64 + lane) * 8;
+                const half4 u0 = to_half4(cu[2 * p][cc]), u1 = to_half4(cu[2 * p + 1][cc]);
+                const half4 y0 = to_half4(cy[2 * p][cc]), y1 = to_half4(cy[2 * p + 1][cc]);
+                *reinterpret_cast<half8*>(A.Ut + o) = half8{u0[0], u0[1], u0[2], u0[3], u1[0], u1[1], u1[2], u1[3]};
+                *reinterpret_cast<half8*>(A.Y0t + o) = half8{y0[0], y0[1], y0[2], y0[3], y1[0], y1[1], y1[2], y1[3]};
+            }
         }
+    }
     // K~^T = (gamma_C / gamma_j) K^T
     {
-        const int row = tid >> 1, p = tid & 1;
-        uint16_t* dst = A.Ktt + (hc * QM_DN_HD + row) * CHK + 32 * p;
+        uint16_t* dst = A.Ktt + hc * CHK * QM_DN_HD;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int r = 0; r < 4; ++r) {
+            const int q = tid + 256 * r, kt = q >> 7, p = (q >> 6) & 1, l = q & 63;
+            const int row = 16 * kt + (l & 15), tk0 = 32 * p + 4 * (l >> 4);
             half8 hv;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int tk = 32 * p + 8 * q + e;
-                hv[e] = (_Float16)((float)Kt[row][tk] * Kd[tk]);
+            for (int e = 0; e < 4; ++e) {
+                hv[e] = (_Float16)((float)Kt[row][tk0 + e] * Kd[tk0 + e]);
+                hv[4 + e] = (_Float16)((float)Kt[row][tk0 + 16 + e] * Kd[tk0 + 16 + e]);
             }
-            *reinterpret_cast<half8*>(dst + 8 * q) = hv;
+            *reinterpret_cast<half8*>(dst + (size_t)q * 8) = hv;
         }
     }
     if (tid == 0) A.gC[hc] = expf(Gs[CHK - 1]);
-    __syncthreads();     // Ks / Qs are free: stage -W and Q~ token-major
+    __syncthreads();     // Ks and Vt are free: stage -W and Q~ token-major
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -380,7 +383,7 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
             for (int e = 0; e < 4; ++e) {
                 const int tk = 16 * i + 4 * lq + e;
                 Ks[tk][col] = (_Float16)(-cw[i][cc][e]);
-                Qs[tk][col] = (_Float16)cq[i][cc][e];
+                Qstage[tk][col] = (_Float16)cq[i][cc][e];
             }
         }
     __syncthreads();
@@ -389,169 +392,225 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
         uint16_t* qdst = A.Qt + hc * CHK * QM_DN_HD;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int piece = tid + 256 * r;          // 1024 pieces of 8 halfs
-            const int row = piece >> 4, col = 8 * (piece & 15);
-            *reinterpret_cast<half8*>(wdst + row * QM_DN_HD + col) = *reinterpret_cast<const half8*>(&Ks[row][col]);
-            *reinterpret_cast<half8*>(qdst + row * QM_DN_HD + col) = *reinterpret_cast<const half8*>(&Qs[row][col]);
+            const int q = tid + 256 * r, i = q >> 8, p = (q >> 6) & 3, l = q & 63;
+            const int row = 16 * i + (l & 15), c0 = 32 * p + 4 * (l >> 4);
+            const half4 w0 = *reinterpret_cast<const half4*>(&Ks[row][c0]);
+            const half4 w1 = *reinterpret_cast<const half4*>(&Ks[row][c0 + 16]);
+            const half4 q0 = *reinterpret_cast<const half4*>(&Qstage[row][c0]);
+            const half4 q1 = *reinterpret_cast<const half4*>(&Qstage[row][c0 + 16]);
+            *reinterpret_cast<half8*>(wdst + (size_t)q * 8) = half8{w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+            *reinterpret_cast<half8*>(qdst + (size_t)q * 8) = half8{q0[0], q0[1], q0[2], q0[3], q1[0], q1[1], q1[2], q1[3]};
         }
     }
 }
 
 // ============================================================================
-// 3. scan: per v-head, sequential over chunks, state in registers
+// 3. scan: sequential over chunks, one wave per (v-head, 16 state rows)
 // ============================================================================
-// Wave w owns state rows 16w..16w+15; for k-col tile t the lane (r, q) =
-// (lane & 15, lane >> 4) holds S[16w + r][16t + 4q .. 16t + 4q + 3].
-extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_scan(DnPrefillArgs A) {
-    __shared__ _Float16 Wb[CHK][136];
-    __shared__ _Float16 Qb[CHK][136];
-    __shared__ _Float16 Kb[QM_DN_HD][72];
-    __shared__ float ys[CHK][132];
-
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-    const int lr = lane & 15, lq = lane >> 4;
-    const int h = blockIdx.x;
-
-    // conv buffer after the prefill: the last three raw inputs (gemv.rs:1141-1146)
-    {
-        const int ch = h * 512 + tid;
-        if (ch < QM_DN_QKV_DIM) {
-            float old[3] = {A.conv_buf[(size_t)ch * 3], A.conv_buf[(size_t)ch * 3 + 1], A.conv_buf[(size_t)ch * 3 + 2]};
-            float nb[3];
-#pragma unroll
-            for (int j = 0; j < 3; ++j) {
-                const int t = A.T - 3 + j;
-                nb[j] = t >= 0 ? bf16_to_f32(A.qkv[(size_t)t * QM_DN_QKV_DIM + ch]) : old[A.T + j];
-            }
-#pragma unroll
-            for (int j = 0; j < 3; ++j) A.conv_buf[(size_t)ch * 3 + j] = nb[j];
-        }
-    }
+// Under the chunked delta rule every state row evolves on its own:
+//   U_r = U~_r - W S_r^T,  Y_r = Y0_r + Q~ S_r^T,  S_r <- gamma_C S_r + U_r^T K~
+// so a v-head's 128 rows split over 8 independent waves (grid 256).  A wave
+// keeps S_r^T (k-cols x 16 rows, fp32) as eight C fragments; for k tile t,
+// lane (r, q) = (lane & 15, lane >> 4) holds S[16 vt + r][16 t + 4q .. +3].
+// All chunk operands arrive in fragment order as 16-byte pieces, piece
+// (j, lane) at byte offset 16 (64 j + lane) of the (head, chunk) block:
+//   -W, Q~   j = 4 i + p: tokens 16 i + (lane & 15), k-cols 32 p + 4 (lane >> 4)
+//            + {0..3} (k step 2p) and + 16 + {0..3} (k step 2p+1);
+//   K~^T     j = 2 kt + p: k-col 16 kt + (lane & 15), tokens 32 p + 4 (lane >> 4)
+//            + {0..3} and + 16 + {0..3};
+//   U~, Y0   j = 2 vt + p: row 16 vt + (lane & 15), tokens 32 p + 4 (lane >> 4)
+//            + {0..3} and + 16 + {0..3}.
+// A 16-byte piece is the A operand of one v_mfma_f32_16x16x32_f16: a product
+// only needs A and B to agree on which k each (lane, element) holds, and the
+// two C fragments of S^T k tiles 2p, 2p+1 (or of U token tiles 2p, 2p+1)
+// concatenated hold exactly the k (token) set of piece p.
+// The next chunk's operands are loaded into registers right after the
+// current chunk's last use of each, so the loads overlap two of the three
+// GEMM phases.  Y leaves in fp32, token-major, for the norm.
+extern "C" __global__ __launch_bounds__(64) void qm_dn_prefill_scan(DnPrefillArgs A) {
+    const int lane = threadIdx.x;
+    // blocks are dealt to the 8 XCDs round-robin: keep a head's 8 row slices
+    // on one XCD so its chunk operands are fetched into one L2
+    const int b = blockIdx.x, xcd = b & 7, idx = b >> 3;
+    const int h = xcd + 8 * (idx >> 3), vt = idx & 7;
+    const int nc = A.nc;
 
     float* Sg = A.state + (size_t)h * QM_DN_HEAD_ELEMS;
     floatx4 S[8];
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
-        const float4 v = ld4(Sg + (size_t)(16 * w + lr) * QM_DN_HD + 16 * t + 4 * lq);
+        const float4 v = ld4(Sg + (size_t)(16 * vt + (lane & 15)) * QM_DN_HD + 16 * t + 4 * (lane >> 4));
         S[t] = floatx4{v.x, v.y, v.z, v.w};
     }
 
-    // per-chunk operand pieces of this thread: 2 of -W, 2 of Q~, 2 of K~^T
-    // (16 bytes each), and this wave's U~^T / Y0^T fragments
-    half8 pw[2], pq[2], pk[2];
-    half4 pu[4], py[4];
-    auto fetch = [&](int c) {
-        const size_t hc = (size_t)h * A.nc + c;
-        const uint16_t* wsrc = A.Wn + hc * CHK * QM_DN_HD;
-        const uint16_t* qsrc = A.Qt + hc * CHK * QM_DN_HD;
-        const uint16_t* ksrc = A.Ktt + hc * QM_DN_HD * CHK;
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            const int piece = tid + 512 * r;
-            pw[r] = *reinterpret_cast<const half8*>(wsrc + 8 * piece);
-            pq[r] = *reinterpret_cast<const half8*>(qsrc + 8 * piece);
-            pk[r] = *reinterpret_cast<const half8*>(ksrc + 8 * piece);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const size_t o = (hc * QM_DN_HD + 16 * w + lr) * CHK + 16 * i + 4 * lq;
-            pu[i] = *reinterpret_cast<const half4*>(A.Ut + o);
-            py[i] = *reinterpret_cast<const half4*>(A.Y0t + o);
-        }
+    half8 wf[16], qf[16], kf[16], uf[2], yf[2];
+    auto blk = [&](const uint16_t* base, int c) {
+        return base + ((size_t)h * nc + c) * (CHK * QM_DN_HD) + (size_t)lane * 8;
     };
-    auto stage = [&]() {
+    // first chunk's operands, issued in the order the loop reissues them
+    // (W; Q~, U~, Y0; K~^T, gamma_C) so that the in-order load counter lets
+    // each phase wait for its own operands only
+    {
+        const uint16_t* pw = blk(A.Wn, 0);
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            const int piece = tid + 512 * r;
-            *reinterpret_cast<half8*>(&Wb[piece >> 4][8 * (piece & 15)]) = pw[r];
-            *reinterpret_cast<half8*>(&Qb[piece >> 4][8 * (piece & 15)]) = pq[r];
-            *reinterpret_cast<half8*>(&Kb[piece >> 3][8 * (piece & 7)]) = pk[r];
+        for (int j = 0; j < 16; ++j) wf[j] = *reinterpret_cast<const half8*>(pw + j * 512);
+        __builtin_amdgcn_sched_barrier(0);
+        const uint16_t* pq = blk(A.Qt, 0);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) qf[j] = *reinterpret_cast<const half8*>(pq + j * 512);
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            uf[p] = *reinterpret_cast<const half8*>(blk(A.Ut, 0) + (2 * vt + p) * 512);
+            yf[p] = *reinterpret_cast<const half8*>(blk(A.Y0t, 0) + (2 * vt + p) * 512);
         }
-    };
+        __builtin_amdgcn_sched_barrier(0);
+        const uint16_t* pk = blk(A.Ktt, 0);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) kf[j] = *reinterpret_cast<const half8*>(pk + j * 512);
+    }
+    float gC = A.gC[(size_t)h * nc];
+    __builtin_amdgcn_sched_barrier(0);
 
-    fetch(0);
-    stage();
-    __syncthreads();
-    const uint16_t* zbase = A.z;
-    for (int c = 0; c < A.nc; ++c) {
-        half4 cu_h[4];
-        floatx4 uu[4], yy[4];
+    for (int c = 0; c < nc; ++c) {
+        const int cn = c + 1 < nc ? c + 1 : c;
+        half8 sb[4];                      // S^T k-tiles 2p, 2p+1 as one B operand
+#pragma unroll
+        for (int p = 0; p < 4; ++p) sb[p] = cat8(to_half4(S[2 * p]), to_half4(S[2 * p + 1]));
+
+        // U = U~ + (-W) S^T
+        floatx4 uu[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            uu[i] = floatx4{(float)pu[i][0], (float)pu[i][1], (float)pu[i][2], (float)pu[i][3]};
-            yy[i] = floatx4{(float)py[i][0], (float)py[i][1], (float)py[i][2], (float)py[i][3]};
+            const half8 src = uf[i >> 1];
+            const int o = 4 * (i & 1);
+            uu[i] = floatx4{(float)src[o], (float)src[o + 1], (float)src[o + 2], (float)src[o + 3]};
+#pragma unroll
+            for (int p = 0; p < 4; ++p)
+                uu[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[4 * i + p], sb[p], uu[i], 0, 0, 0);
         }
-        const float gC = A.gC[(size_t)h * A.nc + c];
-        if (c + 1 < A.nc) fetch(c + 1);
-        half4 sh[8];
+        __builtin_amdgcn_sched_barrier(0);
+        {
+            const uint16_t* pw = blk(A.Wn, cn);
 #pragma unroll
-        for (int t = 0; t < 8; ++t) sh[t] = to_half4(S[t]);
-        // U = U~ - W S^T, Y = Y0 + Q~ S^T   (tokens x rows, K = k-cols)
+            for (int j = 0; j < 16; ++j) wf[j] = *reinterpret_cast<const half8*>(pw + j * 512);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+
+        // Y = Y0 + Q~ S^T
+        floatx4 yy[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
+            const half8 src = yf[i >> 1];
+            const int o = 4 * (i & 1);
+            yy[i] = floatx4{(float)src[o], (float)src[o + 1], (float)src[o + 2], (float)src[o + 3]};
 #pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                const half4 aw = *reinterpret_cast<const half4*>(&Wb[16 * i + lr][16 * t + 4 * lq]);
-                const half4 aq = *reinterpret_cast<const half4*>(&Qb[16 * i + lr][16 * t + 4 * lq]);
-                uu[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(aw, sh[t], uu[i], 0, 0, 0);
-                yy[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(aq, sh[t], yy[i], 0, 0, 0);
+            for (int p = 0; p < 4; ++p)
+                yy[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qf[4 * i + p], sb[p], yy[i], 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        {
+            const uint16_t* pq = blk(A.Qt, cn);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) qf[j] = *reinterpret_cast<const half8*>(pq + j * 512);
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                uf[p] = *reinterpret_cast<const half8*>(blk(A.Ut, cn) + (2 * vt + p) * 512);
+                yf[p] = *reinterpret_cast<const half8*>(blk(A.Y0t, cn) + (2 * vt + p) * 512);
             }
-            cu_h[i] = to_half4(uu[i]);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) ys[16 * i + 4 * lq + e][16 * w + lr] = yy[i][e];
         }
-        // S^T <- gamma_C S^T + K~^T U   (k-cols x rows, K = tokens)
+        __builtin_amdgcn_sched_barrier(0);
+        {
+            // token-major [64][128] block: 16 lanes write 64 contiguous bytes
+            float* yo = A.Yf + ((size_t)h * nc + c) * (CHK * QM_DN_HD) + 4 * (lane >> 4) * QM_DN_HD + 16 * vt + (lane & 15);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) yo[(16 * i + e) * QM_DN_HD] = yy[i][e];
+        }
+
+        // S^T <- gamma_C S^T + K~^T U
+        half8 ub[2];                      // U token tiles 2p, 2p+1 as one B operand
+#pragma unroll
+        for (int p = 0; p < 2; ++p) ub[p] = cat8(to_half4(uu[2 * p]), to_half4(uu[2 * p + 1]));
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             S[t] = S[t] * gC;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const half4 ak = *reinterpret_cast<const half4*>(&Kb[16 * t + lr][16 * i + 4 * lq]);
-                S[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(ak, cu_h[i], S[t], 0, 0, 0);
-            }
+            for (int p = 0; p < 2; ++p)
+                S[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[2 * t + p], ub[p], S[t], 0, 0, 0);
         }
-        __syncthreads();
-        // gated RMSNorm (gemv.rs:1205-1219): thread (token, part) owns rows
-        // 16*part .. 16*part+15 of one token; 8 lanes per token.
+        __builtin_amdgcn_sched_barrier(0);
         {
-            const int tk = tid >> 3, part = tid & 7;
-            const int t = c * CHK + tk;
-            float y[16];
-            float ss = 0.0f;
+            const uint16_t* pk = blk(A.Ktt, cn);
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                y[e] = ys[tk][16 * part + e];
-                ss = fmaf(y[e], y[e], ss);
-            }
-            ss += dpp_f32<0xB1>(ss);
-            ss += dpp_f32<0x4E>(ss);
-            ss += dpp_f32<0x141>(ss);
-            if (t < A.T) {
-                const float inv_rms = 1.0f / sqrtf(ss / (float)QM_DN_HD + 1e-6f);
-                const size_t off = ((size_t)t * QM_DN_V_HEADS + h) * QM_DN_HD + 16 * part;
-                const half8 z0 = *reinterpret_cast<const half8*>(zbase + off);   // raw bits, bf16
-                const half8 z1 = *reinterpret_cast<const half8*>(zbase + off + 8);
-                uint16_t ob[16];
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const uint16_t zb = __builtin_bit_cast(uint16_t, e < 8 ? z0[e] : z1[e - 8]);
-                    const float zz = bf16_to_f32(zb);
-                    const float gm = f16_to_f32(A.norm_w[16 * part + e]);
-                    ob[e] = f32_to_bf16(y[e] * inv_rms * gm * silu_f(zz));
-                }
-                uint4 o0, o1;
-                o0.x = ob[0] | ((uint32_t)ob[1] << 16); o0.y = ob[2] | ((uint32_t)ob[3] << 16);
-                o0.z = ob[4] | ((uint32_t)ob[5] << 16); o0.w = ob[6] | ((uint32_t)ob[7] << 16);
-                o1.x = ob[8] | ((uint32_t)ob[9] << 16); o1.y = ob[10] | ((uint32_t)ob[11] << 16);
-                o1.z = ob[12] | ((uint32_t)ob[13] << 16); o1.w = ob[14] | ((uint32_t)ob[15] << 16);
-                *reinterpret_cast<uint4*>(A.out + off) = o0;
-                *reinterpret_cast<uint4*>(A.out + off + 8) = o1;
-            }
+            for (int j = 0; j < 16; ++j) kf[j] = *reinterpret_cast<const half8*>(pk + j * 512);
+            gC = A.gC[(size_t)h * nc + cn];
         }
-        if (c + 1 < A.nc) stage();
-        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int t = 0; t < 8; ++t)
-        st4(Sg + (size_t)(16 * w + lr) * QM_DN_HD + 16 * t + 4 * lq, make_float4(S[t][0], S[t][1], S[t][2], S[t][3]));
+        st4(Sg + (size_t)(16 * vt + (lane & 15)) * QM_DN_HD + 16 * t + 4 * (lane >> 4),
+            make_float4(S[t][0], S[t][1], S[t][2], S[t][3]));
+}
+
+// ============================================================================
+// 4. norm: gated RMSNorm of Y (gemv.rs:1205-1219) and the conv buffer update
+// ============================================================================
+// One workgroup per (chunk, v-head): wave w takes tokens 16w .. 16w+15, two
+// per pass, 32 lanes per token with 4 consecutive values each, so a pass
+// reads 1 KB of Y and 512 B of z contiguously and writes 512 B of output.
+extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_norm(DnPrefillArgs A) {
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int c = blockIdx.x / QM_DN_V_HEADS, h = blockIdx.x % QM_DN_V_HEADS;
+
+    if (c == 0) {
+        // conv buffer after the prefill: the last three raw inputs (gemv.rs:1141-1146)
+        const int ch = h * 256 + tid;
+        float old[3] = {A.conv_buf[(size_t)ch * 3], A.conv_buf[(size_t)ch * 3 + 1], A.conv_buf[(size_t)ch * 3 + 2]};
+        float nb[3];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const int t = A.T - 3 + j;
+            nb[j] = t >= 0 ? bf16_to_f32(A.qkv[(size_t)t * QM_DN_QKV_DIM + ch]) : old[A.T + j];
+        }
+#pragma unroll
+        for (int j = 0; j < 3; ++j) A.conv_buf[(size_t)ch * 3 + j] = nb[j];
+    }
+
+    const int col = 4 * (lane & 31);
+    const int tk0 = 16 * w + (lane >> 5);
+    const float* ysrc = A.Yf + ((size_t)h * A.nc + c) * (CHK * QM_DN_HD) + col;
+    float4 y[8];
+    uint2 zr[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) y[q] = ld4(ysrc + (tk0 + 2 * q) * QM_DN_HD);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        const int t = min(c * CHK + tk0 + 2 * q, A.T - 1);      // rows past T are not written
+        zr[q] = *reinterpret_cast<const uint2*>(A.z + ((size_t)t * QM_DN_V_HEADS + h) * QM_DN_HD + col);
+    }
+    const uint2 gw = *reinterpret_cast<const uint2*>(A.norm_w + col);
+    const float g0 = f16_to_f32((uint16_t)(gw.x & 0xffffu)), g1 = f16_to_f32((uint16_t)(gw.x >> 16));
+    const float g2 = f16_to_f32((uint16_t)(gw.y & 0xffffu)), g3 = f16_to_f32((uint16_t)(gw.y >> 16));
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        float ss = y[q].x * y[q].x;
+        ss = fmaf(y[q].y, y[q].y, ss);
+        ss = fmaf(y[q].z, y[q].z, ss);
+        ss = fmaf(y[q].w, y[q].w, ss);
+        ss = row_sum16(ss);
+        ss += __shfl_xor(ss, 16);
+        const int t = c * CHK + tk0 + 2 * q;
+        if (t < A.T) {
+            const float inv_rms = 1.0f / sqrtf(ss / (float)QM_DN_HD + 1e-6f);
+            const float z0 = bf16_to_f32((uint16_t)(zr[q].x & 0xffffu)), z1 = bf16_to_f32((uint16_t)(zr[q].x >> 16));
+            const float z2 = bf16_to_f32((uint16_t)(zr[q].y & 0xffffu)), z3 = bf16_to_f32((uint16_t)(zr[q].y >> 16));
+            const uint32_t o01 = f32_to_bf16(y[q].x * inv_rms * g0 * silu_f(z0)) |
+                                 ((uint32_t)f32_to_bf16(y[q].y * inv_rms * g1 * silu_f(z1)) << 16);
+            const uint32_t o23 = f32_to_bf16(y[q].z * inv_rms * g2 * silu_f(z2)) |
+                                 ((uint32_t)f32_to_bf16(y[q].w * inv_rms * g3 * silu_f(z3)) << 16);
+            *reinterpret_cast<uint2*>(A.out + ((size_t)t * QM_DN_V_HEADS + h) * QM_DN_HD + col) = make_uint2(o01, o23);
+        }
+    }
 }

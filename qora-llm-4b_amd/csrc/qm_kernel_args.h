@@ -67,12 +67,14 @@ struct GqaDecodeArgs {
 //   qh, kh  f16 [T_pad][16][128]   L2-normed q (times 1/sqrt(128)) and k
 //   vv      f16 [T_pad][32][128]   activated v
 //   G, beta f32 [32][T_pad]        within-chunk cumulative log decay, beta
-//   Wn, Qt  f16 [32][nc][64][128]  -W = -T diag(beta*gamma) K and
-//                                   Q~ = diag(gamma) Q - P W, token-major
-//   Ut, Y0t f16 [32][nc][128][64]  U~ = T diag(beta) V and Y0 = P U~,
-//                                   transposed (v-row-major)
-//   Ktt     f16 [32][nc][128][64]  K~^T = (diag(gamma_C / gamma) K)^T
+//   Wn, Qt  f16 [32][nc][8192]     -W = -T diag(beta*gamma) K and
+//                                   Q~ = diag(gamma) Q - P W
+//   Ut, Y0t f16 [32][nc][8192]     U~ = T diag(beta) V and Y0 = P U~
+//   Ktt     f16 [32][nc][8192]     K~^T = (diag(gamma_C / gamma) K)^T
 //   gC      f32 [32][nc]           gamma_C = prod of the chunk's decays
+//   Yf      f32 [32][nc][64][128]  Y before the gated norm, token-major
+// The five f16 8192-element blocks per (head, chunk) are stored in the MFMA
+// fragment order the scan kernel loads them in (described there).
 #define QM_DN_CHUNK 64
 struct DnPrefillArgs {
     const uint16_t* qkv;     // bf16 [T][8192]
@@ -97,6 +99,7 @@ struct DnPrefillArgs {
     uint16_t* Y0t;
     uint16_t* Ktt;
     float* gC;
+    float* Yf;
     int32_t T;
     int32_t nc;
 };
