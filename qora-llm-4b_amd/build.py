@@ -26,6 +26,9 @@ HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "--genco", "-O3", "-std=c++17",
     # Keep the compiler from emitting packed-fp32 VALU ops.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in arch VGPRs: no AGPR<->VGPR copies around VALU work on
+    # the accumulators.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall", "-Wno-unused-parameter",
 ]
 

@@ -24,8 +24,11 @@
 //                        - PW and Y0 = PU~, all products on f16 MFMA;
 //   qm_dn_prefill_scan   the sequential part: one wave per (v-head, 16 state
 //                        rows) with its rows of the fp32 state in registers,
-//                        three f16 MFMA GEMMs per chunk, Y out in fp32;
-//   qm_dn_prefill_norm   gated RMSNorm of Y and the conv buffer update.
+//                        two f16 MFMA GEMMs per chunk; stores each chunk's
+//                        entry state in f16;
+//   qm_dn_prefill_out    Y = Y0 + Q~ S_c^T on MFMA, fully parallel over
+//                        (chunk, v-head), fused with the gated RMSNorm and
+//                        the conv buffer update.
 // The scan uses v_mfma_f32_16x16x16_f16 throughout because its fragment
 // layouts chain without lane shuffles: the state's C fragment (4 consecutive
 // k-cols per lane) is the B operand of U and Y, and U's C fragment (4
@@ -53,76 +56,80 @@ QM_DEV half4 to_half4(floatx4 v) {
 // 1. prep: causal conv1d (gemv.rs:1132-1147), SiLU (:1149), per-head L2 norm
 //    and q scale (:1151-1156), gates (:1171-1172).
 // ============================================================================
+// Thread (cg, tg) = (tid & 15, tid >> 4) owns channels 8cg .. 8cg+7 of the
+// head for tokens 4tg .. 4tg+3; the 16 lanes of a row share the tokens, so the
+// per-token L2 norm is a row reduction and every store writes whole 256-byte
+// rows.
 extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_prep(DnPrefillArgs A) {
-    __shared__ float act[CHK][129];
     const int tid = threadIdx.x;
     const int c = blockIdx.x / 64, gi = blockIdx.x % 64;     // 64 heads of 128 channels
     const int t0 = c * CHK;
     const int tpad = A.nc * CHK;
     {
-        // thread: 8 channels (one 16-byte load per row) x 4 tokens; the 7 raw
-        // rows it needs are all loaded before any arithmetic
         const int cg = tid & 15, tg = tid >> 4;
         const int ch0 = gi * 128 + 8 * cg;
+        // the 7 raw rows the thread needs, all loaded (at clamped, always
+        // valid rows) before any arithmetic; rows before the sequence come
+        // from the conv buffer, rows past it are zero
+        uint4 u[7];
+#pragma unroll
+        for (int r = 0; r < 7; ++r) {
+            const int t = min(max(t0 + 4 * tg - 3 + r, 0), A.T - 1);
+            u[r] = *reinterpret_cast<const uint4*>(A.qkv + (size_t)t * QM_DN_QKV_DIM + ch0);
+        }
+        float cb[3][8] = {};
+        if (c == 0) {                                            // x_{-3..-1}
+            asm volatile("" ::: "memory");   // keep these loads inside the branch
+#pragma unroll
+            for (int r = 0; r < 3; ++r) {
+                const int t = min(4 * tg - 3 + r, -1);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) cb[r][e] = A.conv_buf[(size_t)(ch0 + e) * 3 + 3 + t];
+            }
+        }
         float x[7][8];
 #pragma unroll
         for (int r = 0; r < 7; ++r) {
             const int t = t0 + 4 * tg - 3 + r;
-            if (t >= 0 && t < A.T) {
-                const uint4 u = *reinterpret_cast<const uint4*>(A.qkv + (size_t)t * QM_DN_QKV_DIM + ch0);
-                const uint32_t wv[4] = {u.x, u.y, u.z, u.w};
+            const uint32_t wv[4] = {u[r].x, u[r].y, u[r].z, u[r].w};
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    x[r][2 * e] = bf16_to_f32((uint16_t)(wv[e] & 0xffffu));
-                    x[r][2 * e + 1] = bf16_to_f32((uint16_t)(wv[e] >> 16));
-                }
-            } else if (t < 0) {                                  // x_{-3..-1} from the conv buffer
+            for (int e = 0; e < 4; ++e) {
+                x[r][2 * e] = bf16_to_f32((uint16_t)(wv[e] & 0xffffu));
+                x[r][2 * e + 1] = bf16_to_f32((uint16_t)(wv[e] >> 16));
+            }
 #pragma unroll
-                for (int e = 0; e < 8; ++e) x[r][e] = A.conv_buf[(size_t)(ch0 + e) * 3 + 3 + t];
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) x[r][e] = 0.0f;
+            for (int e = 0; e < 8; ++e) {
+                if (r < 3 && t < 0) x[r][e] = cb[r][e];
+                if (t >= A.T) x[r][e] = 0.0f;
             }
         }
         float4 w[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) w[e] = ld4(A.conv_w + (size_t)(ch0 + e) * 4);
+        float scale = 1.0f;
+        uint16_t* base;
+        int rows;
+        if (gi < 32) {
+            scale = gi < 16 ? 1.0f / sqrtf((float)QM_DN_HD) : 1.0f;
+            base = (gi < 16 ? A.qh : A.kh) + (size_t)(gi & 15) * QM_DN_HD + 8 * cg;
+            rows = QM_DN_QK_HEADS;
+        } else {
+            base = A.vv + (size_t)(gi - 32) * QM_DN_HD + 8 * cg;
+            rows = QM_DN_V_HEADS;
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int tok = 4 * tg + j;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                // gemv.rs:1134-1139 order: buffer taps oldest first, then the new token
-                float s = 0.0f;
-                s = __fadd_rn(s, __fmul_rn(x[j][e], w[e].x));
-                s = __fadd_rn(s, __fmul_rn(x[j + 1][e], w[e].y));
-                s = __fadd_rn(s, __fmul_rn(x[j + 2][e], w[e].z));
-                s = __fadd_rn(s, __fmul_rn(x[j + 3][e], w[e].w));
-                act[tok][8 * cg + e] = (t0 + tok < A.T) ? silu_f(s) : 0.0f;
-            }
-        }
-    }
-    __syncthreads();
-
-    // 16 lanes per token, 8 channels each: a store instruction writes four
-    // whole 256-byte rows
-    {
-        const int w = tid >> 6, lane = tid & 63, l16 = lane & 15;
-        float scale = 1.0f;
-        uint16_t* base;
-        if (gi < 32) {
-            scale = gi < 16 ? 1.0f / sqrtf((float)QM_DN_HD) : 1.0f;
-            base = (gi < 16 ? A.qh : A.kh) + (size_t)(gi & 15) * QM_DN_HD;
-        } else {
-            base = A.vv + (size_t)(gi - 32) * QM_DN_HD;
-        }
-        const int rows = gi < 32 ? QM_DN_QK_HEADS : QM_DN_V_HEADS;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int tok = 16 * w + 4 * q + (lane >> 4);
             float v[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] = act[tok][8 * l16 + e];
+            for (int e = 0; e < 8; ++e) {
+                // gemv.rs:1134-1139: taps oldest first, then the new token
+                float s = x[j][e] * w[e].x;
+                s = fmaf(x[j + 1][e], w[e].y, s);
+                s = fmaf(x[j + 2][e], w[e].z, s);
+                s = fmaf(x[j + 3][e], w[e].w, s);
+                v[e] = (t0 + tok < A.T) ? silu_fast(s) : 0.0f;
+            }
             if (gi < 32) {
                 // x /= ||x|| when ||x|| > 1e-12, q *= 1/sqrt(128)
                 float ss = 0.0f;
@@ -137,7 +144,7 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_prep(DnPrefillAr
             half8 hv;
 #pragma unroll
             for (int e = 0; e < 8; ++e) hv[e] = (_Float16)v[e];
-            *reinterpret_cast<half8*>(base + (size_t)(t0 + tok) * rows * QM_DN_HD + 8 * l16) = hv;
+            *reinterpret_cast<half8*>(base + (size_t)(t0 + tok) * rows * QM_DN_HD) = hv;
         }
     }
 
@@ -408,10 +415,13 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
 // 3. scan: sequential over chunks, one wave per (v-head, 16 state rows)
 // ============================================================================
 // Under the chunked delta rule every state row evolves on its own:
-//   U_r = U~_r - W S_r^T,  Y_r = Y0_r + Q~ S_r^T,  S_r <- gamma_C S_r + U_r^T K~
-// so a v-head's 128 rows split over 8 independent waves (grid 256).  A wave
-// keeps S_r^T (k-cols x 16 rows, fp32) as eight C fragments; for k tile t,
-// lane (r, q) = (lane & 15, lane >> 4) holds S[16 vt + r][16 t + 4q .. +3].
+//   U_r = U~_r - W S_r^T,  S_r <- gamma_C S_r + U_r^T K~
+// so a v-head's 128 rows split over 8 independent waves (grid 256).  The
+// output Y_r = Y0_r + Q~ S_r^T only reads the chunk-entry state, so the scan
+// stores that state (in f16, the precision the product consumes it in) and
+// the out kernel forms Y fully in parallel.
+// A wave keeps S_r^T (k-cols x 16 rows, fp32) as eight C fragments; for k
+// tile t, lane (r, q) = (lane & 15, lane >> 4) holds S[16 vt + r][16 t + 4q .. +3].
 // All chunk operands arrive in fragment order as 16-byte pieces, piece
 // (j, lane) at byte offset 16 (64 j + lane) of the (head, chunk) block:
 //   -W, Q~   j = 4 i + p: tokens 16 i + (lane & 15), k-cols 32 p + 4 (lane >> 4)
@@ -419,14 +429,17 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
 //   K~^T     j = 2 kt + p: k-col 16 kt + (lane & 15), tokens 32 p + 4 (lane >> 4)
 //            + {0..3} and + 16 + {0..3};
 //   U~, Y0   j = 2 vt + p: row 16 vt + (lane & 15), tokens 32 p + 4 (lane >> 4)
-//            + {0..3} and + 16 + {0..3}.
+//            + {0..3} and + 16 + {0..3};
+//   S_c      j = 4 vt + p: row 16 vt + (lane & 15), k-cols 32 p + 4 (lane >> 4)
+//            + {0..3} and + 16 + {0..3} (written here).
 // A 16-byte piece is the A operand of one v_mfma_f32_16x16x32_f16: a product
 // only needs A and B to agree on which k each (lane, element) holds, and the
 // two C fragments of S^T k tiles 2p, 2p+1 (or of U token tiles 2p, 2p+1)
 // concatenated hold exactly the k (token) set of piece p.
-// The next chunk's operands are loaded into registers right after the
-// current chunk's last use of each, so the loads overlap two of the three
-// GEMM phases.  Y leaves in fp32, token-major, for the norm.
+// Two chunks' operands are held in registers (the wave is alone on its CU,
+// so the whole register file is available): chunk c + 2's -W and U~ are
+// loaded right after chunk c's U product and its K~^T right after chunk c's
+// state update, into the registers just consumed.
 extern "C" __global__ __launch_bounds__(64) void qm_dn_prefill_scan(DnPrefillArgs A) {
     const int lane = threadIdx.x;
     // blocks are dealt to the 8 XCDs round-robin: keep a head's 8 row slices
@@ -443,41 +456,31 @@ extern "C" __global__ __launch_bounds__(64) void qm_dn_prefill_scan(DnPrefillArg
         S[t] = floatx4{v.x, v.y, v.z, v.w};
     }
 
-    half8 wf[16], qf[16], kf[16], uf[2], yf[2];
     auto blk = [&](const uint16_t* base, int c) {
         return base + ((size_t)h * nc + c) * (CHK * QM_DN_HD) + (size_t)lane * 8;
     };
-    // first chunk's operands, issued in the order the loop reissues them
-    // (W; Q~, U~, Y0; K~^T, gamma_C) so that the in-order load counter lets
-    // each phase wait for its own operands only
-    {
-        const uint16_t* pw = blk(A.Wn, 0);
+    auto load16 = [&](half8 (&dst)[16], const uint16_t* base, int c) {
+        const uint16_t* src = blk(base, c);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) wf[j] = *reinterpret_cast<const half8*>(pw + j * 512);
-        __builtin_amdgcn_sched_barrier(0);
-        const uint16_t* pq = blk(A.Qt, 0);
+        for (int j = 0; j < 16; ++j) dst[j] = *reinterpret_cast<const half8*>(src + j * 512);
+    };
+    auto load_u = [&](half8 (&dst)[2], int c) {
 #pragma unroll
-        for (int j = 0; j < 16; ++j) qf[j] = *reinterpret_cast<const half8*>(pq + j * 512);
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            uf[p] = *reinterpret_cast<const half8*>(blk(A.Ut, 0) + (2 * vt + p) * 512);
-            yf[p] = *reinterpret_cast<const half8*>(blk(A.Y0t, 0) + (2 * vt + p) * 512);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        const uint16_t* pk = blk(A.Ktt, 0);
-#pragma unroll
-        for (int j = 0; j < 16; ++j) kf[j] = *reinterpret_cast<const half8*>(pk + j * 512);
-    }
-    float gC = A.gC[(size_t)h * nc];
-    __builtin_amdgcn_sched_barrier(0);
-
-    for (int c = 0; c < nc; ++c) {
-        const int cn = c + 1 < nc ? c + 1 : c;
+        for (int p = 0; p < 2; ++p) dst[p] = *reinterpret_cast<const half8*>(blk(A.Ut, c) + (2 * vt + p) * 512);
+    };
+    // One chunk: store f16(S_c), U = U~ + (-W) S^T, S^T <- gamma_C S^T + K~^T U.
+    // The operand registers of chunk c are refilled with chunk c + 2 right
+    // after their last use, so every load has about 1.5 chunk periods to land.
+    auto step = [&](int c, half8 (&wf)[16], half8 (&kf)[16], half8 (&uf)[2], float& gC) {
+        const int cn = c + 2 < nc ? c + 2 : nc - 1;
         half8 sb[4];                      // S^T k-tiles 2p, 2p+1 as one B operand
 #pragma unroll
         for (int p = 0; p < 4; ++p) sb[p] = cat8(to_half4(S[2 * p]), to_half4(S[2 * p + 1]));
-
-        // U = U~ + (-W) S^T
+        {
+            uint16_t* so = A.Sc + ((size_t)h * nc + c) * (QM_DN_HD * QM_DN_HD) + (size_t)(4 * vt * 64 + lane) * 8;
+#pragma unroll
+            for (int p = 0; p < 4; ++p) *reinterpret_cast<half8*>(so + p * 512) = sb[p];
+        }
         floatx4 uu[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -489,46 +492,9 @@ extern "C" __global__ __launch_bounds__(64) void qm_dn_prefill_scan(DnPrefillArg
                 uu[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[4 * i + p], sb[p], uu[i], 0, 0, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
-        {
-            const uint16_t* pw = blk(A.Wn, cn);
-#pragma unroll
-            for (int j = 0; j < 16; ++j) wf[j] = *reinterpret_cast<const half8*>(pw + j * 512);
-        }
+        load16(wf, A.Wn, cn);
+        load_u(uf, cn);
         __builtin_amdgcn_sched_barrier(0);
-
-        // Y = Y0 + Q~ S^T
-        floatx4 yy[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const half8 src = yf[i >> 1];
-            const int o = 4 * (i & 1);
-            yy[i] = floatx4{(float)src[o], (float)src[o + 1], (float)src[o + 2], (float)src[o + 3]};
-#pragma unroll
-            for (int p = 0; p < 4; ++p)
-                yy[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qf[4 * i + p], sb[p], yy[i], 0, 0, 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        {
-            const uint16_t* pq = blk(A.Qt, cn);
-#pragma unroll
-            for (int j = 0; j < 16; ++j) qf[j] = *reinterpret_cast<const half8*>(pq + j * 512);
-#pragma unroll
-            for (int p = 0; p < 2; ++p) {
-                uf[p] = *reinterpret_cast<const half8*>(blk(A.Ut, cn) + (2 * vt + p) * 512);
-                yf[p] = *reinterpret_cast<const half8*>(blk(A.Y0t, cn) + (2 * vt + p) * 512);
-            }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        {
-            // token-major [64][128] block: 16 lanes write 64 contiguous bytes
-            float* yo = A.Yf + ((size_t)h * nc + c) * (CHK * QM_DN_HD) + 4 * (lane >> 4) * QM_DN_HD + 16 * vt + (lane & 15);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) yo[(16 * i + e) * QM_DN_HD] = yy[i][e];
-        }
-
-        // S^T <- gamma_C S^T + K~^T U
         half8 ub[2];                      // U token tiles 2p, 2p+1 as one B operand
 #pragma unroll
         for (int p = 0; p < 2; ++p) ub[p] = cat8(to_half4(uu[2 * p]), to_half4(uu[2 * p + 1]));
@@ -540,14 +506,36 @@ extern "C" __global__ __launch_bounds__(64) void qm_dn_prefill_scan(DnPrefillArg
                 S[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[2 * t + p], ub[p], S[t], 0, 0, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
-        {
-            const uint16_t* pk = blk(A.Ktt, cn);
-#pragma unroll
-            for (int j = 0; j < 16; ++j) kf[j] = *reinterpret_cast<const half8*>(pk + j * 512);
-            gC = A.gC[(size_t)h * nc + cn];
-        }
+        load16(kf, A.Ktt, cn);
+        gC = A.gC[(size_t)h * nc + cn];
         __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // chunks 0 and 1 in flight before the loop, in the order the loop
+    // reissues them (-W, U~; K~^T, gamma_C) so the in-order load counter
+    // lets each phase wait for its own operands only
+    half8 wa[16], ka[16], ua[2], wb[16], kb[16], ubf[2];
+    float ga, gb;
+    const int c1 = nc > 1 ? 1 : 0;
+    load16(wa, A.Wn, 0);
+    load_u(ua, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    load16(ka, A.Ktt, 0);
+    ga = A.gC[(size_t)h * nc];
+    __builtin_amdgcn_sched_barrier(0);
+    load16(wb, A.Wn, c1);
+    load_u(ubf, c1);
+    __builtin_amdgcn_sched_barrier(0);
+    load16(kb, A.Ktt, c1);
+    gb = A.gC[(size_t)h * nc + c1];
+    __builtin_amdgcn_sched_barrier(0);
+
+    int c = 0;
+    for (; c + 1 < nc; c += 2) {
+        step(c, wa, ka, ua, ga);
+        step(c + 1, wb, kb, ubf, gb);
     }
+    if (c < nc) step(c, wa, ka, ua, ga);
 #pragma unroll
     for (int t = 0; t < 8; ++t)
         st4(Sg + (size_t)(16 * vt + (lane & 15)) * QM_DN_HD + 16 * t + 4 * (lane >> 4),
@@ -555,14 +543,19 @@ extern "C" __global__ __launch_bounds__(64) void qm_dn_prefill_scan(DnPrefillArg
 }
 
 // ============================================================================
-// 4. norm: gated RMSNorm of Y (gemv.rs:1205-1219) and the conv buffer update
+// 4. out: Y = Y0 + Q~ S_c^T and the gated RMSNorm (gemv.rs:1205-1219), plus
+//    the conv buffer update
 // ============================================================================
-// One workgroup per (chunk, v-head): wave w takes tokens 16w .. 16w+15, two
-// per pass, 32 lanes per token with 4 consecutive values each, so a pass
-// reads 1 KB of Y and 512 B of z contiguously and writes 512 B of output.
-extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_norm(DnPrefillArgs A) {
+// One workgroup per (chunk, v-head).  Wave w forms the 64 x 32 block of Y for
+// rows 32w .. 32w+31 on 16x16x32 f16 MFMA from the fragment-order pieces,
+// stages it in LDS, and the norm then runs 32 lanes per token with 4
+// consecutive values each, so z and the output move 512 contiguous bytes per
+// token pair.
+extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_out(DnPrefillArgs A) {
+    __shared__ float ys[CHK][132];
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int c = blockIdx.x / QM_DN_V_HEADS, h = blockIdx.x % QM_DN_V_HEADS;
+    const size_t hc = (size_t)h * A.nc + c;
 
     if (c == 0) {
         // conv buffer after the prefill: the last three raw inputs (gemv.rs:1141-1146)
@@ -578,18 +571,49 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_norm(DnPrefillAr
         for (int j = 0; j < 3; ++j) A.conv_buf[(size_t)ch * 3 + j] = nb[j];
     }
 
+    // z for this thread's tokens first: it does not depend on anything
     const int col = 4 * (lane & 31);
     const int tk0 = 16 * w + (lane >> 5);
-    const float* ysrc = A.Yf + ((size_t)h * A.nc + c) * (CHK * QM_DN_HD) + col;
-    float4 y[8];
     uint2 zr[8];
-#pragma unroll
-    for (int q = 0; q < 8; ++q) y[q] = ld4(ysrc + (tk0 + 2 * q) * QM_DN_HD);
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
         const int t = min(c * CHK + tk0 + 2 * q, A.T - 1);      // rows past T are not written
         zr[q] = *reinterpret_cast<const uint2*>(A.z + ((size_t)t * QM_DN_V_HEADS + h) * QM_DN_HD + col);
     }
+    {
+        const uint16_t* qsrc = A.Qt + hc * (CHK * QM_DN_HD) + (size_t)lane * 8;
+        const uint16_t* ssrc = A.Sc + hc * (QM_DN_HD * QM_DN_HD) + (size_t)lane * 8;
+        const uint16_t* ysrc = A.Y0t + hc * (CHK * QM_DN_HD) + (size_t)lane * 8;
+        half8 qf[16], sf[2][4], yf[2][2];
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+#pragma unroll
+            for (int p = 0; p < 4; ++p) sf[cc][p] = *reinterpret_cast<const half8*>(ssrc + (4 * (2 * w + cc) + p) * 512);
+#pragma unroll
+            for (int p = 0; p < 2; ++p) yf[cc][p] = *reinterpret_cast<const half8*>(ysrc + (2 * (2 * w + cc) + p) * 512);
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) qf[j] = *reinterpret_cast<const half8*>(qsrc + j * 512);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc) {
+                const half8 src = yf[cc][i >> 1];
+                const int o = 4 * (i & 1);
+                floatx4 y = {(float)src[o], (float)src[o + 1], (float)src[o + 2], (float)src[o + 3]};
+#pragma unroll
+                for (int p = 0; p < 4; ++p)
+                    y = __builtin_amdgcn_mfma_f32_16x16x32_f16(qf[4 * i + p], sf[cc][p], y, 0, 0, 0);
+                const int col = 16 * (2 * w + cc) + (lane & 15);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) ys[16 * i + 4 * (lane >> 4) + e][col] = y[e];
+            }
+    }
+    __syncthreads();
+
+    float4 y[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) y[q] = *reinterpret_cast<const float4*>(&ys[tk0 + 2 * q][col]);
     const uint2 gw = *reinterpret_cast<const uint2*>(A.norm_w + col);
     const float g0 = f16_to_f32((uint16_t)(gw.x & 0xffffu)), g1 = f16_to_f32((uint16_t)(gw.x >> 16));
     const float g2 = f16_to_f32((uint16_t)(gw.y & 0xffffu)), g3 = f16_to_f32((uint16_t)(gw.y >> 16));
@@ -606,10 +630,10 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_norm(DnPrefillAr
             const float inv_rms = 1.0f / sqrtf(ss / (float)QM_DN_HD + 1e-6f);
             const float z0 = bf16_to_f32((uint16_t)(zr[q].x & 0xffffu)), z1 = bf16_to_f32((uint16_t)(zr[q].x >> 16));
             const float z2 = bf16_to_f32((uint16_t)(zr[q].y & 0xffffu)), z3 = bf16_to_f32((uint16_t)(zr[q].y >> 16));
-            const uint32_t o01 = f32_to_bf16(y[q].x * inv_rms * g0 * silu_f(z0)) |
-                                 ((uint32_t)f32_to_bf16(y[q].y * inv_rms * g1 * silu_f(z1)) << 16);
-            const uint32_t o23 = f32_to_bf16(y[q].z * inv_rms * g2 * silu_f(z2)) |
-                                 ((uint32_t)f32_to_bf16(y[q].w * inv_rms * g3 * silu_f(z3)) << 16);
+            const uint32_t o01 = f32_to_bf16(y[q].x * inv_rms * g0 * silu_fast(z0)) |
+                                 ((uint32_t)f32_to_bf16(y[q].y * inv_rms * g1 * silu_fast(z1)) << 16);
+            const uint32_t o23 = f32_to_bf16(y[q].z * inv_rms * g2 * silu_fast(z2)) |
+                                 ((uint32_t)f32_to_bf16(y[q].w * inv_rms * g3 * silu_fast(z3)) << 16);
             *reinterpret_cast<uint2*>(A.out + ((size_t)t * QM_DN_V_HEADS + h) * QM_DN_HD + col) = make_uint2(o01, o23);
         }
     }

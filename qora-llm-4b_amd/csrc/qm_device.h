@@ -57,6 +57,11 @@ QM_DEV uint16_t f32_to_bf16(float f) {   // round to nearest even
 
 // ---- scalar math (gemv.rs:631-659 semantics) -----------------------------
 QM_DEV float silu_f(float x) { return x / (1.0f + expf(-x)); }
+// x * sigmoid(x) from v_exp_f32 (exp(-x) = 2^(-x log2 e)) and v_rcp_f32, a few
+// ulp from silu_f; for the prefill paths, whose bar is bf16-level.
+QM_DEV float silu_fast(float x) {
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
+}
 QM_DEV float softplus_f(float x) { return x > 20.0f ? x : logf(1.0f + expf(x)); }
 QM_DEV float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
 

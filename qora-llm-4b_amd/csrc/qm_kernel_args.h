@@ -72,9 +72,9 @@ struct GqaDecodeArgs {
 //   Ut, Y0t f16 [32][nc][8192]     U~ = T diag(beta) V and Y0 = P U~
 //   Ktt     f16 [32][nc][8192]     K~^T = (diag(gamma_C / gamma) K)^T
 //   gC      f32 [32][nc]           gamma_C = prod of the chunk's decays
-//   Yf      f32 [32][nc][64][128]  Y before the gated norm, token-major
-// The five f16 8192-element blocks per (head, chunk) are stored in the MFMA
-// fragment order the scan kernel loads them in (described there).
+//   Sc      f16 [32][nc][16384]    state entering each chunk
+// The per-(head, chunk) blocks are stored in the MFMA fragment order the
+// scan and out kernels load them in (described at the scan kernel).
 #define QM_DN_CHUNK 64
 struct DnPrefillArgs {
     const uint16_t* qkv;     // bf16 [T][8192]
@@ -99,7 +99,7 @@ struct DnPrefillArgs {
     uint16_t* Y0t;
     uint16_t* Ktt;
     float* gC;
-    float* Yf;
+    uint16_t* Sc;
     int32_t T;
     int32_t nc;
 };

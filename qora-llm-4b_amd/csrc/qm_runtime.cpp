@@ -41,7 +41,7 @@ struct qm_context {
     hipFunction_t f_dnp_prep = nullptr;
     hipFunction_t f_dnp_chunk = nullptr;
     hipFunction_t f_dnp_scan = nullptr;
-    hipFunction_t f_dnp_norm = nullptr;
+    hipFunction_t f_dnp_out = nullptr;
     hipFunction_t f_gqp_kv = nullptr;
     hipFunction_t f_gqp_attn = nullptr;
     void* ws = nullptr;            // general workspace
@@ -144,7 +144,7 @@ int32_t load_function(qm_context* c, hipModule_t m, const char* name, hipFunctio
 
 namespace {
 struct DnPrefillLayout {
-    size_t qh, kh, vv, G, beta, Wn, Qt, Ut, Y0t, Ktt, gC, Yf, total;
+    size_t qh, kh, vv, G, beta, Wn, Qt, Ut, Y0t, Ktt, gC, Sc, total;
 };
 
 DnPrefillLayout dn_prefill_layout(int64_t T) {
@@ -164,7 +164,7 @@ DnPrefillLayout dn_prefill_layout(int64_t T) {
     L.Y0t = o; o += al(blk);
     L.Ktt = o; o += al(blk);
     L.gC = o; o += al(static_cast<size_t>(QM_DN_V_HEADS) * nc * 4);
-    L.Yf = o; o += al(2 * blk);
+    L.Sc = o; o += al(2 * blk);
     L.total = o;
     return L;
 }
@@ -259,7 +259,7 @@ int32_t qm_create(qm_context** out, const qm_config* cfg, const char* code_objec
     if (st == QM_OK) st = load_function(c, mods[3], "qm_dn_prefill_prep", &c->f_dnp_prep);
     if (st == QM_OK) st = load_function(c, mods[3], "qm_dn_prefill_chunk", &c->f_dnp_chunk);
     if (st == QM_OK) st = load_function(c, mods[3], "qm_dn_prefill_scan", &c->f_dnp_scan);
-    if (st == QM_OK) st = load_function(c, mods[3], "qm_dn_prefill_norm", &c->f_dnp_norm);
+    if (st == QM_OK) st = load_function(c, mods[3], "qm_dn_prefill_out", &c->f_dnp_out);
     if (st == QM_OK) st = load_function(c, mods[4], "qm_gqa_prefill_kv", &c->f_gqp_kv);
     if (st == QM_OK) st = load_function(c, mods[4], "qm_gqa_prefill_attn", &c->f_gqp_attn);
     if (st == QM_OK && hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess)
@@ -597,14 +597,14 @@ int32_t qm_deltanet_prefill(qm_context* c, qm_stream stream, int32_t seq_len, co
                      reinterpret_cast<float*>(ws + L.beta), reinterpret_cast<uint16_t*>(ws + L.Wn),
                      reinterpret_cast<uint16_t*>(ws + L.Qt), reinterpret_cast<uint16_t*>(ws + L.Ut),
                      reinterpret_cast<uint16_t*>(ws + L.Y0t), reinterpret_cast<uint16_t*>(ws + L.Ktt),
-                     reinterpret_cast<float*>(ws + L.gC), reinterpret_cast<float*>(ws + L.Yf), seq_len, nc};
+                     reinterpret_cast<float*>(ws + L.gC), reinterpret_cast<uint16_t*>(ws + L.Sc), seq_len, nc};
     st = launch(c, c->f_dnp_prep, static_cast<uint32_t>(nc) * 64, 256, pa, s, "qm_dn_prefill_prep");
     if (st != QM_OK) return st;
     st = launch(c, c->f_dnp_chunk, static_cast<uint32_t>(nc) * QM_DN_V_HEADS, 256, pa, s, "qm_dn_prefill_chunk");
     if (st != QM_OK) return st;
     st = launch(c, c->f_dnp_scan, QM_DN_V_HEADS * 8, 64, pa, s, "qm_dn_prefill_scan");
     if (st != QM_OK) return st;
-    return launch(c, c->f_dnp_norm, static_cast<uint32_t>(nc) * QM_DN_V_HEADS, 256, pa, s, "qm_dn_prefill_norm");
+    return launch(c, c->f_dnp_out, static_cast<uint32_t>(nc) * QM_DN_V_HEADS, 256, pa, s, "qm_dn_prefill_out");
 }
 
 // ---- GQA causal prefill ------------------------------------------------------------
