@@ -8,16 +8,21 @@
 // qm_gqa_prefill_kv    K norm + RoPE -> f16 K cache; V -> f16 V cache and a
 //                      transposed f16 copy V^T (keys contiguous per dim).
 // qm_gqa_prefill_attn  flash attention on MFMA.  A workgroup owns 32 query
-//                      tokens of all four query heads of one kv group (wave
-//                      w = head 4g+w), so every K / V tile staged in LDS
-//                      feeds four heads.  Scores are computed transposed,
+//                      tokens of all four query heads of one kv group (8
+//                      waves: head 4g + (w & 3), 16 rows each, two waves per
+//                      SIMD), so every K / V tile staged in LDS feeds four
+//                      heads.  Scores are computed transposed,
 //                      S^T = K Q^T (keys x rows), with v_mfma_f32_16x16x32:
 //                      a lane of an S^T fragment then holds four consecutive
 //                      keys of one row, which is exactly what the PV product
 //                      (rows x dims, contracting keys) needs as its A operand
 //                      once two 16-key fragments are paired; the V^T operand
-//                      uses the same key pairing.  No lane shuffles between
-//                      the two products.  Online softmax in base 2, fp32.
+//                      uses the same key set per lane (the S^T rows are
+//                      permuted so that set is 8 consecutive keys).  No lane
+//                      shuffles between the two products.  Online softmax in
+//                      base 2, fp32, with a lazily moved reference max.  K / V
+//                      tiles are double-buffered in LDS and copied there by
+//                      LDS DMA while the previous tile computes.
 #include "qm_device.h"
 #include "qm_kernel_args.h"
 #include "qm_gqa_common.h"
@@ -27,9 +32,11 @@ typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 #define KT 64          // keys per tile
+// Rows keep a reference max m and only move it when the tile max exceeds it
+// by more than this (log2 units), so P = 2^(s - m) <= 2^8 stays exact enough
+// in f16 and the O accumulators are rescaled only when a row's max jumps.
+#define RESCALE_SLACK 8.0f
 #define TQ 32          // query tokens per workgroup
-#define KS_STRIDE 264  // f16 per K row in LDS (256 + 8 pad)
-#define VT_STRIDE 72   // f16 per V^T row in LDS (64 + 8 pad)
 
 QM_DEV float4 bf16x4_to_f32(uint2 u) {
     return make_float4(bf16_to_f32((uint16_t)(u.x & 0xffffu)), bf16_to_f32((uint16_t)(u.x >> 16)),
@@ -94,188 +101,204 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_prefill_kv(GqaPrefillAr
 // ---------------------------------------------------------------------------
 // Flash attention.  Lane (lr, lq) = (lane & 15, lane >> 4).
 // ---------------------------------------------------------------------------
-struct PrefillSmem {
-    union {
-        _Float16 qstage[4][TQ][KS_STRIDE];                 // q prep, per wave
-        struct {
-            _Float16 Ks[KT][KS_STRIDE];
-            _Float16 Vts[QM_GQA_HD][VT_STRIDE];
-        } kv;
-    } u;
-    float rowf[4][TQ];
-};
+// LDS (bytes): two tile buffers of 64 KB.  A buffer holds a 64-key tile in
+// MFMA fragment order: 32 K blocks (kk, s) then 32 V^T blocks (dt, ks) of
+// 1 KB, block entry l being the 16 bytes lane l reads for that product, so
+// every fragment read is lane * 16 + an immediate (no bank conflicts, no
+// per-read address registers).  The gather into that order is done by the
+// per-lane source addresses of the LDS DMA.  The q staging area [8 waves]
+// [16 rows][512 B] shares buffer 1 (consumed before tile 1 arrives), rows
+// with their 16-byte chunks XOR swizzled (chunk c at c ^ swz_k(row)); then
+// the per-wave row factors.
+#define SM_BUF 65536
+#define SM_V 32768
+#define SM_ROWF (2 * SM_BUF)
 
-extern "C" __global__ __launch_bounds__(256) void qm_gqa_prefill_attn(GqaPrefillArgs A) {
-    __shared__ PrefillSmem sm;
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+// rows {b..b+3, b+8..b+11, b+16..b+19, b+24..b+27} (a read phase) -> distinct
+// low 4 bits: bits 0,1 stay, bits 3,4 -> 2,3, bit 2 -> 4
+QM_DEV int swz_k(int r) { return (r & 3) | (((r >> 3) & 3) << 2) | (((r >> 2) & 1) << 4); }
+
+// Key held by row i of S^T fragment kk: the four fragments of a 64-key tile
+// are arranged so that, for PV k-step ks = kk >> 1, a lane's pair of
+// fragments 2ks, 2ks+1 holds the 8 consecutive keys 32 ks + 8 lq .. + 7.
+QM_DEV int frag_key(int kk, int i) { return 32 * (kk >> 1) + 8 * (i >> 2) + 4 * (kk & 1) + (i & 3); }
+
+// 16 bytes per lane from global memory straight into LDS: lane l writes
+// lds + 16 l.  Issued as inline asm so that no compiler-inserted wait ties
+// later LDS reads to it; completion is awaited explicitly (vmcnt) before the
+// barrier that publishes the tile.  M0 has no other user in this kernel.
+QM_DEV void dma16(const void* gsrc, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :: "v"(gsrc), "s"(lds) : "memory", "m0");
+}
+
+extern "C" __global__ __launch_bounds__(512) void qm_gqa_prefill_attn(GqaPrefillArgs A) {
+    __shared__ __attribute__((aligned(1024))) char sm[2 * SM_BUF + 8 * 16 * 4];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 15, lq = lane >> 4;
     const int g = blockIdx.x % QM_GQA_KV_HEADS;
     const int nblk = A.s_pad / TQ;
     const int tb = nblk - 1 - (int)(blockIdx.x / QM_GQA_KV_HEADS);   // longest rows first
     const int t0 = tb * TQ;
-    const int qh = 4 * g + w;
+    // wave w: query head 4g + (w & 3), rows r0 .. r0+15 of the block
+    const int qh = 4 * g + (w & 3);
+    const int r0 = t0 + 16 * (w >> 2);
+    const int nkt = (t0 + TQ + KT - 1) / KT;
+    const uint32_t sm_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)sm;
+    float* rowf = reinterpret_cast<float*>(sm + SM_ROWF) + w * 16;
 
-    // 1. q: RMSNorm (1+gamma) + RoPE at its position, f16, B fragments of S^T
-    for (int j = 0; j < TQ; ++j) {
-        const int t = t0 + j;
+    // tile fetch: wave w moves K blocks 4w .. 4w+3 and V^T blocks 4w .. 4w+3
+    const uint16_t* kbase = A.k_cache + (size_t)g * A.cap * QM_GQA_HD;
+    const uint16_t* vbase = A.vt + (size_t)g * QM_GQA_HD * A.s_pad;
+    auto fetch = [&](int kt, int buf) {
+        const int k0 = kt * KT;
+        const uint32_t kdst = sm_lds + buf * SM_BUF, vdst = kdst + SM_V;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int b = 4 * w + j, kk = b >> 3, s = b & 7;       // K block: S^T fragment kk, k-step s
+            const int key = min(k0 + frag_key(kk, lr), A.S - 1);  // rows past S feed masked scores only
+            dma16(kbase + (size_t)key * QM_GQA_HD + 32 * s + 8 * lq, kdst + 1024 * b);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int b = 4 * w + j, dt = b >> 1, ks = b & 1;      // V^T block: dims tile dt, keys step ks
+            dma16(vbase + (size_t)(16 * dt + lr) * A.s_pad + k0 + 32 * ks + 8 * lq, vdst + 1024 * b);
+        }
+    };
+    fetch(0, 0);                             // in flight during the q prep
+
+    // 1. q: RMSNorm (1+gamma) + RoPE at its position, f16, staged in buffer 1
+    char* qs = sm + SM_BUF + w * (16 * 512);
+    for (int j = 0; j < 16; ++j) {
+        const int t = r0 + j;
         float4 x = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         if (t < A.S) {                                              // wave-uniform
             const uint2 raw = *reinterpret_cast<const uint2*>(A.q_gate + ((size_t)t * QM_GQA_HEADS + qh) * (2 * QM_GQA_HD) + 4 * lane);
             x = norm_rope_head(bf16x4_to_f32(raw), A.q_norm, A.rope_cos + (size_t)t * 32,
                                A.rope_sin + (size_t)t * 32, lane);
         }
-        *reinterpret_cast<uint2*>(&sm.u.qstage[w][j][4 * lane]) = f32x4_to_f16(x);
+        *reinterpret_cast<uint2*>(qs + j * 512 + 16 * ((lane >> 1) ^ swz_k(j)) + 8 * (lane & 1)) = f32x4_to_f16(x);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    half8 qf[2][8];                         // B[k = dim][n = row]: 8 dims of row n
+    half8 qf[8];                            // B[k = dim][n = row]: 8 dims of row n
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-        for (int s = 0; s < 8; ++s)
-            qf[rt][s] = *reinterpret_cast<const half8*>(&sm.u.qstage[w][16 * rt + lr][32 * s + 8 * lq]);
+    for (int s = 0; s < 8; ++s)
+        qf[s] = *reinterpret_cast<const half8*>(qs + lr * 512 + 16 * ((4 * s + lq) ^ swz_k(lr)));
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // tile 0 landed (this wave's part)
+    __syncthreads();                        // tile 0 visible; q staging consumed
 
-    floatx4 O[2][16];
+    floatx4 O[16];
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-        for (int dt = 0; dt < 16; ++dt) O[rt][dt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.0f, 0.0f};
+    for (int dt = 0; dt < 16; ++dt) O[dt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_run = -INFINITY, l_run = 0.0f;
     const float sl2 = (1.0f / 16.0f) * 1.4426950408889634f;     // 1/sqrt(256) * log2(e)
+    const int tok = r0 + lr;
 
-    const int nkt = (t0 + TQ + KT - 1) / KT;
     for (int kt = 0; kt < nkt; ++kt) {
-        const int k0 = kt * KT;
-        __syncthreads();                    // previous tile (or q staging) fully consumed
-        // stage K tile [64 keys][256] and V^T tile [256 dims][64 keys]
-#pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            const int piece = tid + 256 * r;                     // 2048 x 16 B each
-            const int key = piece >> 5, col = 8 * (piece & 31);
-            uint4 kv = make_uint4(0, 0, 0, 0);
-            if (k0 + key < A.S)
-                kv = *reinterpret_cast<const uint4*>(A.k_cache + ((size_t)g * A.cap + k0 + key) * QM_GQA_HD + col);
-            *reinterpret_cast<uint4*>(&sm.u.kv.Ks[key][col]) = kv;
-            const int d = piece >> 3, kc = 8 * (piece & 7);
-            const uint4 vv = *reinterpret_cast<const uint4*>(A.vt + ((size_t)g * QM_GQA_HD + d) * A.s_pad + k0 + kc);
-            *reinterpret_cast<uint4*>(&sm.u.kv.Vts[d][kc]) = vv;
-        }
-        __syncthreads();
+        const int k0 = kt * KT, buf = kt & 1;
+        // the other buffer was last read before the previous barrier
+        if (kt + 1 < nkt) fetch(kt + 1, buf ^ 1);
+        const char* Kb = sm + buf * SM_BUF;
+        const char* Vb = Kb + SM_V;
 
-        // S^T = K Q^T: fragment [kk][rt] holds keys k0+16kk+4lq+e of row 16rt+lr
-        floatx4 sT[4][2];
+        // S^T = K Q^T: fragment kk row i is key frag_key(kk, i) of the tile
+        floatx4 sT[4];
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
-            sT[kk][0] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-            sT[kk][1] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+            sT[kk] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int s = 0; s < 8; ++s) {
-                const half8 a = *reinterpret_cast<const half8*>(&sm.u.kv.Ks[16 * kk + lr][32 * s + 8 * lq]);
-                sT[kk][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[0][s], sT[kk][0], 0, 0, 0);
-                sT[kk][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[1][s], sT[kk][1], 0, 0, 0);
+                const half8 a = *reinterpret_cast<const half8*>(Kb + (8 * kk + s) * 1024 + 16 * lane);
+                sT[kk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[s], sT[kk], 0, 0, 0);
             }
         }
-        // online softmax per row (base 2)
-        half8 pf[2][2];
-        float corr[2];
+        // online softmax per row (base 2); only tiles that reach past the
+        // wave's first row need the causal mask
+        const bool diag = k0 + KT - 1 > r0;
+        float mx = -INFINITY;
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
-            const int tok = t0 + 16 * rt + lr;
-            float mx = -INFINITY;
+        for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk)
+            for (int e = 0; e < 4; ++e) {
+                float sc = sT[kk][e] * sl2;
+                if (diag && k0 + frag_key(kk, 4 * lq + e) > tok) sc = -INFINITY;
+                sT[kk][e] = sc;
+                mx = fmaxf(mx, sc);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        // key 0 is visible to every row, so mx is finite from tile 0 on
+        const float m_new = mx > m_run + RESCALE_SLACK ? mx : m_run;
+        const float corr = __builtin_amdgcn_exp2f(m_run - m_new);    // 1 unless moved; 0 on tile 0
+        float ps = 0.0f;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int key = k0 + 16 * kk + 4 * lq + e;
-                    const float s = key <= tok ? sT[kk][rt][e] * sl2 : -INFINITY;
-                    sT[kk][rt][e] = s;
-                    mx = fmaxf(mx, s);
-                }
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float m_new = fmaxf(m_run[rt], mx);
-            corr[rt] = (m_run[rt] == -INFINITY) ? 0.0f : exp2f(m_run[rt] - m_new);
-            float ps = 0.0f;
+        for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk)
+            for (int e = 0; e < 4; ++e) {
+                const float pv = __builtin_amdgcn_exp2f(sT[kk][e] - m_new);
+                sT[kk][e] = pv;
+                ps += pv;
+            }
+        ps += __shfl_xor(ps, 16);
+        ps += __shfl_xor(ps, 32);
+        l_run = l_run * corr + ps;
+        m_run = m_new;
+        // A operand of PV k-step ks: keys 32 ks + 8 lq .. + 7 of row lr
+        half8 pf[2];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float p = (m_new == -INFINITY) ? 0.0f : exp2f(sT[kk][rt][e] - m_new);
-                    sT[kk][rt][e] = p;
-                    ps += p;
-                }
-            ps += __shfl_xor(ps, 16);
-            ps += __shfl_xor(ps, 32);
-            l_run[rt] = l_run[rt] * corr[rt] + ps;
-            m_run[rt] = m_new;
-            // A operand of PV, k-step ks pairs key fragments 2ks and 2ks+1
+        for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    pf[rt][ks][e] = (_Float16)sT[2 * ks][rt][e];
-                    pf[rt][ks][4 + e] = (_Float16)sT[2 * ks + 1][rt][e];
-                }
-        }
-        // rescale O: lane (dim lr, lq) holds rows 16rt + 4lq + e
-        if (lq == 0) {
-            sm.rowf[w][lr] = corr[0];
-            sm.rowf[w][16 + lr] = corr[1];
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
-            const float4 f = *reinterpret_cast<const float4*>(&sm.rowf[w][16 * rt + 4 * lq]);
+            for (int e = 0; e < 4; ++e) {
+                pf[ks][e] = (_Float16)sT[2 * ks][e];
+                pf[ks][4 + e] = (_Float16)sT[2 * ks + 1][e];
+            }
+        // rescale O (lane (dim lr, lq) holds rows 4lq + e) when any row of
+        // the wave moved its reference max
+        if (__any(corr != 1.0f)) {
+            if (lq == 0) rowf[lr] = corr;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const float4 f = *reinterpret_cast<const float4*>(&rowf[4 * lq]);
 #pragma unroll
             for (int dt = 0; dt < 16; ++dt) {
-                O[rt][dt][0] *= f.x; O[rt][dt][1] *= f.y; O[rt][dt][2] *= f.z; O[rt][dt][3] *= f.w;
+                O[dt][0] *= f.x; O[dt][1] *= f.y; O[dt][2] *= f.z; O[dt][3] *= f.w;
             }
+            __builtin_amdgcn_wave_barrier();
         }
-        __builtin_amdgcn_wave_barrier();
-        // O += P V   (16x16x32; B lane (dim, lq) holds keys 32ks+4lq+e and 32ks+16+4lq+e)
+        // O += P V   (16x16x32; B lane (dim, lq) holds keys 32 ks + 8 lq .. + 7)
 #pragma unroll
-        for (int dt = 0; dt < 16; ++dt) {
+        for (int dt = 0; dt < 16; ++dt)
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
-                const half4 v0 = *reinterpret_cast<const half4*>(&sm.u.kv.Vts[16 * dt + lr][32 * ks + 4 * lq]);
-                const half4 v1 = *reinterpret_cast<const half4*>(&sm.u.kv.Vts[16 * dt + lr][32 * ks + 16 + 4 * lq]);
-                half8 b;
-                b[0] = v0[0]; b[1] = v0[1]; b[2] = v0[2]; b[3] = v0[3];
-                b[4] = v1[0]; b[5] = v1[1]; b[6] = v1[2]; b[7] = v1[3];
-                O[0][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[0][ks], b, O[0][dt], 0, 0, 0);
-                O[1][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[1][ks], b, O[1][dt], 0, 0, 0);
+                const half8 b = *reinterpret_cast<const half8*>(Vb + (2 * dt + ks) * 1024 + 16 * lane);
+                O[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[ks], b, O[dt], 0, 0, 0);
             }
-        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // next tile landed (this wave's part)
+        __syncthreads();                    // ... for every wave; this tile fully consumed
     }
 
     // 3. out = (O / l) * sigmoid(gate), bf16 (gemv.rs:1441-1444)
-    __builtin_amdgcn_wave_barrier();
-    if (lq == 0) {
-        sm.rowf[w][lr] = 1.0f / l_run[0];
-        sm.rowf[w][16 + lr] = 1.0f / l_run[1];
-    }
+    if (lq == 0) rowf[lr] = 1.0f / l_run;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const float4 inv = *reinterpret_cast<const float4*>(&rowf[4 * lq]);
+    const float iv[4] = {inv.x, inv.y, inv.z, inv.w};
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-        const float4 inv = *reinterpret_cast<const float4*>(&sm.rowf[w][16 * rt + 4 * lq]);
-        const float iv[4] = {inv.x, inv.y, inv.z, inv.w};
+    for (int e = 0; e < 4; ++e) {
+        const int t = r0 + 4 * lq + e;
+        if (t >= A.S) continue;
+        const uint16_t* gate = A.q_gate + ((size_t)t * QM_GQA_HEADS + qh) * (2 * QM_GQA_HD) + QM_GQA_HD;
+        uint16_t* o = A.out + ((size_t)t * QM_GQA_HEADS + qh) * QM_GQA_HD;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int t = t0 + 16 * rt + 4 * lq + e;
-            if (t >= A.S) continue;
-            const uint16_t* gate = A.q_gate + ((size_t)t * QM_GQA_HEADS + qh) * (2 * QM_GQA_HD) + QM_GQA_HD;
-            uint16_t* o = A.out + ((size_t)t * QM_GQA_HEADS + qh) * QM_GQA_HD;
-#pragma unroll
-            for (int dt = 0; dt < 16; ++dt) {
-                const int d = 16 * dt + lr;
-                const float gv = bf16_to_f32(gate[d]);
-                o[d] = f32_to_bf16((O[rt][dt][e] * iv[e]) * sigmoid_f(gv));
-            }
+        for (int dt = 0; dt < 16; ++dt) {
+            const int d = 16 * dt + lr;
+            const float gv = bf16_to_f32(gate[d]);
+            o[d] = f32_to_bf16((O[dt][e] * iv[e]) * sigmoid_f(gv));
         }
     }
 }

@@ -73,3 +73,26 @@ def test_prefill_8192_rows(ctx):
                                      np.linspace(0, S - 1, 40).astype(np.int64)]))
     ref, kc, vc = run_oracle(w, S, rows=rows)
     check(o, K, V, ref, kc, vc, rows)
+
+
+def test_prefill_score_jumps(ctx):
+    """Later keys that score far above the earlier ones: every query is one
+    vector b; keys from position 150 lean 60% towards b (a jump of well over
+    8 in log2 units, so the running max moves and O is rescaled) and keys
+    from 700 are b itself (a smaller second jump that stays under the
+    reference max's slack, so P grows to ~2^7 before normalisation)."""
+    S = 1000
+    w = W.gqa_prefill_workload(S, seed=11)
+    rng = np.random.default_rng(12)
+    b = rng.standard_normal(256).astype(np.float32)
+    qg = W.bf16_value(w["q_gate"]).reshape(S, 16, 512).copy()
+    qg[:, :, :256] = b
+    k = W.bf16_value(w["k"]).reshape(S, 4, 256).copy()
+    k[150:700] = 0.6 * b + 0.4 * k[150:700]
+    k[700:] = b
+    w["q_gate"] = W.bf16_bits(qg.reshape(w["q_gate"].shape))
+    w["k"] = W.bf16_bits(k.reshape(w["k"].shape))
+    print("case: gqa prefill S=1000 score jumps", flush=True)
+    o, K, V = run_gpu(ctx, w, S, S)
+    ref, kc, vc = run_oracle(w, S)
+    check(o, K, V, ref, kc, vc, np.arange(S))
