@@ -18,7 +18,10 @@
  *     (gemv.rs:1049, gemv.rs:620-621) and its GPU thread turns panics into
  *     Err (gpu_inference.rs:950-975); a Rust caller maps non-zero to Err.
  *   - All pointers named *_dev are device pointers (from qm_alloc or any
- *     hipMalloc); sizes are element counts unless named *bytes.
+ *     hipMalloc); sizes are element counts unless named *bytes.  Device
+ *     pointers given to the mixer calls must be 16-byte aligned (the
+ *     kernels move 16-byte vectors); others are refused with
+ *     QM_ERR_INVALID_ARG.
  *   - Kernels are enqueued asynchronously on `stream` (a hipStream_t; NULL
  *     means the context's own stream).  Nothing synchronises the host
  *     except qm_sync and the d2h copy.

@@ -623,8 +623,7 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_out(DnPrefillArg
         ss = fmaf(y[q].y, y[q].y, ss);
         ss = fmaf(y[q].z, y[q].z, ss);
         ss = fmaf(y[q].w, y[q].w, ss);
-        ss = row_sum16(ss);
-        ss += __shfl_xor(ss, 16);
+        ss = sum_xor16(row_sum16(ss));
         const int t = c * CHK + tk0 + 2 * q;
         if (t < A.T) {
             const float inv_rms = 1.0f / sqrtf(ss / (float)QM_DN_HD + 1e-6f);

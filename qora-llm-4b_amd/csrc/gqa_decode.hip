@@ -71,7 +71,7 @@ QM_DEV void compute_round(WaveState& st, const RoundBuf& rb, const half8 (&afr)[
     float p[4], corr[4];
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
-        const float sc = (c[h] + __shfl_xor(c[h], 16)) * scale;
+        const float sc = sum_xor16(c[h]) * scale;
         const float x = valid ? sc : -INFINITY;
         const float mt = readlane_f32(row_max16(x), 0);
         const float m_new = fmaxf(st.m[h], mt);

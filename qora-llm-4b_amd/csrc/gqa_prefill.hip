@@ -22,7 +22,8 @@
 //                      shuffles between the two products.  Online softmax in
 //                      base 2, fp32, with a lazily moved reference max.  K / V
 //                      tiles are double-buffered in LDS and copied there by
-//                      LDS DMA while the previous tile computes.
+//                      LDS DMA ahead of use; the scores of the next tile run
+//                      on MFMA while the current tile's softmax runs.
 #include "qm_device.h"
 #include "qm_kernel_args.h"
 #include "qm_gqa_common.h"
@@ -101,22 +102,16 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_prefill_kv(GqaPrefillAr
 // ---------------------------------------------------------------------------
 // Flash attention.  Lane (lr, lq) = (lane & 15, lane >> 4).
 // ---------------------------------------------------------------------------
-// LDS (bytes): two tile buffers of 64 KB.  A buffer holds a 64-key tile in
-// MFMA fragment order: 32 K blocks (kk, s) then 32 V^T blocks (dt, ks) of
-// 1 KB, block entry l being the 16 bytes lane l reads for that product, so
-// every fragment read is lane * 16 + an immediate (no bank conflicts, no
-// per-read address registers).  The gather into that order is done by the
-// per-lane source addresses of the LDS DMA.  The q staging area [8 waves]
-// [16 rows][512 B] shares buffer 1 (consumed before tile 1 arrives), rows
-// with their 16-byte chunks XOR swizzled (chunk c at c ^ swz_k(row)); then
-// the per-wave row factors.
-#define SM_BUF 65536
-#define SM_V 32768
-#define SM_ROWF (2 * SM_BUF)
-
-// rows {b..b+3, b+8..b+11, b+16..b+19, b+24..b+27} (a read phase) -> distinct
-// low 4 bits: bits 0,1 stay, bits 3,4 -> 2,3, bit 2 -> 4
-QM_DEV int swz_k(int r) { return (r & 3) | (((r >> 3) & 3) << 2) | (((r >> 2) & 1) << 4); }
+// LDS (bytes): K buffers 0, 1 then V^T buffers 0, 1 of 32 KB each.  A K
+// buffer holds a 64-key tile in MFMA fragment order as 32 blocks (kk, s) of
+// 1 KB, a V^T buffer as 32 blocks (dt, ks); block entry l is the 16 bytes
+// lane l reads for that product, so every fragment read is lane * 16 + an
+// immediate (no bank conflicts, no per-read address registers).  The gather
+// into that order is done by the per-lane source addresses of the LDS DMA.
+// Then the per-wave row factors.
+#define SM_K(b) ((b) * 32768)
+#define SM_V(b) (65536 + (b) * 32768)
+#define SM_ROWF 131072
 
 // Key held by row i of S^T fragment kk: the four fragments of a 64-key tile
 // are arranged so that, for PV k-step ks = kk >> 1, a lane's pair of
@@ -132,8 +127,12 @@ QM_DEV void dma16(const void* gsrc, uint32_t lds) {
                  :: "v"(gsrc), "s"(lds) : "memory", "m0");
 }
 
+// The loop is software-pipelined over tiles: iteration kt computes the
+// scores of tile kt+1 on MFMA while the VALU runs tile kt's softmax in
+// slices between the MFMA groups, then accumulates tile kt's P V.  K tiles
+// are fetched two ahead, V tiles one ahead.
 extern "C" __global__ __launch_bounds__(512) void qm_gqa_prefill_attn(GqaPrefillArgs A) {
-    __shared__ __attribute__((aligned(1024))) char sm[2 * SM_BUF + 8 * 16 * 4];
+    __shared__ __attribute__((aligned(1024))) char sm[SM_ROWF + 8 * 16 * 4];
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 15, lq = lane >> 4;
@@ -148,47 +147,110 @@ extern "C" __global__ __launch_bounds__(512) void qm_gqa_prefill_attn(GqaPrefill
     const uint32_t sm_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)sm;
     float* rowf = reinterpret_cast<float*>(sm + SM_ROWF) + w * 16;
 
-    // tile fetch: wave w moves K blocks 4w .. 4w+3 and V^T blocks 4w .. 4w+3
+    // tile fetch: wave w moves blocks 4w .. 4w+3 of the K and of the V^T tile
     const uint16_t* kbase = A.k_cache + (size_t)g * A.cap * QM_GQA_HD;
     const uint16_t* vbase = A.vt + (size_t)g * QM_GQA_HD * A.s_pad;
-    auto fetch = [&](int kt, int buf) {
+    auto fetch_k = [&](int kt, int buf) {
         const int k0 = kt * KT;
-        const uint32_t kdst = sm_lds + buf * SM_BUF, vdst = kdst + SM_V;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int b = 4 * w + j, kk = b >> 3, s = b & 7;       // K block: S^T fragment kk, k-step s
             const int key = min(k0 + frag_key(kk, lr), A.S - 1);  // rows past S feed masked scores only
-            dma16(kbase + (size_t)key * QM_GQA_HD + 32 * s + 8 * lq, kdst + 1024 * b);
+            dma16(kbase + (size_t)key * QM_GQA_HD + 32 * s + 8 * lq, sm_lds + SM_K(buf) + 1024 * b);
         }
+    };
+    auto fetch_v = [&](int kt, int buf) {
+        const int k0 = kt * KT;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int b = 4 * w + j, dt = b >> 1, ks = b & 1;      // V^T block: dims tile dt, keys step ks
-            dma16(vbase + (size_t)(16 * dt + lr) * A.s_pad + k0 + 32 * ks + 8 * lq, vdst + 1024 * b);
+            dma16(vbase + (size_t)(16 * dt + lr) * A.s_pad + k0 + 32 * ks + 8 * lq, sm_lds + SM_V(buf) + 1024 * b);
         }
     };
-    fetch(0, 0);                             // in flight during the q prep
+    fetch_k(0, 0);                           // in flight during the q prep
+    fetch_v(0, 0);
+    if (nkt > 1) fetch_k(1, 1);
 
-    // 1. q: RMSNorm (1+gamma) + RoPE at its position, f16, staged in buffer 1
-    char* qs = sm + SM_BUF + w * (16 * 512);
-    for (int j = 0; j < 16; ++j) {
-        const int t = r0 + j;
-        float4 x = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (t < A.S) {                                              // wave-uniform
-            const uint2 raw = *reinterpret_cast<const uint2*>(A.q_gate + ((size_t)t * QM_GQA_HEADS + qh) * (2 * QM_GQA_HD) + 4 * lane);
-            x = norm_rope_head(bf16x4_to_f32(raw), A.q_norm, A.rope_cos + (size_t)t * 32,
-                               A.rope_sin + (size_t)t * 32, lane);
-        }
-        *reinterpret_cast<uint2*>(qs + j * 512 + 16 * ((lane >> 1) ^ swz_k(j)) + 8 * (lane & 1)) = f32x4_to_f16(x);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // 1. q: RMSNorm (1+gamma, eps 1e-6; gemv.rs:586-597) and split-half RoPE
+    //    (gemv.rs:604-627) straight into the B fragments: lane (lr, lq) holds
+    //    dims 32 s + 8 lq + e of row r0 + lr, so the row's sum of squares is
+    //    a reduction over the four lanes lr + 16 lq, and each rotation pair
+    //    (i, i + 32), i = 8 lq + e, sits in one lane (s = 0 and s = 1).
     half8 qf[8];                            // B[k = dim][n = row]: 8 dims of row n
+    {
+        const int t = r0 + lr;
+        const int tc = min(t, A.S - 1);     // rows past S: any valid row, then zeroed
+        const uint16_t* qrow = A.q_gate + ((size_t)tc * QM_GQA_HEADS + qh) * (2 * QM_GQA_HD) + 8 * lq;
+        float x[8][8];
+        float ss = 0.0f;
 #pragma unroll
-    for (int s = 0; s < 8; ++s)
-        qf[s] = *reinterpret_cast<const half8*>(qs + lr * 512 + 16 * ((4 * s + lq) ^ swz_k(lr)));
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // tile 0 landed (this wave's part)
-    __syncthreads();                        // tile 0 visible; q staging consumed
+        for (int s = 0; s < 8; ++s) {
+            const uint4 u = *reinterpret_cast<const uint4*>(qrow + 32 * s);
+            const uint32_t wv[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                x[s][2 * e] = t < A.S ? bf16_to_f32((uint16_t)(wv[e] & 0xffffu)) : 0.0f;
+                x[s][2 * e + 1] = t < A.S ? bf16_to_f32((uint16_t)(wv[e] >> 16)) : 0.0f;
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss = fmaf(x[s][e], x[s][e], ss);
+        }
+        ss = sum_xor32(sum_xor16(ss));
+        const float inv = 1.0f / sqrtf(ss / (float)QM_GQA_HD + 1e-6f);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const uint4 gw = *reinterpret_cast<const uint4*>(A.q_norm + 32 * s + 8 * lq);
+            const uint32_t gv[4] = {gw.x, gw.y, gw.z, gw.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                x[s][2 * e] = x[s][2 * e] * inv * (1.0f + f16_to_f32((uint16_t)(gv[e] & 0xffffu)));
+                x[s][2 * e + 1] = x[s][2 * e + 1] * inv * (1.0f + f16_to_f32((uint16_t)(gv[e] >> 16)));
+            }
+        }
+        const float* crow = A.rope_cos + (size_t)tc * 32 + 8 * lq;
+        const float* srow = A.rope_sin + (size_t)tc * 32 + 8 * lq;
+        const float4 c0 = ld4(crow), c1 = ld4(crow + 4), s0 = ld4(srow), s1 = ld4(srow + 4);
+        const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+        const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float x1 = x[0][e], x2 = x[1][e];
+            x[0][e] = x1 * cs[e] - x2 * sn[e];
+            x[1][e] = x2 * cs[e] + x1 * sn[e];
+        }
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qf[s][e] = (_Float16)x[s][e];
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // K0, V0, K1 landed (this wave's part)
+    __syncthreads();                        // ... for every wave
+
+    // S^T = K Q^T of one tile: fragment kk row i is key frag_key(kk, i); K
+    // blocks are read four at a time, one group ahead of their MFMAs, and
+    // slice(grp) runs after MFMA group grp
+    auto scores = [&](const char* Kb, floatx4 (&sT)[4], auto&& slice) {
+        half8 ka[2][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ka[0][j] = *reinterpret_cast<const half8*>(Kb + j * 1024 + 16 * lane);
+#pragma unroll
+        for (int grp = 0; grp < 8; ++grp) {          // group = (kk, half of s)
+            const int cur = grp & 1;
+            if (grp + 1 < 8) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    ka[cur ^ 1][j] = *reinterpret_cast<const half8*>(Kb + (4 * (grp + 1) + j) * 1024 + 16 * lane);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            const int kk = grp >> 1, s0 = 4 * (grp & 1);
+            if ((grp & 1) == 0) sT[kk] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                sT[kk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[cur][j], qf[s0 + j], sT[kk], 0, 0, 0);
+            slice(grp);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
 
     floatx4 O[16];
 #pragma unroll
@@ -197,64 +259,66 @@ extern "C" __global__ __launch_bounds__(512) void qm_gqa_prefill_attn(GqaPrefill
     const float sl2 = (1.0f / 16.0f) * 1.4426950408889634f;     // 1/sqrt(256) * log2(e)
     const int tok = r0 + lr;
 
-    for (int kt = 0; kt < nkt; ++kt) {
-        const int k0 = kt * KT, buf = kt & 1;
-        // the other buffer was last read before the previous barrier
-        if (kt + 1 < nkt) fetch(kt + 1, buf ^ 1);
-        const char* Kb = sm + buf * SM_BUF;
-        const char* Vb = Kb + SM_V;
+    floatx4 sC[4];                          // scores of the tile being finished
+    scores(sm + SM_K(0), sC, [](int) {});
+    __syncthreads();                        // every wave is done with K buffer 0
 
-        // S^T = K Q^T: fragment kk row i is key frag_key(kk, i) of the tile
-        floatx4 sT[4];
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-            sT[kk] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                const half8 a = *reinterpret_cast<const half8*>(Kb + (8 * kk + s) * 1024 + 16 * lane);
-                sT[kk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[s], sT[kk], 0, 0, 0);
-            }
-        }
-        // online softmax per row (base 2); only tiles that reach past the
-        // wave's first row need the causal mask
-        const bool diag = k0 + KT - 1 > r0;
-        float mx = -INFINITY;
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                float sc = sT[kk][e] * sl2;
-                if (diag && k0 + frag_key(kk, 4 * lq + e) > tok) sc = -INFINITY;
-                sT[kk][e] = sc;
-                mx = fmaxf(mx, sc);
-            }
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        // key 0 is visible to every row, so mx is finite from tile 0 on
-        const float m_new = mx > m_run + RESCALE_SLACK ? mx : m_run;
-        const float corr = __builtin_amdgcn_exp2f(m_run - m_new);    // 1 unless moved; 0 on tile 0
-        float ps = 0.0f;
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float pv = __builtin_amdgcn_exp2f(sT[kk][e] - m_new);
-                sT[kk][e] = pv;
-                ps += pv;
-            }
-        ps += __shfl_xor(ps, 16);
-        ps += __shfl_xor(ps, 32);
-        l_run = l_run * corr + ps;
-        m_run = m_new;
-        // A operand of PV k-step ks: keys 32 ks + 8 lq .. + 7 of row lr
+    for (int kt = 0; kt < nkt; ++kt) {
+        const int k0 = kt * KT, b = kt & 1;
+        // K(kt) was consumed by the previous iteration's scores, V(kt-1) by
+        // its P V: both buffers are free since the barrier that ended it
+        if (kt + 2 < nkt) fetch_k(kt + 2, b);
+        if (kt + 1 < nkt) fetch_v(kt + 1, b ^ 1);
+
+        // online softmax of tile kt (base 2), in slices between the MFMA
+        // groups of tile kt+1's scores (computed on whatever K buffer b^1
+        // holds on the last tile, and then discarded)
+        const bool diag = k0 + KT - 1 > r0;     // tile reaches past the wave's first row
+        float mx = -INFINITY, m_new = 0.0f, corr = 1.0f, ps = 0.0f;
         half8 pf[2];
+        auto slice = [&](int grp) {
+            if (grp == 0 || grp == 1) {
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
+                for (int kk = 2 * grp; kk < 2 * grp + 2; ++kk)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                pf[ks][e] = (_Float16)sT[2 * ks][e];
-                pf[ks][4 + e] = (_Float16)sT[2 * ks + 1][e];
+                    for (int e = 0; e < 4; ++e) {
+                        float sc = sC[kk][e] * sl2;
+                        if (diag && k0 + frag_key(kk, 4 * lq + e) > tok) sc = -INFINITY;
+                        sC[kk][e] = sc;
+                        mx = fmaxf(mx, sc);
+                    }
+            } else if (grp == 2) {
+                mx = max_xor32(max_xor16(mx));
+                // key 0 is visible to every row, so mx is finite from tile 0 on
+                m_new = mx > m_run + RESCALE_SLACK ? mx : m_run;
+                corr = __builtin_amdgcn_exp2f(m_run - m_new);        // 1 unless moved; 0 on tile 0
+            } else if (grp == 3 || grp == 4) {
+#pragma unroll
+                for (int kk = 2 * (grp - 3); kk < 2 * (grp - 3) + 2; ++kk)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float pv = __builtin_amdgcn_exp2f(sC[kk][e] - m_new);
+                        sC[kk][e] = pv;
+                        ps += pv;
+                    }
+            } else if (grp == 5) {
+                ps = sum_xor32(sum_xor16(ps));
+                l_run = l_run * corr + ps;
+                m_run = m_new;
+            } else if (grp == 6) {
+                // A operand of PV k-step ks: keys 32 ks + 8 lq .. + 7 of row lr
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        pf[ks][e] = (_Float16)sC[2 * ks][e];
+                        pf[ks][4 + e] = (_Float16)sC[2 * ks + 1][e];
+                    }
             }
+        };
+        floatx4 sN[4];
+        scores(sm + SM_K(b ^ 1), sN, slice);
+
         // rescale O (lane (dim lr, lq) holds rows 4lq + e) when any row of
         // the wave moved its reference max
         if (__any(corr != 1.0f)) {
@@ -269,15 +333,33 @@ extern "C" __global__ __launch_bounds__(512) void qm_gqa_prefill_attn(GqaPrefill
             }
             __builtin_amdgcn_wave_barrier();
         }
-        // O += P V   (16x16x32; B lane (dim, lq) holds keys 32 ks + 8 lq .. + 7)
+        // O += P V   (16x16x32; B lane (dim, lq) holds keys 32 ks + 8 lq .. + 7),
+        // V^T blocks read four at a time, one group ahead of the MFMAs
+        {
+            const char* Vb = sm + SM_V(b);
+            half8 vb[2][4];
 #pragma unroll
-        for (int dt = 0; dt < 16; ++dt)
+            for (int j = 0; j < 4; ++j) vb[0][j] = *reinterpret_cast<const half8*>(Vb + j * 1024 + 16 * lane);
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const half8 b = *reinterpret_cast<const half8*>(Vb + (2 * dt + ks) * 1024 + 16 * lane);
-                O[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[ks], b, O[dt], 0, 0, 0);
+            for (int grp = 0; grp < 8; ++grp) {          // group = dims tiles 2grp, 2grp+1
+                const int cur = grp & 1;
+                if (grp + 1 < 8) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        vb[cur ^ 1][j] = *reinterpret_cast<const half8*>(Vb + (4 * (grp + 1) + j) * 1024 + 16 * lane);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int dt = 2 * grp + (j >> 1), ks = j & 1;
+                    O[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[ks], vb[cur][j], O[dt], 0, 0, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // next tile landed (this wave's part)
+        }
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) sC[kk] = sN[kk];
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // next tiles landed (this wave's part)
         __syncthreads();                    // ... for every wave; this tile fully consumed
     }
 

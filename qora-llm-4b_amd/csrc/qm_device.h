@@ -37,6 +37,27 @@ QM_DEV float readlane_f32(float x, int lane) {
 
 // Sum over the whole wave: row sums then the four row results in a fixed
 // order.  Uniform across the wave.
+// Reductions with lane l ^ 16 / l ^ 32 through the gfx950 VALU row swaps
+// (v_permlane16_swap / v_permlane32_swap): each lane ends up holding its own
+// value and its partner's, in either order, so a commutative op of the pair
+// is the reduction (no LDS round trip as with ds_bpermute).
+QM_DEV float max_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+QM_DEV float max_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+QM_DEV float sum_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+QM_DEV float sum_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 QM_DEV float wave_sum64(float x) {
     x = row_sum16(x);
     float r0 = readlane_f32(x, 0), r1 = readlane_f32(x, 16);

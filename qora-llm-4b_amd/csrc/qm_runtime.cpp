@@ -17,6 +17,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdarg>
+#include <initializer_list>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -70,6 +71,14 @@ int32_t fail(qm_context* c, int32_t code, const char* fmt, ...) {
     va_end(ap);
     if (c) c->err = buf; else g_create_error = buf;
     return code;
+}
+
+// Mixer kernels move data in 16-byte vectors: every device pointer they take
+// must be 16-byte aligned (hipMalloc returns 256-byte aligned memory).
+bool all_aligned16(std::initializer_list<const void*> ptrs) {
+    for (const void* p : ptrs)
+        if (p && (reinterpret_cast<uintptr_t>(p) & 15u) != 0) return false;
+    return true;
 }
 
 #define QM_HIP(c, call)                                                              \
@@ -481,6 +490,8 @@ int32_t qm_deltanet_decode(qm_context* c, qm_stream stream, int32_t batch, int32
         return fail(c, QM_ERR_INVALID_ARG, "qm_deltanet_decode: flags %d", flags);
     if (!qkv || !a || !b || !a_log || !dt_bias || !z || !norm_w || !state || !out)
         return fail(c, QM_ERR_INVALID_ARG, "qm_deltanet_decode: null pointer");
+    if (!all_aligned16({qkv, conv_buf, conv_w, a, b, a_log, dt_bias, z, norm_w, state, out}))
+        return fail(c, QM_ERR_INVALID_ARG, "qm_deltanet_decode: device pointers must be 16-byte aligned");
     if (flags == QM_DN_PREACT && (!conv_buf || !conv_w))
         return fail(c, QM_ERR_INVALID_ARG, "qm_deltanet_decode: layer mode needs conv_buf and conv_w");
     if (state_stride < static_cast<int64_t>(QM_DN_V_HEADS) * QM_DN_HEAD_ELEMS || state_stride % 4)
@@ -525,6 +536,8 @@ int32_t qm_gqa_decode(qm_context* c, qm_stream stream, int32_t batch, const floa
     if (!q_gate || !k_new || !v_new || !q_norm || !k_norm || !rope_cos || !rope_sin || !k_cache ||
         !v_cache || !out)
         return fail(c, QM_ERR_INVALID_ARG, "qm_gqa_decode: null pointer");
+    if (!all_aligned16({q_gate, k_new, v_new, q_norm, k_norm, rope_cos, rope_sin, pos, k_cache, v_cache, out}))
+        return fail(c, QM_ERR_INVALID_ARG, "qm_gqa_decode: device pointers must be 16-byte aligned");
     if (max_pos < 0) return fail(c, QM_ERR_INVALID_ARG, "qm_gqa_decode: max_pos %d", max_pos);
     if (max_pos >= rope_len)
         return fail(c, QM_ERR_ROPE_RANGE, "position %d beyond RoPE table of %d rows", max_pos, rope_len);
@@ -585,6 +598,8 @@ int32_t qm_deltanet_prefill(qm_context* c, qm_stream stream, int32_t seq_len, co
     if (seq_len <= 0) return fail(c, QM_ERR_INVALID_ARG, "qm_deltanet_prefill: seq_len %d", seq_len);
     if (!qkv || !conv_buf || !conv_w || !a || !b || !a_log || !dt_bias || !z || !norm_w || !state || !out)
         return fail(c, QM_ERR_INVALID_ARG, "qm_deltanet_prefill: null pointer");
+    if (!all_aligned16({qkv, conv_buf, conv_w, a, b, a_log, dt_bias, z, norm_w, state, out}))
+        return fail(c, QM_ERR_INVALID_ARG, "qm_deltanet_prefill: device pointers must be 16-byte aligned");
     hipStream_t s = pick(c, stream);
     const DnPrefillLayout L = dn_prefill_layout(seq_len);
     int32_t st = ensure(c, s, L.total);
@@ -617,6 +632,8 @@ int32_t qm_gqa_prefill(qm_context* c, qm_stream stream, int32_t seq_len, const u
     if (seq_len <= 0) return fail(c, QM_ERR_INVALID_ARG, "qm_gqa_prefill: seq_len %d", seq_len);
     if (!q_gate || !k || !v || !q_norm || !k_norm || !rope_cos || !rope_sin || !k_cache || !v_cache || !out)
         return fail(c, QM_ERR_INVALID_ARG, "qm_gqa_prefill: null pointer");
+    if (!all_aligned16({q_gate, k, v, q_norm, k_norm, rope_cos, rope_sin, k_cache, v_cache, out}))
+        return fail(c, QM_ERR_INVALID_ARG, "qm_gqa_prefill: device pointers must be 16-byte aligned");
     if (seq_len > rope_len)
         return fail(c, QM_ERR_ROPE_RANGE, "positions 0..%d beyond RoPE table of %d rows", seq_len - 1, rope_len);
     if (seq_len > cap)

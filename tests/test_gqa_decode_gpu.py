@@ -105,3 +105,11 @@ def test_decode_range_errors(ctx):
         ctx.gqa_decode(1, d["q_gate"], d["k_new"], d["v_new"], d["q_norm"], d["k_norm"], rc, rs, 64,
                        None, 17, d["k_cache"], d["v_cache"], 17, out)
     assert e.value.code == 6
+    with pytest.raises(M.MixerError) as e:      # q_gate 8 bytes off 16-byte alignment
+        ctx.gqa_decode(1, d["q_gate"].offset(8), d["k_new"], d["v_new"], d["q_norm"], d["k_norm"], rc, rs, 16,
+                       None, 4, d["k_cache"], d["v_cache"], 17, out)
+    assert e.value.code == 3                    # QM_ERR_INVALID_ARG
+    with pytest.raises(M.MixerError) as e:      # same for the prefill entry
+        ctx.gqa_prefill(4, d["q_gate"], d["k_new"], d["v_new"], d["q_norm"].offset(2), d["k_norm"], rc, rs, 16,
+                        d["k_cache"], d["v_cache"], 17, out)
+    assert e.value.code == 3                    # QM_ERR_INVALID_ARG
