@@ -255,18 +255,20 @@ def run_dn_decode(args, ctx):
     ctx.sync()
     wall = time.perf_counter() - wall0
     total_ms = t0.elapsed_ms(t1)
-    # per-launch time, eager, events around each launch
+    # per-launch device time: the graph runs the K launches back to back, so
+    # events around it over K give the average launch duration (events around
+    # single eager launches at batch 1 measure host submission gaps instead)
+    k_ms = total_ms / K
     tm = Timer(ctx)
     for t in range(min(K, 64)):
         tm.wrap(lambda: step(Wm + t))
     ctx.sync()
-    k_ms = tm.mean_ms()
     nbytes = dn_decode_bytes(1)
     return {
         "tokens": K, "total_ms": total_ms, "wall_s": wall, "dominant": "qm_dn_decode_t1024",
         "roofline": {"bound": "hbm", "achieved": nbytes / (k_ms * 1e-3), "peak": HBM_PEAK,
                      "unit": "GB/s", "kernel_ms": k_ms, "bytes_per_launch": nbytes},
-        "graph_ms_per_step": total_ms / K,
+        "eager_event_ms_per_launch": tm.mean_ms(),
         "config": {"workload": "DeltaNet decode, 1 layer, batch 1, 16 qk / 32 v heads x 128, fp32 state",
                    "batch": 1, "seq_len": K, "global_batch": 1, "parallelism": "single GPU"},
     }
@@ -288,23 +290,32 @@ def run_gqa_decode(args, ctx):
 
     for _ in range(Wm):
         step()
+    # the timed steps run from one captured graph (split + merge per step);
+    # each step rewrites cache row `pos` and reads rows 0..pos
+    ctx.graph_begin()
+    for _ in range(K):
+        step()
+    g = ctx.graph_end()
     ctx.sync()
-    tm = Timer(ctx)
     t0, t1 = ctx.event(), ctx.event()
     wall0 = time.perf_counter()
     t0.record()
-    for _ in range(K):
-        tm.wrap(step)
+    g.launch()
     t1.record()
     ctx.sync()
     wall = time.perf_counter() - wall0
     total_ms = t0.elapsed_ms(t1)
-    k_ms = tm.mean_ms()
+    k_ms = total_ms / K                      # device time per split + merge pair
+    tm = Timer(ctx)
+    for _ in range(min(K, 64)):
+        tm.wrap(step)
+    ctx.sync()
     nbytes = gqa_decode_bytes(1, pos + 1)
     return {
         "tokens": K, "total_ms": total_ms, "wall_s": wall, "dominant": "qm_gqa_decode_split+merge",
         "roofline": {"bound": "hbm", "achieved": nbytes / (k_ms * 1e-3), "peak": HBM_PEAK,
                      "unit": "GB/s", "kernel_ms": k_ms, "bytes_per_launch": nbytes},
+        "eager_event_ms_per_launch": tm.mean_ms(),
         "config": {"workload": "GQA decode, 1 layer, batch 1, 16q/4kv x 256, position 4096, f16 KV",
                    "batch": 1, "seq_len": pos + 1, "global_batch": 1, "parallelism": "single GPU"},
     }
@@ -341,7 +352,7 @@ def run_dn_prefill(args, ctx):
     flops = dn_prefill_flops(T)
     return {
         "tokens": K * T, "total_ms": total_ms, "wall_s": wall,
-        "dominant": "qm_deltanet_prefill (prep+chunk+scan)",
+        "dominant": "qm_deltanet_prefill (prep+chunk+scan+out)",
         "roofline": {"bound": "mfma", "achieved": flops / (k_ms * 1e-3), "peak": MFMA_BF16_PEAK,
                      "unit": "TFLOP/s", "kernel_ms": k_ms, "flops_per_launch": flops},
         "config": {"workload": "DeltaNet chunked prefill, 1 layer, batch 1, seq 4096, chunk 64, "

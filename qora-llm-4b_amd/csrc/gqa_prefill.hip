@@ -122,10 +122,13 @@ QM_DEV int frag_key(int kk, int i) { return 32 * (kk >> 1) + 8 * (i >> 2) + 4 * 
 // lds + 16 l.  Issued as inline asm so that no compiler-inserted wait ties
 // later LDS reads to it; completion is awaited explicitly (vmcnt) before the
 // barrier that publishes the tile.  M0 has no other user in this kernel.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 QM_DEV void dma16(const void* gsrc, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
                  :: "v"(gsrc), "s"(lds) : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
 // The loop is software-pipelined over tiles: iteration kt computes the
 // scores of tile kt+1 on MFMA while the VALU runs tile kt's softmax in

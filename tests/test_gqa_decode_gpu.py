@@ -113,3 +113,36 @@ def test_decode_range_errors(ctx):
         ctx.gqa_prefill(4, d["q_gate"], d["k_new"], d["v_new"], d["q_norm"].offset(2), d["k_norm"], rc, rs, 16,
                         d["k_cache"], d["v_cache"], 17, out)
     assert e.value.code == 3                    # QM_ERR_INVALID_ARG
+
+
+def test_decode_graph_replay_matches_eager(ctx):
+    """One captured decode step (split + merge) replayed several times, with
+    eager launches and synchronisations in between, matches the eager step
+    bit for bit on every replay (the step is idempotent: it rewrites cache row
+    `pos` and reads rows 0..pos)."""
+    pos = 300
+    w = W.gqa_decode_workload(pos, 2, seed=9)
+    cos, sin = M.rope_table(pos + 1)
+    d = {k: ctx.upload(w[k]) for k in ["q_gate", "k_new", "v_new", "q_norm", "k_norm", "k_cache", "v_cache"]}
+    rc, rs = ctx.upload(cos), ctx.upload(sin)
+    out_e, out_g = ctx.alloc(2 * 16 * 256 * 4), ctx.alloc(2 * 16 * 256 * 4)
+    ctx.reserve(max_batch=2, max_kv_len=pos + 1)
+
+    def step(out):
+        ctx.gqa_decode(2, d["q_gate"], d["k_new"], d["v_new"], d["q_norm"], d["k_norm"], rc, rs, pos + 1,
+                       None, pos, d["k_cache"], d["v_cache"], w["cap"], out)
+
+    print("case: gqa decode graph replay (eager reference)", flush=True)
+    step(out_e)
+    ref = ctx.download(out_e, (2, 16 * 256), np.float32)
+    ctx.graph_begin()
+    step(out_g)
+    g = ctx.graph_end()
+    for rep in range(4):
+        print(f"case: gqa decode graph replay {rep}", flush=True)
+        ctx.fill_normal(out_g, M.QM_F32, 2 * 16 * 256, 0.0, 1.0, seed=rep)   # poison between replays
+        g.launch()
+        ctx.sync()
+        assert np.array_equal(ctx.download(out_g, (2, 16 * 256), np.float32), ref)
+        step(out_e)                                                           # eager work in between
+        ctx.sync()
