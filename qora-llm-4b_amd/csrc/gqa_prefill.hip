@@ -108,10 +108,9 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_prefill_kv(GqaPrefillAr
 // lane l reads for that product, so every fragment read is lane * 16 + an
 // immediate (no bank conflicts, no per-read address registers).  The gather
 // into that order is done by the per-lane source addresses of the LDS DMA.
-// Then the per-wave row factors.
 #define SM_K(b) ((b) * 32768)
 #define SM_V(b) (65536 + (b) * 32768)
-#define SM_ROWF 131072
+#define SM_BYTES 131072
 
 // Key held by row i of S^T fragment kk: the four fragments of a 64-key tile
 // are arranged so that, for PV k-step ks = kk >> 1, a lane's pair of
@@ -135,7 +134,7 @@ QM_DEV void dma16(const void* gsrc, uint32_t lds) {
 // slices between the MFMA groups, then accumulates tile kt's P V.  K tiles
 // are fetched two ahead, V tiles one ahead.
 extern "C" __global__ __launch_bounds__(512) void qm_gqa_prefill_attn(GqaPrefillArgs A) {
-    __shared__ __attribute__((aligned(1024))) char sm[SM_ROWF + 8 * 16 * 4];
+    __shared__ __attribute__((aligned(1024))) char sm[SM_BYTES];
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 15, lq = lane >> 4;
@@ -148,7 +147,6 @@ extern "C" __global__ __launch_bounds__(512) void qm_gqa_prefill_attn(GqaPrefill
     const int r0 = t0 + 16 * (w >> 2);
     const int nkt = (t0 + TQ + KT - 1) / KT;
     const uint32_t sm_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)sm;
-    float* rowf = reinterpret_cast<float*>(sm + SM_ROWF) + w * 16;
 
     // tile fetch: wave w moves blocks 4w .. 4w+3 of the K and of the V^T tile
     const uint16_t* kbase = A.k_cache + (size_t)g * A.cap * QM_GQA_HD;
@@ -221,10 +219,13 @@ extern "C" __global__ __launch_bounds__(512) void qm_gqa_prefill_attn(GqaPrefill
             x[0][e] = x1 * cs[e] - x2 * sn[e];
             x[1][e] = x2 * cs[e] + x1 * sn[e];
         }
+        // the softmax scale 1/sqrt(256) in base 2 is folded into q, so the
+        // scores come out of the MFMA in log2 units
+        const float sl2 = (1.0f / 16.0f) * 1.4426950408889634f;
 #pragma unroll
         for (int s = 0; s < 8; ++s)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) qf[s][e] = (_Float16)x[s][e];
+            for (int e = 0; e < 8; ++e) qf[s][e] = (_Float16)(x[s][e] * sl2);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // K0, V0, K1 landed (this wave's part)
     __syncthreads();                        // ... for every wave
@@ -255,12 +256,16 @@ extern "C" __global__ __launch_bounds__(512) void qm_gqa_prefill_attn(GqaPrefill
         }
     };
 
-    floatx4 O[16];
+    // O[0..15]: P V; O[16]: P times a ones B operand, i.e. the row sums of
+    // P (every column), in the same lane layout and rescaled with the rest
+    floatx4 O[17];
 #pragma unroll
-    for (int dt = 0; dt < 16; ++dt) O[dt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    float m_run = -INFINITY, l_run = 0.0f;
-    const float sl2 = (1.0f / 16.0f) * 1.4426950408889634f;     // 1/sqrt(256) * log2(e)
+    for (int dt = 0; dt < 17; ++dt) O[dt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_run = -INFINITY;
     const int tok = r0 + lr;
+    half8 ones;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ones[e] = (_Float16)1.0f;
 
     floatx4 sC[4];                          // scores of the tile being finished
     scores(sm + SM_K(0), sC, [](int) {});
@@ -277,19 +282,24 @@ extern "C" __global__ __launch_bounds__(512) void qm_gqa_prefill_attn(GqaPrefill
         // groups of tile kt+1's scores (computed on whatever K buffer b^1
         // holds on the last tile, and then discarded)
         const bool diag = k0 + KT - 1 > r0;     // tile reaches past the wave's first row
-        float mx = -INFINITY, m_new = 0.0f, corr = 1.0f, ps = 0.0f;
+        float mx = -INFINITY, m_new = 0.0f, corr = 1.0f;
         half8 pf[2];
         auto slice = [&](int grp) {
             if (grp == 0 || grp == 1) {
+                if (diag) {                     // wave-uniform: only diagonal tiles mask
 #pragma unroll
-                for (int kk = 2 * grp; kk < 2 * grp + 2; ++kk)
+                    for (int kk = 2 * grp; kk < 2 * grp + 2; ++kk)
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        float sc = sC[kk][e] * sl2;
-                        if (diag && k0 + frag_key(kk, 4 * lq + e) > tok) sc = -INFINITY;
-                        sC[kk][e] = sc;
-                        mx = fmaxf(mx, sc);
-                    }
+                        for (int e = 0; e < 4; ++e) {
+                            if (k0 + frag_key(kk, 4 * lq + e) > tok) sC[kk][e] = -INFINITY;
+                            mx = fmaxf(mx, sC[kk][e]);
+                        }
+                } else {
+#pragma unroll
+                    for (int kk = 2 * grp; kk < 2 * grp + 2; ++kk)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) mx = fmaxf(mx, sC[kk][e]);
+                }
             } else if (grp == 2) {
                 mx = max_xor32(max_xor16(mx));
                 // key 0 is visible to every row, so mx is finite from tile 0 on
@@ -299,16 +309,9 @@ extern "C" __global__ __launch_bounds__(512) void qm_gqa_prefill_attn(GqaPrefill
 #pragma unroll
                 for (int kk = 2 * (grp - 3); kk < 2 * (grp - 3) + 2; ++kk)
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float pv = __builtin_amdgcn_exp2f(sC[kk][e] - m_new);
-                        sC[kk][e] = pv;
-                        ps += pv;
-                    }
+                    for (int e = 0; e < 4; ++e) sC[kk][e] = __builtin_amdgcn_exp2f(sC[kk][e] - m_new);
+                if (grp == 4) m_run = m_new;
             } else if (grp == 5) {
-                ps = sum_xor32(sum_xor16(ps));
-                l_run = l_run * corr + ps;
-                m_run = m_new;
-            } else if (grp == 6) {
                 // A operand of PV k-step ks: keys 32 ks + 8 lq .. + 7 of row lr
 #pragma unroll
                 for (int ks = 0; ks < 2; ++ks)
@@ -325,16 +328,13 @@ extern "C" __global__ __launch_bounds__(512) void qm_gqa_prefill_attn(GqaPrefill
         // rescale O (lane (dim lr, lq) holds rows 4lq + e) when any row of
         // the wave moved its reference max
         if (__any(corr != 1.0f)) {
-            if (lq == 0) rowf[lr] = corr;
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            const float4 f = *reinterpret_cast<const float4*>(&rowf[4 * lq]);
+            float f[4];                     // row 4lq + e's factor sits in lane 4lq + e
 #pragma unroll
-            for (int dt = 0; dt < 16; ++dt) {
-                O[dt][0] *= f.x; O[dt][1] *= f.y; O[dt][2] *= f.z; O[dt][3] *= f.w;
+            for (int e = 0; e < 4; ++e) f[e] = __shfl(corr, 4 * lq + e);
+#pragma unroll
+            for (int dt = 0; dt < 17; ++dt) {
+                O[dt][0] *= f[0]; O[dt][1] *= f[1]; O[dt][2] *= f[2]; O[dt][3] *= f[3];
             }
-            __builtin_amdgcn_wave_barrier();
         }
         // O += P V   (16x16x32; B lane (dim, lq) holds keys 32 ks + 8 lq .. + 7),
         // V^T blocks read four at a time, one group ahead of the MFMAs
@@ -359,6 +359,8 @@ extern "C" __global__ __launch_bounds__(512) void qm_gqa_prefill_attn(GqaPrefill
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) O[16] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[ks], ones, O[16], 0, 0, 0);
         }
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) sC[kk] = sN[kk];
@@ -366,13 +368,11 @@ extern "C" __global__ __launch_bounds__(512) void qm_gqa_prefill_attn(GqaPrefill
         __syncthreads();                    // ... for every wave; this tile fully consumed
     }
 
-    // 3. out = (O / l) * sigmoid(gate), bf16 (gemv.rs:1441-1444)
-    if (lq == 0) rowf[lr] = 1.0f / l_run;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const float4 inv = *reinterpret_cast<const float4*>(&rowf[4 * lq]);
-    const float iv[4] = {inv.x, inv.y, inv.z, inv.w};
+    // 3. out = (O / l) * sigmoid(gate), bf16 (gemv.rs:1441-1444); O[16][e]
+    //    is row 4lq + e's sum of P, in this very lane
+    float iv[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) iv[e] = 1.0f / O[16][e];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int t = r0 + 4 * lq + e;
