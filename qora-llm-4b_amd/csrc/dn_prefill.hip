@@ -14,14 +14,14 @@
 //   S_C = gamma_C S0 + U^T diag(gamma_C/gamma) K.
 //
 // Three kernels:
-//   qm_dn_prefill_prep   conv1d + SiLU + L2 norm (+ q scale) + gates, one
-//                        workgroup per (chunk, 128-channel head);
 //   qm_dn_prefill_chunk  everything that does not depend on S0, fully
-//                        parallel over (chunk, v-head): KK^T / QK^T on MFMA,
-//                        [W | U~] by block forward substitution (16x16
-//                        diagonal inverses by substitution in fp32, the
-//                        off-diagonal corrections on MFMA), Q~ = diag(gamma)Q
-//                        - PW and Y0 = PU~, all products on f16 MFMA;
+//                        parallel over (chunk, v-head): the conv1d + SiLU +
+//                        L2 norm of the chunk's q, k, v and the gates into
+//                        LDS, KK^T / QK^T on MFMA, [W | U~] by block forward
+//                        substitution (16x16 diagonal inverses by
+//                        substitution in fp32, the off-diagonal corrections
+//                        on MFMA), Q~ = diag(gamma)Q - PW and Y0 = PU~, all
+//                        products on f16 MFMA;
 //   qm_dn_prefill_scan   the sequential part: one wave per (v-head, 16 state
 //                        rows) with its rows of the fp32 state in registers,
 //                        two f16 MFMA GEMMs per chunk; stores each chunk's
@@ -29,10 +29,6 @@
 //   qm_dn_prefill_out    Y = Y0 + Q~ S_c^T on MFMA, fully parallel over
 //                        (chunk, v-head), fused with the gated RMSNorm and
 //                        the conv buffer update.
-// The scan uses v_mfma_f32_16x16x16_f16 throughout because its fragment
-// layouts chain without lane shuffles: the state's C fragment (4 consecutive
-// k-cols per lane) is the B operand of U and Y, and U's C fragment (4
-// consecutive tokens per lane) is the B operand of the state update.
 #include "qm_device.h"
 #include "qm_kernel_args.h"
 
@@ -53,124 +49,6 @@ QM_DEV half4 to_half4(floatx4 v) {
 }
 
 // ============================================================================
-// 1. prep: causal conv1d (gemv.rs:1132-1147), SiLU (:1149), per-head L2 norm
-//    and q scale (:1151-1156), gates (:1171-1172).
-// ============================================================================
-// Thread (cg, tg) = (tid & 15, tid >> 4) owns channels 8cg .. 8cg+7 of the
-// head for tokens 4tg .. 4tg+3; the 16 lanes of a row share the tokens, so the
-// per-token L2 norm is a row reduction and every store writes whole 256-byte
-// rows.
-extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_prep(DnPrefillArgs A) {
-    const int tid = threadIdx.x;
-    const int c = blockIdx.x / 64, gi = blockIdx.x % 64;     // 64 heads of 128 channels
-    const int t0 = c * CHK;
-    const int tpad = A.nc * CHK;
-    {
-        const int cg = tid & 15, tg = tid >> 4;
-        const int ch0 = gi * 128 + 8 * cg;
-        // the 7 raw rows the thread needs, all loaded (at clamped, always
-        // valid rows) before any arithmetic; rows before the sequence come
-        // from the conv buffer, rows past it are zero
-        uint4 u[7];
-#pragma unroll
-        for (int r = 0; r < 7; ++r) {
-            const int t = min(max(t0 + 4 * tg - 3 + r, 0), A.T - 1);
-            u[r] = *reinterpret_cast<const uint4*>(A.qkv + (size_t)t * QM_DN_QKV_DIM + ch0);
-        }
-        float cb[3][8] = {};
-        if (c == 0) {                                            // x_{-3..-1}
-            asm volatile("" ::: "memory");   // keep these loads inside the branch
-#pragma unroll
-            for (int r = 0; r < 3; ++r) {
-                const int t = min(4 * tg - 3 + r, -1);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) cb[r][e] = A.conv_buf[(size_t)(ch0 + e) * 3 + 3 + t];
-            }
-        }
-        float x[7][8];
-#pragma unroll
-        for (int r = 0; r < 7; ++r) {
-            const int t = t0 + 4 * tg - 3 + r;
-            const uint32_t wv[4] = {u[r].x, u[r].y, u[r].z, u[r].w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                x[r][2 * e] = bf16_to_f32((uint16_t)(wv[e] & 0xffffu));
-                x[r][2 * e + 1] = bf16_to_f32((uint16_t)(wv[e] >> 16));
-            }
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                if (r < 3 && t < 0) x[r][e] = cb[r][e];
-                if (t >= A.T) x[r][e] = 0.0f;
-            }
-        }
-        float4 w[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) w[e] = ld4(A.conv_w + (size_t)(ch0 + e) * 4);
-        float scale = 1.0f;
-        uint16_t* base;
-        int rows;
-        if (gi < 32) {
-            scale = gi < 16 ? 1.0f / sqrtf((float)QM_DN_HD) : 1.0f;
-            base = (gi < 16 ? A.qh : A.kh) + (size_t)(gi & 15) * QM_DN_HD + 8 * cg;
-            rows = QM_DN_QK_HEADS;
-        } else {
-            base = A.vv + (size_t)(gi - 32) * QM_DN_HD + 8 * cg;
-            rows = QM_DN_V_HEADS;
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int tok = 4 * tg + j;
-            float v[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                // gemv.rs:1134-1139: taps oldest first, then the new token
-                float s = x[j][e] * w[e].x;
-                s = fmaf(x[j + 1][e], w[e].y, s);
-                s = fmaf(x[j + 2][e], w[e].z, s);
-                s = fmaf(x[j + 3][e], w[e].w, s);
-                v[e] = (t0 + tok < A.T) ? silu_fast(s) : 0.0f;
-            }
-            if (gi < 32) {
-                // x /= ||x|| when ||x|| > 1e-12, q *= 1/sqrt(128)
-                float ss = 0.0f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
-                ss = row_sum16(ss);
-                const float norm = sqrtf(ss);
-                const float inv = norm > 1e-12f ? 1.0f / norm : 1.0f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = (v[e] * inv) * scale;
-            }
-            half8 hv;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) hv[e] = (_Float16)v[e];
-            *reinterpret_cast<half8*>(base + (size_t)(t0 + tok) * rows * QM_DN_HD) = hv;
-        }
-    }
-
-    if (gi >= 32 && tid < 64) {
-        // log alpha = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b);
-        // padded tokens get alpha = 1, beta = 0 (no effect on the state).
-        const int vh = gi - 32, t = t0 + tid;
-        float g = 0.0f, be = 0.0f;
-        if (t < A.T) {
-            const float a_exp = expf(A.a_log[vh]);
-            const float sp = softplus_f(A.a[(size_t)t * QM_DN_V_HEADS + vh] + A.dt_bias[vh]);
-            g = -a_exp * sp;
-            be = 1.0f / (1.0f + expf(-A.b[(size_t)t * QM_DN_V_HEADS + vh]));
-        }
-        // inclusive prefix sum over the chunk's 64 tokens (one wave)
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const float o = __shfl_up(g, off);
-            if (tid >= off) g += o;
-        }
-        A.G[(size_t)vh * tpad + t] = g;
-        A.beta[(size_t)vh * tpad + t] = be;
-    }
-}
-
-// ============================================================================
 // 2. chunk: per (chunk, v-head), everything independent of the entering state
 // ============================================================================
 // [W | U~] = (I + A)^-1 [diag(beta gamma) K | diag(beta) V] is solved by block
@@ -183,51 +61,135 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_prep(DnPrefillAr
 // the B operand of the next block's correction, so the solve needs no
 // workgroup barrier.
 extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillArgs A) {
-    __shared__ _Float16 Ks[CHK][136];              // K row-major; later -W staging
-    __shared__ _Float16 Kt[QM_DN_HD][72];          // K^T
-    __shared__ _Float16 Vt[QM_DN_HD][72];          // V^T; later Q~ staging
+    __shared__ _Float16 Qs[CHK][136];              // q row-major; later Q~ staging
+    __shared__ _Float16 Ks[CHK][136];              // k row-major; later -W staging
+    __shared__ _Float16 Vs[CHK][136];              // v row-major
     __shared__ _Float16 Pm[CHK][72];               // P (lower, incl. diagonal)
     __shared__ _Float16 Am[CHK][72];               // A (strictly lower)
     __shared__ _Float16 Td[4][16][24];             // (I + A_bb)^-1
     __shared__ float Gs[CHK], Bs[CHK], Eg[CHK], BG[CHK], Kd[CHK];
-    _Float16 (*Qstage)[136] = reinterpret_cast<_Float16 (*)[136]>(&Vt[0][0]);
 
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int c = blockIdx.x / QM_DN_V_HEADS, h = blockIdx.x % QM_DN_V_HEADS;
-    const int qkh = h >> 1;
+    const int qkh = h >> 1;                        // GVA: v-head h reads qk-head h/2 (gemv.rs:1160)
     const int t0 = c * CHK;
-    const int tpad = A.nc * CHK;
     const size_t hc = (size_t)h * A.nc + c;
     const int lr = lane & 15, lq = lane >> 4;
-    const uint16_t* qbase = A.qh + ((size_t)t0 * QM_DN_QK_HEADS + qkh) * QM_DN_HD;   // row stride 16*128
 
-    // ---- 0. K (row-major and transposed), V (transposed), gates
+    // ---- 0. causal conv1d (gemv.rs:1132-1147), SiLU (:1149), per-head L2
+    //      norm and q scale (:1151-1156) of this chunk's q, k (qk-head h/2)
+    //      and v (v-head h), straight into LDS; gates (:1171-1172).
+    //      Thread (cg, tg) = (tid & 15, tid >> 4) owns channels 8cg .. 8cg+7
+    //      for tokens 4tg .. 4tg+3: the 16 lanes of a DPP row share the
+    //      tokens, so the L2 norm is a row reduction.
     {
-        const int i = tid >> 2, p = tid & 3;
-        const uint16_t* kr = A.kh + ((size_t)(t0 + i) * QM_DN_QK_HEADS + qkh) * QM_DN_HD + 32 * p;
-        const uint16_t* vr = A.vv + ((size_t)(t0 + i) * QM_DN_V_HEADS + h) * QM_DN_HD + 32 * p;
-        half8 kv[4], vv[4];
+        const int cg = tid & 15, tg = tid >> 4;
+        int chb[3];                                // first channel of this thread, per part
+        chb[0] = qkh * QM_DN_HD + 8 * cg;
+        chb[1] = QM_DN_QK_DIM + qkh * QM_DN_HD + 8 * cg;
+        chb[2] = 2 * QM_DN_QK_DIM + h * QM_DN_HD + 8 * cg;
+        // all 21 raw rows the thread needs (7 per part), loaded at clamped,
+        // always valid rows before any arithmetic; rows before the sequence
+        // come from the conv buffer, rows past it are zero
+        uint4 u[3][7];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            kv[q] = *reinterpret_cast<const half8*>(kr + 8 * q);
-            vv[q] = *reinterpret_cast<const half8*>(vr + 8 * q);
-        }
+        for (int part = 0; part < 3; ++part)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            *reinterpret_cast<half8*>(&Ks[i][32 * p + 8 * q]) = kv[q];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                Kt[32 * p + 8 * q + e][i] = kv[q][e];
-                Vt[32 * p + 8 * q + e][i] = vv[q][e];
+            for (int r = 0; r < 7; ++r) {
+                const int t = min(max(t0 + 4 * tg - 3 + r, 0), A.T - 1);
+                u[part][r] = *reinterpret_cast<const uint4*>(A.qkv + (size_t)t * QM_DN_QKV_DIM + chb[part]);
             }
+        float4 wt[8], wn[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) wt[e] = ld4(A.conv_w + (size_t)(chb[0] + e) * 4);
+#pragma unroll
+        for (int part = 0; part < 3; ++part) {     // q, k, v
+            const int ch0 = chb[part];
+            if (part < 2) {                        // next part's taps while this one computes
+#pragma unroll
+                for (int e = 0; e < 8; ++e) wn[e] = ld4(A.conv_w + (size_t)(chb[part + 1] + e) * 4);
+            }
+            float cb[3][8] = {};
+            if (c == 0) {                                        // x_{-3..-1}
+                asm volatile("" ::: "memory");   // keep these loads inside the branch
+#pragma unroll
+                for (int r = 0; r < 3; ++r) {
+                    const int t = min(4 * tg - 3 + r, -1);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) cb[r][e] = A.conv_buf[(size_t)(ch0 + e) * 3 + 3 + t];
+                }
+            }
+            float x[7][8];
+#pragma unroll
+            for (int r = 0; r < 7; ++r) {
+                const int t = t0 + 4 * tg - 3 + r;
+                const uint32_t wv[4] = {u[part][r].x, u[part][r].y, u[part][r].z, u[part][r].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    x[r][2 * e] = bf16_to_f32((uint16_t)(wv[e] & 0xffffu));
+                    x[r][2 * e + 1] = bf16_to_f32((uint16_t)(wv[e] >> 16));
+                }
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    if (r < 3 && t < 0) x[r][e] = cb[r][e];
+                    if (t >= A.T) x[r][e] = 0.0f;
+                }
+            }
+            _Float16 (*dst)[136] = part == 0 ? Qs : part == 1 ? Ks : Vs;
+            const float scale = part == 0 ? 1.0f / sqrtf((float)QM_DN_HD) : 1.0f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int tok = 4 * tg + j;
+                float v[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    // gemv.rs:1134-1139: taps oldest first, then the new token
+                    float sacc = x[j][e] * wt[e].x;
+                    sacc = fmaf(x[j + 1][e], wt[e].y, sacc);
+                    sacc = fmaf(x[j + 2][e], wt[e].z, sacc);
+                    sacc = fmaf(x[j + 3][e], wt[e].w, sacc);
+                    v[e] = (t0 + tok < A.T) ? silu_fast(sacc) : 0.0f;
+                }
+                if (part < 2) {
+                    // x /= ||x|| when ||x|| > 1e-12, q *= 1/sqrt(128)
+                    float ss = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
+                    ss = row_sum16(ss);
+                    const float norm = sqrtf(ss);
+                    const float inv = norm > 1e-12f ? 1.0f / norm : 1.0f;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[e] = (v[e] * inv) * scale;
+                }
+                half8 hv;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) hv[e] = (_Float16)v[e];
+                *reinterpret_cast<half8*>(&dst[tok][8 * cg]) = hv;
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) wt[e] = wn[e];
         }
         if (tid < CHK) {
-            const float gg = A.G[(size_t)h * tpad + t0 + tid];
-            const float bb = A.beta[(size_t)h * tpad + t0 + tid];
-            Gs[tid] = gg;
-            Bs[tid] = bb;
-            Eg[tid] = expf(gg);                  // gamma_i
-            BG[tid] = bb * expf(gg);             // beta_i gamma_i
+            // log alpha = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b);
+            // padded tokens get alpha = 1, beta = 0 (no effect on the state);
+            // then the inclusive prefix sum over the chunk (one wave)
+            const int t = t0 + tid;
+            float g = 0.0f, be = 0.0f;
+            if (t < A.T) {
+                const float a_exp = expf(A.a_log[h]);
+                const float sp = softplus_f(A.a[(size_t)t * QM_DN_V_HEADS + h] + A.dt_bias[h]);
+                g = -a_exp * sp;
+                be = 1.0f / (1.0f + expf(-A.b[(size_t)t * QM_DN_V_HEADS + h]));
+            }
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const float o = __shfl_up(g, off);
+                if (tid >= off) g += o;
+            }
+            Gs[tid] = g;
+            Bs[tid] = be;
+            Eg[tid] = expf(g);                   // gamma_i
+            BG[tid] = be * expf(g);              // beta_i gamma_i
         }
     }
     __syncthreads();
@@ -238,8 +200,7 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
         const int i0 = 16 * w;
         half8 aq[4];
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
-            aq[s] = *reinterpret_cast<const half8*>(qbase + (size_t)(i0 + lr) * QM_DN_QK_HEADS * QM_DN_HD + 32 * s + 8 * lq);
+        for (int s = 0; s < 4; ++s) aq[s] = *reinterpret_cast<const half8*>(&Qs[i0 + lr][32 * s + 8 * lq]);
         for (int j = 0; j < 4; ++j) {
             if (j > w) {
 #pragma unroll
@@ -301,7 +262,7 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int tk = 16 * b + 4 * lq + e;
-                r[e] = cc < 2 ? BG[tk] * (float)Kt[col][tk] : Bs[tk] * (float)Vt[col][tk];
+                r[e] = cc < 2 ? BG[tk] * (float)Ks[tk][col] : Bs[tk] * (float)Vs[tk][col];
             }
 #pragma unroll
             for (int k = 0; k < b; ++k) {
@@ -326,8 +287,7 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int tk = 16 * i + 4 * lq + e;
-                const uint16_t qb = qbase[(size_t)tk * QM_DN_QK_HEADS * QM_DN_HD + col];
-                cq[i][cc][e] = Eg[tk] * f16_to_f32(qb);
+                cq[i][cc][e] = Eg[tk] * (float)Qs[tk][col];
             }
             cy[i][cc] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
         }
@@ -373,14 +333,14 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
             half8 hv;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                hv[e] = (_Float16)((float)Kt[row][tk0 + e] * Kd[tk0 + e]);
-                hv[4 + e] = (_Float16)((float)Kt[row][tk0 + 16 + e] * Kd[tk0 + 16 + e]);
+                hv[e] = (_Float16)((float)Ks[tk0 + e][row] * Kd[tk0 + e]);
+                hv[4 + e] = (_Float16)((float)Ks[tk0 + 16 + e][row] * Kd[tk0 + 16 + e]);
             }
             *reinterpret_cast<half8*>(dst + (size_t)q * 8) = hv;
         }
     }
     if (tid == 0) A.gC[hc] = expf(Gs[CHK - 1]);
-    __syncthreads();     // Ks and Vt are free: stage -W and Q~ token-major
+    __syncthreads();     // Ks and Qs are free: stage -W and Q~ token-major
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -390,7 +350,7 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
             for (int e = 0; e < 4; ++e) {
                 const int tk = 16 * i + 4 * lq + e;
                 Ks[tk][col] = (_Float16)(-cw[i][cc][e]);
-                Qstage[tk][col] = (_Float16)cq[i][cc][e];
+                Qs[tk][col] = (_Float16)cq[i][cc][e];
             }
         }
     __syncthreads();
@@ -403,8 +363,8 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
             const int row = 16 * i + (l & 15), c0 = 32 * p + 4 * (l >> 4);
             const half4 w0 = *reinterpret_cast<const half4*>(&Ks[row][c0]);
             const half4 w1 = *reinterpret_cast<const half4*>(&Ks[row][c0 + 16]);
-            const half4 q0 = *reinterpret_cast<const half4*>(&Qstage[row][c0]);
-            const half4 q1 = *reinterpret_cast<const half4*>(&Qstage[row][c0 + 16]);
+            const half4 q0 = *reinterpret_cast<const half4*>(&Qs[row][c0]);
+            const half4 q1 = *reinterpret_cast<const half4*>(&Qs[row][c0 + 16]);
             *reinterpret_cast<half8*>(wdst + (size_t)q * 8) = half8{w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
             *reinterpret_cast<half8*>(qdst + (size_t)q * 8) = half8{q0[0], q0[1], q0[2], q0[3], q1[0], q1[1], q1[2], q1[3]};
         }

@@ -10,6 +10,7 @@
 #define QM_DN_HD         128
 #define QM_DN_CONV_K     4
 #define QM_DN_QKV_DIM    8192      // 2*16*128 + 32*128
+#define QM_DN_QK_DIM     2048      // 16*128: q (and k) part of qkv
 #define QM_DN_V_DIM      4096
 #define QM_DN_HEAD_ELEMS 16384     // 128*128 state floats per v-head
 #define QM_GQA_HEADS     16
@@ -63,10 +64,8 @@ struct GqaDecodeArgs {
     int32_t batch;
 };
 
-// DeltaNet chunked prefill (chunk 64).  Workspace tensors, T_pad = 64 * nc:
-//   qh, kh  f16 [T_pad][16][128]   L2-normed q (times 1/sqrt(128)) and k
-//   vv      f16 [T_pad][32][128]   activated v
-//   G, beta f32 [32][T_pad]        within-chunk cumulative log decay, beta
+// DeltaNet chunked prefill (chunk 64).  Workspace tensors, per (v-head,
+// chunk) block, nc = ceil(T / 64):
 //   Wn, Qt  f16 [32][nc][8192]     -W = -T diag(beta*gamma) K and
 //                                   Q~ = diag(gamma) Q - P W
 //   Ut, Y0t f16 [32][nc][8192]     U~ = T diag(beta) V and Y0 = P U~
@@ -88,11 +87,6 @@ struct DnPrefillArgs {
     const uint16_t* norm_w;  // f16 [128]
     float* state;            // [32][128][128]
     uint16_t* out;           // bf16 [T][4096]
-    uint16_t* qh;
-    uint16_t* kh;
-    uint16_t* vv;
-    float* G;
-    float* beta;
     uint16_t* Wn;
     uint16_t* Qt;
     uint16_t* Ut;

@@ -39,7 +39,6 @@ struct qm_context {
     hipFunction_t f_gqa_split = nullptr;
     hipFunction_t f_gqa_merge = nullptr;
     hipFunction_t f_fill = nullptr;
-    hipFunction_t f_dnp_prep = nullptr;
     hipFunction_t f_dnp_chunk = nullptr;
     hipFunction_t f_dnp_scan = nullptr;
     hipFunction_t f_dnp_out = nullptr;
@@ -153,19 +152,14 @@ int32_t load_function(qm_context* c, hipModule_t m, const char* name, hipFunctio
 
 namespace {
 struct DnPrefillLayout {
-    size_t qh, kh, vv, G, beta, Wn, Qt, Ut, Y0t, Ktt, gC, Sc, total;
+    size_t Wn, Qt, Ut, Y0t, Ktt, gC, Sc, total;
 };
 
 DnPrefillLayout dn_prefill_layout(int64_t T) {
-    const int64_t nc = (T + QM_DN_CHUNK - 1) / QM_DN_CHUNK, tpad = nc * QM_DN_CHUNK;
+    const int64_t nc = (T + QM_DN_CHUNK - 1) / QM_DN_CHUNK;
     auto al = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
     DnPrefillLayout L{};
     size_t o = 0;
-    L.qh = o; o += al(static_cast<size_t>(tpad) * QM_DN_QK_HEADS * QM_DN_HD * 2);
-    L.kh = o; o += al(static_cast<size_t>(tpad) * QM_DN_QK_HEADS * QM_DN_HD * 2);
-    L.vv = o; o += al(static_cast<size_t>(tpad) * QM_DN_V_HEADS * QM_DN_HD * 2);
-    L.G = o; o += al(static_cast<size_t>(tpad) * QM_DN_V_HEADS * 4);
-    L.beta = o; o += al(static_cast<size_t>(tpad) * QM_DN_V_HEADS * 4);
     const size_t blk = static_cast<size_t>(QM_DN_V_HEADS) * nc * QM_DN_CHUNK * QM_DN_HD * 2;
     L.Wn = o; o += al(blk);
     L.Qt = o; o += al(blk);
@@ -265,7 +259,6 @@ int32_t qm_create(qm_context** out, const qm_config* cfg, const char* code_objec
     if (st == QM_OK) st = load_function(c, mods[1], "qm_gqa_decode_split", &c->f_gqa_split);
     if (st == QM_OK) st = load_function(c, mods[1], "qm_gqa_decode_merge", &c->f_gqa_merge);
     if (st == QM_OK) st = load_function(c, mods[2], "qm_fill_normal", &c->f_fill);
-    if (st == QM_OK) st = load_function(c, mods[3], "qm_dn_prefill_prep", &c->f_dnp_prep);
     if (st == QM_OK) st = load_function(c, mods[3], "qm_dn_prefill_chunk", &c->f_dnp_chunk);
     if (st == QM_OK) st = load_function(c, mods[3], "qm_dn_prefill_scan", &c->f_dnp_scan);
     if (st == QM_OK) st = load_function(c, mods[3], "qm_dn_prefill_out", &c->f_dnp_out);
@@ -607,14 +600,10 @@ int32_t qm_deltanet_prefill(qm_context* c, qm_stream stream, int32_t seq_len, co
     char* ws = static_cast<char*>(c->ws);
     const int32_t nc = (seq_len + QM_DN_CHUNK - 1) / QM_DN_CHUNK;
     DnPrefillArgs pa{qkv, conv_buf, conv_w, a, b, a_log, dt_bias, z, norm_w, state, out,
-                     reinterpret_cast<uint16_t*>(ws + L.qh), reinterpret_cast<uint16_t*>(ws + L.kh),
-                     reinterpret_cast<uint16_t*>(ws + L.vv), reinterpret_cast<float*>(ws + L.G),
-                     reinterpret_cast<float*>(ws + L.beta), reinterpret_cast<uint16_t*>(ws + L.Wn),
+                     reinterpret_cast<uint16_t*>(ws + L.Wn),
                      reinterpret_cast<uint16_t*>(ws + L.Qt), reinterpret_cast<uint16_t*>(ws + L.Ut),
                      reinterpret_cast<uint16_t*>(ws + L.Y0t), reinterpret_cast<uint16_t*>(ws + L.Ktt),
                      reinterpret_cast<float*>(ws + L.gC), reinterpret_cast<uint16_t*>(ws + L.Sc), seq_len, nc};
-    st = launch(c, c->f_dnp_prep, static_cast<uint32_t>(nc) * 64, 256, pa, s, "qm_dn_prefill_prep");
-    if (st != QM_OK) return st;
     st = launch(c, c->f_dnp_chunk, static_cast<uint32_t>(nc) * QM_DN_V_HEADS, 256, pa, s, "qm_dn_prefill_chunk");
     if (st != QM_OK) return st;
     st = launch(c, c->f_dnp_scan, QM_DN_V_HEADS * 8, 64, pa, s, "qm_dn_prefill_scan");
