@@ -13,6 +13,8 @@ Workloads (synthetic, seeded; inputs resident in HBM before timing):
               fp32 state), one step = one prefill call.
   gqa_prefill one GQA layer, causal prefill of 8192 tokens (bf16 in, f16 KV
               cache written), one step = one prefill call.
+--gqa-chunk N sets the keys per GQA decode split workgroup (default: the
+library's choice).
 Prints one JSON line with throughput, the dominant kernel's roofline
 position (average launch time from HIP events on the launch stream) and the
 CPU oracle timed on this host on a bounded sample of the same workload.
@@ -533,6 +535,8 @@ def main():
     ap.add_argument("--workload", default="stack",
                     choices=["stack", "dn_decode", "gqa_decode", "dn_prefill", "gqa_prefill"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--gqa-chunk", type=int, default=0,
+                    help="keys per GQA decode split workgroup (multiple of 64; 0 = the library's choice)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="before timing, copy 1 GiB device-to-device once (a dispatch of known "
                          "traffic for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -547,6 +551,8 @@ def main():
     args.warmup = defaults[1] if args.warmup is None else args.warmup
 
     ctx = M.Context(0)
+    if args.gqa_chunk:
+        ctx.set_option(M.QM_OPT_GQA_DECODE_CHUNK, args.gqa_chunk)
     if args.calibrate_copy:
         src, dst = ctx.alloc(1 << 30), ctx.alloc(1 << 30)
         ctx.fill_normal(src, M.QM_F32, (1 << 30) // 4, 0.0, 1.0, 7)
