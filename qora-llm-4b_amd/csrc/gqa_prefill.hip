@@ -7,11 +7,11 @@
 //
 // qm_gqa_prefill_kv    K norm + RoPE -> f16 K cache; V -> f16 V cache and a
 //                      transposed f16 copy V^T (keys contiguous per dim).
-// qm_gqa_prefill_attn  flash attention on MFMA.  A workgroup owns 32 query
-//                      tokens of all four query heads of one kv group (8
-//                      waves: head 4g + (w & 3), 16 rows each, two waves per
-//                      SIMD), so every K / V tile staged in LDS feeds four
-//                      heads.  Scores are computed transposed,
+// qm_gqa_prefill_attn  flash attention on MFMA.  A workgroup owns 48 query
+//                      tokens of all four query heads of one kv group (12
+//                      waves: head 4g + (w & 3), 16 rows each, three waves
+//                      per SIMD), so every K / V tile staged in LDS feeds
+//                      four heads.  Scores are computed transposed,
 //                      S^T = K Q^T (keys x rows), with v_mfma_f32_16x16x32:
 //                      a lane of an S^T fragment then holds four consecutive
 //                      keys of one row, which is exactly what the PV product
@@ -22,8 +22,7 @@
 //                      shuffles between the two products.  Online softmax in
 //                      base 2, fp32, with a lazily moved reference max.  K / V
 //                      tiles are double-buffered in LDS and copied there by
-//                      LDS DMA ahead of use; the scores of the next tile run
-//                      on MFMA while the current tile's softmax runs.
+//                      LDS DMA one tile ahead of use.
 #include "qm_device.h"
 #include "qm_kernel_args.h"
 #include "qm_gqa_common.h"
@@ -37,7 +36,6 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 // by more than this (log2 units), so P = 2^(s - m) <= 2^8 stays exact enough
 // in f16 and the O accumulators are rescaled only when a row's max jumps.
 #define RESCALE_SLACK 8.0f
-#define TQ 32          // query tokens per workgroup
 
 QM_DEV float4 bf16x4_to_f32(uint2 u) {
     return make_float4(bf16_to_f32((uint16_t)(u.x & 0xffffu)), bf16_to_f32((uint16_t)(u.x >> 16)),
@@ -129,48 +127,49 @@ QM_DEV void dma16(const void* gsrc, uint32_t lds) {
 }
 #pragma clang diagnostic pop
 
-// The loop is software-pipelined over tiles: iteration kt computes the
-// scores of tile kt+1 on MFMA while the VALU runs tile kt's softmax in
-// slices between the MFMA groups, then accumulates tile kt's P V.  K tiles
-// are fetched two ahead, V tiles one ahead.
-extern "C" __global__ __launch_bounds__(512) void qm_gqa_prefill_attn(GqaPrefillArgs A) {
+// A workgroup owns 48 query rows of the four query heads of one kv group:
+// 12 waves, wave w on head 4g + (w & 3) and rows 16 (w >> 2) .. +15, three
+// waves per SIMD, so one wave's LDS and softmax latency hides behind the
+// other waves' MFMAs.  Each iteration fetches the next K / V^T tile by LDS
+// DMA (the tile's 64 blocks dealt round-robin over the waves), then computes
+// the current tile's scores, softmax and P V.
+#define TQ3 48
+
+extern "C" __global__ __launch_bounds__(768) void qm_gqa_prefill_attn(GqaPrefillArgs A) {
     __shared__ __attribute__((aligned(1024))) char sm[SM_BYTES];
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 15, lq = lane >> 4;
     const int g = blockIdx.x % QM_GQA_KV_HEADS;
-    const int nblk = A.s_pad / TQ;
+    const int nblk = (A.S + TQ3 - 1) / TQ3;
     const int tb = nblk - 1 - (int)(blockIdx.x / QM_GQA_KV_HEADS);   // longest rows first
-    const int t0 = tb * TQ;
-    // wave w: query head 4g + (w & 3), rows r0 .. r0+15 of the block
+    const int t0 = tb * TQ3;
     const int qh = 4 * g + (w & 3);
     const int r0 = t0 + 16 * (w >> 2);
-    const int nkt = (t0 + TQ + KT - 1) / KT;
+    // tiles up to the block's last row, within the zero-padded V^T copy
+    const int nkt = min((t0 + TQ3 + KT - 1) / KT, A.s_pad / KT);
     const uint32_t sm_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)sm;
 
-    // tile fetch: wave w moves blocks 4w .. 4w+3 of the K and of the V^T tile
+    // tile fetch: block b = w + 12 j of the tile's 64 (K blocks 0..31, V^T 32..63)
     const uint16_t* kbase = A.k_cache + (size_t)g * A.cap * QM_GQA_HD;
     const uint16_t* vbase = A.vt + (size_t)g * QM_GQA_HD * A.s_pad;
-    auto fetch_k = [&](int kt, int buf) {
+    auto fetch = [&](int kt, int buf) {
         const int k0 = kt * KT;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int b = 4 * w + j, kk = b >> 3, s = b & 7;       // K block: S^T fragment kk, k-step s
-            const int key = min(k0 + frag_key(kk, lr), A.S - 1);  // rows past S feed masked scores only
-            dma16(kbase + (size_t)key * QM_GQA_HD + 32 * s + 8 * lq, sm_lds + SM_K(buf) + 1024 * b);
+        for (int j = 0; j < 6; ++j) {
+            const int b = w + 12 * j;
+            if (b < 32) {
+                const int kk = b >> 3, s = b & 7;                  // K block: S^T fragment kk, k-step s
+                const int key = min(k0 + frag_key(kk, lr), A.S - 1);  // rows past S feed masked scores only
+                dma16(kbase + (size_t)key * QM_GQA_HD + 32 * s + 8 * lq, sm_lds + SM_K(buf) + 1024 * b);
+            } else if (b < 64) {
+                const int dt = (b - 32) >> 1, ks = b & 1;          // V^T block: dims tile dt, keys step ks
+                dma16(vbase + (size_t)(16 * dt + lr) * A.s_pad + k0 + 32 * ks + 8 * lq,
+                      sm_lds + SM_V(buf) + 1024 * (b - 32));
+            }
         }
     };
-    auto fetch_v = [&](int kt, int buf) {
-        const int k0 = kt * KT;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int b = 4 * w + j, dt = b >> 1, ks = b & 1;      // V^T block: dims tile dt, keys step ks
-            dma16(vbase + (size_t)(16 * dt + lr) * A.s_pad + k0 + 32 * ks + 8 * lq, sm_lds + SM_V(buf) + 1024 * b);
-        }
-    };
-    fetch_k(0, 0);                           // in flight during the q prep
-    fetch_v(0, 0);
-    if (nkt > 1) fetch_k(1, 1);
+    fetch(0, 0);                             // in flight during the q prep
 
     // 1. q: RMSNorm (1+gamma, eps 1e-6; gemv.rs:586-597) and split-half RoPE
     //    (gemv.rs:604-627) straight into the B fragments: lane (lr, lq) holds
@@ -182,79 +181,66 @@ extern "C" __global__ __launch_bounds__(512) void qm_gqa_prefill_attn(GqaPrefill
         const int t = r0 + lr;
         const int tc = min(t, A.S - 1);     // rows past S: any valid row, then zeroed
         const uint16_t* qrow = A.q_gate + ((size_t)tc * QM_GQA_HEADS + qh) * (2 * QM_GQA_HD) + 8 * lq;
-        float x[8][8];
+        uint4 u[8];                         // the row's 64 dims of this lane, packed bf16
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            u[s] = *reinterpret_cast<const uint4*>(qrow + 32 * s);
+            if (t >= A.S) u[s] = make_uint4(0, 0, 0, 0);
+        }
+        auto unpack = [](uint4 v, float (&x)[8]) {
+            const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                x[2 * e] = bf16_to_f32((uint16_t)(wv[e] & 0xffffu));
+                x[2 * e + 1] = bf16_to_f32((uint16_t)(wv[e] >> 16));
+            }
+        };
         float ss = 0.0f;
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-            const uint4 u = *reinterpret_cast<const uint4*>(qrow + 32 * s);
-            const uint32_t wv[4] = {u.x, u.y, u.z, u.w};
+            float x[8];
+            unpack(u[s], x);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                x[s][2 * e] = t < A.S ? bf16_to_f32((uint16_t)(wv[e] & 0xffffu)) : 0.0f;
-                x[s][2 * e + 1] = t < A.S ? bf16_to_f32((uint16_t)(wv[e] >> 16)) : 0.0f;
-            }
-#pragma unroll
-            for (int e = 0; e < 8; ++e) ss = fmaf(x[s][e], x[s][e], ss);
+            for (int e = 0; e < 8; ++e) ss = fmaf(x[e], x[e], ss);
         }
         ss = sum_xor32(sum_xor16(ss));
         const float inv = 1.0f / sqrtf(ss / (float)QM_GQA_HD + 1e-6f);
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
+        // the softmax scale 1/sqrt(256) in base 2 is folded into q, so the
+        // scores come out of the MFMA in log2 units
+        const float sl2 = (1.0f / 16.0f) * 1.4426950408889634f;
+        auto normed = [&](int s, float (&x)[8]) {     // x * inv * (1 + gamma)
+            unpack(u[s], x);
             const uint4 gw = *reinterpret_cast<const uint4*>(A.q_norm + 32 * s + 8 * lq);
             const uint32_t gv[4] = {gw.x, gw.y, gw.z, gw.w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                x[s][2 * e] = x[s][2 * e] * inv * (1.0f + f16_to_f32((uint16_t)(gv[e] & 0xffffu)));
-                x[s][2 * e + 1] = x[s][2 * e + 1] * inv * (1.0f + f16_to_f32((uint16_t)(gv[e] >> 16)));
+                x[2 * e] = x[2 * e] * inv * (1.0f + f16_to_f32((uint16_t)(gv[e] & 0xffffu)));
+                x[2 * e + 1] = x[2 * e + 1] * inv * (1.0f + f16_to_f32((uint16_t)(gv[e] >> 16)));
+            }
+        };
+        {
+            float x1[8], x2[8];
+            normed(0, x1);
+            normed(1, x2);
+            const float* crow = A.rope_cos + (size_t)tc * 32 + 8 * lq;
+            const float* srow = A.rope_sin + (size_t)tc * 32 + 8 * lq;
+            const float4 c0 = ld4(crow), c1 = ld4(crow + 4), s0 = ld4(srow), s1 = ld4(srow + 4);
+            const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+            const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                qf[0][e] = (_Float16)((x1[e] * cs[e] - x2[e] * sn[e]) * sl2);
+                qf[1][e] = (_Float16)((x2[e] * cs[e] + x1[e] * sn[e]) * sl2);
             }
         }
-        const float* crow = A.rope_cos + (size_t)tc * 32 + 8 * lq;
-        const float* srow = A.rope_sin + (size_t)tc * 32 + 8 * lq;
-        const float4 c0 = ld4(crow), c1 = ld4(crow + 4), s0 = ld4(srow), s1 = ld4(srow + 4);
-        const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-        const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float x1 = x[0][e], x2 = x[1][e];
-            x[0][e] = x1 * cs[e] - x2 * sn[e];
-            x[1][e] = x2 * cs[e] + x1 * sn[e];
+        for (int s = 2; s < 8; ++s) {
+            float x[8];
+            normed(s, x);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qf[s][e] = (_Float16)(x[e] * sl2);
         }
-        // the softmax scale 1/sqrt(256) in base 2 is folded into q, so the
-        // scores come out of the MFMA in log2 units
-        const float sl2 = (1.0f / 16.0f) * 1.4426950408889634f;
-#pragma unroll
-        for (int s = 0; s < 8; ++s)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) qf[s][e] = (_Float16)(x[s][e] * sl2);
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // K0, V0, K1 landed (this wave's part)
-    __syncthreads();                        // ... for every wave
-
-    // S^T = K Q^T of one tile: fragment kk row i is key frag_key(kk, i); K
-    // blocks are read four at a time, one group ahead of their MFMAs, and
-    // slice(grp) runs after MFMA group grp
-    auto scores = [&](const char* Kb, floatx4 (&sT)[4], auto&& slice) {
-        half8 ka[2][4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) ka[0][j] = *reinterpret_cast<const half8*>(Kb + j * 1024 + 16 * lane);
-#pragma unroll
-        for (int grp = 0; grp < 8; ++grp) {          // group = (kk, half of s)
-            const int cur = grp & 1;
-            if (grp + 1 < 8) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    ka[cur ^ 1][j] = *reinterpret_cast<const half8*>(Kb + (4 * (grp + 1) + j) * 1024 + 16 * lane);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            const int kk = grp >> 1, s0 = 4 * (grp & 1);
-            if ((grp & 1) == 0) sT[kk] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                sT[kk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[cur][j], qf[s0 + j], sT[kk], 0, 0, 0);
-            slice(grp);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    };
 
     // O[0..15]: P V; O[16]: P times a ones B operand, i.e. the row sums of
     // P (every column), in the same lane layout and rescaled with the rest
@@ -267,64 +253,68 @@ extern "C" __global__ __launch_bounds__(512) void qm_gqa_prefill_attn(GqaPrefill
 #pragma unroll
     for (int e = 0; e < 8; ++e) ones[e] = (_Float16)1.0f;
 
-    floatx4 sC[4];                          // scores of the tile being finished
-    scores(sm + SM_K(0), sC, [](int) {});
-    __syncthreads();                        // every wave is done with K buffer 0
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // tile 0 landed (this wave's part)
+    __syncthreads();                        // ... for every wave
 
     for (int kt = 0; kt < nkt; ++kt) {
         const int k0 = kt * KT, b = kt & 1;
-        // K(kt) was consumed by the previous iteration's scores, V(kt-1) by
-        // its P V: both buffers are free since the barrier that ended it
-        if (kt + 2 < nkt) fetch_k(kt + 2, b);
-        if (kt + 1 < nkt) fetch_v(kt + 1, b ^ 1);
+        // the other buffer was last read before the previous barrier
+        if (kt + 1 < nkt) fetch(kt + 1, b ^ 1);
+        const char* Kb = sm + SM_K(b);
+        const char* Vb = sm + SM_V(b);
 
-        // online softmax of tile kt (base 2), in slices between the MFMA
-        // groups of tile kt+1's scores (computed on whatever K buffer b^1
-        // holds on the last tile, and then discarded)
-        const bool diag = k0 + KT - 1 > r0;     // tile reaches past the wave's first row
-        float mx = -INFINITY, m_new = 0.0f, corr = 1.0f;
-        half8 pf[2];
-        auto slice = [&](int grp) {
-            if (grp == 0 || grp == 1) {
-                if (diag) {                     // wave-uniform: only diagonal tiles mask
+        // S^T = K Q^T: fragment kk row i is key frag_key(kk, i) of the tile;
+        // K blocks read two at a time, one pair ahead of their MFMAs
+        floatx4 sT[4];
+        {
+            half8 ka[2][2];
 #pragma unroll
-                    for (int kk = 2 * grp; kk < 2 * grp + 2; ++kk)
+            for (int j = 0; j < 2; ++j) ka[0][j] = *reinterpret_cast<const half8*>(Kb + j * 1024 + 16 * lane);
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            if (k0 + frag_key(kk, 4 * lq + e) > tok) sC[kk][e] = -INFINITY;
-                            mx = fmaxf(mx, sC[kk][e]);
-                        }
-                } else {
+            for (int grp = 0; grp < 16; ++grp) {         // pair = blocks 2grp, 2grp+1 = (kk, s)
+                const int cur = grp & 1;
+                if (grp + 1 < 16) {
 #pragma unroll
-                    for (int kk = 2 * grp; kk < 2 * grp + 2; ++kk)
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) mx = fmaxf(mx, sC[kk][e]);
+                    for (int j = 0; j < 2; ++j)
+                        ka[cur ^ 1][j] = *reinterpret_cast<const half8*>(Kb + (2 * (grp + 1) + j) * 1024 + 16 * lane);
                 }
-            } else if (grp == 2) {
-                mx = max_xor32(max_xor16(mx));
-                // key 0 is visible to every row, so mx is finite from tile 0 on
-                m_new = mx > m_run + RESCALE_SLACK ? mx : m_run;
-                corr = __builtin_amdgcn_exp2f(m_run - m_new);        // 1 unless moved; 0 on tile 0
-            } else if (grp == 3 || grp == 4) {
+                const int kk = grp >> 2, s0 = 2 * (grp & 3);
+                if ((grp & 3) == 0) sT[kk] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int kk = 2 * (grp - 3); kk < 2 * (grp - 3) + 2; ++kk)
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) sC[kk][e] = __builtin_amdgcn_exp2f(sC[kk][e] - m_new);
-                if (grp == 4) m_run = m_new;
-            } else if (grp == 5) {
-                // A operand of PV k-step ks: keys 32 ks + 8 lq .. + 7 of row lr
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        pf[ks][e] = (_Float16)sC[2 * ks][e];
-                        pf[ks][4 + e] = (_Float16)sC[2 * ks + 1][e];
-                    }
+                for (int j = 0; j < 2; ++j)
+                    sT[kk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[cur][j], qf[s0 + j], sT[kk], 0, 0, 0);
             }
-        };
-        floatx4 sN[4];
-        scores(sm + SM_K(b ^ 1), sN, slice);
-
+        }
+        // online softmax (base 2); only tiles that reach past the wave's
+        // first row need the causal mask
+        float mx = -INFINITY;
+        if (k0 + KT - 1 > r0) {                 // wave-uniform
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (k0 + frag_key(kk, 4 * lq + e) > tok) sT[kk][e] = -INFINITY;
+                    mx = fmaxf(mx, sT[kk][e]);
+                }
+        } else {
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) mx = fmaxf(mx, sT[kk][e]);
+        }
+        mx = max_xor32(max_xor16(mx));
+        // key 0 is visible to every row, so mx is finite from tile 0 on
+        const float m_new = mx > m_run + RESCALE_SLACK ? mx : m_run;
+        const float corr = __builtin_amdgcn_exp2f(m_run - m_new);      // 1 unless moved; 0 on tile 0
+        m_run = m_new;
+        half8 pf[2];                            // PV A operand: keys 32 ks + 8 lq .. + 7 of row lr
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                pf[ks][e] = (_Float16)__builtin_amdgcn_exp2f(sT[2 * ks][e] - m_new);
+                pf[ks][4 + e] = (_Float16)__builtin_amdgcn_exp2f(sT[2 * ks + 1][e] - m_new);
+            }
         // rescale O (lane (dim lr, lq) holds rows 4lq + e) when any row of
         // the wave moved its reference max
         if (__any(corr != 1.0f)) {
@@ -337,34 +327,27 @@ extern "C" __global__ __launch_bounds__(512) void qm_gqa_prefill_attn(GqaPrefill
             }
         }
         // O += P V   (16x16x32; B lane (dim, lq) holds keys 32 ks + 8 lq .. + 7),
-        // V^T blocks read four at a time, one group ahead of the MFMAs
+        // V^T blocks read two at a time, one pair ahead of the MFMAs
         {
-            const char* Vb = sm + SM_V(b);
-            half8 vb[2][4];
+            half8 vb[2][2];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) vb[0][j] = *reinterpret_cast<const half8*>(Vb + j * 1024 + 16 * lane);
+            for (int j = 0; j < 2; ++j) vb[0][j] = *reinterpret_cast<const half8*>(Vb + j * 1024 + 16 * lane);
 #pragma unroll
-            for (int grp = 0; grp < 8; ++grp) {          // group = dims tiles 2grp, 2grp+1
-                const int cur = grp & 1;
-                if (grp + 1 < 8) {
+            for (int dt = 0; dt < 16; ++dt) {            // pair = blocks (dt, 0), (dt, 1)
+                const int cur = dt & 1;
+                if (dt + 1 < 16) {
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        vb[cur ^ 1][j] = *reinterpret_cast<const half8*>(Vb + (4 * (grp + 1) + j) * 1024 + 16 * lane);
+                    for (int j = 0; j < 2; ++j)
+                        vb[cur ^ 1][j] = *reinterpret_cast<const half8*>(Vb + (2 * (dt + 1) + j) * 1024 + 16 * lane);
                 }
-                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int dt = 2 * grp + (j >> 1), ks = j & 1;
-                    O[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[ks], vb[cur][j], O[dt], 0, 0, 0);
-                }
-                __builtin_amdgcn_sched_barrier(0);
+                for (int ks = 0; ks < 2; ++ks)
+                    O[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[ks], vb[cur][ks], O[dt], 0, 0, 0);
             }
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) O[16] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[ks], ones, O[16], 0, 0, 0);
         }
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) sC[kk] = sN[kk];
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // next tiles landed (this wave's part)
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // next tile landed (this wave's part)
         __syncthreads();                    // ... for every wave; this tile fully consumed
     }
 

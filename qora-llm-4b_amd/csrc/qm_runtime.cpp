@@ -637,7 +637,8 @@ int32_t qm_gqa_prefill(qm_context* c, qm_stream stream, int32_t seq_len, const u
     st = launch(c, c->f_gqp_kv, static_cast<uint32_t>(s_pad / 64) * QM_GQA_KV_HEADS, 256, ga, s,
                 "qm_gqa_prefill_kv");
     if (st != QM_OK) return st;
-    return launch(c, c->f_gqp_attn, static_cast<uint32_t>(s_pad / 32) * QM_GQA_KV_HEADS, 512, ga, s,
+    // 48 query rows per workgroup, 12 waves
+    return launch(c, c->f_gqp_attn, static_cast<uint32_t>((seq_len + 47) / 48) * QM_GQA_KV_HEADS, 768, ga, s,
                   "qm_gqa_prefill_attn");
 }
 
