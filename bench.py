@@ -354,7 +354,7 @@ def run_dn_prefill(args, ctx):
     flops = dn_prefill_flops(T)
     return {
         "tokens": K * T, "total_ms": total_ms, "wall_s": wall,
-        "dominant": "qm_deltanet_prefill (prep+chunk+scan+out)",
+        "dominant": "qm_deltanet_prefill (chunk+scan+out)",
         "roofline": {"bound": "mfma", "achieved": flops / (k_ms * 1e-3), "peak": MFMA_BF16_PEAK,
                      "unit": "TFLOP/s", "kernel_ms": k_ms, "flops_per_launch": flops},
         "config": {"workload": "DeltaNet chunked prefill, 1 layer, batch 1, seq 4096, chunk 64, "
