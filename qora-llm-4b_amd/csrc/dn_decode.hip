@@ -95,6 +95,13 @@ QM_DEV void dn_decode_body(const DnDecodeArgs& A) {
     float vr[RPG];
 #pragma unroll
     for (int i = 0; i < RPG; ++i) vr[i] = act[2 * 2048 + vh * QM_DN_HD + g + GROUPS * i];
+    // The epilogue's inputs (norm weight, z gate) do not depend on the
+    // update: fetch them with the state so the norm costs no extra round trip.
+    float gz = 0.0f;
+    if (tid < QM_DN_HD) {
+        const float zz = A.z[(size_t)b * QM_DN_V_DIM + vh * QM_DN_HD + tid];
+        gz = f16_to_f32(A.norm_w[tid]) * silu_f(zz);
+    }
 
     float4 q0 = ld4(act + qkh * QM_DN_HD + 4 * l), q1 = ld4(act + qkh * QM_DN_HD + 64 + 4 * l);
     float4 k0 = ld4(act + 2048 + qkh * QM_DN_HD + 4 * l), k1 = ld4(act + 2048 + qkh * QM_DN_HD + 64 + 4 * l);
@@ -129,15 +136,15 @@ QM_DEV void dn_decode_body(const DnDecodeArgs& A) {
     __syncthreads();
 
     // gemv.rs:865-883: per-head RMSNorm (plain gamma, eps 1e-6) * silu(z).
-    // The sum of squares runs over rows 0..127 in order, as the reference.
+    // Waves 0 and 1 each reduce the 128 squares with the same wave tree, so
+    // both hold the same sum (the reference sums rows in order; the
+    // difference is a rounding of the sum, ~1e-7 relative).
     if (tid < QM_DN_HD) {
-        float ss = 0.0f;
-#pragma unroll 8
-        for (int r = 0; r < QM_DN_HD; ++r) ss = __fadd_rn(ss, __fmul_rn(ys[r], ys[r]));
+        const int ln = tid & 63;
+        const float y0 = ys[ln], y1 = ys[64 + ln];
+        const float ss = wave_sum64(fmaf(y1, y1, y0 * y0));
         const float inv_rms = 1.0f / sqrtf(ss / (float)QM_DN_HD + 1e-6f);
-        const float gm = f16_to_f32(A.norm_w[tid]);
-        const float zz = A.z[(size_t)b * QM_DN_V_DIM + vh * QM_DN_HD + tid];
-        A.out[(size_t)b * QM_DN_V_DIM + vh * QM_DN_HD + tid] = ys[tid] * inv_rms * gm * silu_f(zz);
+        A.out[(size_t)b * QM_DN_V_DIM + vh * QM_DN_HD + tid] = ys[tid] * inv_rms * gz;
     }
 }
 

@@ -109,17 +109,21 @@ QM_DEV void compute_round(WaveState& st, const RoundBuf& rb, const half8 (&afr)[
     __builtin_amdgcn_wave_barrier();
 }
 
+// The output gate of query head qh, dims 4*lane .. 4*lane+3 (gemv.rs:1008-1011),
+// loaded ahead of the attention so its latency is hidden.
+QM_DEV float4 gqa_gate(const GqaDecodeArgs& A, int b, int qh, int lane) {
+    return ld4(A.q_gate + ((size_t)b * QM_GQA_HEADS + qh) * (2 * QM_GQA_HD) + QM_GQA_HD + 4 * lane);
+}
+
 // Gate and store one head's output: out = (acc / l) * sigmoid(gate).
-QM_DEV void gqa_store_out(const GqaDecodeArgs& A, int b, int qh, int lane, float o0, float o1,
-                          float o2, float o3, float Ls) {
+QM_DEV void gqa_store_out(const GqaDecodeArgs& A, int b, int qh, int lane, float4 o, float Ls,
+                          float4 gv) {
     const float inv = 1.0f / Ls;
-    const float* gate = A.q_gate + ((size_t)b * QM_GQA_HEADS + qh) * (2 * QM_GQA_HD) + QM_GQA_HD + 4 * lane;
-    const float4 gv = ld4(gate);
     float4 r;
-    r.x = (o0 * inv) * sigmoid_f(gv.x);
-    r.y = (o1 * inv) * sigmoid_f(gv.y);
-    r.z = (o2 * inv) * sigmoid_f(gv.z);
-    r.w = (o3 * inv) * sigmoid_f(gv.w);
+    r.x = (o.x * inv) * sigmoid_f(gv.x);
+    r.y = (o.y * inv) * sigmoid_f(gv.y);
+    r.z = (o.z * inv) * sigmoid_f(gv.z);
+    r.w = (o.w * inv) * sigmoid_f(gv.w);
     st4(A.out + ((size_t)b * QM_GQA_HEADS + qh) * QM_GQA_HD + 4 * lane, r);
 }
 
@@ -135,28 +139,35 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_decode_split(GqaDecodeA
     const int bg = bid / A.nsplit;
     const int g = bg % QM_GQA_KV_HEADS;
     const int b = bg / QM_GQA_KV_HEADS;
-    int pos = A.pos ? A.pos[b] : A.max_pos;
-    pos = pos < 0 ? 0 : (pos > A.max_pos ? A.max_pos : pos);
-    const int L = pos + 1;
     const int t_begin = split * A.chunk;
-    const int t_end = min(t_begin + A.chunk, L);
-
-    const float* cos_row = A.rope_cos + (size_t)pos * (QM_GQA_ROT / 2);
-    const float* sin_row = A.rope_sin + (size_t)pos * (QM_GQA_ROT / 2);
     const size_t kv_base = ((size_t)b * QM_GQA_KV_HEADS + g) * (size_t)A.cap * QM_GQA_HD;
     const uint16_t* kbase = A.k_cache + kv_base;
     const uint16_t* vbase = A.v_cache + kv_base;
 
-    // 4a. Wave w takes rounds t_begin + 64*r + 16*w (r = 0 .. nr-1).  A
-    //     split that does not append issues its first round now, so the
-    //     loads overlap the q preparation.
+    // 4a. Wave w takes rounds t_begin + 64*r + 16*w (r = 0 .. nr-1).  The
+    //     first round is issued before pos has arrived, bounded by max_pos
+    //     (pos <= max_pos), so it overlaps the pos load and the q
+    //     preparation; keys past the real end are masked when the round is
+    //     computed.  The split that appends loads it again after the append.
+    const int arow = lane & 15, aq = lane >> 4;
+    RoundBuf ra, rb;
+    {
+        const int t_end0 = min(t_begin + A.chunk, A.max_pos + 1);
+        if (t_begin + 16 * w < t_end0) load_round(ra, kbase, vbase, t_begin + 16 * w, t_end0 - 1, arow, aq, lane);
+    }
+    float4 gv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (A.nsplit == 1) gv = gqa_gate(A, b, 4 * g + w, lane);
+
+    int pos = A.pos ? A.pos[b] : A.max_pos;
+    pos = pos < 0 ? 0 : (pos > A.max_pos ? A.max_pos : pos);
+    const int L = pos + 1;
+    const int t_end = min(t_begin + A.chunk, L);
+    const float* cos_row = A.rope_cos + (size_t)pos * (QM_GQA_ROT / 2);
+    const float* sin_row = A.rope_sin + (size_t)pos * (QM_GQA_ROT / 2);
     const bool appends = (t_begin <= pos && pos < t_end);
     const int span = t_end - t_begin - 16 * w;
     const int nr = __builtin_amdgcn_readfirstlane(span > 0 ? (span + 63) / 64 : 0);
     const int t_last = t_end - 1;
-    const int arow = lane & 15, aq = lane >> 4;
-    RoundBuf ra, rb;
-    if (!appends && nr > 0) load_round(ra, kbase, vbase, t_begin + 16 * w, t_last, arow, aq, lane);
 
     // 1. q prep: wave w handles query head 4g+w (gemv.rs:927-949).
     {
@@ -253,7 +264,7 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_decode_split(GqaDecodeA
             o.x += a.x * f; o.y += a.y * f; o.z += a.z * f; o.w += a.w * f;
         }
         if (A.nsplit == 1) {
-            gqa_store_out(A, b, 4 * g + h, lane, o.x, o.y, o.z, o.w, Ls);
+            gqa_store_out(A, b, 4 * g + h, lane, o, Ls, gv);
         } else {
             float* P = A.partial + ((((size_t)b * QM_GQA_KV_HEADS + g) * A.nsplit + split) * 4 + h) * GQA_PART_STRIDE;
             st4(P + 4 * lane, o);
@@ -262,35 +273,72 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_decode_split(GqaDecodeA
     }
 }
 
-// Merge the split partials of (b, g) in split order and apply the gate.
-// Thread (h = tid / 64, lane) owns dims 4*lane..4*lane+3 of query head 4g+h.
-// Two passes with loads independent of the running sums (the global max
-// first, then the weighted sums), so the loads of many splits are in flight
-// together instead of one dependent round trip per split.
-extern "C" __global__ __launch_bounds__(256) void qm_gqa_decode_merge(GqaDecodeArgs A) {
-    const int tid = threadIdx.x, h = tid >> 6, lane = tid & 63;
-    const int g = blockIdx.x % QM_GQA_KV_HEADS;
-    const int b = blockIdx.x / QM_GQA_KV_HEADS;
-    const float* P0 = A.partial + (((size_t)b * QM_GQA_KV_HEADS + g) * A.nsplit * 4 + h) * GQA_PART_STRIDE;
+// Merge the split partials of query head 4g+h of sequence b and apply the
+// gate.  Workgroup (b, g, h) has 16 waves; wave w folds splits w, w+16,
+// w+32, w+48 (then the next 64, ...) with all four partials' loads in
+// flight, so up to 64 splits cost one memory round trip, and the 16 wave
+// results combine through LDS.  Lane l owns dims 4l .. 4l+3.
+extern "C" __global__ __launch_bounds__(1024) void qm_gqa_decode_merge(GqaDecodeArgs A) {
+    __shared__ float4 wo[16][64];
+    __shared__ float wm[16], wl[16];
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int h = blockIdx.x & 3;
+    const int g = (blockIdx.x >> 2) % QM_GQA_KV_HEADS;
+    const int b = blockIdx.x / (4 * QM_GQA_KV_HEADS);
+    const int nsplit = A.nsplit;
+    float4 gv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (w == 0) gv = gqa_gate(A, b, 4 * g + h, lane);
+    const float* P0 = A.partial + (((size_t)b * QM_GQA_KV_HEADS + g) * nsplit * 4 + h) * GQA_PART_STRIDE;
     const size_t step = 4 * GQA_PART_STRIDE;
-    float M = -INFINITY;
-#pragma unroll 8
-    for (int s = 0; s < A.nsplit; ++s) M = fmaxf(M, P0[s * step + 256]);
-    float Ls = 0.0f;
-    float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f;
-#pragma unroll 8
-    for (int s = 0; s < A.nsplit; ++s) {
-        const float* P = P0 + s * step;
-        const float ms = P[256];
-        const float ls = P[257];
-        const float4 a = ld4(P + 4 * lane);
+
+    float mw = -INFINITY, lw = 0.0f;
+    float4 ow = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int s0 = w; s0 < nsplit; s0 += 64) {
+        float4 a[4];
+        float ms[4], ls[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int s = s0 + 16 * j;
+            const bool ok = s < nsplit;                  // wave-uniform
+            const float* P = P0 + (size_t)(ok ? s : s0) * step;
+            a[j] = ld4(P + 4 * lane);
+            ms[j] = ok ? P[256] : -INFINITY;
+            ls[j] = P[257];
+        }
         // empty splits (sequence shorter than max_pos) carry m = -inf
-        const float f = (ms == -INFINITY) ? 0.0f : expf(ms - M);
-        Ls = fmaf(ls, f, Ls);
-        o0 = fmaf(a.x, f, o0);
-        o1 = fmaf(a.y, f, o1);
-        o2 = fmaf(a.z, f, o2);
-        o3 = fmaf(a.w, f, o3);
+        const float nm = fmaxf(mw, fmaxf(fmaxf(ms[0], ms[1]), fmaxf(ms[2], ms[3])));
+        if (nm == -INFINITY) continue;                   // wave-uniform
+        const float c = expf(mw - nm);                   // 0 while mw = -inf
+        lw *= c;
+        ow.x *= c; ow.y *= c; ow.z *= c; ow.w *= c;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float f = (ms[j] == -INFINITY) ? 0.0f : expf(ms[j] - nm);
+            lw = fmaf(ls[j], f, lw);
+            ow.x = fmaf(a[j].x, f, ow.x);
+            ow.y = fmaf(a[j].y, f, ow.y);
+            ow.z = fmaf(a[j].z, f, ow.z);
+            ow.w = fmaf(a[j].w, f, ow.w);
+        }
+        mw = nm;
     }
-    gqa_store_out(A, b, 4 * g + h, lane, o0, o1, o2, o3, Ls);
+    if (lane == 0) { wm[w] = mw; wl[w] = lw; }
+    wo[w][lane] = ow;
+    __syncthreads();
+    if (w == 0) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int ww = 0; ww < 16; ++ww) M = fmaxf(M, wm[ww]);
+        float Ls = 0.0f;
+        float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int ww = 0; ww < 16; ++ww) {
+            const float f = (wm[ww] == -INFINITY) ? 0.0f : expf(wm[ww] - M);
+            const float4 x = wo[ww][lane];
+            Ls = fmaf(wl[ww], f, Ls);
+            o.x = fmaf(x.x, f, o.x); o.y = fmaf(x.y, f, o.y);
+            o.z = fmaf(x.z, f, o.z); o.w = fmaf(x.w, f, o.w);
+        }
+        gqa_store_out(A, b, 4 * g + h, lane, o, Ls, gv);
+    }
 }

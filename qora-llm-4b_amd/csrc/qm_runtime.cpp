@@ -512,11 +512,12 @@ int32_t qm_deltanet_decode(qm_context* c, qm_stream stream, int32_t batch, int32
 
 // ---- GQA decode --------------------------------------------------------------------
 // Keys per split workgroup: about 2048 workgroups per launch (8 per CU) with
-// at least 256 keys each, at most 2048.
+// at least 128 keys each (two 16-key rounds per wave, both in flight at
+// once), at most 2048.
 static int64_t gqa_auto_chunk(int64_t len, int32_t batch) {
     int64_t want = (len * batch * QM_GQA_KV_HEADS + 2047) / 2048;
     int64_t ch = ((want + 63) / 64) * 64;
-    return std::max<int64_t>(256, std::min<int64_t>(ch, 2048));
+    return std::max<int64_t>(128, std::min<int64_t>(ch, 2048));
 }
 
 int32_t qm_gqa_decode(qm_context* c, qm_stream stream, int32_t batch, const float* q_gate,
@@ -551,7 +552,7 @@ int32_t qm_gqa_decode(qm_context* c, qm_stream stream, int32_t batch, const floa
                      static_cast<int32_t>(chunk), static_cast<int32_t>(nsplit), batch};
     st = launch(c, c->f_gqa_split, static_cast<uint32_t>(grid), 256, ga, s, "qm_gqa_decode_split");
     if (st != QM_OK || nsplit == 1) return st;
-    return launch(c, c->f_gqa_merge, static_cast<uint32_t>(batch) * QM_GQA_KV_HEADS, 256, ga, s,
+    return launch(c, c->f_gqa_merge, static_cast<uint32_t>(batch) * QM_GQA_KV_HEADS * 4, 1024, ga, s,
                   "qm_gqa_decode_merge");
 }
 
@@ -563,13 +564,13 @@ int32_t qm_reserve(qm_context* c, int32_t max_batch, int32_t max_kv_len, int32_t
         // Bound on batch * nsplit over every batch <= max_batch and length
         // <= max_kv_len.  Automatic chunks: below the 2048 cap a chunk holds
         // at least len*batch/512 keys, so nsplit <= ceil(512/batch); at the
-        // cap nsplit = ceil(len/2048); and always nsplit <= ceil(len/64).
+        // cap nsplit = ceil(len/2048); and always nsplit <= ceil(len/128).
         const int64_t L = max_kv_len, B = max_batch;
         int64_t bn;
         if (c->opt_gqa_chunk) {
             bn = B * ((L + c->opt_gqa_chunk - 1) / c->opt_gqa_chunk);
         } else {
-            bn = std::min<int64_t>(B * ((L + 255) / 256), std::max<int64_t>(512 + B, B * ((L + 2047) / 2048)));
+            bn = std::min<int64_t>(B * ((L + 127) / 128), std::max<int64_t>(512 + B, B * ((L + 2047) / 2048)));
         }
         ws = std::max(ws, static_cast<size_t>(bn) * QM_GQA_KV_HEADS * 4 * 260 * sizeof(float));
     }

@@ -91,6 +91,18 @@ def test_decode_chunk_invariance(ctx, chunk):
     assert np.abs(got - ref).max() <= TOL
 
 
+def test_decode_many_splits_ragged(ctx):
+    """79 splits per sequence (more than one 64-split pass of the merge), and a
+    short sequence whose splits past its end are empty (m = -inf)."""
+    positions = [5000, 70]
+    w = W.gqa_decode_workload(5000, 2, seed=11)
+    print("case: gqa decode chunk=64 ragged", positions, flush=True)
+    got, _, _ = run_gpu(ctx, w, positions, 5001, chunk=64)
+    ref, _, _ = run_oracle(w, positions, 5001)
+    print(f"max|dout|={np.abs(got - ref).max():.3e}")
+    assert np.abs(got - ref).max() <= TOL
+
+
 def test_decode_range_errors(ctx):
     w = W.gqa_decode_workload(16, 1, cap=17, seed=4)
     cos, sin = M.rope_table(16)
