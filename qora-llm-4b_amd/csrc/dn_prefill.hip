@@ -22,10 +22,11 @@
 //                        substitution in fp32, the off-diagonal corrections
 //                        on MFMA), Q~ = diag(gamma)Q - PW and Y0 = PU~, all
 //                        products on f16 MFMA;
-//   qm_dn_prefill_scan   the sequential part: one wave per (v-head, 16 state
-//                        rows) with its rows of the fp32 state in registers,
-//                        two f16 MFMA GEMMs per chunk; stores each chunk's
-//                        entry state in f16;
+//   qm_dn_prefill_scan   the sequential part: one 4-wave workgroup per
+//                        (v-head, 16 state rows) with its rows of the fp32
+//                        state in registers, two f16 MFMA GEMMs per chunk
+//                        split over the waves; stores each chunk's entry
+//                        state in f16;
 //   qm_dn_prefill_out    Y = Y0 + Q~ S_c^T on MFMA, fully parallel over
 //                        (chunk, v-head), fused with the gated RMSNorm and
 //                        the conv buffer update.
@@ -67,7 +68,8 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
     __shared__ _Float16 Pm[CHK][72];               // P (lower, incl. diagonal)
     __shared__ _Float16 Am[CHK][72];               // A (strictly lower)
     __shared__ _Float16 Td[4][16][24];             // (I + A_bb)^-1
-    __shared__ float Gs[CHK], Bs[CHK], Eg[CHK], BG[CHK], Kd[CHK];
+    __shared__ __attribute__((aligned(16))) float Gs[CHK];
+    __shared__ float Bs[CHK], Eg[CHK], BG[CHK], Kd[CHK];
 
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int c = blockIdx.x / QM_DN_V_HEADS, h = blockIdx.x % QM_DN_V_HEADS;
@@ -88,9 +90,17 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
         chb[0] = qkh * QM_DN_HD + 8 * cg;
         chb[1] = QM_DN_QK_DIM + qkh * QM_DN_HD + 8 * cg;
         chb[2] = 2 * QM_DN_QK_DIM + h * QM_DN_HD + 8 * cg;
+        // gate inputs (wave 0) first: they are consumed last
+        float ga = 0.0f, gb = 0.0f;
+        if (tid < CHK) {
+            const int t = min(t0 + tid, A.T - 1);
+            ga = A.a[(size_t)t * QM_DN_V_HEADS + h];
+            gb = A.b[(size_t)t * QM_DN_V_HEADS + h];
+        }
+        const float a_log_h = A.a_log[h], dt_bias_h = A.dt_bias[h];
         // all 21 raw rows the thread needs (7 per part), loaded at clamped,
         // always valid rows before any arithmetic; rows before the sequence
-        // come from the conv buffer, rows past it are zero
+        // come from the conv buffer, and the tokens past it are zeroed below
         uint4 u[3][7];
 #pragma unroll
         for (int part = 0; part < 3; ++part)
@@ -102,6 +112,7 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
         float4 wt[8], wn[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) wt[e] = ld4(A.conv_w + (size_t)(chb[0] + e) * 4);
+        const bool tail = t0 + CHK > A.T;          // last chunk, partly past the sequence
 #pragma unroll
         for (int part = 0; part < 3; ++part) {     // q, k, v
             const int ch0 = chb[part];
@@ -109,30 +120,28 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
 #pragma unroll
                 for (int e = 0; e < 8; ++e) wn[e] = ld4(A.conv_w + (size_t)(chb[part + 1] + e) * 4);
             }
-            float cb[3][8] = {};
-            if (c == 0) {                                        // x_{-3..-1}
-                asm volatile("" ::: "memory");   // keep these loads inside the branch
-#pragma unroll
-                for (int r = 0; r < 3; ++r) {
-                    const int t = min(4 * tg - 3 + r, -1);
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) cb[r][e] = A.conv_buf[(size_t)(ch0 + e) * 3 + 3 + t];
-                }
-            }
             float x[7][8];
 #pragma unroll
             for (int r = 0; r < 7; ++r) {
-                const int t = t0 + 4 * tg - 3 + r;
                 const uint32_t wv[4] = {u[part][r].x, u[part][r].y, u[part][r].z, u[part][r].w};
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     x[r][2 * e] = bf16_to_f32((uint16_t)(wv[e] & 0xffffu));
                     x[r][2 * e + 1] = bf16_to_f32((uint16_t)(wv[e] >> 16));
                 }
+            }
+            // the masks are wave-uniform branches: interior chunks skip them
+            if (c == 0) {                          // x_{-3..-1} from the conv buffer
+                asm volatile("" ::: "memory");    // keep these loads inside the branch
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    if (r < 3 && t < 0) x[r][e] = cb[r][e];
-                    if (t >= A.T) x[r][e] = 0.0f;
+                for (int r = 0; r < 3; ++r) {
+                    const int t = 4 * tg - 3 + r;
+                    const int tb = min(t, -1);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float cbv = A.conv_buf[(size_t)(ch0 + e) * 3 + 3 + tb];
+                        if (t < 0) x[r][e] = cbv;
+                    }
                 }
             }
             _Float16 (*dst)[136] = part == 0 ? Qs : part == 1 ? Ks : Vs;
@@ -148,7 +157,7 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
                     sacc = fmaf(x[j + 1][e], wt[e].y, sacc);
                     sacc = fmaf(x[j + 2][e], wt[e].z, sacc);
                     sacc = fmaf(x[j + 3][e], wt[e].w, sacc);
-                    v[e] = (t0 + tok < A.T) ? silu_fast(sacc) : 0.0f;
+                    v[e] = silu_fast(sacc);
                 }
                 if (part < 2) {
                     // x /= ||x|| when ||x|| > 1e-12, q *= 1/sqrt(128)
@@ -156,10 +165,9 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
 #pragma unroll
                     for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
                     ss = row_sum16(ss);
-                    const float norm = sqrtf(ss);
-                    const float inv = norm > 1e-12f ? 1.0f / norm : 1.0f;
+                    const float f = (ss > 1e-24f ? __builtin_amdgcn_rsqf(ss) : 1.0f) * scale;
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) v[e] = (v[e] * inv) * scale;
+                    for (int e = 0; e < 8; ++e) v[e] *= f;
                 }
                 half8 hv;
 #pragma unroll
@@ -169,17 +177,26 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
 #pragma unroll
             for (int e = 0; e < 8; ++e) wt[e] = wn[e];
         }
+        if (tail) {
+            // Tokens past the sequence read clamped rows above; their rows
+            // are zeroed here (a token's conv and norm involve only itself
+            // and earlier rows, so no valid token saw them).
+#pragma unroll
+            for (int part = 0; part < 3; ++part) {
+                _Float16 (*dst)[136] = part == 0 ? Qs : part == 1 ? Ks : Vs;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (t0 + 4 * tg + j >= A.T) *reinterpret_cast<half8*>(&dst[4 * tg + j][8 * cg]) = half8{};
+            }
+        }
         if (tid < CHK) {
             // log alpha = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b);
             // padded tokens get alpha = 1, beta = 0 (no effect on the state);
             // then the inclusive prefix sum over the chunk (one wave)
-            const int t = t0 + tid;
             float g = 0.0f, be = 0.0f;
-            if (t < A.T) {
-                const float a_exp = expf(A.a_log[h]);
-                const float sp = softplus_f(A.a[(size_t)t * QM_DN_V_HEADS + h] + A.dt_bias[h]);
-                g = -a_exp * sp;
-                be = 1.0f / (1.0f + expf(-A.b[(size_t)t * QM_DN_V_HEADS + h]));
+            if (t0 + tid < A.T) {
+                g = -expf(a_log_h) * softplus_f(ga + dt_bias_h);
+                be = 1.0f / (1.0f + expf(-gb));
             }
 #pragma unroll
             for (int off = 1; off < 64; off <<= 1) {
@@ -195,37 +212,42 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
     __syncthreads();
     if (tid < CHK) Kd[tid] = expf(Gs[CHK - 1] - Gs[tid]);     // gamma_C / gamma_i
 
-    // ---- 1. KK^T and QK^T (16x16x32 f16), masked and decayed -> A, P (f16)
+    // ---- 1. KK^T and QK^T (16x16x32 f16), masked and decayed -> A, P (f16).
+    //      Computed transposed, C = K_j K_i^T and K_j Q_i^T: lane (lr, lq)
+    //      then holds row i = 16w + lr, columns 16j + 4lq .. +3, one 8-byte
+    //      store per matrix and tile.  Decays exp(G_i - G_jj) on v_exp_f32
+    //      with the exponent clamped at 0 (the masked upper part).
     {
-        const int i0 = 16 * w;
-        half8 aq[4];
+        const int i = 16 * w + lr;
+        const float gi = Gs[i], bi = Bs[i];
+        half8 bk[4], bq[4];                        // B operands: row i's k, q
 #pragma unroll
-        for (int s = 0; s < 4; ++s) aq[s] = *reinterpret_cast<const half8*>(&Qs[i0 + lr][32 * s + 8 * lq]);
+        for (int s = 0; s < 4; ++s) {
+            bk[s] = *reinterpret_cast<const half8*>(&Ks[i][32 * s + 8 * lq]);
+            bq[s] = *reinterpret_cast<const half8*>(&Qs[i][32 * s + 8 * lq]);
+        }
         for (int j = 0; j < 4; ++j) {
-            if (j > w) {
+            half4 ha = {}, hp = {};
+            if (j <= w) {                          // wave-uniform
+                floatx4 ckk = {0.0f, 0.0f, 0.0f, 0.0f}, cqk = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const half8 ak = *reinterpret_cast<const half8*>(&Ks[16 * j + lr][32 * s + 8 * lq]);
+                    ckk = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak, bk[s], ckk, 0, 0, 0);
+                    cqk = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak, bq[s], cqk, 0, 0, 0);
+                }
+                const float4 gj = *reinterpret_cast<const float4*>(&Gs[16 * j + 4 * lq]);
+                const float gjv[4] = {gj.x, gj.y, gj.z, gj.w};
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    Pm[i0 + 4 * lq + e][16 * j + lr] = (_Float16)0.0f;
-                    Am[i0 + 4 * lq + e][16 * j + lr] = (_Float16)0.0f;
+                    const int jj = 16 * j + 4 * lq + e;
+                    const float dec = __builtin_amdgcn_exp2f(fminf(gi - gjv[e], 0.0f) * 1.4426950408889634f);
+                    ha[e] = (_Float16)(jj < i ? bi * dec * ckk[e] : 0.0f);
+                    hp[e] = (_Float16)(jj <= i ? dec * cqk[e] : 0.0f);
                 }
-                continue;
             }
-            floatx4 ckk = {0.0f, 0.0f, 0.0f, 0.0f}, cqk = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const int kk = 32 * s + 8 * lq;
-                const half8 ak = *reinterpret_cast<const half8*>(&Ks[i0 + lr][kk]);
-                const half8 bk = *reinterpret_cast<const half8*>(&Ks[16 * j + lr][kk]);
-                ckk = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak, bk, ckk, 0, 0, 0);
-                cqk = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq[s], bk, cqk, 0, 0, 0);
-            }
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int i = i0 + 4 * lq + e, jj = 16 * j + lr;
-                const float dec = jj <= i ? expf(Gs[i] - Gs[jj]) : 0.0f;
-                Am[i][jj] = (_Float16)(jj < i ? Bs[i] * dec * ckk[e] : 0.0f);
-                Pm[i][jj] = (_Float16)(jj <= i ? dec * cqk[e] : 0.0f);
-            }
+            *reinterpret_cast<half4*>(&Am[i][16 * j + 4 * lq]) = ha;
+            *reinterpret_cast<half4*>(&Pm[i][16 * j + 4 * lq]) = hp;
         }
     }
     __syncthreads();
@@ -372,16 +394,16 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
 }
 
 // ============================================================================
-// 3. scan: sequential over chunks, one wave per (v-head, 16 state rows)
+// 3. scan: sequential over chunks, one workgroup per (v-head, 16 state rows)
 // ============================================================================
 // Under the chunked delta rule every state row evolves on its own:
 //   U_r = U~_r - W S_r^T,  S_r <- gamma_C S_r + U_r^T K~
-// so a v-head's 128 rows split over 8 independent waves (grid 256).  The
+// so a v-head's 128 rows split over 8 independent slices (grid 256).  The
 // output Y_r = Y0_r + Q~ S_r^T only reads the chunk-entry state, so the scan
 // stores that state (in f16, the precision the product consumes it in) and
 // the out kernel forms Y fully in parallel.
-// A wave keeps S_r^T (k-cols x 16 rows, fp32) as eight C fragments; for k
-// tile t, lane (r, q) = (lane & 15, lane >> 4) holds S[16 vt + r][16 t + 4q .. +3].
+// S_r^T (k-cols x 16 rows, fp32) is held as eight C fragments; for k tile
+// t, lane (r, q) = (lane & 15, lane >> 4) holds S[16 vt + r][16 t + 4q .. +3].
 // All chunk operands arrive in fragment order as 16-byte pieces, piece
 // (j, lane) at byte offset 16 (64 j + lane) of the (head, chunk) block:
 //   -W, Q~   j = 4 i + p: tokens 16 i + (lane & 15), k-cols 32 p + 4 (lane >> 4)
@@ -396,110 +418,128 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
 // only needs A and B to agree on which k each (lane, element) holds, and the
 // two C fragments of S^T k tiles 2p, 2p+1 (or of U token tiles 2p, 2p+1)
 // concatenated hold exactly the k (token) set of piece p.
-// Two chunks' operands are held in registers (the wave is alone on its CU,
-// so the whole register file is available): chunk c + 2's -W and U~ are
-// loaded right after chunk c's U product and its K~^T right after chunk c's
-// state update, into the registers just consumed.
-extern "C" __global__ __launch_bounds__(64) void qm_dn_prefill_scan(DnPrefillArgs A) {
-    const int lane = threadIdx.x;
+// A workgroup of four waves (one per SIMD) owns one (v-head, 16 rows) slice,
+// so the per-chunk chain is split four ways: wave w forms U's token tile w
+// (4 MFMAs) and updates S^T k-tiles 2w, 2w+1 (4 MFMAs).  The f16 U tiles and
+// S pieces are exchanged through LDS, two barriers per chunk; a wave writes
+// S piece w, which is also what the out kernel reads for S_c.
+// Single buffers suffice: a wave writes Sx (Ux) only after passing the
+// barrier that every wave reaches after its last read of the previous
+// contents.  Each wave's operands for chunk c + 4 are loaded right after
+// their last use in chunk c.
+extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillArgs A) {
+    __shared__ half8 Sx[4][64];                  // S^T piece p (k-tiles 2p, 2p+1), f16
+    __shared__ half4 Ux[4][64];                  // U token tile i, f16
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     // blocks are dealt to the 8 XCDs round-robin: keep a head's 8 row slices
     // on one XCD so its chunk operands are fetched into one L2
     const int b = blockIdx.x, xcd = b & 7, idx = b >> 3;
     const int h = xcd + 8 * (idx >> 3), vt = idx & 7;
     const int nc = A.nc;
+    const size_t hbase = (size_t)h * nc;
 
-    float* Sg = A.state + (size_t)h * QM_DN_HEAD_ELEMS;
-    floatx4 S[8];
+    float* Srow = A.state + (size_t)h * QM_DN_HEAD_ELEMS + (size_t)(16 * vt + (lane & 15)) * QM_DN_HD + 4 * (lane >> 4);
+    floatx4 S[2];                                // S^T k-tiles 2w, 2w+1 (fp32)
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        const float4 v = ld4(Sg + (size_t)(16 * vt + (lane & 15)) * QM_DN_HD + 16 * t + 4 * (lane >> 4));
+    for (int t = 0; t < 2; ++t) {
+        const float4 v = ld4(Srow + 16 * (2 * w + t));
         S[t] = floatx4{v.x, v.y, v.z, v.w};
     }
 
     auto blk = [&](const uint16_t* base, int c) {
-        return base + ((size_t)h * nc + c) * (CHK * QM_DN_HD) + (size_t)lane * 8;
+        return base + (hbase + c) * (CHK * QM_DN_HD) + (size_t)lane * 8;
     };
-    auto load16 = [&](half8 (&dst)[16], const uint16_t* base, int c) {
-        const uint16_t* src = blk(base, c);
-#pragma unroll
-        for (int j = 0; j < 16; ++j) dst[j] = *reinterpret_cast<const half8*>(src + j * 512);
+    struct Ops {
+        half8 w[4];                              // -W pieces 4w .. 4w+3 (token block w)
+        half4 u;                                 // U~ token tile w
+        half8 k[4];                              // K~^T pieces 4w .. 4w+3 (k-tiles 2w, 2w+1)
     };
-    auto load_u = [&](half8 (&dst)[2], int c) {
+    auto load_w = [&](Ops& o, int c) {
+        const uint16_t* ws = blk(A.Wn, c) + 4 * w * 512;
 #pragma unroll
-        for (int p = 0; p < 2; ++p) dst[p] = *reinterpret_cast<const half8*>(blk(A.Ut, c) + (2 * vt + p) * 512);
+        for (int p = 0; p < 4; ++p) o.w[p] = *reinterpret_cast<const half8*>(ws + p * 512);
     };
-    // One chunk: store f16(S_c), U = U~ + (-W) S^T, S^T <- gamma_C S^T + K~^T U.
-    // The operand registers of chunk c are refilled with chunk c + 2 right
-    // after their last use, so every load has about 1.5 chunk periods to land.
-    auto step = [&](int c, half8 (&wf)[16], half8 (&kf)[16], half8 (&uf)[2], float& gC) {
-        const int cn = c + 2 < nc ? c + 2 : nc - 1;
-        half8 sb[4];                      // S^T k-tiles 2p, 2p+1 as one B operand
+    auto load_uk = [&](Ops& o, int c) {
+        o.u = *reinterpret_cast<const half4*>(blk(A.Ut, c) + (2 * vt + (w >> 1)) * 512 + 4 * (w & 1));
+        const uint16_t* ks = blk(A.Ktt, c) + 4 * w * 512;
 #pragma unroll
-        for (int p = 0; p < 4; ++p) sb[p] = cat8(to_half4(S[2 * p]), to_half4(S[2 * p + 1]));
-        {
-            uint16_t* so = A.Sc + ((size_t)h * nc + c) * (QM_DN_HD * QM_DN_HD) + (size_t)(4 * vt * 64 + lane) * 8;
+        for (int j = 0; j < 4; ++j) o.k[j] = *reinterpret_cast<const half8*>(ks + j * 512);
+    };
+    auto sc_store = [&](int c, half8 v) {
+        *reinterpret_cast<half8*>(A.Sc + (hbase + c) * (QM_DN_HD * QM_DN_HD) + (size_t)((4 * vt + w) * 64 + lane) * 8) = v;
+    };
+    // gamma_C of 64 chunks at a time, one per lane (a vector load, so LDS
+    // waits never wait on it), the next 64 fetched half way through
+    auto load_g = [&](int c0) { return A.gC[hbase + min(c0 + lane, nc - 1)]; };
+    float gv = load_g(0), gn = 0.0f;
+
+    // One chunk: U tile w = U~ + (-W) S^T; exchange U; S^T tiles <- gamma_C
+    // S^T + K~^T U; exchange S and store it as the next chunk's entry state.
+    auto step = [&](int c, Ops& o) {
+        if ((c & 63) == 32) gn = load_g(c + 32);
+        if ((c & 63) == 0 && c) gv = gn;
+        const float g = readlane_f32(gv, c & 63);
+        half8 sb[4];
 #pragma unroll
-            for (int p = 0; p < 4; ++p) *reinterpret_cast<half8*>(so + p * 512) = sb[p];
-        }
-        floatx4 uu[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const half8 src = uf[i >> 1];
-            const int o = 4 * (i & 1);
-            uu[i] = floatx4{(float)src[o], (float)src[o + 1], (float)src[o + 2], (float)src[o + 3]};
-#pragma unroll
-            for (int p = 0; p < 4; ++p)
-                uu[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[4 * i + p], sb[p], uu[i], 0, 0, 0);
-        }
+        for (int p = 0; p < 4; ++p) sb[p] = Sx[p][lane];
+        floatx4 u0 = {(float)o.u[0], (float)o.u[1], (float)o.u[2], (float)o.u[3]};
+        floatx4 u1 = {0.0f, 0.0f, 0.0f, 0.0f};
+        u0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.w[0], sb[0], u0, 0, 0, 0);
+        u1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.w[1], sb[1], u1, 0, 0, 0);
+        u0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.w[2], sb[2], u0, 0, 0, 0);
+        u1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.w[3], sb[3], u1, 0, 0, 0);
+        // this chunk's -W is consumed: fetch chunk c + 4's now, the rest of
+        // its operands after the state update, so the loads are spread over
+        // the chunk
+        const int cn = min(c + 4, nc - 1);
         __builtin_amdgcn_sched_barrier(0);
-        load16(wf, A.Wn, cn);
-        load_u(uf, cn);
+        load_w(o, cn);
         __builtin_amdgcn_sched_barrier(0);
-        half8 ub[2];                      // U token tiles 2p, 2p+1 as one B operand
+        Ux[w][lane] = to_half4(u0 + u1);
+        __syncthreads();
+        half8 ub[2];
 #pragma unroll
-        for (int p = 0; p < 2; ++p) ub[p] = cat8(to_half4(uu[2 * p]), to_half4(uu[2 * p + 1]));
+        for (int p = 0; p < 2; ++p) ub[p] = cat8(Ux[2 * p][lane], Ux[2 * p + 1][lane]);
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            S[t] = S[t] * gC;
+        for (int t = 0; t < 2; ++t) {
+            S[t] = S[t] * g;
 #pragma unroll
             for (int p = 0; p < 2; ++p)
-                S[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[2 * t + p], ub[p], S[t], 0, 0, 0);
+                S[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.k[2 * t + p], ub[p], S[t], 0, 0, 0);
         }
+        const half8 mine = cat8(to_half4(S[0]), to_half4(S[1]));
         __builtin_amdgcn_sched_barrier(0);
-        load16(kf, A.Ktt, cn);
-        gC = A.gC[(size_t)h * nc + cn];
+        load_uk(o, cn);
         __builtin_amdgcn_sched_barrier(0);
+        Sx[w][lane] = mine;
+        if (c + 1 < nc) sc_store(c + 1, mine);
+        __syncthreads();
     };
 
-    // chunks 0 and 1 in flight before the loop, in the order the loop
-    // reissues them (-W, U~; K~^T, gamma_C) so the in-order load counter
-    // lets each phase wait for its own operands only
-    half8 wa[16], ka[16], ua[2], wb[16], kb[16], ubf[2];
-    float ga, gb;
-    const int c1 = nc > 1 ? 1 : 0;
-    load16(wa, A.Wn, 0);
-    load_u(ua, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    load16(ka, A.Ktt, 0);
-    ga = A.gC[(size_t)h * nc];
-    __builtin_amdgcn_sched_barrier(0);
-    load16(wb, A.Wn, c1);
-    load_u(ubf, c1);
-    __builtin_amdgcn_sched_barrier(0);
-    load16(kb, A.Ktt, c1);
-    gb = A.gC[(size_t)h * nc + c1];
-    __builtin_amdgcn_sched_barrier(0);
-
-    int c = 0;
-    for (; c + 1 < nc; c += 2) {
-        step(c, wa, ka, ua, ga);
-        step(c + 1, wb, kb, ubf, gb);
-    }
-    if (c < nc) step(c, wa, ka, ua, ga);
+    // four chunks of operands in flight (a wave has a SIMD to itself)
+    Ops ops[4];
 #pragma unroll
-    for (int t = 0; t < 8; ++t)
-        st4(Sg + (size_t)(16 * vt + (lane & 15)) * QM_DN_HD + 16 * t + 4 * (lane >> 4),
-            make_float4(S[t][0], S[t][1], S[t][2], S[t][3]));
+    for (int i = 0; i < 4; ++i) {
+        load_w(ops[i], min(i, nc - 1));
+        load_uk(ops[i], min(i, nc - 1));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    {
+        const half8 mine = cat8(to_half4(S[0]), to_half4(S[1]));
+        Sx[w][lane] = mine;
+        sc_store(0, mine);
+    }
+    __syncthreads();
+    int c = 0;
+    for (; c + 3 < nc; c += 4) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) step(c + i, ops[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+        if (c + i < nc) step(c + i, ops[i]);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) st4(Srow + 16 * (2 * w + t), make_float4(S[t][0], S[t][1], S[t][2], S[t][3]));
 }
 
 // ============================================================================
