@@ -57,6 +57,8 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_prefill_kv(GqaPrefillAr
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int g = blockIdx.x % QM_GQA_KV_HEADS;
     const int t0 = (blockIdx.x / QM_GQA_KV_HEADS) * 64;
+    // the attention kernel that follows takes its row blocks from these
+    if (blockIdx.x == 0 && tid < QM_GQA_KV_HEADS) A.queue[tid] = 0;
     // K: wave w normalises and rotates tokens t0+16w .. t0+16w+15
     for (int j = 0; j < 16; ++j) {
         const int t = t0 + 16 * w + j;
@@ -127,246 +129,290 @@ QM_DEV void dma16(const void* gsrc, uint32_t lds) {
 }
 #pragma clang diagnostic pop
 
-// A workgroup owns 48 query rows of the four query heads of one kv group:
-// 12 waves, wave w on head 4g + (w & 3) and rows 16 (w >> 2) .. +15, three
+// A row block is 48 query rows of the four query heads of one kv group: 12
+// waves, wave w on head 4g + (w & 3) and rows 16 (w >> 2) .. +15, three
 // waves per SIMD, so one wave's LDS and softmax latency hides behind the
 // other waves' MFMAs.  Each iteration fetches the next K / V^T tile by LDS
 // DMA (the tile's 64 blocks dealt round-robin over the waves), then computes
 // the current tile's scores, softmax and P V.
+// The kernel is persistent: one workgroup per CU, workgroup b serving kv
+// group b & 3 (workgroups are dealt to the XCDs round-robin, so each XCD's L2
+// holds one group's K / V).  Row blocks are taken longest first from a
+// per-group atomic counter, so the causal triangle's unequal blocks balance
+// across CUs (a fixed assignment left some CUs with a third more tiles than
+// others).  A workgroup whose own queue is empty takes the remaining (short)
+// blocks of the other groups, which evens out the XCDs' speeds.
 #define TQ3 48
 
 extern "C" __global__ __launch_bounds__(768) void qm_gqa_prefill_attn(GqaPrefillArgs A) {
     __shared__ __attribute__((aligned(1024))) char sm[SM_BYTES];
-    const int tid = threadIdx.x, lane = tid & 63;
+    __shared__ int item_s;
+    const int tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int lr = lane & 15, lq = lane >> 4;
-    const int g = blockIdx.x % QM_GQA_KV_HEADS;
     const int nblk = (A.S + TQ3 - 1) / TQ3;
-    const int tb = nblk - 1 - (int)(blockIdx.x / QM_GQA_KV_HEADS);   // longest rows first
-    const int t0 = tb * TQ3;
-    const int qh = 4 * g + (w & 3);
-    const int r0 = t0 + 16 * (w >> 2);
-    // tiles up to the block's last row, within the zero-padded V^T copy
-    const int nkt = min((t0 + TQ3 + KT - 1) / KT, A.s_pad / KT);
     const uint32_t sm_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)sm;
-
-    // tile fetch: block b = w + 12 j of the tile's 64 (K blocks 0..31, V^T 32..63)
-    const uint16_t* kbase = A.k_cache + (size_t)g * A.cap * QM_GQA_HD;
-    const uint16_t* vbase = A.vt + (size_t)g * QM_GQA_HD * A.s_pad;
-    auto fetch = [&](int kt, int buf) {
-        const int k0 = kt * KT;
-#pragma unroll
-        for (int j = 0; j < 6; ++j) {
-            const int b = w + 12 * j;
-            if (b < 32) {
-                const int kk = b >> 3, s = b & 7;                  // K block: S^T fragment kk, k-step s
-                const int key = min(k0 + frag_key(kk, lr), A.S - 1);  // rows past S feed masked scores only
-                dma16(kbase + (size_t)key * QM_GQA_HD + 32 * s + 8 * lq, sm_lds + SM_K(buf) + 1024 * b);
-            } else if (b < 64) {
-                const int dt = (b - 32) >> 1, ks = b & 1;          // V^T block: dims tile dt, keys step ks
-                dma16(vbase + (size_t)(16 * dt + lr) * A.s_pad + k0 + 32 * ks + 8 * lq,
-                      sm_lds + SM_V(buf) + 1024 * (b - 32));
-            }
+    // item = group * nblk + block index; own group first, then the others
+    auto claim = [&](int g0) {
+        for (int k = 0; k < QM_GQA_KV_HEADS; ++k) {
+            const int gg = (g0 + k) & (QM_GQA_KV_HEADS - 1);
+            const int i = atomicAdd(A.queue + gg, 1);
+            if (i < nblk) return gg * nblk + i;
         }
+        return -1;
     };
-    fetch(0, 0);                             // in flight during the q prep
 
-    // 1. q: RMSNorm (1+gamma, eps 1e-6; gemv.rs:586-597) and split-half RoPE
-    //    (gemv.rs:604-627) straight into the B fragments: lane (lr, lq) holds
-    //    dims 32 s + 8 lq + e of row r0 + lr, so the row's sum of squares is
-    //    a reduction over the four lanes lr + 16 lq, and each rotation pair
-    //    (i, i + 32), i = 8 lq + e, sits in one lane (s = 0 and s = 1).
-    half8 qf[8];                            // B[k = dim][n = row]: 8 dims of row n
-    {
-        const int t = r0 + lr;
-        const int tc = min(t, A.S - 1);     // rows past S: any valid row, then zeroed
-        const uint16_t* qrow = A.q_gate + ((size_t)tc * QM_GQA_HEADS + qh) * (2 * QM_GQA_HD) + 8 * lq;
-        uint4 u[8];                         // the row's 64 dims of this lane, packed bf16
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            u[s] = *reinterpret_cast<const uint4*>(qrow + 32 * s);
-            if (t >= A.S) u[s] = make_uint4(0, 0, 0, 0);
-        }
-        auto unpack = [](uint4 v, float (&x)[8]) {
-            const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                x[2 * e] = bf16_to_f32((uint16_t)(wv[e] & 0xffffu));
-                x[2 * e + 1] = bf16_to_f32((uint16_t)(wv[e] >> 16));
-            }
-        };
-        float ss = 0.0f;
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            float x[8];
-            unpack(u[s], x);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) ss = fmaf(x[e], x[e], ss);
-        }
-        ss = sum_xor32(sum_xor16(ss));
-        const float inv = 1.0f / sqrtf(ss / (float)QM_GQA_HD + 1e-6f);
-        // the softmax scale 1/sqrt(256) in base 2 is folded into q, so the
-        // scores come out of the MFMA in log2 units
-        const float sl2 = (1.0f / 16.0f) * 1.4426950408889634f;
-        auto normed = [&](int s, float (&x)[8]) {     // x * inv * (1 + gamma)
-            unpack(u[s], x);
-            const uint4 gw = *reinterpret_cast<const uint4*>(A.q_norm + 32 * s + 8 * lq);
-            const uint32_t gv[4] = {gw.x, gw.y, gw.z, gw.w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                x[2 * e] = x[2 * e] * inv * (1.0f + f16_to_f32((uint16_t)(gv[e] & 0xffffu)));
-                x[2 * e + 1] = x[2 * e + 1] * inv * (1.0f + f16_to_f32((uint16_t)(gv[e] >> 16)));
-            }
-        };
-        {
-            float x1[8], x2[8];
-            normed(0, x1);
-            normed(1, x2);
-            const float* crow = A.rope_cos + (size_t)tc * 32 + 8 * lq;
-            const float* srow = A.rope_sin + (size_t)tc * 32 + 8 * lq;
-            const float4 c0 = ld4(crow), c1 = ld4(crow + 4), s0 = ld4(srow), s1 = ld4(srow + 4);
-            const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-            const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                qf[0][e] = (_Float16)((x1[e] * cs[e] - x2[e] * sn[e]) * sl2);
-                qf[1][e] = (_Float16)((x2[e] * cs[e] + x1[e] * sn[e]) * sl2);
-            }
-        }
-#pragma unroll
-        for (int s = 2; s < 8; ++s) {
-            float x[8];
-            normed(s, x);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) qf[s][e] = (_Float16)(x[e] * sl2);
-        }
-    }
+    const int home = blockIdx.x & (QM_GQA_KV_HEADS - 1);
+    if (tid == 0) item_s = claim(home);
+    __syncthreads();
+    int item = item_s;
+    while (item >= 0) {                     // workgroup-uniform
+        const int g = item / nblk;
+        const uint16_t* kbase = A.k_cache + (size_t)g * A.cap * QM_GQA_HD;
+        const uint16_t* vbase = A.vt + (size_t)g * QM_GQA_HD * A.s_pad;
+        // the next block is claimed three tiles before this one ends: late
+        // enough to keep the longest-first order, early enough to hide the
+        // atomic's latency
+        int nxt = 0;
+        // lane-derived addresses are recomputed per row block (cheap)
+        // rather than held across blocks, which would spill them
+        int lane = tid & 63;
+        asm volatile("" : "+v"(lane));
+        const int lr = lane & 15, lq = lane >> 4;
+        const int tb = nblk - 1 - (item - g * nblk);   // longest rows first
+        const int t0 = tb * TQ3;
+        const int qh = 4 * g + (w & 3);
+        const int r0 = t0 + 16 * (w >> 2);
+        // tiles up to the block's last row, within the zero-padded V^T copy
+        const int nkt = min((t0 + TQ3 + KT - 1) / KT, A.s_pad / KT);
 
-    // O[0..15]: P V; O[16]: P times a ones B operand, i.e. the row sums of
-    // P (every column), in the same lane layout and rescaled with the rest
-    floatx4 O[17];
+        // tile fetch: block b = w + 12 j of the tile's 64 (K blocks 0..31, V^T 32..63)
+        auto fetch = [&](int kt, int buf) {
+            const int k0 = kt * KT;
 #pragma unroll
-    for (int dt = 0; dt < 17; ++dt) O[dt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    float m_run = -INFINITY;
-    const int tok = r0 + lr;
-    half8 ones;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) ones[e] = (_Float16)1.0f;
-
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // tile 0 landed (this wave's part)
-    __syncthreads();                        // ... for every wave
-
-    for (int kt = 0; kt < nkt; ++kt) {
-        const int k0 = kt * KT, b = kt & 1;
-        // the other buffer was last read before the previous barrier
-        if (kt + 1 < nkt) fetch(kt + 1, b ^ 1);
-        const char* Kb = sm + SM_K(b);
-        const char* Vb = sm + SM_V(b);
-
-        // S^T = K Q^T: fragment kk row i is key frag_key(kk, i) of the tile;
-        // K blocks read two at a time, one pair ahead of their MFMAs
-        floatx4 sT[4];
-        {
-            half8 ka[2][2];
-#pragma unroll
-            for (int j = 0; j < 2; ++j) ka[0][j] = *reinterpret_cast<const half8*>(Kb + j * 1024 + 16 * lane);
-#pragma unroll
-            for (int grp = 0; grp < 16; ++grp) {         // pair = blocks 2grp, 2grp+1 = (kk, s)
-                const int cur = grp & 1;
-                if (grp + 1 < 16) {
-#pragma unroll
-                    for (int j = 0; j < 2; ++j)
-                        ka[cur ^ 1][j] = *reinterpret_cast<const half8*>(Kb + (2 * (grp + 1) + j) * 1024 + 16 * lane);
+            for (int j = 0; j < 6; ++j) {
+                const int b = w + 12 * j;
+                if (b < 32) {
+                    const int kk = b >> 3, s = b & 7;                  // K block: S^T fragment kk, k-step s
+                    const int key = min(k0 + frag_key(kk, lr), A.S - 1);  // rows past S feed masked scores only
+                    dma16(kbase + (size_t)key * QM_GQA_HD + 32 * s + 8 * lq, sm_lds + SM_K(buf) + 1024 * b);
+                } else if (b < 64) {
+                    const int dt = (b - 32) >> 1, ks = b & 1;          // V^T block: dims tile dt, keys step ks
+                    dma16(vbase + (size_t)(16 * dt + lr) * A.s_pad + k0 + 32 * ks + 8 * lq,
+                          sm_lds + SM_V(buf) + 1024 * (b - 32));
                 }
-                const int kk = grp >> 2, s0 = 2 * (grp & 3);
-                if ((grp & 3) == 0) sT[kk] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    sT[kk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[cur][j], qf[s0 + j], sT[kk], 0, 0, 0);
             }
-        }
-        // online softmax (base 2); only tiles that reach past the wave's
-        // first row need the causal mask
-        float mx = -INFINITY;
-        if (k0 + KT - 1 > r0) {                 // wave-uniform
+        };
+        fetch(0, 0);                             // in flight during the q prep
+
+        // 1. q: RMSNorm (1+gamma, eps 1e-6; gemv.rs:586-597) and split-half RoPE
+        //    (gemv.rs:604-627) straight into the B fragments: lane (lr, lq) holds
+        //    dims 32 s + 8 lq + e of row r0 + lr, so the row's sum of squares is
+        //    a reduction over the four lanes lr + 16 lq, and each rotation pair
+        //    (i, i + 32), i = 8 lq + e, sits in one lane (s = 0 and s = 1).
+        half8 qf[8];                            // B[k = dim][n = row]: 8 dims of row n
+        {
+            const int t = r0 + lr;
+            const int tc = min(t, A.S - 1);     // rows past S: any valid row, then zeroed
+            const uint16_t* qrow = A.q_gate + ((size_t)tc * QM_GQA_HEADS + qh) * (2 * QM_GQA_HD) + 8 * lq;
+            uint4 u[8];                         // the row's 64 dims of this lane, packed bf16
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk)
+            for (int s = 0; s < 8; ++s) {
+                u[s] = *reinterpret_cast<const uint4*>(qrow + 32 * s);
+                if (t >= A.S) u[s] = make_uint4(0, 0, 0, 0);
+            }
+            auto unpack = [](uint4 v, float (&x)[8]) {
+                const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    if (k0 + frag_key(kk, 4 * lq + e) > tok) sT[kk][e] = -INFINITY;
-                    mx = fmaxf(mx, sT[kk][e]);
+                    x[2 * e] = bf16_to_f32((uint16_t)(wv[e] & 0xffffu));
+                    x[2 * e + 1] = bf16_to_f32((uint16_t)(wv[e] >> 16));
                 }
-        } else {
+            };
+            float ss = 0.0f;
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk)
+            for (int s = 0; s < 8; ++s) {
+                float x[8];
+                unpack(u[s], x);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) mx = fmaxf(mx, sT[kk][e]);
-        }
-        mx = max_xor32(max_xor16(mx));
-        // key 0 is visible to every row, so mx is finite from tile 0 on
-        const float m_new = mx > m_run + RESCALE_SLACK ? mx : m_run;
-        const float corr = __builtin_amdgcn_exp2f(m_run - m_new);      // 1 unless moved; 0 on tile 0
-        m_run = m_new;
-        half8 pf[2];                            // PV A operand: keys 32 ks + 8 lq .. + 7 of row lr
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                pf[ks][e] = (_Float16)__builtin_amdgcn_exp2f(sT[2 * ks][e] - m_new);
-                pf[ks][4 + e] = (_Float16)__builtin_amdgcn_exp2f(sT[2 * ks + 1][e] - m_new);
+                for (int e = 0; e < 8; ++e) ss = fmaf(x[e], x[e], ss);
             }
-        // rescale O (lane (dim lr, lq) holds rows 4lq + e) when any row of
-        // the wave moved its reference max
-        if (__any(corr != 1.0f)) {
-            float f[4];                     // row 4lq + e's factor sits in lane 4lq + e
+            ss = sum_xor32(sum_xor16(ss));
+            const float inv = 1.0f / sqrtf(ss / (float)QM_GQA_HD + 1e-6f);
+            // the softmax scale 1/sqrt(256) in base 2 is folded into q, so the
+            // scores come out of the MFMA in log2 units
+            const float sl2 = (1.0f / 16.0f) * 1.4426950408889634f;
+            auto normed = [&](int s, float (&x)[8]) {     // x * inv * (1 + gamma)
+                unpack(u[s], x);
+                const uint4 gw = *reinterpret_cast<const uint4*>(A.q_norm + 32 * s + 8 * lq);
+                const uint32_t gv[4] = {gw.x, gw.y, gw.z, gw.w};
 #pragma unroll
-            for (int e = 0; e < 4; ++e) f[e] = __shfl(corr, 4 * lq + e);
+                for (int e = 0; e < 4; ++e) {
+                    x[2 * e] = x[2 * e] * inv * (1.0f + f16_to_f32((uint16_t)(gv[e] & 0xffffu)));
+                    x[2 * e + 1] = x[2 * e + 1] * inv * (1.0f + f16_to_f32((uint16_t)(gv[e] >> 16)));
+                }
+            };
+            {
+                float x1[8], x2[8];
+                normed(0, x1);
+                normed(1, x2);
+                const float* crow = A.rope_cos + (size_t)tc * 32 + 8 * lq;
+                const float* srow = A.rope_sin + (size_t)tc * 32 + 8 * lq;
+                const float4 c0 = ld4(crow), c1 = ld4(crow + 4), s0 = ld4(srow), s1 = ld4(srow + 4);
+                const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+                const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
 #pragma unroll
-            for (int dt = 0; dt < 17; ++dt) {
-                O[dt][0] *= f[0]; O[dt][1] *= f[1]; O[dt][2] *= f[2]; O[dt][3] *= f[3];
+                for (int e = 0; e < 8; ++e) {
+                    qf[0][e] = (_Float16)((x1[e] * cs[e] - x2[e] * sn[e]) * sl2);
+                    qf[1][e] = (_Float16)((x2[e] * cs[e] + x1[e] * sn[e]) * sl2);
+                }
+            }
+#pragma unroll
+            for (int s = 2; s < 8; ++s) {
+                float x[8];
+                normed(s, x);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) qf[s][e] = (_Float16)(x[e] * sl2);
             }
         }
-        // O += P V   (16x16x32; B lane (dim, lq) holds keys 32 ks + 8 lq .. + 7),
-        // V^T blocks read two at a time, one pair ahead of the MFMAs
-        {
-            half8 vb[2][2];
+
+        // O[0..15]: P V; O[16]: P times a ones B operand, i.e. the row sums of
+        // P (every column), in the same lane layout and rescaled with the rest
+        floatx4 O[17];
 #pragma unroll
-            for (int j = 0; j < 2; ++j) vb[0][j] = *reinterpret_cast<const half8*>(Vb + j * 1024 + 16 * lane);
+        for (int dt = 0; dt < 17; ++dt) O[dt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        float m_run = -INFINITY;
+        const int tok = r0 + lr;
+        half8 ones;
 #pragma unroll
-            for (int dt = 0; dt < 16; ++dt) {            // pair = blocks (dt, 0), (dt, 1)
-                const int cur = dt & 1;
-                if (dt + 1 < 16) {
+        for (int e = 0; e < 8; ++e) ones[e] = (_Float16)1.0f;
+
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // tile 0 landed (this wave's part)
+        __syncthreads();                        // ... for every wave
+
+        const int kt_claim = max(nkt - 3, 0);
+        for (int kt = 0; kt < nkt; ++kt) {
+            if (tid == 0 && kt == kt_claim) nxt = claim(home);
+            const int k0 = kt * KT, b = kt & 1;
+            // the other buffer was last read before the previous barrier
+            if (kt + 1 < nkt) fetch(kt + 1, b ^ 1);
+            const char* Kb = sm + SM_K(b);
+            const char* Vb = sm + SM_V(b);
+
+            // S^T = K Q^T: fragment kk row i is key frag_key(kk, i) of the tile;
+            // K blocks read two at a time, one pair ahead of their MFMAs
+            floatx4 sT[4];
+            {
+                half8 ka[2][2];
+#pragma unroll
+                for (int j = 0; j < 2; ++j) ka[0][j] = *reinterpret_cast<const half8*>(Kb + j * 1024 + 16 * lane);
+#pragma unroll
+                for (int grp = 0; grp < 16; ++grp) {         // pair = blocks 2grp, 2grp+1 = (kk, s)
+                    const int cur = grp & 1;
+                    if (grp + 1 < 16) {
+#pragma unroll
+                        for (int j = 0; j < 2; ++j)
+                            ka[cur ^ 1][j] = *reinterpret_cast<const half8*>(Kb + (2 * (grp + 1) + j) * 1024 + 16 * lane);
+                    }
+                    const int kk = grp >> 2, s0 = 2 * (grp & 3);
+                    if ((grp & 3) == 0) sT[kk] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                     for (int j = 0; j < 2; ++j)
-                        vb[cur ^ 1][j] = *reinterpret_cast<const half8*>(Vb + (2 * (dt + 1) + j) * 1024 + 16 * lane);
+                        sT[kk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[cur][j], qf[s0 + j], sT[kk], 0, 0, 0);
+                }
+            }
+            // online softmax (base 2); only tiles that reach past the wave's
+            // first row need the causal mask
+            float mx = -INFINITY;
+            if (k0 + KT - 1 > r0) {                 // wave-uniform
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        if (k0 + frag_key(kk, 4 * lq + e) > tok) sT[kk][e] = -INFINITY;
+                        mx = fmaxf(mx, sT[kk][e]);
+                    }
+            } else {
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) mx = fmaxf(mx, sT[kk][e]);
+            }
+            mx = max_xor32(max_xor16(mx));
+            // key 0 is visible to every row, so mx is finite from tile 0 on
+            const float m_new = mx > m_run + RESCALE_SLACK ? mx : m_run;
+            const float corr = __builtin_amdgcn_exp2f(m_run - m_new);      // 1 unless moved; 0 on tile 0
+            m_run = m_new;
+            half8 pf[2];                            // PV A operand: keys 32 ks + 8 lq .. + 7 of row lr
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    pf[ks][e] = (_Float16)__builtin_amdgcn_exp2f(sT[2 * ks][e] - m_new);
+                    pf[ks][4 + e] = (_Float16)__builtin_amdgcn_exp2f(sT[2 * ks + 1][e] - m_new);
+                }
+            // rescale O (lane (dim lr, lq) holds rows 4lq + e) when any row of
+            // the wave moved its reference max
+            if (__any(corr != 1.0f)) {
+                float f[4];                     // row 4lq + e's factor sits in lane 4lq + e
+#pragma unroll
+                for (int e = 0; e < 4; ++e) f[e] = __shfl(corr, 4 * lq + e);
+#pragma unroll
+                for (int dt = 0; dt < 17; ++dt) {
+                    O[dt][0] *= f[0]; O[dt][1] *= f[1]; O[dt][2] *= f[2]; O[dt][3] *= f[3];
+                }
+            }
+            // O += P V   (16x16x32; B lane (dim, lq) holds keys 32 ks + 8 lq .. + 7),
+            // V^T blocks read two at a time, one pair ahead of the MFMAs
+            {
+                half8 vb[2][2];
+#pragma unroll
+                for (int j = 0; j < 2; ++j) vb[0][j] = *reinterpret_cast<const half8*>(Vb + j * 1024 + 16 * lane);
+#pragma unroll
+                for (int dt = 0; dt < 16; ++dt) {            // pair = blocks (dt, 0), (dt, 1)
+                    const int cur = dt & 1;
+                    if (dt + 1 < 16) {
+#pragma unroll
+                        for (int j = 0; j < 2; ++j)
+                            vb[cur ^ 1][j] = *reinterpret_cast<const half8*>(Vb + (2 * (dt + 1) + j) * 1024 + 16 * lane);
+                    }
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks)
+                        O[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[ks], vb[cur][ks], O[dt], 0, 0, 0);
                 }
 #pragma unroll
-                for (int ks = 0; ks < 2; ++ks)
-                    O[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[ks], vb[cur][ks], O[dt], 0, 0, 0);
+                for (int ks = 0; ks < 2; ++ks) O[16] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[ks], ones, O[16], 0, 0, 0);
             }
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) O[16] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[ks], ones, O[16], 0, 0, 0);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // next tile landed (this wave's part)
+            __syncthreads();                    // ... for every wave; this tile fully consumed
         }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // next tile landed (this wave's part)
-        __syncthreads();                    // ... for every wave; this tile fully consumed
-    }
 
-    // 3. out = (O / l) * sigmoid(gate), bf16 (gemv.rs:1441-1444); O[16][e]
-    //    is row 4lq + e's sum of P, in this very lane
-    float iv[4];
+        // 3. out = (O / l) * sigmoid(gate), bf16 (gemv.rs:1441-1444); O[16][e]
+        //    is row 4lq + e's sum of P, in this very lane.  Every gate load is
+        //    issued before the first store: the compiler cannot tell the two
+        //    pointers apart, and interleaved they cost one memory round trip
+        //    per element.
+        uint16_t gbuf[4][16];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) iv[e] = 1.0f / O[16][e];
+        for (int e = 0; e < 4; ++e) {
+            const int tc = min(r0 + 4 * lq + e, A.S - 1);
+            const uint16_t* gate = A.q_gate + ((size_t)tc * QM_GQA_HEADS + qh) * (2 * QM_GQA_HD) + QM_GQA_HD + lr;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int t = r0 + 4 * lq + e;
-        if (t >= A.S) continue;
-        const uint16_t* gate = A.q_gate + ((size_t)t * QM_GQA_HEADS + qh) * (2 * QM_GQA_HD) + QM_GQA_HD;
-        uint16_t* o = A.out + ((size_t)t * QM_GQA_HEADS + qh) * QM_GQA_HD;
-#pragma unroll
-        for (int dt = 0; dt < 16; ++dt) {
-            const int d = 16 * dt + lr;
-            const float gv = bf16_to_f32(gate[d]);
-            o[d] = f32_to_bf16((O[dt][e] * iv[e]) * sigmoid_f(gv));
+            for (int dt = 0; dt < 16; ++dt) gbuf[e][dt] = gate[16 * dt];
         }
+        float iv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) iv[e] = 1.0f / O[16][e];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int t = r0 + 4 * lq + e;
+            if (t >= A.S) continue;
+            uint16_t* o = A.out + ((size_t)t * QM_GQA_HEADS + qh) * QM_GQA_HD + lr;
+#pragma unroll
+            for (int dt = 0; dt < 16; ++dt)
+                o[16 * dt] = f32_to_bf16((O[dt][e] * iv[e]) * sigmoid_fast(bf16_to_f32(gbuf[e][dt])));
+        }
+        if (tid == 0) item_s = nxt;
+        __syncthreads();
+        item = item_s;
     }
 }

@@ -85,6 +85,10 @@ QM_DEV float silu_fast(float x) {
 }
 QM_DEV float softplus_f(float x) { return x > 20.0f ? x : logf(1.0f + expf(x)); }
 QM_DEV float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+// 1 / (1 + 2^(-x log2 e)) on v_exp_f32 / v_rcp_f32 (about 1 ulp each)
+QM_DEV float sigmoid_fast(float x) {
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
+}
 
 // ---- memory helpers ------------------------------------------------------
 QM_DEV float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }

@@ -113,6 +113,7 @@ struct GqaPrefillArgs {
     uint16_t* v_cache;
     uint16_t* vt;            // f16 [4][256][s_pad]
     uint16_t* out;           // bf16 [S][16][256]
+    int32_t* queue;          // [4] next row block per kv head (zeroed by the kv kernel)
     int64_t cap;
     int32_t S;
     int32_t s_pad;

@@ -49,6 +49,7 @@ struct qm_context {
     std::string err;
     int64_t opt_dn_threads = 0;
     int64_t opt_gqa_chunk = 0;
+    int num_cu = 0;                // compute units of the device
 };
 
 struct qm_graph {
@@ -155,6 +156,11 @@ struct DnPrefillLayout {
     size_t Wn, Qt, Ut, Y0t, Ktt, gC, Sc, total;
 };
 
+// GQA prefill workspace: the transposed V copy, then the row-block queue.
+size_t gqa_prefill_vt_bytes(size_t s_pad) {
+    return (static_cast<size_t>(QM_GQA_KV_HEADS) * QM_GQA_HD * s_pad * 2 + 255) & ~static_cast<size_t>(255);
+}
+
 DnPrefillLayout dn_prefill_layout(int64_t T) {
     const int64_t nc = (T + QM_DN_CHUNK - 1) / QM_DN_CHUNK;
     auto al = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
@@ -236,6 +242,9 @@ int32_t qm_create(qm_context** out, const qm_config* cfg, const char* code_objec
     qm_context* c = new qm_context();
     c->device = device;
     c->cfg = want;
+    if (hipDeviceGetAttribute(&c->num_cu, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+        c->num_cu <= 0)
+        c->num_cu = 256;
     std::string dir = code_object_dir ? code_object_dir : library_dir();
     const char* files[] = {"qm_dn_decode.hsaco", "qm_gqa_decode.hsaco", "qm_util.hsaco",
                            "qm_dn_prefill.hsaco", "qm_gqa_prefill.hsaco"};
@@ -577,7 +586,7 @@ int32_t qm_reserve(qm_context* c, int32_t max_batch, int32_t max_kv_len, int32_t
     if (max_prefill_tokens > 0) {
         ws = std::max(ws, dn_prefill_layout(max_prefill_tokens).total);
         const size_t s_pad = (static_cast<size_t>(max_prefill_tokens) + 63) / 64 * 64;
-        ws = std::max(ws, static_cast<size_t>(QM_GQA_KV_HEADS) * QM_GQA_HD * s_pad * 2);
+        ws = std::max(ws, gqa_prefill_vt_bytes(s_pad) + 256);
     }
     return ensure(c, c->stream, ws);
 }
@@ -631,15 +640,20 @@ int32_t qm_gqa_prefill(qm_context* c, qm_stream stream, int32_t seq_len, const u
                     static_cast<long long>(cap));
     hipStream_t s = pick(c, stream);
     const int32_t s_pad = (seq_len + 63) / 64 * 64;
-    int32_t st = ensure(c, s, static_cast<size_t>(QM_GQA_KV_HEADS) * QM_GQA_HD * s_pad * 2);
+    const size_t vt_bytes = gqa_prefill_vt_bytes(s_pad);
+    int32_t st = ensure(c, s, vt_bytes + 256);
     if (st != QM_OK) return st;
     GqaPrefillArgs ga{q_gate, k, v, q_norm, k_norm, rope_cos, rope_sin, k_cache, v_cache,
-                      static_cast<uint16_t*>(c->ws), out, cap, seq_len, s_pad};
+                      static_cast<uint16_t*>(c->ws), out,
+                      reinterpret_cast<int32_t*>(static_cast<char*>(c->ws) + vt_bytes), cap, seq_len, s_pad};
     st = launch(c, c->f_gqp_kv, static_cast<uint32_t>(s_pad / 64) * QM_GQA_KV_HEADS, 256, ga, s,
                 "qm_gqa_prefill_kv");
     if (st != QM_OK) return st;
-    // 48 query rows per workgroup, 12 waves
-    return launch(c, c->f_gqp_attn, static_cast<uint32_t>((seq_len + 47) / 48) * QM_GQA_KV_HEADS, 768, ga, s,
+    // persistent: one workgroup per CU (a multiple of the 4 kv groups), no
+    // more than there are 48-row blocks
+    const int32_t nblk = (seq_len + 47) / 48;
+    const int32_t per_group = std::max(1, std::min(c->num_cu / QM_GQA_KV_HEADS, nblk));
+    return launch(c, c->f_gqp_attn, static_cast<uint32_t>(per_group) * QM_GQA_KV_HEADS, 768, ga, s,
                   "qm_gqa_prefill_attn");
 }
 
