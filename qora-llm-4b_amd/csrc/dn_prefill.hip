@@ -49,8 +49,19 @@ QM_DEV half4 to_half4(floatx4 v) {
     return r;
 }
 
+// Per-v-head LDS of the chunk kernel.
+struct ChunkHeadLds {
+    _Float16 Vs[CHK][136];                         // v row-major
+    _Float16 pm[CHK][72];                          // P (lower, incl. diagonal)
+    _Float16 am[CHK][72];                          // A (strictly lower)
+    _Float16 Td[4][16][24];                        // (I + A_bb)^-1
+    __attribute__((aligned(16))) float Gs[CHK];
+    float Bs[CHK], Eg[CHK], BG[CHK];
+    __attribute__((aligned(16))) float Kd[CHK];
+};
+
 // ============================================================================
-// 2. chunk: per (chunk, v-head), everything independent of the entering state
+// 2. chunk: per (chunk, pair of v-heads sharing a qk-head), everything independent of the entering state
 // ============================================================================
 // [W | U~] = (I + A)^-1 [diag(beta gamma) K | diag(beta) V] is solved by block
 // forward substitution over the four 16-token blocks b:
@@ -61,49 +72,59 @@ QM_DEV half4 to_half4(floatx4 v) {
 // an X_k fragment (4 consecutive tokens of one column per lane) is already
 // the B operand of the next block's correction, so the solve needs no
 // workgroup barrier.
-extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillArgs A) {
-    __shared__ _Float16 Qs[CHK][136];              // q row-major; later Q~ staging
-    __shared__ _Float16 Ks[CHK][136];              // k row-major; later -W staging
-    __shared__ _Float16 Vs[CHK][136];              // v row-major
-    __shared__ _Float16 Pm[CHK][72];               // P (lower, incl. diagonal)
-    __shared__ _Float16 Am[CHK][72];               // A (strictly lower)
-    __shared__ _Float16 Td[4][16][24];             // (I + A_bb)^-1
-    __shared__ __attribute__((aligned(16))) float Gs[CHK];
-    __shared__ float Bs[CHK], Eg[CHK], BG[CHK], Kd[CHK];
+extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillArgs A) {
+    __shared__ _Float16 Qs[CHK][136];              // q row-major (both v-heads)
+    __shared__ _Float16 Ks[CHK][136];              // k row-major (both v-heads)
+    __shared__ ChunkHeadLds hl[2];
 
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-    const int c = blockIdx.x / QM_DN_V_HEADS, h = blockIdx.x % QM_DN_V_HEADS;
-    const int qkh = h >> 1;                        // GVA: v-head h reads qk-head h/2 (gemv.rs:1160)
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int hh = tid >> 8;                       // v-head of the pair: waves 0-3 / 4-7
+    const int w = (tid >> 6) & 3;                  // wave within its head's group
+    const int ht = tid & 255;                      // thread within its head's group
+    // GVA: v-heads 2 qkh and 2 qkh + 1 read qk-head qkh (gemv.rs:1160)
+    const int c = blockIdx.x / QM_DN_QK_HEADS, qkh = blockIdx.x % QM_DN_QK_HEADS;
+    const int h = 2 * qkh + hh;
     const int t0 = c * CHK;
     const size_t hc = (size_t)h * A.nc + c;
     const int lr = lane & 15, lq = lane >> 4;
+    ChunkHeadLds& H = hl[hh];
+    _Float16 (&Vs)[CHK][136] = H.Vs;
+    _Float16 (&Pm)[CHK][72] = H.pm;
+    _Float16 (&Am)[CHK][72] = H.am;
+    _Float16 (&Td)[4][16][24] = H.Td;
+    float (&Gs)[CHK] = H.Gs;
+    float (&Bs)[CHK] = H.Bs;
+    float (&Eg)[CHK] = H.Eg;
+    float (&BG)[CHK] = H.BG;
+    float (&Kd)[CHK] = H.Kd;
 
     // ---- 0. causal conv1d (gemv.rs:1132-1147), SiLU (:1149), per-head L2
-    //      norm and q scale (:1151-1156) of this chunk's q, k (qk-head h/2)
-    //      and v (v-head h), straight into LDS; gates (:1171-1172).
-    //      Thread (cg, tg) = (tid & 15, tid >> 4) owns channels 8cg .. 8cg+7
-    //      for tokens 4tg .. 4tg+3: the 16 lanes of a DPP row share the
-    //      tokens, so the L2 norm is a row reduction.
+    //      norm and q scale (:1151-1156) of this chunk's q, k (qk-head qkh,
+    //      once for both v-heads) and the two v-heads' v, straight into LDS;
+    //      gates (:1171-1172).  Threads 0-255 do q and v of head 2qkh,
+    //      threads 256-511 k and v of head 2qkh+1.  Thread (cg, tg) =
+    //      (ht & 15, ht >> 4) owns channels 8cg .. 8cg+7 for tokens 4tg ..
+    //      4tg+3: the 16 lanes of a DPP row share the tokens, so the L2 norm
+    //      is a row reduction.
     {
-        const int cg = tid & 15, tg = tid >> 4;
-        int chb[3];                                // first channel of this thread, per part
-        chb[0] = qkh * QM_DN_HD + 8 * cg;
-        chb[1] = QM_DN_QK_DIM + qkh * QM_DN_HD + 8 * cg;
-        chb[2] = 2 * QM_DN_QK_DIM + h * QM_DN_HD + 8 * cg;
-        // gate inputs (wave 0) first: they are consumed last
+        const int cg = ht & 15, tg = ht >> 4;
+        int chb[2];                                // first channel of this thread, per part
+        chb[0] = hh * QM_DN_QK_DIM + qkh * QM_DN_HD + 8 * cg;          // q or k
+        chb[1] = 2 * QM_DN_QK_DIM + h * QM_DN_HD + 8 * cg;             // v of head h
+        // gate inputs (wave 0 of each head) first: they are consumed last
         float ga = 0.0f, gb = 0.0f;
-        if (tid < CHK) {
-            const int t = min(t0 + tid, A.T - 1);
+        if (ht < CHK) {
+            const int t = min(t0 + ht, A.T - 1);
             ga = A.a[(size_t)t * QM_DN_V_HEADS + h];
             gb = A.b[(size_t)t * QM_DN_V_HEADS + h];
         }
         const float a_log_h = A.a_log[h], dt_bias_h = A.dt_bias[h];
-        // all 21 raw rows the thread needs (7 per part), loaded at clamped,
+        // all 14 raw rows the thread needs (7 per part), loaded at clamped,
         // always valid rows before any arithmetic; rows before the sequence
         // come from the conv buffer, and the tokens past it are zeroed below
-        uint4 u[3][7];
+        uint4 u[2][7];
 #pragma unroll
-        for (int part = 0; part < 3; ++part)
+        for (int part = 0; part < 2; ++part)
 #pragma unroll
             for (int r = 0; r < 7; ++r) {
                 const int t = min(max(t0 + 4 * tg - 3 + r, 0), A.T - 1);
@@ -114,9 +135,9 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
         for (int e = 0; e < 8; ++e) wt[e] = ld4(A.conv_w + (size_t)(chb[0] + e) * 4);
         const bool tail = t0 + CHK > A.T;          // last chunk, partly past the sequence
 #pragma unroll
-        for (int part = 0; part < 3; ++part) {     // q, k, v
+        for (int part = 0; part < 2; ++part) {     // q or k, then v
             const int ch0 = chb[part];
-            if (part < 2) {                        // next part's taps while this one computes
+            if (part < 1) {                        // next part's taps while this one computes
 #pragma unroll
                 for (int e = 0; e < 8; ++e) wn[e] = ld4(A.conv_w + (size_t)(chb[part + 1] + e) * 4);
             }
@@ -144,8 +165,8 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
                     }
                 }
             }
-            _Float16 (*dst)[136] = part == 0 ? Qs : part == 1 ? Ks : Vs;
-            const float scale = part == 0 ? 1.0f / sqrtf((float)QM_DN_HD) : 1.0f;
+            _Float16 (*dst)[136] = part == 1 ? Vs : (hh == 0 ? Qs : Ks);
+            const float scale = (part == 0 && hh == 0) ? 1.0f / sqrtf((float)QM_DN_HD) : 1.0f;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int tok = 4 * tg + j;
@@ -159,7 +180,7 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
                     sacc = fmaf(x[j + 3][e], wt[e].w, sacc);
                     v[e] = silu_fast(sacc);
                 }
-                if (part < 2) {
+                if (part == 0) {
                     // x /= ||x|| when ||x|| > 1e-12, q *= 1/sqrt(128)
                     float ss = 0.0f;
 #pragma unroll
@@ -182,35 +203,35 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
             // are zeroed here (a token's conv and norm involve only itself
             // and earlier rows, so no valid token saw them).
 #pragma unroll
-            for (int part = 0; part < 3; ++part) {
-                _Float16 (*dst)[136] = part == 0 ? Qs : part == 1 ? Ks : Vs;
+            for (int part = 0; part < 2; ++part) {
+                _Float16 (*dst)[136] = part == 1 ? Vs : (hh == 0 ? Qs : Ks);
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                     if (t0 + 4 * tg + j >= A.T) *reinterpret_cast<half8*>(&dst[4 * tg + j][8 * cg]) = half8{};
             }
         }
-        if (tid < CHK) {
+        if (ht < CHK) {
             // log alpha = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b);
             // padded tokens get alpha = 1, beta = 0 (no effect on the state);
             // then the inclusive prefix sum over the chunk (one wave)
             float g = 0.0f, be = 0.0f;
-            if (t0 + tid < A.T) {
+            if (t0 + ht < A.T) {
                 g = -expf(a_log_h) * softplus_f(ga + dt_bias_h);
                 be = 1.0f / (1.0f + expf(-gb));
             }
 #pragma unroll
             for (int off = 1; off < 64; off <<= 1) {
                 const float o = __shfl_up(g, off);
-                if (tid >= off) g += o;
+                if (ht >= off) g += o;
             }
-            Gs[tid] = g;
-            Bs[tid] = be;
-            Eg[tid] = expf(g);                   // gamma_i
-            BG[tid] = be * expf(g);              // beta_i gamma_i
+            Gs[ht] = g;
+            Bs[ht] = be;
+            Eg[ht] = expf(g);                   // gamma_i
+            BG[ht] = be * expf(g);              // beta_i gamma_i
         }
     }
     __syncthreads();
-    if (tid < CHK) Kd[tid] = expf(Gs[CHK - 1] - Gs[tid]);     // gamma_C / gamma_i
+    if (ht < CHK) Kd[ht] = expf(Gs[CHK - 1] - Gs[ht]);       // gamma_C / gamma_i
 
     // ---- 1. KK^T and QK^T (16x16x32 f16), masked and decayed -> A, P (f16).
     //      Computed transposed, C = K_j K_i^T and K_j Q_i^T: lane (lr, lq)
@@ -272,7 +293,7 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
 
     // ---- 3. [W | U~] by block forward substitution (16x16x16 f16)
     //      tiles: cc = 0,1 -> W k-col tiles 2w+cc; cc = 2,3 -> U~ v-col tiles 2w+cc-2
-    floatx4 cw[4][2], cu[4][2];
+    floatx4 cu[4][2];
     half4 xh[4][4];                                   // X_b fragments as f16 B operands
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
@@ -294,7 +315,7 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
             floatx4 x = {0.0f, 0.0f, 0.0f, 0.0f};
             x = __builtin_amdgcn_mfma_f32_16x16x16f16(tb, to_half4(r), x, 0, 0, 0);
             xh[b][cc] = to_half4(x);
-            if (cc < 2) cw[b][cc] = x; else cu[b][cc - 2] = x;
+            if (cc >= 2) cu[b][cc - 2] = x;
         }
     }
 
@@ -345,52 +366,56 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_chunk(DnPrefillA
             }
         }
     }
-    // K~^T = (gamma_C / gamma_j) K^T
-    {
-        uint16_t* dst = A.Ktt + hc * CHK * QM_DN_HD;
+    // -W, Q~ and K~^T want four consecutive columns of one token (or tokens
+    // of one column) per lane, the transpose of a C fragment.  A C fragment
+    // read as an A operand is the transposed tile, so one 16x16x16 product
+    // with an identity B operand transposes it in registers (exactly: every
+    // product is x * 1 or x * 0 in fp32).
+    half4 idm;                                    // B[k][n] = (k == n): lane (n, kq) holds k = 4kq .. +3
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int q = tid + 256 * r, kt = q >> 7, p = (q >> 6) & 1, l = q & 63;
-            const int row = 16 * kt + (l & 15), tk0 = 32 * p + 4 * (l >> 4);
-            half8 hv;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                hv[e] = (_Float16)((float)Ks[tk0 + e][row] * Kd[tk0 + e]);
-                hv[4 + e] = (_Float16)((float)Ks[tk0 + 16 + e][row] * Kd[tk0 + 16 + e]);
-            }
-            *reinterpret_cast<half8*>(dst + (size_t)q * 8) = hv;
-        }
-    }
-    if (tid == 0) A.gC[hc] = expf(Gs[CHK - 1]);
-    __syncthreads();     // Ks and Qs are free: stage -W and Q~ token-major
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
-            const int col = 16 * (2 * w + cc) + lr;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int tk = 16 * i + 4 * lq + e;
-                Ks[tk][col] = (_Float16)(-cw[i][cc][e]);
-                Qs[tk][col] = (_Float16)cq[i][cc][e];
-            }
-        }
-    __syncthreads();
+    for (int e = 0; e < 4; ++e) idm[e] = (_Float16)(4 * lq + e == lr ? 1.0f : 0.0f);
+    auto transpose = [&](half4 a) {
+        return to_half4(__builtin_amdgcn_mfma_f32_16x16x16f16(a, idm, floatx4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0));
+    };
+    // -W and Q~: piece 4i + w holds col tiles 2w, 2w+1 of token block i
     {
         uint16_t* wdst = A.Wn + hc * CHK * QM_DN_HD;
         uint16_t* qdst = A.Qt + hc * CHK * QM_DN_HD;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int q = tid + 256 * r, i = q >> 8, p = (q >> 6) & 3, l = q & 63;
-            const int row = 16 * i + (l & 15), c0 = 32 * p + 4 * (l >> 4);
-            const half4 w0 = *reinterpret_cast<const half4*>(&Ks[row][c0]);
-            const half4 w1 = *reinterpret_cast<const half4*>(&Ks[row][c0 + 16]);
-            const half4 q0 = *reinterpret_cast<const half4*>(&Qs[row][c0]);
-            const half4 q1 = *reinterpret_cast<const half4*>(&Qs[row][c0 + 16]);
-            *reinterpret_cast<half8*>(wdst + (size_t)q * 8) = half8{w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
-            *reinterpret_cast<half8*>(qdst + (size_t)q * 8) = half8{q0[0], q0[1], q0[2], q0[3], q1[0], q1[1], q1[2], q1[3]};
+        for (int i = 0; i < 4; ++i) {
+            const half4 w0 = transpose(-xh[i][0]), w1 = transpose(-xh[i][1]);
+            const half4 q0 = transpose(to_half4(cq[i][0])), q1 = transpose(to_half4(cq[i][1]));
+            const size_t o = (size_t)((4 * i + w) * 64 + lane) * 8;
+            *reinterpret_cast<half8*>(wdst + o) = cat8(w0, w1);
+            *reinterpret_cast<half8*>(qdst + o) = cat8(q0, q1);
         }
     }
+    // K~^T = (gamma_C / gamma_j) K^T: piece 2kt + p, kt = 2w, 2w+1, holds
+    // token blocks 2p, 2p+1 of k-col tile kt; the A operand of a K tile is a
+    // row read (token 16 tau + lr, cols 16 kt + 4 lq .. +3)
+    {
+        uint16_t* dst = A.Ktt + hc * CHK * QM_DN_HD;
+        float4 kd[4];
+#pragma unroll
+        for (int tau = 0; tau < 4; ++tau) kd[tau] = *reinterpret_cast<const float4*>(&Kd[16 * tau + 4 * lq]);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int kt = 2 * w + t;
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                half4 hv[2];
+#pragma unroll
+                for (int hb = 0; hb < 2; ++hb) {
+                    const int tau = 2 * p + hb;
+                    const half4 a = *reinterpret_cast<const half4*>(&Ks[16 * tau + lr][16 * kt + 4 * lq]);
+                    const floatx4 kc = __builtin_amdgcn_mfma_f32_16x16x16f16(a, idm, floatx4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                    hv[hb] = to_half4(floatx4{kc[0] * kd[tau].x, kc[1] * kd[tau].y, kc[2] * kd[tau].z, kc[3] * kd[tau].w});
+                }
+                *reinterpret_cast<half8*>(dst + (size_t)((2 * kt + p) * 64 + lane) * 8) = cat8(hv[0], hv[1]);
+            }
+        }
+    }
+    if (ht == 0) A.gC[hc] = expf(Gs[CHK - 1]);
 }
 
 // ============================================================================

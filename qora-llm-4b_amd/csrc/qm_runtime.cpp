@@ -614,7 +614,7 @@ int32_t qm_deltanet_prefill(qm_context* c, qm_stream stream, int32_t seq_len, co
                      reinterpret_cast<uint16_t*>(ws + L.Qt), reinterpret_cast<uint16_t*>(ws + L.Ut),
                      reinterpret_cast<uint16_t*>(ws + L.Y0t), reinterpret_cast<uint16_t*>(ws + L.Ktt),
                      reinterpret_cast<float*>(ws + L.gC), reinterpret_cast<uint16_t*>(ws + L.Sc), seq_len, nc};
-    st = launch(c, c->f_dnp_chunk, static_cast<uint32_t>(nc) * QM_DN_V_HEADS, 256, pa, s, "qm_dn_prefill_chunk");
+    st = launch(c, c->f_dnp_chunk, static_cast<uint32_t>(nc) * QM_DN_QK_HEADS, 512, pa, s, "qm_dn_prefill_chunk");
     if (st != QM_OK) return st;
     st = launch(c, c->f_dnp_scan, QM_DN_V_HEADS * 8, 256, pa, s, "qm_dn_prefill_scan");
     if (st != QM_OK) return st;
