@@ -59,14 +59,54 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_prefill_kv(GqaPrefillAr
     const int t0 = (blockIdx.x / QM_GQA_KV_HEADS) * 64;
     // the attention kernel that follows takes its row blocks from these
     if (blockIdx.x == 0 && tid < QM_GQA_KV_HEADS) A.queue[tid] = 0;
-    // K: wave w normalises and rotates tokens t0+16w .. t0+16w+15
-    for (int j = 0; j < 16; ++j) {
-        const int t = t0 + 16 * w + j;
-        if (t >= A.S) break;                                     // wave-uniform
-        const uint2 raw = *reinterpret_cast<const uint2*>(A.k + ((size_t)t * QM_GQA_KV_HEADS + g) * QM_GQA_HD + 4 * lane);
-        const float4 x = norm_rope_head(bf16x4_to_f32(raw), A.k_norm, A.rope_cos + (size_t)t * 32,
-                                        A.rope_sin + (size_t)t * 32, lane);
-        *reinterpret_cast<uint2*>(A.k_cache + ((size_t)g * A.cap + t) * QM_GQA_HD + 4 * lane) = f32x4_to_f16(x);
+    // K: wave w normalises and rotates tokens t0+16w .. t0+16w+15.  All 16
+    // rows are loaded (at clamped, valid rows) before any arithmetic, so the
+    // wave waits for one memory round trip, not one per token.
+    {
+        uint2 raw[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int t = min(t0 + 16 * w + j, A.S - 1);
+            raw[j] = *reinterpret_cast<const uint2*>(A.k + ((size_t)t * QM_GQA_KV_HEADS + g) * QM_GQA_HD + 4 * lane);
+        }
+        const uint2 gw = *reinterpret_cast<const uint2*>(A.k_norm + 4 * lane);
+        const float g1[4] = {1.0f + f16_to_f32((uint16_t)(gw.x & 0xffffu)), 1.0f + f16_to_f32((uint16_t)(gw.x >> 16)),
+                             1.0f + f16_to_f32((uint16_t)(gw.y & 0xffffu)), 1.0f + f16_to_f32((uint16_t)(gw.y >> 16))};
+        // RoPE rows four tokens at a time, loaded by every lane (lanes 0..15
+        // use them) so no per-token branch serializes the loads
+        const int i0 = (lane & 7) * 4;
+#pragma unroll
+        for (int jb = 0; jb < 16; jb += 4) {
+            float4 cr[4], sr[4];
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                const int tc = min(t0 + 16 * w + jb + jj, A.S - 1);
+                cr[jj] = ld4(A.rope_cos + (size_t)tc * 32 + i0);
+                sr[jj] = ld4(A.rope_sin + (size_t)tc * 32 + i0);
+            }
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                const int t = t0 + 16 * w + jb + jj;
+                // gemv.rs:586-597 (RMSNorm, 1 + gamma) and :604-627 (split-half RoPE)
+                float4 x = bf16x4_to_f32(raw[jb + jj]);
+                float ss = x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
+                ss = wave_sum64(ss);
+                const float inv = 1.0f / sqrtf(ss / (float)QM_GQA_HD + 1e-6f);
+                x.x = x.x * inv * g1[0]; x.y = x.y * inv * g1[1];
+                x.z = x.z * inv * g1[2]; x.w = x.w * inv * g1[3];
+                float4 pr;                                        // rotation partner (lane ^ 8)
+                pr.x = dpp_f32<0x128>(x.x); pr.y = dpp_f32<0x128>(x.y);
+                pr.z = dpp_f32<0x128>(x.z); pr.w = dpp_f32<0x128>(x.w);
+                // x1 c - x2 s (lanes 0..7), x2 c + x1 s (lanes 8..15)
+                const float4 ps = lane < 8 ? make_float4(-pr.x, -pr.y, -pr.z, -pr.w) : pr;
+                float4 y;
+                y.x = x.x * cr[jj].x + ps.x * sr[jj].x; y.y = x.y * cr[jj].y + ps.y * sr[jj].y;
+                y.z = x.z * cr[jj].z + ps.z * sr[jj].z; y.w = x.w * cr[jj].w + ps.w * sr[jj].w;
+                if (lane < 16) x = y;
+                if (t < A.S)                                      // wave-uniform
+                    *reinterpret_cast<uint2*>(A.k_cache + ((size_t)g * A.cap + t) * QM_GQA_HD + 4 * lane) = f32x4_to_f16(x);
+            }
+        }
     }
     // V: rows to the cache, and through LDS to V^T
     {
