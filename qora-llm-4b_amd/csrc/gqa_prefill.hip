@@ -192,8 +192,10 @@ extern "C" __global__ __launch_bounds__(768) void qm_gqa_prefill_attn(GqaPrefill
     const int nblk = (A.S + TQ3 - 1) / TQ3;
     const uint32_t sm_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)sm;
     // item = group * nblk + block index; own group first, then the others
-    auto claim = [&](int g0) {
-        for (int k = 0; k < QM_GQA_KV_HEADS; ++k) {
+    // (the own group's index may already have been drawn: first)
+    auto claim = [&](int g0, int first) {
+        if (first < nblk) return g0 * nblk + first;
+        for (int k = 1; k < QM_GQA_KV_HEADS; ++k) {
             const int gg = (g0 + k) & (QM_GQA_KV_HEADS - 1);
             const int i = atomicAdd(A.queue + gg, 1);
             if (i < nblk) return gg * nblk + i;
@@ -202,7 +204,7 @@ extern "C" __global__ __launch_bounds__(768) void qm_gqa_prefill_attn(GqaPrefill
     };
 
     const int home = blockIdx.x & (QM_GQA_KV_HEADS - 1);
-    if (tid == 0) item_s = claim(home);
+    if (tid == 0) item_s = claim(home, atomicAdd(A.queue + home, 1));
     __syncthreads();
     int item = item_s;
     while (item >= 0) {                     // workgroup-uniform
@@ -254,11 +256,19 @@ extern "C" __global__ __launch_bounds__(768) void qm_gqa_prefill_attn(GqaPrefill
             const int t = r0 + lr;
             const int tc = min(t, A.S - 1);     // rows past S: any valid row, then zeroed
             const uint16_t* qrow = A.q_gate + ((size_t)tc * QM_GQA_HEADS + qh) * (2 * QM_GQA_HD) + 8 * lq;
-            uint4 u[8];                         // the row's 64 dims of this lane, packed bf16
+            // every load of the prep (q row, gamma, RoPE row) is issued before
+            // any arithmetic, so the prep waits for one memory round trip
+            uint4 u[8], gq[8];                  // the row's 64 dims of this lane, packed bf16; gamma
 #pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                u[s] = *reinterpret_cast<const uint4*>(qrow + 32 * s);
-                if (t >= A.S) u[s] = make_uint4(0, 0, 0, 0);
+            for (int s = 0; s < 8; ++s) u[s] = *reinterpret_cast<const uint4*>(qrow + 32 * s);
+#pragma unroll
+            for (int s = 0; s < 8; ++s) gq[s] = *reinterpret_cast<const uint4*>(A.q_norm + 32 * s + 8 * lq);
+            const float* crow = A.rope_cos + (size_t)tc * 32 + 8 * lq;
+            const float* srow = A.rope_sin + (size_t)tc * 32 + 8 * lq;
+            const float4 c0 = ld4(crow), c1 = ld4(crow + 4), s0 = ld4(srow), s1 = ld4(srow + 4);
+            if (t >= A.S) {
+#pragma unroll
+                for (int s = 0; s < 8; ++s) u[s] = make_uint4(0, 0, 0, 0);
             }
             auto unpack = [](uint4 v, float (&x)[8]) {
                 const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
@@ -283,8 +293,7 @@ extern "C" __global__ __launch_bounds__(768) void qm_gqa_prefill_attn(GqaPrefill
             const float sl2 = (1.0f / 16.0f) * 1.4426950408889634f;
             auto normed = [&](int s, float (&x)[8]) {     // x * inv * (1 + gamma)
                 unpack(u[s], x);
-                const uint4 gw = *reinterpret_cast<const uint4*>(A.q_norm + 32 * s + 8 * lq);
-                const uint32_t gv[4] = {gw.x, gw.y, gw.z, gw.w};
+                const uint32_t gv[4] = {gq[s].x, gq[s].y, gq[s].z, gq[s].w};
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     x[2 * e] = x[2 * e] * inv * (1.0f + f16_to_f32((uint16_t)(gv[e] & 0xffffu)));
@@ -295,9 +304,6 @@ extern "C" __global__ __launch_bounds__(768) void qm_gqa_prefill_attn(GqaPrefill
                 float x1[8], x2[8];
                 normed(0, x1);
                 normed(1, x2);
-                const float* crow = A.rope_cos + (size_t)tc * 32 + 8 * lq;
-                const float* srow = A.rope_sin + (size_t)tc * 32 + 8 * lq;
-                const float4 c0 = ld4(crow), c1 = ld4(crow + 4), s0 = ld4(srow), s1 = ld4(srow + 4);
                 const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
                 const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
 #pragma unroll
@@ -331,7 +337,9 @@ extern "C" __global__ __launch_bounds__(768) void qm_gqa_prefill_attn(GqaPrefill
 
         const int kt_claim = max(nkt - 3, 0);
         for (int kt = 0; kt < nkt; ++kt) {
-            if (tid == 0 && kt == kt_claim) nxt = claim(home);
+            // the home queue's next index is drawn here; its latency hides
+            // behind the remaining tiles, and it is resolved at the end
+            if (tid == 0 && kt == kt_claim) nxt = atomicAdd(A.queue + home, 1);
             const int k0 = kt * KT, b = kt & 1;
             // the other buffer was last read before the previous barrier
             if (kt + 1 < nkt) fetch(kt + 1, b ^ 1);
@@ -451,7 +459,7 @@ extern "C" __global__ __launch_bounds__(768) void qm_gqa_prefill_attn(GqaPrefill
             for (int dt = 0; dt < 16; ++dt)
                 o[16 * dt] = f32_to_bf16((O[dt][e] * iv[e]) * sigmoid_fast(bf16_to_f32(gbuf[e][dt])));
         }
-        if (tid == 0) item_s = nxt;
+        if (tid == 0) item_s = claim(home, nxt);
         __syncthreads();
         item = item_s;
     }
