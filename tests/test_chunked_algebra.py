@@ -1,5 +1,5 @@
 """CPU check of the chunked (WY/UT) DeltaNet prefill algebra used by the
-qm_dn_prefill_{prep,chunk,scan} kernels.
+qm_dn_prefill_{chunk,scan,out} kernels.
 
 The kernels evaluate, per chunk of C tokens with state S0 entering,
   A = strictly-lower(beta_i gamma_i/gamma_j k_i.k_j), T = (I + A)^-1,
@@ -108,7 +108,7 @@ def test_chunked_algebra_matches_sequential_oracle(Tn, C):
     S_or, buf = S0.copy(), buf0.copy()
     ref = O.deltanet_prefill(cfg, qkv, a, b, z, conv_w, a_log, dt_bias, gw.view(np.uint16), S_or, buf)
 
-    # activation exactly as the prep kernel: causal conv with the buffer, SiLU, L2 norm, q scale
+    # activation exactly as the chunk kernel: causal conv with the buffer, SiLU, L2 norm, q scale
     x = np.vstack([buf0.T.astype(np.float64), qkv.astype(np.float64)])
     conv = sum(x[j:j + Tn] * conv_w[:, j].astype(np.float64) for j in range(4))
     act = conv / (1 + np.exp(-conv))
