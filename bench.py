@@ -408,6 +408,135 @@ def run_gqa_prefill(args, ctx):
 CPU_SAMPLE_S = 10.0        # minimum seconds of CPU work per baseline sample
 
 
+Q4_LAYER_PROJ = ("in_proj_qkv", "in_proj_z", "in_proj_a", "in_proj_b", "out_proj",
+                 "gate_proj", "up_proj", "down_proj")
+Q4_LAYERS = 24   # DeltaNet layers of the 4B stack
+
+
+def q4_gemv_bytes(k: int, n: int) -> int:
+    """Algorithmic HBM bytes of one Q4 GEMV: codes, scales, x in, y out."""
+    return k * n // 2 + k * (n // 32) * 2 + 4 * k + 4 * n
+
+
+def q4_weight_bytes(k: int, n: int) -> int:
+    return k * n // 2 + k * (n // 32) * 2
+
+
+def run_q4_proj(args, ctx):
+    """One decode token through the Q4 projections of the 24 DeltaNet layers,
+    each layer with its own weights (1.52 GB, far beyond the 256 MB MALL, so
+    every launch streams its weights from HBM).  Per layer, four launches:
+      1. input RMSNorm + in_proj_qkv, in_proj_z, in_proj_a, in_proj_b;
+      2. out_proj + residual;
+      3. post-attention RMSNorm + gate_proj, up_proj + SiLU gate;
+      4. down_proj + residual
+    (gemv.rs:740-742,788-789,865,886-897; the mixer itself runs between 1
+    and 2 and is measured by the other workloads)."""
+    K, Wm = args.steps, args.warmup
+    shapes = {nm: W.Q4_PROJ_SHAPES[nm] for nm in Q4_LAYER_PROJ}
+    seed = [3000]
+
+    def fill(buf, dtype, count, std, mean=0.0):
+        ctx.fill_normal(buf, dtype, count, mean, std, seed[0])
+        seed[0] += 1
+
+    def weight(k, n):
+        # the device layout directly (codes [n/T][k][T/2], scales [n/32][k]):
+        # any byte is a valid pair of codes; scales ~ absmax/7 of N(0, 0.02) groups
+        codes = ctx.alloc(k * n // 2)
+        fill(codes, M.QM_F16, k * n // 4, 1.0)
+        gscales = ctx.alloc(max(16, k * (n // 32) * 2))
+        fill(gscales, M.QM_F16, k * (n // 32), 0.0012, 0.006)
+        return codes, gscales
+
+    layers = [{nm: weight(*shapes[nm]) for nm in Q4_LAYER_PROJ} for _ in range(Q4_LAYERS)]
+    norms = ctx.alloc(2560 * 2)
+    fill(norms, M.QM_F16, 2560, 0.1)
+    h = ctx.alloc(2560 * 4)
+    fill(h, M.QM_F32, 2560, 1.0)
+    mixer_out = ctx.alloc(4096 * 4)
+    fill(mixer_out, M.QM_F32, 4096, 1.0)
+    ys = {nm: ctx.alloc(shapes[nm][1] * 4) for nm in ("in_proj_qkv", "in_proj_z", "in_proj_a", "in_proj_b")}
+    inter = ctx.alloc(9216 * 4)
+    ctx.reserve(max_batch=1)
+    timers = {kind: Timer(ctx) for kind in ("in", "out", "gate_up", "down")}
+
+    def step(timed):
+        for L in layers:
+            calls = {
+                "in": lambda: ctx.q4_gemv_multi(2560, h, [
+                    (shapes[nm][1], L[nm][0], L[nm][1], ys[nm])
+                    for nm in ("in_proj_qkv", "in_proj_z", "in_proj_a", "in_proj_b")], norm_w=norms),
+                "out": lambda: ctx.q4_gemv_multi(4096, mixer_out, [
+                    (2560, L["out_proj"][0], L["out_proj"][1], h, h)]),
+                "gate_up": lambda: ctx.q4_gate_up(2560, 9216, h, norms, *L["gate_proj"], *L["up_proj"], inter),
+                "down": lambda: ctx.q4_gemv_multi(9216, inter, [
+                    (2560, L["down_proj"][0], L["down_proj"][1], h, h)]),
+            }
+            for kind, call in calls.items():
+                timers[kind].wrap(call) if timed else call()
+
+    for _ in range(Wm):
+        step(False)
+    ctx.sync()
+    t0, t1 = ctx.event(), ctx.event()
+    wall0 = time.perf_counter()
+    t0.record()
+    for _ in range(K):
+        step(True)
+    t1.record()
+    ctx.sync()
+    wall = time.perf_counter() - wall0
+    total_ms = t0.elapsed_ms(t1)
+    graph_ms = float("nan")
+    if not args.no_graph:
+        # the same step captured once and replayed (no host launch cost)
+        ctx.graph_begin()
+        step(False)
+        g = ctx.graph_end()
+        g.launch()
+        ctx.sync()
+        g0, g1 = ctx.event(), ctx.event()
+        g0.record()
+        for _ in range(K):
+            g.launch()
+        g1.record()
+        ctx.sync()
+        graph_ms = g0.elapsed_ms(g1) / K
+        g.close()
+    wb = {nm: q4_weight_bytes(*shapes[nm]) for nm in Q4_LAYER_PROJ}
+    kbytes = {   # weights + activations read + outputs written, per launch
+        "in": sum(wb[nm] for nm in ("in_proj_qkv", "in_proj_z", "in_proj_a", "in_proj_b"))
+              + 2560 * 6 + 4 * (8192 + 4096 + 64),
+        "out": wb["out_proj"] + 4096 * 4 + 2560 * 8,
+        "gate_up": wb["gate_proj"] + wb["up_proj"] + 2560 * 6 + 9216 * 4,
+        "down": wb["down_proj"] + 9216 * 4 + 2560 * 8,
+    }
+    names = {"in": "qm_q4_gemv (RMSNorm + in_proj_qkv/z/a/b)", "out": "qm_q4_gemv (out_proj + residual)",
+             "gate_up": "qm_q4_gate_up (RMSNorm + gate/up + SiLU)", "down": "qm_q4_gemv (down_proj + residual)"}
+    kernels = {names[kd]: {"avg_ms": timers[kd].mean_ms(), "bytes": kbytes[kd],
+                           "GB_s": kbytes[kd] / timers[kd].mean_ms() / 1e6,
+                           "frac_hbm": kbytes[kd] / (timers[kd].mean_ms() * 1e-3) / HBM_PEAK}
+               for kd in timers}
+    step_bytes = Q4_LAYERS * sum(kbytes.values())
+    gu_ms = timers["gate_up"].mean_ms()
+    return {
+        "tokens": K, "total_ms": total_ms, "wall_s": wall,
+        "dominant": names["gate_up"],
+        "roofline": {"bound": "hbm", "achieved": kbytes["gate_up"] / (gu_ms * 1e-3), "peak": HBM_PEAK,
+                     "kernel_ms": gu_ms, "bytes_per_launch": kbytes["gate_up"]},
+        "kernels": kernels,
+        "step_frac_hbm": step_bytes / (total_ms / K * 1e-3) / HBM_PEAK,
+        "graph_ms_per_step": graph_ms,
+        "graph_step_frac_hbm": step_bytes / (graph_ms * 1e-3) / HBM_PEAK,
+        "config": {"workload": "Q4 decode projections of the 24 DeltaNet layers: input RMSNorm + "
+                               "in_proj_qkv 2560x8192, in_proj_z 2560x4096, in_proj_a/b 2560x32; "
+                               "out_proj 4096x2560 + residual; RMSNorm + gate/up 2560x9216 + SiLU; "
+                               "down_proj 9216x2560 + residual; batch 1, one weight set per layer",
+                   "batch": 1, "seq_len": 1, "global_batch": 1, "parallelism": "single GPU"},
+    }
+
+
 def _repeat_for(fn, min_s=CPU_SAMPLE_S, max_iters=10 ** 6):
     """Call fn() until min_s seconds have elapsed; returns (calls, seconds)."""
     n, t0 = 0, time.perf_counter()
@@ -473,6 +602,25 @@ def cpu_baseline(workload: str) -> dict:
                 "sample": f"{int(done['rows'])} of the last rows of the 8192-token causal prefill "
                           f"(gemv.rs:1402-1444), heads over {att_threads} threads, extrapolated "
                           f"linearly in row-key pairs ({dt:.1f} s)"}
+    if workload == "q4_proj":
+        rng = np.random.default_rng(8)
+        ws = {nm: W.q4_random_weight(*W.Q4_PROJ_SHAPES[nm], rng) for nm in Q4_LAYER_PROJ}
+        x = rng.standard_normal(2560, dtype=np.float32)
+        mix = rng.standard_normal(4096, dtype=np.float32)
+        gam = W.f16_bits(0.1 * rng.standard_normal(2560, dtype=np.float32))
+
+        def sample():
+            xn = O.rms_norm(x, gam)
+            for nm in ("in_proj_qkv", "in_proj_z", "in_proj_a", "in_proj_b"):
+                O.q4_gemv(xn, *ws[nm])
+            h = x + O.q4_gemv(mix, *ws["out_proj"])
+            inter = O.q4_gate_up(O.rms_norm(h, gam), *ws["gate_proj"], *ws["up_proj"])
+            O.q4_gemv(inter, *ws["down_proj"])
+        n, dt = _repeat_for(sample)
+        return {"value": n / dt / Q4_LAYERS, "unit": "tokens/s", "cores": 1, "kind": "port",
+                "sample": f"{n} DeltaNet-layer sets of the Q4 projections, norms and residuals "
+                          f"(scalar gemv_q4_inner restatement, one thread, {dt:.1f} s); "
+                          f"tokens/s = layer sets/s / 24"}
     if workload == "gqa_decode":
         pos = 4096
         w = W.gqa_decode_workload(pos, 1, seed=1)
@@ -533,8 +681,11 @@ def main():
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="stack",
-                    choices=["stack", "dn_decode", "gqa_decode", "dn_prefill", "gqa_prefill"])
+                    choices=["stack", "dn_decode", "gqa_decode", "dn_prefill", "gqa_prefill", "q4_proj"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="skip the graph-replayed timing (rocprofv3's kernel tracer crashes in "
+                         "hipGraphLaunch of a captured q4_proj step)")
     ap.add_argument("--gqa-chunk", type=int, default=0,
                     help="keys per GQA decode split workgroup (multiple of 64; 0 = the library's choice)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -546,7 +697,7 @@ def main():
               "(sharding is a design note, not a launched path); run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     defaults = {"stack": (32, 4), "dn_decode": (256, 16), "gqa_decode": (200, 20),
-                "dn_prefill": (20, 3), "gqa_prefill": (10, 2)}[args.workload]
+                "dn_prefill": (20, 3), "gqa_prefill": (10, 2), "q4_proj": (50, 5)}[args.workload]
     args.steps = args.steps or defaults[0]
     args.warmup = defaults[1] if args.warmup is None else args.warmup
 
@@ -561,7 +712,8 @@ def main():
         src.close()
         dst.close()
     run = {"stack": run_stack, "dn_decode": run_dn_decode, "gqa_decode": run_gqa_decode,
-           "dn_prefill": run_dn_prefill, "gqa_prefill": run_gqa_prefill}[args.workload]
+           "dn_prefill": run_dn_prefill, "gqa_prefill": run_gqa_prefill,
+           "q4_proj": run_q4_proj}[args.workload]
     r = run(args, ctx)
     ctx.sync()
     ctx.close()
@@ -581,13 +733,15 @@ def main():
     line = {
         "metric": {"stack": "mixer tokens/s (decode, 32-layer hybrid stack) on 1x MI355X",
                    "dn_prefill": "mixer tokens/s (prefill) on 1x MI355X",
-                   "gqa_prefill": "mixer tokens/s (prefill) on 1x MI355X"}.get(
+                   "gqa_prefill": "mixer tokens/s (prefill) on 1x MI355X",
+                   "q4_proj": "Q4 projection tokens/s (decode) on 1x MI355X"}.get(
                        args.workload, "mixer tokens/s (decode) on 1x MI355X"),
         "value": value, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": r["total_ms"] / args.steps,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16" if args.workload in ("dn_prefill", "gqa_prefill") else "f32",
-        "data": "synthetic (seeded normal inputs, random-init state and f16 KV cache)",
+        "data": ("synthetic (seeded random Q4 codes, f16 scales and normal inputs)" if args.workload == "q4_proj"
+                 else "synthetic (seeded normal inputs, random-init state and f16 KV cache)"),
         "config": r["config"],
         "roofline": rl,
     }
@@ -595,7 +749,7 @@ def main():
         tf = ROOT / "profiles" / "traffic_stack_gqa_decode.json"
         if tf.exists():   # measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (see the profile summary)
             line["roofline"]["traffic"] = json.loads(tf.read_text())["traffic_bytes_per_launch"]
-    for k in ("kernels", "step_frac_hbm", "graph_ms_per_step"):
+    for k in ("kernels", "step_frac_hbm", "graph_ms_per_step", "graph_step_frac_hbm"):
         if k in r:
             line[k] = r[k]
     if not args.no_cpu_baseline:

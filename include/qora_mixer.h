@@ -241,6 +241,71 @@ int32_t qm_gqa_prefill(qm_context* ctx, qm_stream stream, int32_t seq_len,
                        uint16_t* k_cache_dev, uint16_t* v_cache_dev,
                        int64_t cache_capacity, uint16_t* out_dev);
 
+/* ---- Q4 projections --------------------------------------------------- */
+/* A Q4Weight (gemv.rs:29-34, written by quantize_q4, convert.rs:437-467)
+ * maps k inputs to n outputs, n a multiple of 32 (the reference stores
+ * narrower matrices as f16, convert.rs:360-364; QM_ERR_SHAPE here):
+ *   W[i][j] = scale[i][j/32] * (q[i][j] - 8),
+ * reference layout: packed u8 [k][n/2], row i byte 16 g + t holding the
+ * codes of columns 32 g + 2t (low nibble) and 32 g + 2t + 1 (high nibble);
+ * scales f16 [k][n/32].
+ * On the device a weight lives tile-major: codes u8 [n/T][k][T/2] and
+ * gscales f16 [n/32][k], T = 8 columns when n < 4096, else 16 (each column
+ * tile one contiguous stream; sizes as in the reference layout).
+ * qm_q4_repack converts once at load time, as the reference's wgpu loader
+ * repacks Q4 weights for its backend (q4_weight_to_gpu, gpu_loader.rs:
+ * 82-106).  packed/scales/codes/gscales are device pointers. */
+int32_t qm_q4_repack(qm_context* ctx, qm_stream stream, int32_t k, int32_t n,
+                     const uint8_t* packed_dev, const uint16_t* scales_dev,
+                     uint8_t* codes_dev, uint16_t* gscales_dev);
+
+/* y = x W for one input row: replaces gemv_q4, gemv.rs:451-467 (inner loop
+ * gemv_q4_inner :412-445, AVX-512 twin gemv_q4_avx512 simd.rs:73-139), the
+ * Weight::Q4 arm of gemv() (gemv.rs:286-291) that the decode projections
+ * call: in_proj_qkv/a/b/z and out_proj (gemv.rs:742,788-789,865,886),
+ * q/k/v/o_proj (:928,941-942,1014) and down_proj (:895,1021).
+ * x_dev f32 [k]; codes_dev, gscales_dev the repacked weight; y_dev f32 [n].
+ * Sums run in fp32 in a fixed order (bit-reproducible run to run); they
+ * differ from the reference's k-ordered sums by fp32 reassociation only. */
+int32_t qm_q4_gemv(qm_context* ctx, qm_stream stream, int32_t k, int32_t n,
+                   const float* x_dev, const uint8_t* codes_dev,
+                   const uint16_t* gscales_dev, float* y_dev);
+
+/* Up to four projections of the same input row in one launch (a launch
+ * has a fixed cost of a few microseconds, comparable to streaming a
+ * 2560x4096 Q4 weight), with the reference's neighbouring steps fused:
+ *   norm_w_dev  NULL, or f16 [k]: x is first replaced by rms_norm(x, norm_w)
+ *               (1 + gamma, eps 1e-6; gemv.rs:571-579), as the decode layers
+ *               do before their input projections (gemv.rs:740, and the
+ *               attention layer's equivalent) -- x_dev itself is not written;
+ *   residual_dev NULL, or f32 [n]: y = residual + x W (the residual adds
+ *               after out_proj / o_proj and down_proj, gemv.rs:889-890,896);
+ *               may alias y_dev.
+ * E.g. the four gemv() calls on x_norm at the top of the DeltaNet decode
+ * (in_proj_qkv, in_proj_a, in_proj_b, in_proj_z, gemv.rs:742,788-789,865)
+ * are one call with norm_w = input_norm; the three of the attention decode
+ * (q/k/v_proj, gemv.rs:928,941-942) another. */
+typedef struct {
+    int32_t n;                   /* outputs of weight i (multiple of 32) */
+    const uint8_t* codes_dev;    /* [n/T][k][T/2] */
+    const uint16_t* gscales_dev; /* f16 [n/32][k] */
+    float* y_dev;                /* f32 [n] */
+    const float* residual_dev;   /* NULL or f32 [n] */
+} qm_q4_out;
+int32_t qm_q4_gemv_multi(qm_context* ctx, qm_stream stream, int32_t k,
+                         const float* x_dev, const uint16_t* norm_w_dev,
+                         int32_t count, const qm_q4_out* outs);
+
+/* The MLP's first half: out = silu(xn Wg) * (xn Wu) with xn = x, or
+ * rms_norm(x, norm_w) when norm_w_dev is not NULL (replaces rms_norm +
+ * fused_gate_up_q4, gemv.rs:893-894 and :469-526).  Both weights k x n,
+ * device layout; out_dev f32 [n]. */
+int32_t qm_q4_gate_up(qm_context* ctx, qm_stream stream, int32_t k, int32_t n,
+                      const float* x_dev, const uint16_t* norm_w_dev,
+                      const uint8_t* gate_codes_dev, const uint16_t* gate_gscales_dev,
+                      const uint8_t* up_codes_dev, const uint16_t* up_gscales_dev,
+                      float* out_dev);
+
 #ifdef __cplusplus
 }
 #endif

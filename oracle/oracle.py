@@ -59,6 +59,10 @@ _SIG = {
                              _I32, _P, _I32], _I32),
     "or_attn_prefill": ([C.POINTER(OrConfig), _I32, _P, _P, _P, _P, _P, _P, _P, _I32, _P, _P, _P,
                          _P, _I32, _I32], _I32),
+    "or_q4_quantize": ([_P, _I32, _I32, _P, _P], None),
+    "or_q4_gemv": ([_P, _P, _P, _I32, _I32, _P], None),
+    "or_q4_gemm": ([_P, _I32, _P, _P, _I32, _I32, _P, _I32], None),
+    "or_q4_gate_up": ([_P, _P, _P, _P, _P, _I32, _I32, _P], None),
 }
 
 _lib = None
@@ -255,3 +259,53 @@ def attn_prefill(cfg, q_gate_all, k_all, v_all, q_norm_f16, k_norm_f16, cos, sin
     if st != 0:
         raise IndexError("RoPE position beyond table")
     return out, kc, vc
+
+
+# ---- Q4 projections ------------------------------------------------------------
+def q4_quantize(w):
+    """convert.rs:437-467.  w f32 [k, n] (n % 32 == 0) -> (packed u8 [k, n/2], scales f16 bits [k, n/32])."""
+    w = _f32(w)
+    k, n = w.shape
+    assert n % 32 == 0
+    packed = np.empty((k, n // 2), np.uint8)
+    scales = np.empty((k, n // 32), np.uint16)
+    lib().or_q4_quantize(w.ctypes.data, k, n, packed.ctypes.data, scales.ctypes.data)
+    return packed, scales
+
+
+def q4_gemv(x, packed, scales):
+    """gemv.rs:412-445 over all k rows: y = x @ W."""
+    x = _f32(x)
+    packed = np.ascontiguousarray(packed, np.uint8)
+    scales = np.ascontiguousarray(scales, np.uint16)
+    k, n = packed.shape[0], packed.shape[1] * 2
+    assert x.size == k
+    y = np.empty(n, np.float32)
+    lib().or_q4_gemv(x.ctypes.data, packed.ctypes.data, scales.ctypes.data, k, n, y.ctypes.data)
+    return y
+
+
+def q4_gemm(x, packed, scales, nthreads=8):
+    """gemv.rs:529-542: rows of x [m, k] through gemv_q4_inner."""
+    x = _f32(x)
+    packed = np.ascontiguousarray(packed, np.uint8)
+    scales = np.ascontiguousarray(scales, np.uint16)
+    k, n = packed.shape[0], packed.shape[1] * 2
+    m = x.shape[0]
+    assert x.shape[1] == k
+    y = np.empty((m, n), np.float32)
+    lib().or_q4_gemm(x.ctypes.data, m, packed.ctypes.data, scales.ctypes.data, k, n, y.ctypes.data,
+                     nthreads)
+    return y
+
+
+def q4_gate_up(x, g_packed, g_scales, u_packed, u_scales):
+    """gemv.rs:469-526: silu(x @ Wg) * (x @ Wu)."""
+    x = _f32(x)
+    gp, up = (np.ascontiguousarray(a, np.uint8) for a in (g_packed, u_packed))
+    gs, us = (np.ascontiguousarray(a, np.uint16) for a in (g_scales, u_scales))
+    k, n = gp.shape[0], gp.shape[1] * 2
+    out = np.empty(n, np.float32)
+    lib().or_q4_gate_up(x.ctypes.data, gp.ctypes.data, gs.ctypes.data, up.ctypes.data,
+                        us.ctypes.data, k, n, out.ctypes.data)
+    return out

@@ -537,3 +537,92 @@ int32_t or_attn_prefill(const or_config* cfg, int32_t S, const float* q_gate_all
     free(q_all); free(g_all);
     return 0;
 }
+
+/* ------------------------------------------------------------------ */
+/* Q4 projections                                                       */
+/* ------------------------------------------------------------------ */
+/* Rust `(v).round() as i32`: half away from zero, NaN -> 0, saturating. */
+static int32_t rust_round_i32(float v) {
+    if (v != v) return 0;
+    float r = roundf(v);
+    if (r >= 2147483647.0f) return 2147483647;
+    if (r <= -2147483648.0f) return (int32_t)-2147483647 - 1;
+    return (int32_t)r;
+}
+
+/* convert.rs:437-467 */
+void or_q4_quantize(const float* data, int32_t k, int32_t n, uint8_t* packed,
+                    uint16_t* scales) {
+    const int32_t gs = 32, groups = n / gs;
+    size_t pi = 0, si = 0;
+    for (int32_t ki = 0; ki < k; ++ki)
+        for (int32_t g = 0; g < groups; ++g) {
+            const float* grp = data + (size_t)ki * n + (size_t)g * gs;
+            /* :448-449 absmax via f32::max (a NaN operand is ignored) */
+            float absmax = 0.0f;
+            for (int32_t j = 0; j < gs; ++j) {
+                float a = fabsf(grp[j]);
+                absmax = (a != a) ? absmax : (absmax != absmax ? a : (a > absmax ? a : absmax));
+            }
+            float scale = absmax > 0.0f ? absmax / 7.0f : 0.0f;   /* :450 */
+            scales[si++] = or_f32_to_f16(scale);                   /* :451 */
+            float inv = scale > 0.0f ? 1.0f / scale : 0.0f;        /* :454 */
+            for (int32_t j = 0; j < gs; j += 2) {                  /* :455-459 */
+                int32_t q0 = rust_round_i32(grp[j] * inv);
+                int32_t q1 = rust_round_i32(grp[j + 1] * inv);
+                q0 = (q0 < -8 ? -8 : (q0 > 7 ? 7 : q0)) + 8;
+                q1 = (q1 < -8 ? -8 : (q1 > 7 ? 7 : q1)) + 8;
+                packed[pi++] = (uint8_t)((uint32_t)q0 | ((uint32_t)q1 << 4));
+            }
+        }
+}
+
+/* gemv.rs:412-445, k range [0, k) */
+void or_q4_gemv(const float* x, const uint8_t* packed, const uint16_t* scales,
+                int32_t k, int32_t n, float* y) {
+    const int32_t groups = n / 32, ppg = 16, ppr = groups * ppg;
+    for (int32_t j = 0; j < n; ++j) y[j] = 0.0f;
+    for (int32_t ki = 0; ki < k; ++ki) {
+        float val = x[ki];
+        if (val == 0.0f) continue;
+        for (int32_t g = 0; g < groups; ++g) {
+            float s = or_f16_to_f32(scales[(size_t)ki * groups + g]) * val;
+            if (s == 0.0f) continue;
+            float lut[16];
+            for (int32_t i = 0; i < 16; ++i) lut[i] = s * (float)(i - 8);
+            lut[8] = 0.0f;                /* the reference's literal 0.0 (s * 0 could be -0) */
+            lut[9] = s;                   /* the literal s (s * 1.0 is s) */
+            const uint8_t* po = packed + (size_t)ki * ppr + (size_t)g * ppg;
+            float* oo = y + (size_t)g * 32;
+            for (int32_t j = 0; j < ppg; ++j) {
+                uint8_t b = po[j];
+                oo[2 * j] += lut[b & 0x0F];
+                oo[2 * j + 1] += lut[b >> 4];
+            }
+        }
+    }
+}
+
+/* gemv.rs:529-542 */
+void or_q4_gemm(const float* x, int32_t m, const uint8_t* packed,
+                const uint16_t* scales, int32_t k, int32_t n, float* y,
+                int32_t nthreads) {
+    if (nthreads < 1) nthreads = 1;
+    #pragma omp parallel for num_threads(nthreads) schedule(static)
+    for (int32_t t = 0; t < m; ++t)
+        or_q4_gemv(x + (size_t)t * k, packed, scales, k, n, y + (size_t)t * n);
+}
+
+/* gemv.rs:469-526: the scalar fallback over one k chunk, then
+ * out = (g / (1 + exp(-g))) * u (:523-524) */
+void or_q4_gate_up(const float* x, const uint8_t* g_packed,
+                   const uint16_t* g_scales, const uint8_t* u_packed,
+                   const uint16_t* u_scales, int32_t k, int32_t n, float* out) {
+    float* g = (float*)malloc(sizeof(float) * (size_t)n);
+    float* u = (float*)malloc(sizeof(float) * (size_t)n);
+    or_q4_gemv(x, g_packed, g_scales, k, n, g);
+    or_q4_gemv(x, u_packed, u_scales, k, n, u);
+    for (int32_t j = 0; j < n; ++j) out[j] = (g[j] / (1.0f + expf(-g[j]))) * u[j];
+    free(g);
+    free(u);
+}

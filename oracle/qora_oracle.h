@@ -152,6 +152,28 @@ int32_t or_attn_prefill(const or_config* cfg, int32_t S, const float* q_gate_all
                      float* out, const int32_t* rows, int32_t n_rows,
                      int32_t nthreads);
 
+/* --- Q4 projections ------------------------------------------------- */
+/* quantize_q4, convert.rs:437-467: data [k][n] f32 (n % 32 == 0) ->
+ * packed [k][n/2] (per 32-column group: 16 bytes, low nibble = even
+ * column) and scales [k][n/32] f16 = absmax/7.                          */
+void or_q4_quantize(const float* data, int32_t k, int32_t n, uint8_t* packed,
+                    uint16_t* scales);
+/* gemv_q4_inner over the full k range, gemv.rs:412-445 (scalar path; the
+ * AVX-512 twin simd.rs:73-139 forms the same lut values and sums in the
+ * same order): y[n] = x[k] @ W.                                          */
+void or_q4_gemv(const float* x, const uint8_t* packed, const uint16_t* scales,
+                int32_t k, int32_t n, float* y);
+/* gemm_q4, gemv.rs:529-542: each of the m rows of x [m][k] independently
+ * through gemv_q4_inner; y [m][n].                                      */
+void or_q4_gemm(const float* x, int32_t m, const uint8_t* packed,
+                const uint16_t* scales, int32_t k, int32_t n, float* y,
+                int32_t nthreads);
+/* fused_gate_up_q4, gemv.rs:469-526 (one k chunk): out[j] =
+ * silu(g[j]) * u[j] with g = x @ Wg, u = x @ Wu.                         */
+void or_q4_gate_up(const float* x, const uint8_t* g_packed,
+                   const uint16_t* g_scales, const uint8_t* u_packed,
+                   const uint16_t* u_scales, int32_t k, int32_t n, float* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,234 @@
+// q4_proj.hip -- Q4 projections (the GEMVs around the token mixer) for gfx950.
+//
+// A Q4Weight (gemv.rs:29-34) maps k inputs to n outputs.  Each input row is
+// cut into groups of 32 output columns with one f16 scale (absmax / 7) and 16
+// bytes of 4-bit codes q, value = scale * (q - 8); byte j of a group holds
+// column 2j in its low nibble and 2j + 1 in its high nibble (quantize_q4,
+// convert.rs:437-467).  The reference stores it row-major:
+//   packed u8 [k][n/2], scales f16 [k][n/32].
+// On the device a weight is kept tile-major (qm_q4_repack, once at load
+// time, as the reference's wgpu loader repacks for its backend,
+// gpu_loader.rs:82-106): column tiles of T = 16 columns (T = 8 when
+// n < 4096, so that even a 2560-wide weight spreads over 320 workgroups),
+//   codes u8 [n/T][k][T/2], gscales f16 [n/32][k],
+// so that everything one output tile needs is one contiguous stream.
+//
+// qm_q4_gemv computes y = x W (gemv_q4, gemv.rs:451-467, inner loop
+// :412-445) for one input row, for up to four weights that share x in one
+// launch (a launch costs a few microseconds of fixed time, about what a
+// 2560x4096 weight takes to stream).  Optional fusions, each what the
+// reference does right around that gemv call:
+//   - x <- rms_norm(x, gamma) first (1 + gamma, eps 1e-6; gemv.rs:571-579),
+//     as before in_proj_* / q,k,v_proj and before the MLP (gemv.rs:740,893);
+//   - y <- residual + x W (the residual adds after out_proj / o_proj and
+//     down_proj, gemv.rs:889-890,896);
+//   - qm_q4_gate_up: silu(x Wg) * (x Wu) for one tile of both weights per
+//     workgroup (fused_gate_up_q4, gemv.rs:469-526).
+// One workgroup owns one column tile and all k rows, so the result needs
+// no second pass: lane t takes rows t, t + 512, ..., and loads its 8 rows'
+// codes, scales, x (and norm weights) before any arithmetic, at clamped
+// rows so that no load waits behind a branch.  The T partial sums of every
+// lane are reduced through LDS in a fixed order (bit-reproducible run to
+// run).  Dequantization costs ~2.4 VALU ops per weight: the codes are split
+// into low and high nibble bytes by two masks, each byte converts with one
+// v_cvt_f32_ubyteN, and the fma uses q itself, the -8 offset being applied
+// once per lane through sum(scale * x).  The RMSNorm is applied by
+// linearity: y = inv_rms * (x (1 + gamma)) W, so its sum of squares comes
+// from the same x loads and the factor scales the column sums.
+#include "qm_device.h"
+#include "qm_kernel_args.h"
+
+#define Q4_THREADS 512
+#define Q4_STEPS 8          // rows per lane in flight
+
+template <int T> struct Q4Codes;                          // T/2 bytes of codes
+template <> struct Q4Codes<16> { typedef uint2 type; };
+template <> struct Q4Codes<8> { typedef uint32_t type; };
+
+QM_DEV void q4_word(float* acc, uint32_t w, float sx) {  // 8 codes: columns 0..7 of acc
+    uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+    // opaque to the optimiser, which would otherwise fold each mask into a
+    // per-nibble bit-field extract (one more op each)
+    asm volatile("" : "+v"(lo), "+v"(hi));
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        acc[2 * b] = fmaf((float)((lo >> (8 * b)) & 0xffu), sx, acc[2 * b]);
+        acc[2 * b + 1] = fmaf((float)((hi >> (8 * b)) & 0xffu), sx, acc[2 * b + 1]);
+    }
+}
+QM_DEV void q4_accumulate(float (&acc)[16], uint2 c, float sx) { q4_word(acc, c.x, sx); q4_word(acc + 8, c.y, sx); }
+QM_DEV void q4_accumulate(float (&acc)[8], uint32_t c, float sx) { q4_word(acc, c, sx); }
+
+// Sum over the workgroup's lanes of each of the T columns (valid in threads
+// < T): THREADS / T parts of T lanes, then the parts, in a fixed order.
+template <int T, int THREADS>
+QM_DEV float q4_reduce(float (*red)[17], float (*red2)[16], const float (&acc)[T], float bias, int tid) {
+#pragma unroll
+    for (int j = 0; j < T; ++j) red[tid][j] = fmaf(-8.0f, bias, acc[j]);
+    __syncthreads();
+    {
+        const int j = tid % T, p = tid / T;
+        float sum = 0.0f;
+#pragma unroll
+        for (int l = 0; l < T; ++l) sum += red[T * p + l][j];
+        red2[p / (16 / T) % (THREADS / 16)][j + T * (p % (16 / T))] = sum;
+    }
+    __syncthreads();
+    float sum = 0.0f;
+    if (tid < T) {
+#pragma unroll
+        for (int p = 0; p < THREADS / T; ++p) sum += red2[p / (16 / T)][tid + T * (p % (16 / T))];
+    }
+    return sum;
+}
+
+// Sum of ss over the workgroup (every thread gets it).
+template <int THREADS>
+QM_DEV float q4_block_sum(float ss, float* red, int tid) {
+    ss = wave_sum64(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    float t = 0.0f;
+#pragma unroll
+    for (int w = 0; w < THREADS / 64; ++w) t += red[w];
+    return t;
+}
+
+template <bool GATE_UP, int T, int STEPS, int THREADS>
+QM_DEV void q4_tile(const Q4GemvArgs& A, int p, int tile, float (*red)[17], float (*red2)[16]) {
+    typedef typename Q4Codes<T>::type CodeT;
+    const int tid = threadIdx.x;
+    const int K = A.k;
+    const int g = tile / (32 / T);                        // the tile's 32-column scale group
+    const CodeT* codes = reinterpret_cast<const CodeT*>(A.codes[p]) + (size_t)tile * K;
+    const uint16_t* gsc = A.gscales[p] + (size_t)g * K;
+    const CodeT* codes_u = GATE_UP ? reinterpret_cast<const CodeT*>(A.codes[1]) + (size_t)tile * K : nullptr;
+    const uint16_t* gsc_u = GATE_UP ? A.gscales[1] + (size_t)g * K : nullptr;
+    // the norm weights are read from a valid array either way (without a
+    // norm, the weight's own scales, value unused): a conditional load would
+    // wait for its data before the next step's loads issue
+    const uint16_t* nwp = A.norm_w ? A.norm_w : gsc;
+
+    float acc[T], acc_u[GATE_UP ? T : 1];
+#pragma unroll
+    for (int j = 0; j < T; ++j) acc[j] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < (GATE_UP ? T : 1); ++j) acc_u[j] = 0.0f;
+    float bsum = 0.0f, bsum_u = 0.0f, ss = 0.0f;
+    for (int k0 = 0; k0 < K; k0 += THREADS * STEPS) {
+        CodeT pk[STEPS], pu[GATE_UP ? STEPS : 1];
+        uint16_t sc[STEPS], su[GATE_UP ? STEPS : 1], nw[STEPS];
+        float xv[STEPS];
+#pragma unroll
+        for (int s = 0; s < STEPS; ++s) {
+            const int k = min(k0 + tid + THREADS * s, K - 1);
+            pk[s] = codes[k];
+            sc[s] = gsc[k];
+            if (GATE_UP) {
+                pu[s] = codes_u[k];
+                su[s] = gsc_u[k];
+            }
+            xv[s] = A.x[k];
+            nw[s] = nwp[k];
+        }
+#pragma unroll
+        for (int s = 0; s < STEPS; ++s) {
+            // rows past k (wave-uniform except in the last wave) add nothing
+            if (k0 + THREADS * s + (tid & ~63) >= K) break;
+            const float xl = k0 + tid + THREADS * s < K ? xv[s] : 0.0f;
+            ss = fmaf(xl, xl, ss);
+            const float xn = A.norm_w ? xl * (1.0f + f16_to_f32(nw[s])) : xl;   // gemv.rs:575 but inv_rms
+            const float sx = f16_to_f32(sc[s]) * xn;                           // gemv.rs:429: scale * x_k
+            bsum += sx;
+            q4_accumulate(acc, pk[s], sx);
+            if (GATE_UP) {
+                const float sxu = f16_to_f32(su[s]) * xn;
+                bsum_u += sxu;
+                q4_accumulate(reinterpret_cast<float(&)[T]>(acc_u), pu[s], sxu);
+            }
+        }
+    }
+
+    // gemv.rs:573: 1 / sqrt(mean(x^2) + 1e-6)
+    const float inv = A.norm_w ? 1.0f / sqrtf(q4_block_sum<THREADS>(ss, &red2[0][0], tid) / (float)K + 1e-6f)
+                               : 1.0f;
+    __syncthreads();
+    const float y = inv * q4_reduce<T, THREADS>(red, red2, acc, bsum, tid);
+    if (GATE_UP) {
+        __syncthreads();
+        const float u = inv * q4_reduce<T, THREADS>(red, red2, reinterpret_cast<const float(&)[T]>(acc_u), bsum_u, tid);
+        // gemv.rs:524: (g / (1 + exp(-g))) * u
+        if (tid < T) A.y[0][T * (size_t)tile + tid] = (y / (1.0f + expf(-y))) * u;
+    } else if (tid < T) {
+        const size_t c = T * (size_t)tile + tid;
+        A.y[p][c] = A.residual[p] ? A.residual[p][c] + y : y;
+    }
+}
+
+template <bool GATE_UP, int STEPS, int THREADS>
+QM_DEV void q4_gemv_body(const Q4GemvArgs& A) {
+    __shared__ float red[THREADS][17];
+    __shared__ float red2[THREADS / 16][16];
+    // which weight: workgroups wstart[p] .. wstart[p+1]-1 are weight p's
+    // tiles (gate / up: weights 0 and 1 share the tile index)
+    int p = 0;
+    if (!GATE_UP) {
+#pragma unroll
+        for (int q = 1; q < QM_Q4_MAX_OUT; ++q)
+            if (q < A.count && (int)blockIdx.x >= A.wstart[q]) p = q;
+    }
+    const int tile = (int)blockIdx.x - A.wstart[p];
+    if (A.tile[p] == 16) q4_tile<GATE_UP, 16, STEPS, THREADS>(A, p, tile, red, red2);
+    else q4_tile<GATE_UP, 8, STEPS, THREADS>(A, p, tile, red, red2);
+}
+
+extern "C" __global__ __launch_bounds__(Q4_THREADS) void qm_q4_gemv(Q4GemvArgs A) {
+    q4_gemv_body<false, Q4_STEPS, Q4_THREADS>(A);
+}
+
+extern "C" __global__ __launch_bounds__(Q4_THREADS) void qm_q4_gate_up(Q4GemvArgs A) {
+    q4_gemv_body<true, Q4_STEPS, Q4_THREADS>(A);
+}
+
+// Reference layout -> tile-major.  Workgroup = 64 rows x 16 groups: each
+// thread reads one 16-byte group block and one scale (consecutive along a
+// row), and writes the block's 32 / T tile slices (consecutive along k
+// within a tile: 64 rows x T/2 bytes).
+extern "C" __global__ __launch_bounds__(256) void qm_q4_repack(Q4RepackArgs A) {
+    __shared__ uint4 tc[16][65];
+    __shared__ uint16_t ts[16][66];
+    const int tid = threadIdx.x;
+    const int G = A.n / 32, T = A.tile;
+    const int gb = blockIdx.x % ((G + 15) / 16), kb = blockIdx.x / ((G + 15) / 16);
+    const int k0 = kb * 64, g0 = gb * 16;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const int r = p * 16 + (tid >> 4), j = tid & 15;
+        const int k = k0 + r, g = g0 + j;
+        if (k < A.k && g < G) {
+            tc[j][r] = *reinterpret_cast<const uint4*>(A.packed + (size_t)k * (A.n / 2) + 16 * (size_t)g);
+            ts[j][r] = A.scales[(size_t)k * G + g];
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const int j = p * 4 + (tid >> 6), r = tid & 63;
+        const int k = k0 + r, g = g0 + j;
+        if (k < A.k && g < G) {
+            const uint4 v = tc[j][r];
+            if (T == 16) {
+                uint2* dst = reinterpret_cast<uint2*>(A.codes);
+                dst[(size_t)(2 * g) * A.k + k] = make_uint2(v.x, v.y);
+                dst[(size_t)(2 * g + 1) * A.k + k] = make_uint2(v.z, v.w);
+            } else {
+                uint32_t* dst = reinterpret_cast<uint32_t*>(A.codes);
+                dst[(size_t)(4 * g) * A.k + k] = v.x;
+                dst[(size_t)(4 * g + 1) * A.k + k] = v.y;
+                dst[(size_t)(4 * g + 2) * A.k + k] = v.z;
+                dst[(size_t)(4 * g + 3) * A.k + k] = v.w;
+            }
+            A.gscales[(size_t)g * A.k + k] = ts[j][r];
+        }
+    }
+}

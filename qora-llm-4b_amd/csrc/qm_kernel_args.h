@@ -119,6 +119,38 @@ struct GqaPrefillArgs {
     int32_t s_pad;
 };
 
+// Q4 GEMV (one input row) on the tile-major device layout, for up to
+// QM_Q4_MAX_OUT weights sharing x: one workgroup per column tile, weight p
+// taking workgroups wstart[p] .. wstart[p+1]-1 with tiles of tile[p]
+// columns.  The gate/up kernel takes gate = weight 0, up = weight 1 (same
+// shape), y[0] = silu(x Wg) * (x Wu).
+#define QM_Q4_MAX_OUT 4
+// Column-tile width of the device layout of a weight with n outputs.
+#define QM_Q4_TILE(n) ((n) < 4096 ? 8 : 16)
+struct Q4GemvArgs {
+    const float* x;                        // [k]
+    const uint16_t* norm_w;                // null, or f16 [k]: x <- rms_norm(x, 1 + norm_w)
+    const uint8_t* codes[QM_Q4_MAX_OUT];   // [n_p/T][k][T/2]
+    const uint16_t* gscales[QM_Q4_MAX_OUT];// f16 [n_p/32][k]
+    float* y[QM_Q4_MAX_OUT];               // [n_p]
+    const float* residual[QM_Q4_MAX_OUT];  // null, or f32 [n_p]: y = residual + x W
+    int32_t tile[QM_Q4_MAX_OUT];           // T of weight p (8 or 16)
+    int32_t wstart[QM_Q4_MAX_OUT + 1];
+    int32_t k;
+    int32_t count;
+};
+
+// Reference Q4Weight layout -> tile-major device layout.
+struct Q4RepackArgs {
+    const uint8_t* packed;   // [k][n/2]
+    const uint16_t* scales;  // f16 [k][n/32]
+    uint8_t* codes;          // [n/T][k][T/2]
+    uint16_t* gscales;       // f16 [n/32][k]
+    int32_t k;
+    int32_t n;
+    int32_t tile;            // T = QM_Q4_TILE(n)
+};
+
 // Counter-based normal generator fill.
 struct FillArgs {
     void* dst;

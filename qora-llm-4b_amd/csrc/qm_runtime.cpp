@@ -44,6 +44,11 @@ struct qm_context {
     hipFunction_t f_dnp_out = nullptr;
     hipFunction_t f_gqp_kv = nullptr;
     hipFunction_t f_gqp_attn = nullptr;
+    hipFunction_t f_q4_gemv = nullptr;
+    hipFunction_t f_q4_repack = nullptr;
+    hipFunction_t f_q4_gate_up = nullptr;
+    int q4_threads = 0;            // the Q4 kernels' workgroup sizes (their launch bounds)
+    int q4_gu_threads = 0;
     void* ws = nullptr;            // general workspace
     size_t ws_bytes = 0;
     std::string err;
@@ -247,9 +252,9 @@ int32_t qm_create(qm_context** out, const qm_config* cfg, const char* code_objec
         c->num_cu = 256;
     std::string dir = code_object_dir ? code_object_dir : library_dir();
     const char* files[] = {"qm_dn_decode.hsaco", "qm_gqa_decode.hsaco", "qm_util.hsaco",
-                           "qm_dn_prefill.hsaco", "qm_gqa_prefill.hsaco"};
-    constexpr int kModules = 5;
-    hipModule_t mods[kModules] = {nullptr, nullptr, nullptr, nullptr, nullptr};
+                           "qm_dn_prefill.hsaco", "qm_gqa_prefill.hsaco", "qm_q4_proj.hsaco"};
+    constexpr int kModules = 6;
+    hipModule_t mods[kModules] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
     for (int i = 0; i < kModules; ++i) {
         std::string path = dir + "/" + files[i];
         hipError_t e = hipModuleLoad(&mods[i], path.c_str());
@@ -273,6 +278,14 @@ int32_t qm_create(qm_context** out, const qm_config* cfg, const char* code_objec
     if (st == QM_OK) st = load_function(c, mods[3], "qm_dn_prefill_out", &c->f_dnp_out);
     if (st == QM_OK) st = load_function(c, mods[4], "qm_gqa_prefill_kv", &c->f_gqp_kv);
     if (st == QM_OK) st = load_function(c, mods[4], "qm_gqa_prefill_attn", &c->f_gqp_attn);
+    if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemv", &c->f_q4_gemv);
+    if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_repack", &c->f_q4_repack);
+    if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gate_up", &c->f_q4_gate_up);
+    if (st == QM_OK &&
+        (hipFuncGetAttribute(&c->q4_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, c->f_q4_gemv) != hipSuccess ||
+         hipFuncGetAttribute(&c->q4_gu_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, c->f_q4_gate_up) !=
+             hipSuccess))
+        st = fail(c, QM_ERR_CODE_OBJECT, "qm_q4_gemv: cannot read its workgroup size");
     if (st == QM_OK && hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess)
         st = fail(c, QM_ERR_HIP, "hipStreamCreate failed");
     if (st != QM_OK) {
@@ -655,6 +668,98 @@ int32_t qm_gqa_prefill(qm_context* c, qm_stream stream, int32_t seq_len, const u
     const int32_t per_group = std::max(1, std::min(c->num_cu / QM_GQA_KV_HEADS, nblk));
     return launch(c, c->f_gqp_attn, static_cast<uint32_t>(per_group) * QM_GQA_KV_HEADS, 768, ga, s,
                   "qm_gqa_prefill_attn");
+}
+
+// ---- Q4 projections ---------------------------------------------------------------
+
+namespace {
+int32_t q4_check(qm_context* c, const char* what, int32_t k, int32_t n) {
+    if (k <= 0 || n <= 0) return fail(c, QM_ERR_INVALID_ARG, "%s: k %d, n %d", what, k, n);
+    if (n % 32 != 0)
+        return fail(c, QM_ERR_SHAPE, "%s: n = %d is not a multiple of the 32-column group", what, n);
+    return QM_OK;
+}
+}  // namespace
+
+int32_t qm_q4_repack(qm_context* c, qm_stream stream, int32_t k, int32_t n, const uint8_t* packed,
+                     const uint16_t* scales, uint8_t* codes, uint16_t* gscales) {
+    if (!c) return QM_ERR_INVALID_ARG;
+    int32_t st = q4_check(c, "qm_q4_repack", k, n);
+    if (st != QM_OK) return st;
+    if (!packed || !scales || !codes || !gscales)
+        return fail(c, QM_ERR_INVALID_ARG, "qm_q4_repack: null pointer");
+    if (!all_aligned16({packed, scales, codes, gscales}))
+        return fail(c, QM_ERR_INVALID_ARG, "qm_q4_repack: device pointers must be 16-byte aligned");
+    Q4RepackArgs ra{packed, scales, codes, gscales, k, n, QM_Q4_TILE(n)};
+    const uint32_t grid = static_cast<uint32_t>((n / 32 + 15) / 16) * static_cast<uint32_t>((k + 63) / 64);
+    return launch(c, c->f_q4_repack, grid, 256, ra, pick(c, stream), "qm_q4_repack");
+}
+
+int32_t qm_q4_gemv_multi(qm_context* c, qm_stream stream, int32_t k, const float* x, const uint16_t* norm_w,
+                         int32_t count, const qm_q4_out* outs) {
+    if (!c) return QM_ERR_INVALID_ARG;
+    if (count < 1 || count > QM_Q4_MAX_OUT || !outs || !x)
+        return fail(c, QM_ERR_INVALID_ARG, "qm_q4_gemv_multi: %d outputs (1..%d) or null pointer", count,
+                    QM_Q4_MAX_OUT);
+    if (!all_aligned16({x, norm_w}))
+        return fail(c, QM_ERR_INVALID_ARG, "qm_q4_gemv: device pointers must be 16-byte aligned");
+    Q4GemvArgs qa{};
+    qa.x = x;
+    qa.norm_w = norm_w;
+    qa.k = k;
+    qa.count = count;
+    int32_t tiles = 0;
+    for (int32_t i = 0; i < count; ++i) {
+        const qm_q4_out& o = outs[i];
+        int32_t st = q4_check(c, "qm_q4_gemv", k, o.n);
+        if (st != QM_OK) return st;
+        if (!o.codes_dev || !o.gscales_dev || !o.y_dev)
+            return fail(c, QM_ERR_INVALID_ARG, "qm_q4_gemv: null pointer (output %d)", i);
+        if (!all_aligned16({o.codes_dev, o.gscales_dev, o.y_dev, o.residual_dev}))
+            return fail(c, QM_ERR_INVALID_ARG, "qm_q4_gemv: device pointers must be 16-byte aligned");
+        qa.codes[i] = o.codes_dev;
+        qa.gscales[i] = o.gscales_dev;
+        qa.y[i] = o.y_dev;
+        qa.residual[i] = o.residual_dev;
+        qa.tile[i] = QM_Q4_TILE(o.n);
+        qa.wstart[i] = tiles;
+        tiles += o.n / qa.tile[i];
+    }
+    for (int32_t i = count; i < QM_Q4_MAX_OUT; ++i) qa.tile[i] = 16;
+    for (int32_t i = count; i <= QM_Q4_MAX_OUT; ++i) qa.wstart[i] = tiles;
+    return launch(c, c->f_q4_gemv, static_cast<uint32_t>(tiles), static_cast<uint32_t>(c->q4_threads), qa,
+                  pick(c, stream), "qm_q4_gemv");
+}
+
+int32_t qm_q4_gemv(qm_context* c, qm_stream stream, int32_t k, int32_t n, const float* x,
+                   const uint8_t* codes, const uint16_t* gscales, float* y) {
+    const qm_q4_out o{n, codes, gscales, y, nullptr};
+    return qm_q4_gemv_multi(c, stream, k, x, nullptr, 1, &o);
+}
+
+int32_t qm_q4_gate_up(qm_context* c, qm_stream stream, int32_t k, int32_t n, const float* x,
+                      const uint16_t* norm_w, const uint8_t* gate_codes, const uint16_t* gate_gscales,
+                      const uint8_t* up_codes, const uint16_t* up_gscales, float* out) {
+    if (!c) return QM_ERR_INVALID_ARG;
+    int32_t st = q4_check(c, "qm_q4_gate_up", k, n);
+    if (st != QM_OK) return st;
+    if (!x || !gate_codes || !gate_gscales || !up_codes || !up_gscales || !out)
+        return fail(c, QM_ERR_INVALID_ARG, "qm_q4_gate_up: null pointer");
+    if (!all_aligned16({x, norm_w, gate_codes, gate_gscales, up_codes, up_gscales, out}))
+        return fail(c, QM_ERR_INVALID_ARG, "qm_q4_gate_up: device pointers must be 16-byte aligned");
+    Q4GemvArgs qa{};
+    qa.x = x;
+    qa.norm_w = norm_w;
+    qa.codes[0] = gate_codes;
+    qa.gscales[0] = gate_gscales;
+    qa.codes[1] = up_codes;
+    qa.gscales[1] = up_gscales;
+    qa.y[0] = out;
+    qa.tile[0] = qa.tile[1] = QM_Q4_TILE(n);
+    qa.k = k;
+    qa.count = 2;
+    return launch(c, c->f_q4_gate_up, static_cast<uint32_t>(n / qa.tile[0]), static_cast<uint32_t>(c->q4_gu_threads), qa,
+                  pick(c, stream), "qm_q4_gate_up");
 }
 
 }  // extern "C"

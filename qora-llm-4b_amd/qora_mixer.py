@@ -37,6 +37,11 @@ GQA_HEADS, GQA_KV_HEADS, GQA_HD, GQA_ROT = 16, 4, 256, 64
 ROPE_THETA = 10_000_000.0
 
 
+class QmQ4Out(C.Structure):
+    _fields_ = [("n", C.c_int32), ("codes_dev", C.c_void_p), ("gscales_dev", C.c_void_p),
+                ("y_dev", C.c_void_p), ("residual_dev", C.c_void_p)]
+
+
 class QmConfig(C.Structure):
     _fields_ = [(n, C.c_int32) for n in (
         "num_qk_heads", "num_v_heads", "dn_head_dim", "conv_kernel",
@@ -85,6 +90,10 @@ _SIGNATURES = {
     "qm_deltanet_prefill": [_P, _P, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P],
     "qm_gqa_decode": [_P, _P, _I32, _P, _P, _P, _P, _P, _P, _P, _I32, _P, _I32, _P, _P, _I64, _P],
     "qm_gqa_prefill": [_P, _P, _I32, _P, _P, _P, _P, _P, _P, _P, _I32, _P, _P, _I64, _P],
+    "qm_q4_repack": [_P, _P, _I32, _I32, _P, _P, _P, _P],
+    "qm_q4_gemv": [_P, _P, _I32, _I32, _P, _P, _P, _P],
+    "qm_q4_gemv_multi": [_P, _P, _I32, _P, _P, _I32, _P],
+    "qm_q4_gate_up": [_P, _P, _I32, _I32, _P, _P, _P, _P, _P, _P, _P],
 }
 _RESTYPES = {"qm_default_config": None, "qm_status_string": C.c_char_p, "qm_last_error": C.c_char_p}
 
@@ -286,6 +295,31 @@ class Context:
             self.h, self.stream, seq_len, _addr(q_gate), _addr(k), _addr(v), _addr(q_norm),
             _addr(k_norm), _addr(rope_cos), _addr(rope_sin), rope_len, _addr(k_cache),
             _addr(v_cache), cap, _addr(out)))
+
+    def q4_repack(self, k, n, packed, scales, codes, gscales):
+        """Reference Q4Weight layout (packed [k][n/2], scales [k][n/32]) -> the
+        tile-major device layout (codes [n/T][k][T/2], gscales [n/32][k], T = 8 if n < 4096 else 16)."""
+        self._check(self.lib.qm_q4_repack(self.h, self.stream, k, n, _addr(packed), _addr(scales),
+                                          _addr(codes), _addr(gscales)))
+
+    def q4_gemv(self, k, n, x, codes, gscales, y):
+        """y[n] = x[k] @ W for a Q4 weight in the device layout."""
+        self._check(self.lib.qm_q4_gemv(self.h, self.stream, k, n, _addr(x), _addr(codes),
+                                        _addr(gscales), _addr(y)))
+
+    def q4_gemv_multi(self, k, x, outs, norm_w=None):
+        """outs: [(n, codes, gscales, y) or (n, codes, gscales, y, residual), ...]
+        (1..4 weights sharing x); norm_w: optional f16 [k] RMSNorm weight."""
+        arr = (QmQ4Out * len(outs))(*[
+            QmQ4Out(o[0], _addr(o[1]), _addr(o[2]), _addr(o[3]), _addr(o[4]) if len(o) > 4 else None)
+            for o in outs])
+        self._check(self.lib.qm_q4_gemv_multi(self.h, self.stream, k, _addr(x), _addr(norm_w), len(outs), arr))
+
+    def q4_gate_up(self, k, n, x, norm_w, gate_codes, gate_gscales, up_codes, up_gscales, out):
+        """out[n] = silu(xn @ Wg) * (xn @ Wu), xn = rms_norm(x, norm_w) or x."""
+        self._check(self.lib.qm_q4_gate_up(self.h, self.stream, k, n, _addr(x), _addr(norm_w),
+                                           _addr(gate_codes), _addr(gate_gscales), _addr(up_codes),
+                                           _addr(up_gscales), _addr(out)))
 
 
 class Event:

@@ -103,3 +103,53 @@ def gqa_prefill_workload(S: int, seed: int = 3) -> dict:
         "q_norm": f16_bits(0.1 * rng.standard_normal(GQA_HD, dtype=np.float32)),
         "k_norm": f16_bits(0.1 * rng.standard_normal(GQA_HD, dtype=np.float32)),
     }
+
+
+# ---- Q4 projections (gemv.rs:29-34 layout) -------------------------------------
+# (k input rows, n outputs) of the QORA-4B projections around the mixer
+# (config.rs:42-79: hidden 2560, intermediate 9216).
+Q4_PROJ_SHAPES = {
+    "in_proj_qkv": (2560, 8192), "in_proj_z": (2560, 4096), "in_proj_a": (2560, 32),
+    "in_proj_b": (2560, 32), "out_proj": (4096, 2560), "q_proj": (2560, 8192),
+    "k_proj": (2560, 1024), "v_proj": (2560, 1024), "o_proj": (4096, 2560),
+    "gate_proj": (2560, 9216), "up_proj": (2560, 9216), "down_proj": (9216, 2560),
+}
+
+
+def q4_dequant(packed: np.ndarray, scales: np.ndarray) -> np.ndarray:
+    """W [k, n] f32 from Q4 codes: scale(row, n // 32) * (q - 8), low nibble = even column."""
+    packed = np.asarray(packed, np.uint8)
+    k, half = packed.shape
+    q = np.empty((k, 2 * half), np.int32)
+    q[:, 0::2] = packed & 0x0F
+    q[:, 1::2] = packed >> 4
+    s = f16_value(scales).astype(np.float32)
+    return np.repeat(s, 32, axis=1) * (q - 8).astype(np.float32)
+
+
+def q4_tile(n: int) -> int:
+    """Column-tile width of the device layout (QM_Q4_TILE)."""
+    return 8 if n < 4096 else 16
+
+
+def q4_device_layout(packed: np.ndarray, scales: np.ndarray):
+    """Reference layout -> device layout: codes [n/T, k, T/2], gscales [n/32, k]."""
+    packed = np.asarray(packed, np.uint8)
+    k, half = packed.shape
+    t = q4_tile(2 * half)
+    codes = np.ascontiguousarray(packed.reshape(k, 2 * half // t, t // 2).transpose(1, 0, 2))
+    return codes, np.ascontiguousarray(np.asarray(scales, np.uint16).T)
+
+
+def q4_random_weight(k: int, n: int, rng: np.random.Generator, scale: float = 0.006):
+    """Valid Q4 codes and f16 scales of the size a quantized N(0, 0.02)
+    weight has (absmax / 7 of 32 draws ~ 0.006)."""
+    packed = rng.integers(0, 256, (k, n // 2), dtype=np.uint8)
+    scales = f16_bits(scale * (1.0 + 0.2 * rng.standard_normal((k, n // 32), dtype=np.float32)))
+    return packed, scales
+
+
+def q4_gemv_workload(k: int, n: int, seed: int = 5) -> dict:
+    rng = np.random.default_rng(seed)
+    packed, scales = q4_random_weight(k, n, rng)
+    return {"x": rng.standard_normal(k, dtype=np.float32), "packed": packed, "scales": scales}

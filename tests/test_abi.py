@@ -27,7 +27,7 @@ def declared_symbols() -> list[str]:
 def test_header_declares_mixer_entries():
     syms = declared_symbols()
     for s in ["qm_create", "qm_destroy", "qm_deltanet_decode", "qm_deltanet_prefill",
-              "qm_gqa_decode", "qm_gqa_prefill", "qm_status_string", "qm_last_error"]:
+              "qm_gqa_decode", "qm_gqa_prefill", "qm_q4_gemv", "qm_status_string", "qm_last_error"]:
         assert s in syms
 
 
@@ -40,7 +40,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_code_objects_are_gfx950_bundles():
-    for name in ["qm_dn_decode", "qm_gqa_decode", "qm_util", "qm_dn_prefill", "qm_gqa_prefill"]:
+    for name in ["qm_dn_decode", "qm_gqa_decode", "qm_util", "qm_dn_prefill", "qm_gqa_prefill", "qm_q4_proj"]:
         p = M.LIB_DIR / f"{name}.hsaco"
         assert p.exists(), p
         data = p.read_bytes()

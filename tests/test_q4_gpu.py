@@ -1,0 +1,184 @@
+"""GPU parity: Q4 projections (qm_q4_repack, qm_q4_gemv) vs the CPU oracle.
+
+The weight goes to the device in the reference layout and is repacked
+there; the repack must equal the numpy tile-major transposition exactly.
+The oracle restates gemv_q4_inner (gemv.rs:412-445) with the reference's
+k-ordered fp32 sums; the kernel sums in another fixed order.  Bar: per
+output column |y - y_ref| <= 1e-5 * sum_k |x_k W_kj| (fp32 reassociation
+over up to 12000 terms), and bit-identical results run to run.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import load_mixer, load_oracle, load_workloads
+
+pytestmark = pytest.mark.gpu
+
+M = load_mixer()
+O = load_oracle()
+W = load_workloads()
+
+
+def repack(ctx, packed, scales):
+    k, n = packed.shape[0], packed.shape[1] * 2
+    dp, ds = ctx.upload(packed), ctx.upload(scales)
+    codes, gsc = ctx.alloc(k * n // 2), ctx.alloc(max(16, k * (n // 32) * 2))
+    ctx.q4_repack(k, n, dp, ds, codes, gsc)
+    return codes, gsc
+
+
+def run_gpu(ctx, x, packed, scales):
+    k, n = packed.shape[0], packed.shape[1] * 2
+    codes, gsc = repack(ctx, packed, scales)
+    dx, y = ctx.upload(x), ctx.alloc(n * 4)
+    ctx.q4_gemv(k, n, dx, codes, gsc, y)
+    return ctx.download(y, (n,), np.float32)
+
+
+def check(got, x, packed, scales):
+    ref = O.q4_gemv(x, packed, scales)
+    mag = np.abs(x).astype(np.float64) @ np.abs(W.q4_dequant(packed, scales)).astype(np.float64)
+    err = np.abs(got.astype(np.float64) - ref)
+    print(f"max|d| {err.max():.3e}  max|d|/mag {(err / (mag + 1e-30)).max():.3e}")
+    assert np.all(err <= 1e-5 * mag + 1e-30)
+
+
+@pytest.mark.parametrize("name", ["in_proj_qkv", "in_proj_a", "in_proj_z", "out_proj", "k_proj", "down_proj"])
+def test_q4_gemv_projection_shapes(ctx, name):
+    k, n = W.Q4_PROJ_SHAPES[name]
+    w = W.q4_gemv_workload(k, n, seed=k + n)
+    w["x"][::5] = 0.0
+    print(f"case: q4 gemv {name} k={k} n={n}", flush=True)
+    got = run_gpu(ctx, w["x"], w["packed"], w["scales"])
+    check(got, w["x"], w["packed"], w["scales"])
+    again = run_gpu(ctx, w["x"], w["packed"], w["scales"])
+    assert np.array_equal(got, again)
+
+
+@pytest.mark.parametrize("k,n", [(1, 32), (37, 64), (513, 96), (1000, 2592), (4096, 32), (4097, 288),
+                                 (12000, 64)])
+def test_q4_gemv_ragged(ctx, k, n):
+    w = W.q4_gemv_workload(k, n, seed=k)
+    print(f"case: q4 gemv ragged k={k} n={n}", flush=True)
+    check(run_gpu(ctx, w["x"], w["packed"], w["scales"]), w["x"], w["packed"], w["scales"])
+
+
+def test_q4_gemv_multi_layer_projections(ctx):
+    """in_proj_qkv, in_proj_z, in_proj_a, in_proj_b of one input in one launch,
+    each output as its own qm_q4_gemv would give it (bit for bit) and within
+    the bar of the oracle."""
+    rng = np.random.default_rng(21)
+    x = rng.standard_normal(2560).astype(np.float32)
+    names = ["in_proj_qkv", "in_proj_z", "in_proj_a", "in_proj_b"]
+    ws = [W.q4_random_weight(*W.Q4_PROJ_SHAPES[nm], rng) for nm in names]
+    dev = [repack(ctx, p, s) for p, s in ws]
+    ns = [W.Q4_PROJ_SHAPES[nm][1] for nm in names]
+    ys = [ctx.alloc(n * 4) for n in ns]
+    dx = ctx.upload(x)
+    print("case: q4 gemv multi (qkv, z, a, b)", flush=True)
+    ctx.q4_gemv_multi(2560, dx, [(n, c, g, y) for n, (c, g), y in zip(ns, dev, ys)])
+    for (p, s), n, (c, g), y in zip(ws, ns, dev, ys):
+        got = ctx.download(y, (n,), np.float32)
+        check(got, x, p, s)
+        single = ctx.alloc(n * 4)
+        ctx.q4_gemv(2560, n, dx, c, g, single)
+        assert np.array_equal(got, ctx.download(single, (n,), np.float32))
+    with pytest.raises(M.MixerError) as e:
+        ctx.q4_gemv_multi(2560, dx, [(ns[0], dev[0][0], dev[0][1], ys[0])] * 5)
+    assert e.value.code == 3
+
+
+@pytest.mark.parametrize("k,n", [(2560, 8192), (37, 96), (1, 32), (130, 544), (70, 4096)])
+def test_q4_repack_is_the_tile_major_transpose(ctx, k, n):
+    rng = np.random.default_rng(k + n)
+    packed, scales = W.q4_random_weight(k, n, rng)
+    print(f"case: q4 repack k={k} n={n}", flush=True)
+    codes, gsc = repack(ctx, packed, scales)
+    want_c, want_s = W.q4_device_layout(packed, scales)
+    assert np.array_equal(ctx.download(codes, want_c.shape, np.uint8), want_c)
+    assert np.array_equal(ctx.download(gsc, want_s.shape, np.uint16), want_s)
+
+
+def test_q4_gemv_quantized_weight(ctx):
+    """A weight quantized by the oracle's quantize_q4 (not random codes)."""
+    rng = np.random.default_rng(9)
+    wf = (0.02 * rng.standard_normal((2560, 1024))).astype(np.float32)
+    packed, scales = O.q4_quantize(wf)
+    x = rng.standard_normal(2560).astype(np.float32)
+    print("case: q4 gemv quantized weight", flush=True)
+    check(run_gpu(ctx, x, packed, scales), x, packed, scales)
+
+
+def test_q4_gemv_errors(ctx):
+    w = W.q4_gemv_workload(64, 64, seed=1)
+    dx, y = ctx.upload(w["x"]), ctx.alloc(64 * 4)
+    dp, ds = repack(ctx, w["packed"], w["scales"])
+    with pytest.raises(M.MixerError) as e:
+        ctx.q4_gemv(64, 48, dx, dp, ds, y)           # n not a multiple of 32
+    assert e.value.code == 4
+    with pytest.raises(M.MixerError) as e:
+        ctx.q4_gemv(64, 64, dx.offset(4), dp, ds, y)  # misaligned x
+    assert e.value.code == 3
+    with pytest.raises(M.MixerError) as e:
+        ctx.q4_gemv(0, 64, dx, dp, ds, y)
+    assert e.value.code == 3
+    with pytest.raises(M.MixerError) as e:
+        ctx.q4_repack(64, 40, dp, ds, dp, ds)        # n not a multiple of 32
+    assert e.value.code == 4
+
+
+def _mag(x, packed, scales):
+    return np.abs(x).astype(np.float64) @ np.abs(W.q4_dequant(packed, scales)).astype(np.float64)
+
+
+def test_q4_gemv_multi_norm_and_residual(ctx):
+    """rms_norm(x, 1 + gamma) fused ahead of three projections, and a
+    residual add (in place, y = residual) on one of them (gemv.rs:571-579,
+    :889-890)."""
+    rng = np.random.default_rng(31)
+    k = 2560
+    x = (3.0 * rng.standard_normal(k)).astype(np.float32)
+    gamma = W.f16_bits(0.1 * rng.standard_normal(k).astype(np.float32))
+    xn = O.rms_norm(x, gamma)
+    shapes = [(k, 1024), (k, 8192), (k, 32)]
+    ws = [W.q4_random_weight(kk, n, rng) for kk, n in shapes]
+    dev = [repack(ctx, p, s) for p, s in ws]
+    res = rng.standard_normal(8192).astype(np.float32)
+    ys = [ctx.alloc(1024 * 4), ctx.upload(res), ctx.alloc(32 * 4)]
+    dx, dg = ctx.upload(x), ctx.upload(gamma)
+    print("case: q4 gemv multi with rms norm and in-place residual", flush=True)
+    outs = [(1024, dev[0][0], dev[0][1], ys[0]), (8192, dev[1][0], dev[1][1], ys[1], ys[1]),
+            (32, dev[2][0], dev[2][1], ys[2])]
+    ctx.q4_gemv_multi(k, dx, outs, norm_w=dg)
+    for i, ((p, s), (_, n)) in enumerate(zip(ws, shapes)):
+        got = ctx.download(ys[i], (n,), np.float32).astype(np.float64)
+        ref = O.q4_gemv(xn, p, s).astype(np.float64) + (res if i == 1 else 0.0)
+        mag = _mag(xn, p, s) + (np.abs(res) if i == 1 else 0.0)
+        print(f"out {i}: max|d|/mag {(np.abs(got - ref) / mag).max():.3e}")
+        assert np.all(np.abs(got - ref) <= 1e-5 * mag + 1e-30)
+    assert np.array_equal(ctx.download(dx, (k,), np.float32), x)       # x itself is not written
+
+
+@pytest.mark.parametrize("norm", [False, True])
+def test_q4_gate_up(ctx, norm):
+    """silu(xn Wg) * (xn Wu) (fused_gate_up_q4, gemv.rs:469-526) for the
+    2560 x 9216 MLP weights, with and without the fused rms_norm."""
+    rng = np.random.default_rng(41 + norm)
+    k, n = 2560, 9216
+    x = rng.standard_normal(k).astype(np.float32)
+    gamma = W.f16_bits(0.1 * rng.standard_normal(k).astype(np.float32))
+    xn = O.rms_norm(x, gamma) if norm else x
+    (gp, gs), (up, us) = W.q4_random_weight(k, n, rng), W.q4_random_weight(k, n, rng)
+    (gc, gg), (uc, ug) = repack(ctx, gp, gs), repack(ctx, up, us)
+    out = ctx.alloc(n * 4)
+    print(f"case: q4 gate/up norm={norm}", flush=True)
+    ctx.q4_gate_up(k, n, ctx.upload(x), ctx.upload(gamma) if norm else None, gc, gg, uc, ug, out)
+    got = ctx.download(out, (n,), np.float32).astype(np.float64)
+    ref = O.q4_gate_up(xn, gp, gs, up, us).astype(np.float64)
+    g = O.q4_gemv(xn, gp, gs).astype(np.float64)
+    u = O.q4_gemv(xn, up, us).astype(np.float64)
+    bound = 1e-5 * (1.2 * _mag(xn, gp, gs) * np.abs(u) + 1.1 * np.abs(g) * _mag(xn, up, us)) + 1e-30
+    print(f"max|d| {np.abs(got - ref).max():.3e}  max|d|/bound {(np.abs(got - ref) / bound).max():.3e}")
+    assert np.all(np.abs(got - ref) <= bound)
