@@ -13,6 +13,10 @@
 //   forward_attn_decode_gpu      gpu_inference.rs:247-254
 //   prefill_deltanet_layer_gpu   gpu_inference.rs:436-441
 //   prefill_attn_layer_gpu       gpu_inference.rs:670-677
+//   GpuQ4Weight, gemv_gpu, ...   the Q4 projections around the mixer:
+//                                Q4Weight gemv.rs:29-34, gemv() :286-291,
+//                                fused_gate_up_gemv :304-315, rms_norm
+//                                :571-579, loader repack gpu_loader.rs:82-106
 // Each forward takes the projection outputs (the caller keeps in_proj /
 // q/k/v_proj) and returns the mixer output (the out_proj / o_proj input).
 // State and cache objects are updated in place, as the reference's &mut
@@ -25,6 +29,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <initializer_list>
 #include <stdexcept>
 #include <string>
 #include <utility>
@@ -236,6 +241,78 @@ inline void prefill_attn_layer_gpu(Context& ctx, std::size_t seq_len, const uint
                              rope_len, kv.k.as<uint16_t>(), kv.v.as<uint16_t>(),
                              static_cast<int64_t>(kv.capacity), out));
     kv.seq_len = seq_len;
+}
+
+// ---- Q4 projections ----------------------------------------------------------
+
+// A Q4Weight (gemv.rs:29-34) on the device: uploaded in the reference layout
+// (packed [k][n/2], scales f16 [k][n/32]) and repacked there into the
+// library's tile-major layout, the role q4_weight_to_gpu plays for the
+// reference's backend (gpu_loader.rs:82-106).
+struct GpuQ4Weight {
+    DeviceBuffer codes, gscales;
+    std::size_t k = 0, n = 0;
+
+    static GpuQ4Weight upload(Context& ctx, const uint8_t* packed, const uint16_t* scales, std::size_t k,
+                              std::size_t n) {
+        const std::size_t pb = k * n / 2, sb = k * (n / 32) * 2;
+        DeviceBuffer p(ctx, pb), s(ctx, sb < 16 ? 16 : sb);
+        p.upload(packed, pb);
+        s.upload(scales, sb);
+        GpuQ4Weight w;
+        w.k = k;
+        w.n = n;
+        w.codes = DeviceBuffer(ctx, pb);
+        w.gscales = DeviceBuffer(ctx, sb < 16 ? 16 : sb);
+        ctx.check(qm_q4_repack(ctx.get(), nullptr, static_cast<int32_t>(k), static_cast<int32_t>(n),
+                               p.as<uint8_t>(), s.as<uint16_t>(), w.codes.as<uint8_t>(), w.gscales.as<uint16_t>()));
+        ctx.sync();   // the staging copies are freed on return
+        return w;
+    }
+    qm_q4_out out(float* y, const float* residual = nullptr) const {
+        return qm_q4_out{static_cast<int32_t>(n), codes.as<uint8_t>(), gscales.as<uint16_t>(), y, residual};
+    }
+};
+
+// gemv(input, &Weight::Q4) (gemv.rs:286-291): y = x W.  Device pointers.
+inline void gemv_gpu(Context& ctx, const float* x, const GpuQ4Weight& w, float* y, qm_stream stream = nullptr) {
+    ctx.check(qm_q4_gemv(ctx.get(), stream, static_cast<int32_t>(w.k), static_cast<int32_t>(w.n), x,
+                         w.codes.as<uint8_t>(), w.gscales.as<uint16_t>(), y));
+}
+
+// x_norm = rms_norm(x, norm) followed by the gemv calls on it (up to four),
+// as the top of forward_deltanet_decode (gemv.rs:740-742,788-789,865) and
+// of forward_attn_decode (:926-942) do: one launch.
+inline void rms_norm_gemv_gpu(Context& ctx, const float* x, const uint16_t* norm_w,
+                              std::initializer_list<std::pair<const GpuQ4Weight*, float*>> outs,
+                              qm_stream stream = nullptr) {
+    qm_q4_out o[4];
+    int32_t cnt = 0;
+    std::size_t k = 0;
+    for (const auto& e : outs) {
+        if (cnt == 4) throw MixerError(QM_ERR_INVALID_ARG, "rms_norm_gemv_gpu: at most four weights");
+        o[cnt++] = e.first->out(e.second);
+        k = e.first->k;
+    }
+    ctx.check(qm_q4_gemv_multi(ctx.get(), stream, static_cast<int32_t>(k), x, norm_w, cnt, o));
+}
+
+// hidden += v W: the out_proj / o_proj / down_proj residual adds
+// (gemv.rs:886-890,895-896); hidden is updated in place.
+inline void gemv_residual_gpu(Context& ctx, const float* v, const GpuQ4Weight& w, float* hidden,
+                              qm_stream stream = nullptr) {
+    const qm_q4_out o = w.out(hidden, hidden);
+    ctx.check(qm_q4_gemv_multi(ctx.get(), stream, static_cast<int32_t>(w.k), v, nullptr, 1, &o));
+}
+
+// fused_gate_up_gemv(rms_norm(x, norm), gate, up) (gemv.rs:893-894,304-315):
+// out = silu(xn Wg) * (xn Wu); norm_w may be null (no norm).
+inline void rms_norm_fused_gate_up_gpu(Context& ctx, const float* x, const uint16_t* norm_w,
+                                       const GpuQ4Weight& gate, const GpuQ4Weight& up, float* out,
+                                       qm_stream stream = nullptr) {
+    ctx.check(qm_q4_gate_up(ctx.get(), stream, static_cast<int32_t>(gate.k), static_cast<int32_t>(gate.n), x,
+                            norm_w, gate.codes.as<uint8_t>(), gate.gscales.as<uint16_t>(), up.codes.as<uint8_t>(),
+                            up.gscales.as<uint16_t>(), out));
 }
 
 }  // namespace qor4b

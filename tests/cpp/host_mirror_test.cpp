@@ -209,6 +209,75 @@ void attention_flow(Context& ctx, const Qor4bConfig& cfg) {
     expect(raised, "gqa decode past the RoPE table raises (missing = 1)", raised ? 0 : 1, 0.5);
 }
 
+// The Q4 projections of one DeltaNet decode layer through the mirror
+// (gemv.rs:740-742,788-789,865,886-897) against the oracle's rms_norm and
+// gemv_q4_inner restatements: qkv/z/a/b of the normed input, the out_proj
+// residual, and the MLP (normed gate/up, down residual).
+void q4_layer_flow(Context& ctx) {
+    Rng r(23);
+    const std::size_t H = 2560;
+    struct Shape { std::size_t k, n; };
+    const Shape sh[8] = {{H, 8192}, {H, 4096}, {H, 32}, {H, 32}, {4096, H}, {H, 9216}, {H, 9216}, {9216, H}};
+    std::vector<std::vector<uint8_t>> packed(8);
+    std::vector<std::vector<uint16_t>> scales(8);
+    std::vector<GpuQ4Weight> w;
+    for (int i = 0; i < 8; ++i) {
+        std::vector<float> f = normals(r, sh[i].k * sh[i].n, 0.02f);
+        packed[i].resize(sh[i].k * sh[i].n / 2);
+        scales[i].resize(sh[i].k * sh[i].n / 32);
+        or_q4_quantize(f.data(), (int32_t)sh[i].k, (int32_t)sh[i].n, packed[i].data(), scales[i].data());
+        w.push_back(GpuQ4Weight::upload(ctx, packed[i].data(), scales[i].data(), sh[i].k, sh[i].n));
+    }
+    std::vector<float> x = normals(r, H), mix = normals(r, 4096);
+    std::vector<float> g1 = normals(r, H, 0.1f), g2 = normals(r, H, 0.1f);
+    std::vector<uint16_t> n1 = to_f16(g1), n2 = to_f16(g2);
+    DeviceBuffer dx = upload(ctx, x), dmix = upload(ctx, mix), dn1 = upload(ctx, n1), dn2 = upload(ctx, n2);
+    DeviceBuffer y0(ctx, 8192 * 4), y1(ctx, 4096 * 4), y2(ctx, 32 * 4), y3(ctx, 32 * 4), inter(ctx, 9216 * 4);
+    DeviceBuffer h = upload(ctx, x);
+
+    rms_norm_gemv_gpu(ctx, dx.as<float>(), dn1.as<uint16_t>(),
+                      {{&w[0], y0.as<float>()}, {&w[1], y1.as<float>()}, {&w[2], y2.as<float>()},
+                       {&w[3], y3.as<float>()}});
+    gemv_residual_gpu(ctx, dmix.as<float>(), w[4], h.as<float>());
+    rms_norm_fused_gate_up_gpu(ctx, h.as<float>(), dn2.as<uint16_t>(), w[5], w[6], inter.as<float>());
+    // down_proj residual is checked against the GPU's own MLP input
+    std::vector<float> inter_g(9216), h_mid(H);
+    inter.download(inter_g.data(), 9216 * 4);
+    h.download(h_mid.data(), H * 4);
+    gemv_residual_gpu(ctx, inter.as<float>(), w[7], h.as<float>());
+    ctx.sync();
+
+    std::vector<float> xn(H), ref(9216), got(9216);
+    or_rms_norm(x.data(), (int32_t)H, n1.data(), xn.data());
+    DeviceBuffer* ys[4] = {&y0, &y1, &y2, &y3};
+    const char* names[4] = {"q4 rms_norm + in_proj_qkv (rel)", "q4 rms_norm + in_proj_z (rel)",
+                            "q4 rms_norm + in_proj_a (rel)", "q4 rms_norm + in_proj_b (rel)"};
+    for (int i = 0; i < 4; ++i) {
+        or_q4_gemv(xn.data(), packed[i].data(), scales[i].data(), (int32_t)H, (int32_t)sh[i].n, ref.data());
+        ys[i]->download(got.data(), sh[i].n * 4);
+        const double e = rel_err(got.data(), ref.data(), sh[i].n);
+        expect(e <= 1e-5, names[i], e, 1e-5);
+    }
+    // out_proj residual: h = x + mix W
+    or_q4_gemv(mix.data(), packed[4].data(), scales[4].data(), 4096, (int32_t)H, ref.data());
+    for (std::size_t j = 0; j < H; ++j) ref[j] += x[j];
+    double e = rel_err(h_mid.data(), ref.data(), H);
+    expect(e <= 1e-5, "q4 out_proj + residual (rel)", e, 1e-5);
+    // MLP gate/up on rms_norm(h)
+    std::vector<float> hn(H);
+    or_rms_norm(h_mid.data(), (int32_t)H, n2.data(), hn.data());
+    or_q4_gate_up(hn.data(), packed[5].data(), scales[5].data(), packed[6].data(), scales[6].data(), (int32_t)H,
+                  9216, ref.data());
+    e = rel_err(inter_g.data(), ref.data(), 9216);
+    expect(e <= 1e-4, "q4 rms_norm + gate/up + silu (rel)", e, 1e-4);
+    // down_proj residual
+    or_q4_gemv(inter_g.data(), packed[7].data(), scales[7].data(), 9216, (int32_t)H, ref.data());
+    for (std::size_t j = 0; j < H; ++j) ref[j] += h_mid[j];
+    h.download(got.data(), H * 4);
+    e = rel_err(got.data(), ref.data(), H);
+    expect(e <= 1e-5, "q4 down_proj + residual (rel)", e, 1e-5);
+}
+
 }  // namespace
 
 int main() {
@@ -217,6 +286,7 @@ int main() {
         Context ctx(cfg);
         deltanet_flow(ctx, cfg);
         attention_flow(ctx, cfg);
+        q4_layer_flow(ctx);
     } catch (const std::exception& e) {
         std::printf("exception: %s\n", e.what());
         return 2;
