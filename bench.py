@@ -537,6 +537,54 @@ def run_q4_proj(args, ctx):
     }
 
 
+def run_q4_gemm(args, ctx):
+    """The prefill form of a Q4 projection: in_proj_qkv (2560 x 8192) for a
+    4096-token prompt on MFMA, f16 input rows (the RMSNormed hidden state),
+    bf16 output (what the chunked DeltaNet prefill reads)."""
+    K, Wm = args.steps, args.warmup
+    m, (k, n) = 4096, W.Q4_PROJ_SHAPES["in_proj_qkv"]
+    seed = [4000]
+
+    def fill(buf, dtype, count, std, mean=0.0):
+        ctx.fill_normal(buf, dtype, count, mean, std, seed[0])
+        seed[0] += 1
+
+    codes = ctx.alloc(k * n // 2)
+    fill(codes, M.QM_F16, k * n // 4, 1.0)                # any byte is a valid pair of codes
+    gscales = ctx.alloc(k * (n // 32) * 2)
+    fill(gscales, M.QM_F16, k * (n // 32), 0.0012, 0.006)
+    x = ctx.alloc(m * k * 2)
+    fill(x, M.QM_F16, m * k, 1.0)
+    y = ctx.alloc(m * n * 2)
+    tm = Timer(ctx)
+
+    def step():
+        ctx.q4_gemm(m, k, n, x, codes, gscales, y_bf16=y)
+
+    for _ in range(Wm):
+        step()
+    ctx.sync()
+    t0, t1 = ctx.event(), ctx.event()
+    wall0 = time.perf_counter()
+    t0.record()
+    for _ in range(K):
+        tm.wrap(step)
+    t1.record()
+    ctx.sync()
+    wall = time.perf_counter() - wall0
+    flops = 2 * m * k * n
+    k_ms = tm.mean_ms()
+    return {
+        "tokens": K * m, "total_ms": t0.elapsed_ms(t1), "wall_s": wall,
+        "dominant": "qm_q4_gemm (in_proj_qkv, 4096 x 2560 x 8192)",
+        "roofline": {"bound": "mfma", "achieved": flops / (k_ms * 1e-3), "peak": MFMA_BF16_PEAK,
+                     "kernel_ms": k_ms, "flops_per_launch": flops},
+        "config": {"workload": "Q4 prefill projection in_proj_qkv: 4096 tokens x 2560 -> 8192, f16 input, "
+                               "Q4 weight dequantized to f16 on MFMA, bf16 output",
+                   "batch": 1, "seq_len": m, "global_batch": 1, "parallelism": "single GPU"},
+    }
+
+
 def _repeat_for(fn, min_s=CPU_SAMPLE_S, max_iters=10 ** 6):
     """Call fn() until min_s seconds have elapsed; returns (calls, seconds)."""
     n, t0 = 0, time.perf_counter()
@@ -621,6 +669,14 @@ def cpu_baseline(workload: str) -> dict:
                 "sample": f"{n} DeltaNet-layer sets of the Q4 projections, norms and residuals "
                           f"(scalar gemv_q4_inner restatement, one thread, {dt:.1f} s); "
                           f"tokens/s = layer sets/s / 24"}
+    if workload == "q4_gemm":
+        rng = np.random.default_rng(9)
+        packed, scales = W.q4_random_weight(*W.Q4_PROJ_SHAPES["in_proj_qkv"], rng)
+        xs = W.f16_value(W.f16_bits(rng.standard_normal((8, 2560), dtype=np.float32)))
+        n, dt = _repeat_for(lambda: O.q4_gemm(xs, packed, scales, nthreads=1))
+        return {"value": 8 * n / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
+                "sample": f"{n} calls of gemm_q4 on 8 rows (scalar gemv_q4_inner restatement, one thread, "
+                          f"{dt:.1f} s)"}
     if workload == "gqa_decode":
         pos = 4096
         w = W.gqa_decode_workload(pos, 1, seed=1)
@@ -681,7 +737,8 @@ def main():
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="stack",
-                    choices=["stack", "dn_decode", "gqa_decode", "dn_prefill", "gqa_prefill", "q4_proj"])
+                    choices=["stack", "dn_decode", "gqa_decode", "dn_prefill", "gqa_prefill", "q4_proj",
+                             "q4_gemm"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
                     help="skip the graph-replayed timing (rocprofv3's kernel tracer crashes in "
@@ -697,7 +754,7 @@ def main():
               "(sharding is a design note, not a launched path); run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     defaults = {"stack": (32, 4), "dn_decode": (256, 16), "gqa_decode": (200, 20),
-                "dn_prefill": (20, 3), "gqa_prefill": (10, 2), "q4_proj": (50, 5)}[args.workload]
+                "dn_prefill": (20, 3), "gqa_prefill": (10, 2), "q4_proj": (50, 5), "q4_gemm": (20, 3)}[args.workload]
     args.steps = args.steps or defaults[0]
     args.warmup = defaults[1] if args.warmup is None else args.warmup
 
@@ -713,7 +770,7 @@ def main():
         dst.close()
     run = {"stack": run_stack, "dn_decode": run_dn_decode, "gqa_decode": run_gqa_decode,
            "dn_prefill": run_dn_prefill, "gqa_prefill": run_gqa_prefill,
-           "q4_proj": run_q4_proj}[args.workload]
+           "q4_proj": run_q4_proj, "q4_gemm": run_q4_gemm}[args.workload]
     r = run(args, ctx)
     ctx.sync()
     ctx.close()
@@ -734,13 +791,14 @@ def main():
         "metric": {"stack": "mixer tokens/s (decode, 32-layer hybrid stack) on 1x MI355X",
                    "dn_prefill": "mixer tokens/s (prefill) on 1x MI355X",
                    "gqa_prefill": "mixer tokens/s (prefill) on 1x MI355X",
-                   "q4_proj": "Q4 projection tokens/s (decode) on 1x MI355X"}.get(
+                   "q4_proj": "Q4 projection tokens/s (decode) on 1x MI355X",
+                   "q4_gemm": "Q4 projection tokens/s (prefill) on 1x MI355X"}.get(
                        args.workload, "mixer tokens/s (decode) on 1x MI355X"),
         "value": value, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": r["total_ms"] / args.steps,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16" if args.workload in ("dn_prefill", "gqa_prefill") else "f32",
-        "data": ("synthetic (seeded random Q4 codes, f16 scales and normal inputs)" if args.workload == "q4_proj"
+        "dtype": {"dn_prefill": "bf16", "gqa_prefill": "bf16", "q4_gemm": "f16"}.get(args.workload, "f32"),
+        "data": ("synthetic (seeded random Q4 codes, f16 scales and normal inputs)" if args.workload.startswith("q4")
                  else "synthetic (seeded normal inputs, random-init state and f16 KV cache)"),
         "config": r["config"],
         "roofline": rl,

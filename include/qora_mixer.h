@@ -306,6 +306,29 @@ int32_t qm_q4_gate_up(qm_context* ctx, qm_stream stream, int32_t k, int32_t n,
                       const uint8_t* up_codes_dev, const uint16_t* up_gscales_dev,
                       float* out_dev);
 
+/* ---- Q4 projections for prefill (seq_len > 1) ------------------------- */
+/* The f16 input of qm_q4_gemm: each of the m rows of x_dev (f32 [m][k]) as
+ * rms_norm(row, norm_w) (1 + gamma, eps 1e-6; gemv.rs:571-579), or simply
+ * converted when norm_w_dev is NULL.  out_dev f16 [m][k]; k % 4 == 0. */
+int32_t qm_rms_norm_f16(qm_context* ctx, qm_stream stream, int32_t m, int32_t k,
+                        const float* x_dev, const uint16_t* norm_w_dev,
+                        uint16_t* out_dev);
+
+/* y = x W (+ residual) for m input rows on MFMA: replaces gemm_q4,
+ * gemv.rs:529-542 (gemm() on a Q4 weight, :295-300), which the prefill
+ * layers call for every projection (gemv.rs:1114-1117,1222,1231-1239,
+ * 1366-1385,1447-1467).  x_dev f16 [m][k] (k % 32 == 0, else QM_ERR_SHAPE);
+ * codes_dev/gscales_dev a weight in the device layout (qm_q4_repack);
+ * residual_dev NULL or f32 [m][n]; exactly one of y_dev (f32 [m][n]) and
+ * y_bf16_dev (bf16 [m][n], e.g. the in_proj_qkv / in_proj_z outputs that
+ * qm_deltanet_prefill reads) is non-NULL.  W is dequantized to f16 per
+ * element (s * (q - 8), one rounding) and x is f16: a bf16-path result,
+ * within 1e-3 of sum_k |x_k W_kj| of the fp32 reference per element. */
+int32_t qm_q4_gemm(qm_context* ctx, qm_stream stream, int32_t m, int32_t k, int32_t n,
+                   const uint16_t* x_dev, const uint8_t* codes_dev,
+                   const uint16_t* gscales_dev, const float* residual_dev,
+                   float* y_dev, uint16_t* y_bf16_dev);
+
 #ifdef __cplusplus
 }
 #endif

@@ -232,3 +232,159 @@ extern "C" __global__ __launch_bounds__(256) void qm_q4_repack(Q4RepackArgs A) {
         }
     }
 }
+
+// ---------------------------------------------------------------------------
+// Prefill: C[m][n] = X[m][k] W on MFMA (gemm_q4, gemv.rs:529-542, for
+// seq_len > 1).  X is f16 (qm_rms_norm_f16 produces it from the f32 hidden
+// state, fusing the layer's RMSNorm); W stays Q4 in HBM and is dequantized
+// to f16 on its way into LDS, s * (q - 8) rounded once to f16.
+// Workgroup tile 128 x 128, four waves of 64 x 64 (4 x 4 tiles of
+// v_mfma_f32_16x16x32_f16), k steps of 32 double-buffered in LDS with one
+// barrier per step: step t + 1's X rows and codes are loaded into registers
+// before step t's MFMAs and stored to the other buffer after them.
+// LDS rows are k-contiguous, X as [m][k] and W as [n][k], padded to 40 f16
+// (80 bytes) so the 16 rows of a fragment read land in 16 distinct bank
+// slots; a lane's A operand (row m, k 8kg .. +7) and B operand (column n,
+// k 8kg .. +7) are then one 16-byte read each.
+// ---------------------------------------------------------------------------
+#define GM_TM 128
+#define GM_TN 128
+#define GM_TK 32
+#define GM_LDK 40
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+extern "C" __global__ __launch_bounds__(256) void qm_q4_gemm(Q4GemmArgs A) {
+    __shared__ __attribute__((aligned(16))) _Float16 sA[2][GM_TM][GM_LDK];
+    __shared__ __attribute__((aligned(16))) _Float16 sB[2][GM_TN][GM_LDK];
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int nbn = (A.n + GM_TN - 1) / GM_TN;
+    // consecutive workgroups walk n within one row block: the row block's X
+    // (k x 128 f16) is reused from L2 across its column tiles
+    const int bm = (int)blockIdx.x / nbn, bn = (int)blockIdx.x % nbn;
+    const int m0 = bm * GM_TM, n0 = bn * GM_TN;
+    const int wm = w >> 1, wn = w & 1;
+    const int T = A.tile, K = A.k;
+    const int nk = K / GM_TK;
+
+    // X staging: thread -> row tid / 2, 16 k at 16 (tid & 1)
+    const int ar = tid >> 1, ah = tid & 1;
+    const uint16_t* xrow = A.x + (size_t)min(m0 + ar, A.m - 1) * K + 16 * ah;
+    // W staging: thread -> 8-column block c8 = tid / 16 of the tile, row pair
+    // rp = tid % 16 (rows 2rp, 2rp + 1 of the step); a block is 4 code bytes
+    // of one row (T = 16: half of a tile row, T = 8: a whole one)
+    const int c8 = tid >> 4, rp = tid & 15;
+    const int ncl = min(n0 + 8 * c8, A.n - 8);          // valid block for loads
+    const uint8_t* bcodes = A.codes + (size_t)(ncl / T) * K * (T / 2) + (ncl % T) / 2;
+    const uint16_t* bsc = A.gscales + (size_t)(ncl / 32) * K;
+
+    const size_t cstride = (size_t)(T / 2);
+    uint4 ra0, ra1;
+    uint32_t rb0, rb1;
+    uint16_t rs0, rs1;
+#define GM_GLOAD(kt)                                                                   \
+    do {                                                                               \
+        const int k0_ = (kt) * GM_TK;                                                  \
+        ra0 = *reinterpret_cast<const uint4*>(xrow + k0_);                            \
+        ra1 = *reinterpret_cast<const uint4*>(xrow + k0_ + 8);                        \
+        rb0 = *reinterpret_cast<const uint32_t*>(bcodes + (size_t)(k0_ + 2 * rp) * cstride);     \
+        rb1 = *reinterpret_cast<const uint32_t*>(bcodes + (size_t)(k0_ + 2 * rp + 1) * cstride); \
+        rs0 = bsc[k0_ + 2 * rp];                                                       \
+        rs1 = bsc[k0_ + 2 * rp + 1];                                                   \
+    } while (0)
+    // column 8 c8 + c of rows 2rp, 2rp + 1: byte c / 2 of each row's block,
+    // low nibble for even c; the two rows' f16 weights form one 4-byte store
+#define GM_LSTORE(buf)                                                                 \
+    do {                                                                               \
+        *reinterpret_cast<uint4*>(&sA[buf][ar][16 * ah]) = ra0;                       \
+        *reinterpret_cast<uint4*>(&sA[buf][ar][16 * ah + 8]) = ra1;                   \
+        const float s0_ = f16_to_f32(rs0), s1_ = f16_to_f32(rs1);                     \
+        _Pragma("unroll") for (int c = 0; c < 8; ++c) {                               \
+            const float q0 = (float)((rb0 >> (4 * c)) & 15u) - 8.0f;                  \
+            const float q1 = (float)((rb1 >> (4 * c)) & 15u) - 8.0f;                  \
+            const uint32_t pr = (uint32_t)f32_to_f16(s0_ * q0) | ((uint32_t)f32_to_f16(s1_ * q1) << 16); \
+            *reinterpret_cast<uint32_t*>(&sB[buf][8 * c8 + c][2 * rp]) = pr;          \
+        }                                                                              \
+    } while (0)
+
+    floatx4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    GM_GLOAD(0);
+    GM_LSTORE(0);
+    __syncthreads();
+    const int fr = lane & 15, fk = 8 * (lane >> 4);
+    for (int kt = 0; kt < nk; ++kt) {
+        const int b = kt & 1;
+        if (kt + 1 < nk) GM_GLOAD(kt + 1);
+        half8 af[4], bf[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const half8*>(&sA[b][64 * wm + 16 * i + fr][fk]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bf[j] = *reinterpret_cast<const half8*>(&sB[b][64 * wn + 16 * j + fr][fk]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        // the other buffer was last read in step kt - 1, before the barrier
+        if (kt + 1 < nk) GM_LSTORE(b ^ 1);
+        __syncthreads();
+    }
+
+#undef GM_GLOAD
+#undef GM_LSTORE
+    // C fragment: lane (n = lane & 15, mg = lane >> 4) holds rows 4 mg .. +3
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int col = n0 + 64 * wn + 16 * j + fr;
+        if (col >= A.n) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int row = m0 + 64 * wm + 16 * i + 4 * (lane >> 4) + e;
+                if (row >= A.m) continue;
+                const size_t o = (size_t)row * A.n + col;
+                float v = acc[i][j][e];
+                if (A.residual) v += A.residual[o];
+                if (A.y_bf16) A.y_bf16[o] = f32_to_bf16(v);
+                else A.y[o] = v;
+            }
+    }
+}
+
+// rms_norm (1 + gamma, eps 1e-6; gemv.rs:571-579) of each of m rows of f32
+// x [m][k], written as the f16 input of qm_q4_gemm; without a norm weight,
+// the plain f16 conversion.  One workgroup per row.
+extern "C" __global__ __launch_bounds__(256) void qm_rms_norm_f16(RmsNormArgs A) {
+    __shared__ float red[4];
+    const int tid = threadIdx.x, row = blockIdx.x;
+    const float* x = A.x + (size_t)row * A.k;
+    float ss = 0.0f;
+    for (int i = 4 * tid; i < A.k; i += 1024) {
+        const float4 v = ld4(x + i);
+        ss = fmaf(v.x, v.x, ss); ss = fmaf(v.y, v.y, ss); ss = fmaf(v.z, v.z, ss); ss = fmaf(v.w, v.w, ss);
+    }
+    ss = wave_sum64(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    const float inv = A.norm_w ? 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)A.k + 1e-6f) : 1.0f;
+    uint16_t* out = A.out + (size_t)row * A.k;
+    for (int i = 4 * tid; i < A.k; i += 1024) {
+        const float4 v = ld4(x + i);
+        float g[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+        if (A.norm_w) {
+            const uint2 gw = *reinterpret_cast<const uint2*>(A.norm_w + i);
+            g[0] = 1.0f + f16_to_f32((uint16_t)(gw.x & 0xffffu)); g[1] = 1.0f + f16_to_f32((uint16_t)(gw.x >> 16));
+            g[2] = 1.0f + f16_to_f32((uint16_t)(gw.y & 0xffffu)); g[3] = 1.0f + f16_to_f32((uint16_t)(gw.y >> 16));
+        }
+        const uint32_t lo = (uint32_t)f32_to_f16(v.x * inv * g[0]) | ((uint32_t)f32_to_f16(v.y * inv * g[1]) << 16);
+        const uint32_t hi = (uint32_t)f32_to_f16(v.z * inv * g[2]) | ((uint32_t)f32_to_f16(v.w * inv * g[3]) << 16);
+        *reinterpret_cast<uint2*>(out + i) = make_uint2(lo, hi);
+    }
+}

@@ -151,6 +151,30 @@ struct Q4RepackArgs {
     int32_t tile;            // T = QM_Q4_TILE(n)
 };
 
+// Q4 prefill GEMM: y[m][n] = x[m][k] W (+ residual), x f16, W in the
+// device layout; output f32 (y) or bf16 (y_bf16 non-null).  k % 32 == 0.
+struct Q4GemmArgs {
+    const uint16_t* x;       // f16 [m][k]
+    const uint8_t* codes;    // [n/T][k][T/2]
+    const uint16_t* gscales; // f16 [n/32][k]
+    float* y;                // f32 [m][n]
+    uint16_t* y_bf16;        // or bf16 [m][n]
+    const float* residual;   // null, or f32 [m][n]
+    int32_t m;
+    int32_t k;
+    int32_t n;
+    int32_t tile;            // QM_Q4_TILE(n)
+};
+
+// Per-row RMSNorm (or plain conversion) of f32 [m][k] into f16.
+struct RmsNormArgs {
+    const float* x;          // [m][k]
+    const uint16_t* norm_w;  // null or f16 [k]
+    uint16_t* out;           // f16 [m][k]
+    int32_t m;
+    int32_t k;
+};
+
 // Counter-based normal generator fill.
 struct FillArgs {
     void* dst;

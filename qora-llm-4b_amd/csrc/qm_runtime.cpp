@@ -47,6 +47,8 @@ struct qm_context {
     hipFunction_t f_q4_gemv = nullptr;
     hipFunction_t f_q4_repack = nullptr;
     hipFunction_t f_q4_gate_up = nullptr;
+    hipFunction_t f_q4_gemm = nullptr;
+    hipFunction_t f_rms_f16 = nullptr;
     int q4_threads = 0;            // the Q4 kernels' workgroup sizes (their launch bounds)
     int q4_gu_threads = 0;
     void* ws = nullptr;            // general workspace
@@ -281,6 +283,8 @@ int32_t qm_create(qm_context** out, const qm_config* cfg, const char* code_objec
     if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemv", &c->f_q4_gemv);
     if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_repack", &c->f_q4_repack);
     if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gate_up", &c->f_q4_gate_up);
+    if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemm", &c->f_q4_gemm);
+    if (st == QM_OK) st = load_function(c, mods[5], "qm_rms_norm_f16", &c->f_rms_f16);
     if (st == QM_OK &&
         (hipFuncGetAttribute(&c->q4_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, c->f_q4_gemv) != hipSuccess ||
          hipFuncGetAttribute(&c->q4_gu_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, c->f_q4_gate_up) !=
@@ -760,6 +764,35 @@ int32_t qm_q4_gate_up(qm_context* c, qm_stream stream, int32_t k, int32_t n, con
     qa.count = 2;
     return launch(c, c->f_q4_gate_up, static_cast<uint32_t>(n / qa.tile[0]), static_cast<uint32_t>(c->q4_gu_threads), qa,
                   pick(c, stream), "qm_q4_gate_up");
+}
+
+int32_t qm_rms_norm_f16(qm_context* c, qm_stream stream, int32_t m, int32_t k, const float* x,
+                        const uint16_t* norm_w, uint16_t* out) {
+    if (!c) return QM_ERR_INVALID_ARG;
+    if (m <= 0 || k <= 0 || k % 4 != 0)
+        return fail(c, QM_ERR_INVALID_ARG, "qm_rms_norm_f16: m %d, k %d (k a multiple of 4)", m, k);
+    if (!x || !out) return fail(c, QM_ERR_INVALID_ARG, "qm_rms_norm_f16: null pointer");
+    if (!all_aligned16({x, norm_w, out}))
+        return fail(c, QM_ERR_INVALID_ARG, "qm_rms_norm_f16: device pointers must be 16-byte aligned");
+    RmsNormArgs ra{x, norm_w, out, m, k};
+    return launch(c, c->f_rms_f16, static_cast<uint32_t>(m), 256, ra, pick(c, stream), "qm_rms_norm_f16");
+}
+
+int32_t qm_q4_gemm(qm_context* c, qm_stream stream, int32_t m, int32_t k, int32_t n, const uint16_t* x,
+                   const uint8_t* codes, const uint16_t* gscales, const float* residual, float* y,
+                   uint16_t* y_bf16) {
+    if (!c) return QM_ERR_INVALID_ARG;
+    int32_t st = q4_check(c, "qm_q4_gemm", k, n);
+    if (st != QM_OK) return st;
+    if (m <= 0) return fail(c, QM_ERR_INVALID_ARG, "qm_q4_gemm: m %d", m);
+    if (k % 32 != 0) return fail(c, QM_ERR_SHAPE, "qm_q4_gemm: k = %d is not a multiple of 32", k);
+    if (!x || !codes || !gscales || (!y) == (!y_bf16))
+        return fail(c, QM_ERR_INVALID_ARG, "qm_q4_gemm: null pointer, or not exactly one of y / y_bf16");
+    if (!all_aligned16({x, codes, gscales, residual, y, y_bf16}))
+        return fail(c, QM_ERR_INVALID_ARG, "qm_q4_gemm: device pointers must be 16-byte aligned");
+    Q4GemmArgs ga{x, codes, gscales, y, y_bf16, residual, m, k, n, QM_Q4_TILE(n)};
+    const uint32_t grid = static_cast<uint32_t>((m + 127) / 128) * static_cast<uint32_t>((n + 127) / 128);
+    return launch(c, c->f_q4_gemm, grid, 256, ga, pick(c, stream), "qm_q4_gemm");
 }
 
 }  // extern "C"

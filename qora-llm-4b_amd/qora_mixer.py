@@ -94,6 +94,8 @@ _SIGNATURES = {
     "qm_q4_gemv": [_P, _P, _I32, _I32, _P, _P, _P, _P],
     "qm_q4_gemv_multi": [_P, _P, _I32, _P, _P, _I32, _P],
     "qm_q4_gate_up": [_P, _P, _I32, _I32, _P, _P, _P, _P, _P, _P, _P],
+    "qm_rms_norm_f16": [_P, _P, _I32, _I32, _P, _P, _P],
+    "qm_q4_gemm": [_P, _P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P],
 }
 _RESTYPES = {"qm_default_config": None, "qm_status_string": C.c_char_p, "qm_last_error": C.c_char_p}
 
@@ -314,6 +316,15 @@ class Context:
             QmQ4Out(o[0], _addr(o[1]), _addr(o[2]), _addr(o[3]), _addr(o[4]) if len(o) > 4 else None)
             for o in outs])
         self._check(self.lib.qm_q4_gemv_multi(self.h, self.stream, k, _addr(x), _addr(norm_w), len(outs), arr))
+
+    def rms_norm_f16(self, m, k, x, norm_w, out):
+        """out f16 [m, k] = rms_norm(x, norm_w) per row (or plain f16 if norm_w is None)."""
+        self._check(self.lib.qm_rms_norm_f16(self.h, self.stream, m, k, _addr(x), _addr(norm_w), _addr(out)))
+
+    def q4_gemm(self, m, k, n, x, codes, gscales, y=None, y_bf16=None, residual=None):
+        """y (f32) or y_bf16 [m, n] = x (f16 [m, k]) @ W (+ residual)."""
+        self._check(self.lib.qm_q4_gemm(self.h, self.stream, m, k, n, _addr(x), _addr(codes), _addr(gscales),
+                                        _addr(residual), _addr(y), _addr(y_bf16)))
 
     def q4_gate_up(self, k, n, x, norm_w, gate_codes, gate_gscales, up_codes, up_gscales, out):
         """out[n] = silu(xn @ Wg) * (xn @ Wu), xn = rms_norm(x, norm_w) or x."""

@@ -182,3 +182,67 @@ def test_q4_gate_up(ctx, norm):
     bound = 1e-5 * (1.2 * _mag(xn, gp, gs) * np.abs(u) + 1.1 * np.abs(g) * _mag(xn, up, us)) + 1e-30
     print(f"max|d| {np.abs(got - ref).max():.3e}  max|d|/bound {(np.abs(got - ref) / bound).max():.3e}")
     assert np.all(np.abs(got - ref) <= bound)
+
+
+# ---- prefill: qm_rms_norm_f16 + qm_q4_gemm ----------------------------------------
+def test_rms_norm_f16(ctx):
+    """Per-row rms_norm (gemv.rs:571-579) into f16: within one f16 rounding of
+    the oracle's fp32 rows (plus fp32 reassociation of the sum of squares)."""
+    rng = np.random.default_rng(51)
+    m, k = 9, 2560
+    x = (2.0 * rng.standard_normal((m, k))).astype(np.float32)
+    gamma = W.f16_bits(0.1 * rng.standard_normal(k).astype(np.float32))
+    out = ctx.alloc(m * k * 2)
+    print("case: rms_norm_f16", flush=True)
+    ctx.rms_norm_f16(m, k, ctx.upload(x), ctx.upload(gamma), out)
+    got = W.f16_value(ctx.download(out, (m, k), np.uint16)).astype(np.float64)
+    ref = np.stack([O.rms_norm(r, gamma) for r in x]).astype(np.float64)
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -10 + 1e-7)
+    ctx.rms_norm_f16(m, k, ctx.upload(x), None, out)                 # plain conversion
+    assert np.array_equal(ctx.download(out, (m, k), np.uint16), W.f16_bits(x))
+
+
+@pytest.mark.parametrize("name,m,mode", [("in_proj_qkv", 200, "bf16"), ("in_proj_z", 37, "bf16"),
+                                         ("out_proj", 64, "residual"), ("in_proj_a", 130, "f32"),
+                                         ("down_proj", 129, "residual"), ("k_proj", 1, "f32")])
+def test_q4_gemm(ctx, name, m, mode):
+    """gemm_q4 (gemv.rs:529-542) on MFMA: y = x W (+ residual), x f16; bar
+    |y - y_ref| <= 1e-3 * sum_k |x_k W_kj| per element (W rounded to f16 per
+    element), plus the bf16 rounding of the output when it is bf16."""
+    k, n = W.Q4_PROJ_SHAPES[name]
+    rng = np.random.default_rng(m + n)
+    packed, scales = W.q4_random_weight(k, n, rng)
+    codes, gsc = repack(ctx, packed, scales)
+    x16 = W.f16_bits(rng.standard_normal((m, k)).astype(np.float32))
+    xv = W.f16_value(x16)
+    res = rng.standard_normal((m, n)).astype(np.float32) if mode == "residual" else None
+    print(f"case: q4 gemm {name} m={m} {mode}", flush=True)
+    y = ctx.alloc(m * n * (2 if mode == "bf16" else 4))
+    ctx.q4_gemm(m, k, n, ctx.upload(x16), codes, gsc,
+                y=None if mode == "bf16" else y, y_bf16=y if mode == "bf16" else None,
+                residual=None if res is None else ctx.upload(res))
+    if mode == "bf16":
+        got = W.bf16_value(ctx.download(y, (m, n), np.uint16)).astype(np.float64)
+    else:
+        got = ctx.download(y, (m, n), np.float32).astype(np.float64)
+    ref = O.q4_gemm(xv, packed, scales).astype(np.float64)
+    mag = np.abs(xv).astype(np.float64) @ np.abs(W.q4_dequant(packed, scales)).astype(np.float64)
+    if res is not None:
+        ref += res
+        mag += np.abs(res)
+    bound = 1e-3 * mag + (np.abs(ref) * 2.0 ** -8 if mode == "bf16" else 0.0) + 1e-30
+    print(f"max|d|/bound {(np.abs(got - ref) / bound).max():.3e}  rel {np.abs(got - ref).max() / np.abs(ref).max():.3e}")
+    assert np.all(np.abs(got - ref) <= bound)
+
+
+def test_q4_gemm_errors(ctx):
+    w = W.q4_gemv_workload(48, 64, seed=3)
+    codes, gsc = repack(ctx, w["packed"], w["scales"])
+    x = ctx.alloc(4 * 48 * 2)
+    y = ctx.alloc(4 * 64 * 4)
+    with pytest.raises(M.MixerError) as e:             # k not a multiple of 32
+        ctx.q4_gemm(4, 48, 64, x, codes, gsc, y=y)
+    assert e.value.code == 4
+    with pytest.raises(M.MixerError) as e:             # both outputs given
+        ctx.q4_gemm(4, 32, 64, x, codes, gsc, y=y, y_bf16=y)
+    assert e.value.code == 3
