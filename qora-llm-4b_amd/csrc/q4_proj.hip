@@ -238,24 +238,25 @@ extern "C" __global__ __launch_bounds__(256) void qm_q4_repack(Q4RepackArgs A) {
 // seq_len > 1).  X is f16 (qm_rms_norm_f16 produces it from the f32 hidden
 // state, fusing the layer's RMSNorm); W stays Q4 in HBM and is dequantized
 // to f16 on its way into LDS, s * (q - 8) rounded once to f16.
-// Workgroup tile 128 x 128, four waves of 64 x 64 (4 x 4 tiles of
-// v_mfma_f32_16x16x32_f16), k steps of 32 double-buffered in LDS with one
-// barrier per step: step t + 1's X rows and codes are loaded into registers
-// before step t's MFMAs and stored to the other buffer after them.
-// LDS rows are k-contiguous, X as [m][k] and W as [n][k], padded to 40 f16
-// (80 bytes) so the 16 rows of a fragment read land in 16 distinct bank
-// slots; a lane's A operand (row m, k 8kg .. +7) and B operand (column n,
-// k 8kg .. +7) are then one 16-byte read each.
+// Workgroup tile 128 x 256, four waves of 64 x 128 (4 x 8 tiles of
+// v_mfma_f32_16x16x32_f16: 12 fragment reads feed 32 MFMAs), k steps of 32
+// double-buffered in LDS with one barrier per step: step t + 1's X rows and
+// codes are loaded into registers before step t's MFMAs and stored to the
+// other buffer after them.  LDS rows are k-contiguous, X as [m][k] and W as
+// [n][k], padded to 40 f16 (80 bytes) so the 16 rows of a fragment read land
+// in 16 distinct bank slots; a lane's A operand (row m, k 8kg .. +7) and B
+// operand (column n, k 8kg .. +7) are then one 16-byte read each.
 // ---------------------------------------------------------------------------
 #define GM_TM 128
-#define GM_TN 128
+#define GM_TN 256
 #define GM_TK 32
 #define GM_LDK 40
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2 __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-extern "C" __global__ __launch_bounds__(256) void qm_q4_gemm(Q4GemmArgs A) {
+extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm(Q4GemmArgs A) {
     __shared__ __attribute__((aligned(16))) _Float16 sA[2][GM_TM][GM_LDK];
     __shared__ __attribute__((aligned(16))) _Float16 sB[2][GM_TN][GM_LDK];
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
@@ -271,48 +272,59 @@ extern "C" __global__ __launch_bounds__(256) void qm_q4_gemm(Q4GemmArgs A) {
     // X staging: thread -> row tid / 2, 16 k at 16 (tid & 1)
     const int ar = tid >> 1, ah = tid & 1;
     const uint16_t* xrow = A.x + (size_t)min(m0 + ar, A.m - 1) * K + 16 * ah;
-    // W staging: thread -> 8-column block c8 = tid / 16 of the tile, row pair
-    // rp = tid % 16 (rows 2rp, 2rp + 1 of the step); a block is 4 code bytes
+    // W staging: thread -> 8-column block c8 = tid / 8 of the tile, rows
+    // 4 rq .. 4 rq + 3 of the step (rq = tid % 8); a block is 4 code bytes
     // of one row (T = 16: half of a tile row, T = 8: a whole one)
-    const int c8 = tid >> 4, rp = tid & 15;
+    const int c8 = tid >> 3, rq = tid & 7;
     const int ncl = min(n0 + 8 * c8, A.n - 8);          // valid block for loads
-    const uint8_t* bcodes = A.codes + (size_t)(ncl / T) * K * (T / 2) + (ncl % T) / 2;
-    const uint16_t* bsc = A.gscales + (size_t)(ncl / 32) * K;
-
     const size_t cstride = (size_t)(T / 2);
+    const uint8_t* bcodes = A.codes + (size_t)(ncl / T) * K * cstride + (ncl % T) / 2 + 4 * rq * cstride;
+    const uint16_t* bsc = A.gscales + (size_t)(ncl / 32) * K + 4 * rq;
+
     uint4 ra0, ra1;
-    uint32_t rb0, rb1;
-    uint16_t rs0, rs1;
+    uint32_t rb[4];
+    uint2 rs;                                            // 4 f16 scales of rows 4rq .. +3
 #define GM_GLOAD(kt)                                                                   \
     do {                                                                               \
         const int k0_ = (kt) * GM_TK;                                                  \
         ra0 = *reinterpret_cast<const uint4*>(xrow + k0_);                            \
         ra1 = *reinterpret_cast<const uint4*>(xrow + k0_ + 8);                        \
-        rb0 = *reinterpret_cast<const uint32_t*>(bcodes + (size_t)(k0_ + 2 * rp) * cstride);     \
-        rb1 = *reinterpret_cast<const uint32_t*>(bcodes + (size_t)(k0_ + 2 * rp + 1) * cstride); \
-        rs0 = bsc[k0_ + 2 * rp];                                                       \
-        rs1 = bsc[k0_ + 2 * rp + 1];                                                   \
+        _Pragma("unroll") for (int i_ = 0; i_ < 4; ++i_)                               \
+            rb[i_] = *reinterpret_cast<const uint32_t*>(bcodes + (size_t)(k0_ + i_) * cstride); \
+        rs = *reinterpret_cast<const uint2*>(bsc + k0_);                              \
     } while (0)
-    // column 8 c8 + c of rows 2rp, 2rp + 1: byte c / 2 of each row's block,
-    // low nibble for even c; the two rows' f16 weights form one 4-byte store
+    // Columns 2b, 2b + 1 of a row pair come from byte b of each row's block.
+    // v_perm_b32 puts the first row's byte at bits 0-7 and the second's at
+    // bits 16-23; masking a nibble pair into 0x6400 | q gives the f16 pair
+    // (1024 + q), and packed f16 ops make it s * (q - 8): exact, then one
+    // rounding of the product (the same bits as rounding s * (q - 8) from
+    // fp32).  Column n's four rows are one 8-byte store.
 #define GM_LSTORE(buf)                                                                 \
     do {                                                                               \
         *reinterpret_cast<uint4*>(&sA[buf][ar][16 * ah]) = ra0;                       \
         *reinterpret_cast<uint4*>(&sA[buf][ar][16 * ah + 8]) = ra1;                   \
-        const float s0_ = f16_to_f32(rs0), s1_ = f16_to_f32(rs1);                     \
-        _Pragma("unroll") for (int c = 0; c < 8; ++c) {                               \
-            const float q0 = (float)((rb0 >> (4 * c)) & 15u) - 8.0f;                  \
-            const float q1 = (float)((rb1 >> (4 * c)) & 15u) - 8.0f;                  \
-            const uint32_t pr = (uint32_t)f32_to_f16(s0_ * q0) | ((uint32_t)f32_to_f16(s1_ * q1) << 16); \
-            *reinterpret_cast<uint32_t*>(&sB[buf][8 * c8 + c][2 * rp]) = pr;          \
+        const half2 s01 = __builtin_bit_cast(half2, rs.x), s23 = __builtin_bit_cast(half2, rs.y); \
+        _Pragma("unroll") for (int b_ = 0; b_ < 4; ++b_) {                            \
+            const uint32_t sel = 0x0c040c00u + 0x00010001u * b_;                       \
+            const uint32_t p01 = __builtin_amdgcn_perm(rb[1], rb[0], sel);             \
+            const uint32_t p23 = __builtin_amdgcn_perm(rb[3], rb[2], sel);             \
+            const half2 k1032 = half2{1032.0f16, 1032.0f16};                           \
+            const half2 l01 = (__builtin_bit_cast(half2, (p01 & 0x000f000fu) | 0x64006400u) - k1032) * s01; \
+            const half2 h01 = (__builtin_bit_cast(half2, ((p01 >> 4) & 0x000f000fu) | 0x64006400u) - k1032) * s01; \
+            const half2 l23 = (__builtin_bit_cast(half2, (p23 & 0x000f000fu) | 0x64006400u) - k1032) * s23; \
+            const half2 h23 = (__builtin_bit_cast(half2, ((p23 >> 4) & 0x000f000fu) | 0x64006400u) - k1032) * s23; \
+            *reinterpret_cast<uint2*>(&sB[buf][8 * c8 + 2 * b_][4 * rq]) =            \
+                make_uint2(__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23)); \
+            *reinterpret_cast<uint2*>(&sB[buf][8 * c8 + 2 * b_ + 1][4 * rq]) =        \
+                make_uint2(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23)); \
         }                                                                              \
     } while (0)
 
-    floatx4 acc[4][4];
+    floatx4 acc[4][8];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < 8; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
     GM_GLOAD(0);
     GM_LSTORE(0);
@@ -321,27 +333,27 @@ extern "C" __global__ __launch_bounds__(256) void qm_q4_gemm(Q4GemmArgs A) {
     for (int kt = 0; kt < nk; ++kt) {
         const int b = kt & 1;
         if (kt + 1 < nk) GM_GLOAD(kt + 1);
-        half8 af[4], bf[4];
+        half8 af[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const half8*>(&sA[b][64 * wm + 16 * i + fr][fk]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) bf[j] = *reinterpret_cast<const half8*>(&sB[b][64 * wn + 16 * j + fr][fk]);
+        for (int j = 0; j < 8; ++j) {
+            const half8 bf = *reinterpret_cast<const half8*>(&sB[b][128 * wn + 16 * j + fr][fk]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+            for (int i = 0; i < 4; ++i)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf, acc[i][j], 0, 0, 0);
+        }
         // the other buffer was last read in step kt - 1, before the barrier
         if (kt + 1 < nk) GM_LSTORE(b ^ 1);
         __syncthreads();
     }
-
 #undef GM_GLOAD
 #undef GM_LSTORE
+
     // C fragment: lane (n = lane & 15, mg = lane >> 4) holds rows 4 mg .. +3
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int col = n0 + 64 * wn + 16 * j + fr;
+    for (int j = 0; j < 8; ++j) {
+        const int col = n0 + 128 * wn + 16 * j + fr;
         if (col >= A.n) continue;
 #pragma unroll
         for (int i = 0; i < 4; ++i)

@@ -791,7 +791,7 @@ int32_t qm_q4_gemm(qm_context* c, qm_stream stream, int32_t m, int32_t k, int32_
     if (!all_aligned16({x, codes, gscales, residual, y, y_bf16}))
         return fail(c, QM_ERR_INVALID_ARG, "qm_q4_gemm: device pointers must be 16-byte aligned");
     Q4GemmArgs ga{x, codes, gscales, y, y_bf16, residual, m, k, n, QM_Q4_TILE(n)};
-    const uint32_t grid = static_cast<uint32_t>((m + 127) / 128) * static_cast<uint32_t>((n + 127) / 128);
+    const uint32_t grid = static_cast<uint32_t>((m + 127) / 128) * static_cast<uint32_t>((n + 255) / 256);
     return launch(c, c->f_q4_gemm, grid, 256, ga, pick(c, stream), "qm_q4_gemm");
 }
 
