@@ -317,17 +317,31 @@ int32_t qm_rms_norm_f16(qm_context* ctx, qm_stream stream, int32_t m, int32_t k,
 /* y = x W (+ residual) for m input rows on MFMA: replaces gemm_q4,
  * gemv.rs:529-542 (gemm() on a Q4 weight, :295-300), which the prefill
  * layers call for every projection (gemv.rs:1114-1117,1222,1231-1239,
- * 1366-1385,1447-1467).  x_dev f16 [m][k] (k % 32 == 0, else QM_ERR_SHAPE);
- * codes_dev/gscales_dev a weight in the device layout (qm_q4_repack);
- * residual_dev NULL or f32 [m][n]; exactly one of y_dev (f32 [m][n]) and
- * y_bf16_dev (bf16 [m][n], e.g. the in_proj_qkv / in_proj_z outputs that
- * qm_deltanet_prefill reads) is non-NULL.  W is dequantized to f16 per
- * element (s * (q - 8), one rounding) and x is f16: a bf16-path result,
- * within 1e-3 of sum_k |x_k W_kj| of the fp32 reference per element. */
+ * 1366-1385,1447-1467).  x_dev [m][k] (k % 32 == 0, else QM_ERR_SHAPE) of
+ * x_dtype QM_F16 (from qm_rms_norm_f16) or QM_BF16 (a mixer prefill output,
+ * rounded to f16 as it is read); codes_dev/gscales_dev a weight in the
+ * device layout (qm_q4_repack); residual_dev NULL or f32 [m][n] (may alias
+ * y_dev); exactly one of y_dev (f32 [m][n]) and y_bf16_dev (bf16 [m][n],
+ * e.g. the in_proj_qkv / in_proj_z outputs that qm_deltanet_prefill reads)
+ * is non-NULL.  W is dequantized to f16 per element (s * (q - 8), one
+ * rounding) and x is f16: a bf16-path result, within 1e-3 of
+ * sum_k |x_k W_kj| of the fp32 reference per element. */
 int32_t qm_q4_gemm(qm_context* ctx, qm_stream stream, int32_t m, int32_t k, int32_t n,
-                   const uint16_t* x_dev, const uint8_t* codes_dev,
+                   const uint16_t* x_dev, int32_t x_dtype, const uint8_t* codes_dev,
                    const uint16_t* gscales_dev, const float* residual_dev,
                    float* y_dev, uint16_t* y_bf16_dev);
+
+/* The prefill MLP's gate and up projections and their SiLU product
+ * (gemv.rs:1231-1237: gemm(gate_proj), gemm(up_proj), then
+ * silu(g) * u per element) in one launch: out_f16_dev [m][n] =
+ * f16(silu(x Wg) * (x Wu)), the input of the down_proj qm_q4_gemm.  Both
+ * weights are k x n in the device layout; x as for qm_q4_gemm.  Values of
+ * the product beyond the f16 range become +-inf. */
+int32_t qm_q4_gemm_gate_up(qm_context* ctx, qm_stream stream, int32_t m, int32_t k, int32_t n,
+                           const uint16_t* x_dev, int32_t x_dtype,
+                           const uint8_t* gate_codes_dev, const uint16_t* gate_gscales_dev,
+                           const uint8_t* up_codes_dev, const uint16_t* up_gscales_dev,
+                           uint16_t* out_f16_dev);
 
 #ifdef __cplusplus
 }

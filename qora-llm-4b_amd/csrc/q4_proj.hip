@@ -256,15 +256,33 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2 __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm(Q4GemmArgs A) {
+// Two bf16 values (one 32-bit word) as two f16, each rounded to nearest even.
+__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t v) {
+    const half2 h = half2{(_Float16)__builtin_bit_cast(float, v << 16),
+                          (_Float16)__builtin_bit_cast(float, v & 0xffff0000u)};
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+__device__ __forceinline__ uint4 bf16x8_to_f16x8(uint4 v) {
+    return make_uint4(bf16x2_to_f16x2(v.x), bf16x2_to_f16x2(v.y), bf16x2_to_f16x2(v.z), bf16x2_to_f16x2(v.w));
+}
+
+// XBF16: x is bf16, converted to f16 as it is staged.  GU: the gate/up form.
+// The workgroup's 256 W rows of LDS are then 16-column fragments of the gate
+// and up weights alternately, over 128 output columns, so a wave's fragments
+// j (gate) and j + 1 (up) hold the same outputs and the epilogue writes
+// silu(g) * u as f16.
+template <bool XBF16, bool GU>
+__device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
     __shared__ __attribute__((aligned(16))) _Float16 sA[2][GM_TM][GM_LDK];
     __shared__ __attribute__((aligned(16))) _Float16 sB[2][GM_TN][GM_LDK];
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-    const int nbn = (A.n + GM_TN - 1) / GM_TN;
+    constexpr int NCOLS = GU ? GM_TN / 2 : GM_TN;       // output columns per workgroup
+    const int nbn = (A.n + NCOLS - 1) / NCOLS;
     // consecutive workgroups walk n within one row block: the row block's X
     // (k x 128 f16) is reused from L2 across its column tiles
     const int bm = (int)blockIdx.x / nbn, bn = (int)blockIdx.x % nbn;
-    const int m0 = bm * GM_TM, n0 = bn * GM_TN;
+    const int m0 = bm * GM_TM, n0 = bn * NCOLS;
     const int wm = w >> 1, wn = w & 1;
     const int T = A.tile, K = A.k;
     const int nk = K / GM_TK;
@@ -276,10 +294,15 @@ extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm(Q4GemmArgs A) {
     // 4 rq .. 4 rq + 3 of the step (rq = tid % 8); a block is 4 code bytes
     // of one row (T = 16: half of a tile row, T = 8: a whole one)
     const int c8 = tid >> 3, rq = tid & 7;
-    const int ncl = min(n0 + 8 * c8, A.n - 8);          // valid block for loads
+    // GU: LDS rows 8 c8 .. +7 are half of fragment c8 / 2, of the up weight
+    // when that fragment is odd
+    const bool up = GU && ((c8 >> 1) & 1);
+    const int ccol = GU ? 16 * (c8 >> 2) + 8 * (c8 & 1) : 8 * c8;
+    const int ncl = min(n0 + ccol, A.n - 8);            // valid block for loads
     const size_t cstride = (size_t)(T / 2);
-    const uint8_t* bcodes = A.codes + (size_t)(ncl / T) * K * cstride + (ncl % T) / 2 + 4 * rq * cstride;
-    const uint16_t* bsc = A.gscales + (size_t)(ncl / 32) * K + 4 * rq;
+    const uint8_t* bcodes = (up ? A.codes2 : A.codes) + (size_t)(ncl / T) * K * cstride + (ncl % T) / 2 +
+                            4 * rq * cstride;
+    const uint16_t* bsc = (up ? A.gscales2 : A.gscales) + (size_t)(ncl / 32) * K + 4 * rq;
 
     uint4 ra0, ra1;
     uint32_t rb[4];
@@ -301,8 +324,8 @@ extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm(Q4GemmArgs A) {
     // fp32).  Column n's four rows are one 8-byte store.
 #define GM_LSTORE(buf)                                                                 \
     do {                                                                               \
-        *reinterpret_cast<uint4*>(&sA[buf][ar][16 * ah]) = ra0;                       \
-        *reinterpret_cast<uint4*>(&sA[buf][ar][16 * ah + 8]) = ra1;                   \
+        *reinterpret_cast<uint4*>(&sA[buf][ar][16 * ah]) = XBF16 ? bf16x8_to_f16x8(ra0) : ra0; \
+        *reinterpret_cast<uint4*>(&sA[buf][ar][16 * ah + 8]) = XBF16 ? bf16x8_to_f16x8(ra1) : ra1; \
         const half2 s01 = __builtin_bit_cast(half2, rs.x), s23 = __builtin_bit_cast(half2, rs.y); \
         _Pragma("unroll") for (int b_ = 0; b_ < 4; ++b_) {                            \
             const uint32_t sel = 0x0c040c00u + 0x00010001u * b_;                       \
@@ -351,6 +374,23 @@ extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm(Q4GemmArgs A) {
 #undef GM_LSTORE
 
     // C fragment: lane (n = lane & 15, mg = lane >> 4) holds rows 4 mg .. +3
+    if constexpr (GU) {
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+            const int col = n0 + 64 * wn + 8 * j + fr;
+            if (col >= A.n) continue;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int row = m0 + 64 * wm + 16 * i + 4 * (lane >> 4) + e;
+                    if (row >= A.m) continue;
+                    const float g = acc[i][j][e], u = acc[i][j + 1][e];
+                    A.y_f16[(size_t)row * A.n + col] = __builtin_bit_cast(uint16_t, (_Float16)(g / (1.0f + expf(-g)) * u));
+                }
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const int col = n0 + 128 * wn + 16 * j + fr;
@@ -369,6 +409,11 @@ extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm(Q4GemmArgs A) {
             }
     }
 }
+
+extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm(Q4GemmArgs A) { q4_gemm_body<false, false>(A); }
+extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm_xbf16(Q4GemmArgs A) { q4_gemm_body<true, false>(A); }
+extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm_gu(Q4GemmArgs A) { q4_gemm_body<false, true>(A); }
+extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm_gu_xbf16(Q4GemmArgs A) { q4_gemm_body<true, true>(A); }
 
 // rms_norm (1 + gamma, eps 1e-6; gemv.rs:571-579) of each of m rows of f32
 // x [m][k], written as the f16 input of qm_q4_gemm; without a norm weight,

@@ -47,7 +47,7 @@ struct qm_context {
     hipFunction_t f_q4_gemv = nullptr;
     hipFunction_t f_q4_repack = nullptr;
     hipFunction_t f_q4_gate_up = nullptr;
-    hipFunction_t f_q4_gemm = nullptr;
+    hipFunction_t f_q4_gemm[2][2] = {};  // [x bf16][gate/up form]
     hipFunction_t f_rms_f16 = nullptr;
     int q4_threads = 0;            // the Q4 kernels' workgroup sizes (their launch bounds)
     int q4_gu_threads = 0;
@@ -283,7 +283,10 @@ int32_t qm_create(qm_context** out, const qm_config* cfg, const char* code_objec
     if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemv", &c->f_q4_gemv);
     if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_repack", &c->f_q4_repack);
     if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gate_up", &c->f_q4_gate_up);
-    if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemm", &c->f_q4_gemm);
+    if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemm", &c->f_q4_gemm[0][0]);
+    if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemm_xbf16", &c->f_q4_gemm[1][0]);
+    if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemm_gu", &c->f_q4_gemm[0][1]);
+    if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemm_gu_xbf16", &c->f_q4_gemm[1][1]);
     if (st == QM_OK) st = load_function(c, mods[5], "qm_rms_norm_f16", &c->f_rms_f16);
     if (st == QM_OK &&
         (hipFuncGetAttribute(&c->q4_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, c->f_q4_gemv) != hipSuccess ||
@@ -778,21 +781,47 @@ int32_t qm_rms_norm_f16(qm_context* c, qm_stream stream, int32_t m, int32_t k, c
     return launch(c, c->f_rms_f16, static_cast<uint32_t>(m), 256, ra, pick(c, stream), "qm_rms_norm_f16");
 }
 
-int32_t qm_q4_gemm(qm_context* c, qm_stream stream, int32_t m, int32_t k, int32_t n, const uint16_t* x,
-                   const uint8_t* codes, const uint16_t* gscales, const float* residual, float* y,
-                   uint16_t* y_bf16) {
-    if (!c) return QM_ERR_INVALID_ARG;
-    int32_t st = q4_check(c, "qm_q4_gemm", k, n);
+namespace {
+int32_t q4_gemm_check(qm_context* c, const char* name, int32_t m, int32_t k, int32_t n, int32_t x_dtype) {
+    int32_t st = q4_check(c, name, k, n);
     if (st != QM_OK) return st;
-    if (m <= 0) return fail(c, QM_ERR_INVALID_ARG, "qm_q4_gemm: m %d", m);
-    if (k % 32 != 0) return fail(c, QM_ERR_SHAPE, "qm_q4_gemm: k = %d is not a multiple of 32", k);
+    if (m <= 0) return fail(c, QM_ERR_INVALID_ARG, "%s: m %d", name, m);
+    if (k % 32 != 0) return fail(c, QM_ERR_SHAPE, "%s: k = %d is not a multiple of 32", name, k);
+    if (x_dtype != QM_F16 && x_dtype != QM_BF16)
+        return fail(c, QM_ERR_INVALID_ARG, "%s: x_dtype %d (QM_F16 or QM_BF16)", name, x_dtype);
+    return QM_OK;
+}
+}  // namespace
+
+int32_t qm_q4_gemm(qm_context* c, qm_stream stream, int32_t m, int32_t k, int32_t n, const uint16_t* x,
+                   int32_t x_dtype, const uint8_t* codes, const uint16_t* gscales, const float* residual,
+                   float* y, uint16_t* y_bf16) {
+    if (!c) return QM_ERR_INVALID_ARG;
+    int32_t st = q4_gemm_check(c, "qm_q4_gemm", m, k, n, x_dtype);
+    if (st != QM_OK) return st;
     if (!x || !codes || !gscales || (!y) == (!y_bf16))
         return fail(c, QM_ERR_INVALID_ARG, "qm_q4_gemm: null pointer, or not exactly one of y / y_bf16");
     if (!all_aligned16({x, codes, gscales, residual, y, y_bf16}))
         return fail(c, QM_ERR_INVALID_ARG, "qm_q4_gemm: device pointers must be 16-byte aligned");
-    Q4GemmArgs ga{x, codes, gscales, y, y_bf16, residual, m, k, n, QM_Q4_TILE(n)};
+    Q4GemmArgs ga{x, codes, gscales, nullptr, nullptr, y, y_bf16, nullptr, residual, m, k, n, QM_Q4_TILE(n)};
     const uint32_t grid = static_cast<uint32_t>((m + 127) / 128) * static_cast<uint32_t>((n + 255) / 256);
-    return launch(c, c->f_q4_gemm, grid, 256, ga, pick(c, stream), "qm_q4_gemm");
+    return launch(c, c->f_q4_gemm[x_dtype == QM_BF16][0], grid, 256, ga, pick(c, stream), "qm_q4_gemm");
+}
+
+int32_t qm_q4_gemm_gate_up(qm_context* c, qm_stream stream, int32_t m, int32_t k, int32_t n, const uint16_t* x,
+                           int32_t x_dtype, const uint8_t* gate_codes, const uint16_t* gate_gscales,
+                           const uint8_t* up_codes, const uint16_t* up_gscales, uint16_t* out_f16) {
+    if (!c) return QM_ERR_INVALID_ARG;
+    int32_t st = q4_gemm_check(c, "qm_q4_gemm_gate_up", m, k, n, x_dtype);
+    if (st != QM_OK) return st;
+    if (!x || !gate_codes || !gate_gscales || !up_codes || !up_gscales || !out_f16)
+        return fail(c, QM_ERR_INVALID_ARG, "qm_q4_gemm_gate_up: null pointer");
+    if (!all_aligned16({x, gate_codes, gate_gscales, up_codes, up_gscales, out_f16}))
+        return fail(c, QM_ERR_INVALID_ARG, "qm_q4_gemm_gate_up: device pointers must be 16-byte aligned");
+    Q4GemmArgs ga{x,       gate_codes, gate_gscales, up_codes, up_gscales, nullptr, nullptr, out_f16,
+                  nullptr, m,          k,            n,        QM_Q4_TILE(n)};
+    const uint32_t grid = static_cast<uint32_t>((m + 127) / 128) * static_cast<uint32_t>((n + 127) / 128);
+    return launch(c, c->f_q4_gemm[x_dtype == QM_BF16][1], grid, 256, ga, pick(c, stream), "qm_q4_gemm_gate_up");
 }
 
 }  // extern "C"

@@ -95,7 +95,8 @@ _SIGNATURES = {
     "qm_q4_gemv_multi": [_P, _P, _I32, _P, _P, _I32, _P],
     "qm_q4_gate_up": [_P, _P, _I32, _I32, _P, _P, _P, _P, _P, _P, _P],
     "qm_rms_norm_f16": [_P, _P, _I32, _I32, _P, _P, _P],
-    "qm_q4_gemm": [_P, _P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P],
+    "qm_q4_gemm": [_P, _P, _I32, _I32, _I32, _P, _I32, _P, _P, _P, _P, _P],
+    "qm_q4_gemm_gate_up": [_P, _P, _I32, _I32, _I32, _P, _I32, _P, _P, _P, _P, _P],
 }
 _RESTYPES = {"qm_default_config": None, "qm_status_string": C.c_char_p, "qm_last_error": C.c_char_p}
 
@@ -321,10 +322,17 @@ class Context:
         """out f16 [m, k] = rms_norm(x, norm_w) per row (or plain f16 if norm_w is None)."""
         self._check(self.lib.qm_rms_norm_f16(self.h, self.stream, m, k, _addr(x), _addr(norm_w), _addr(out)))
 
-    def q4_gemm(self, m, k, n, x, codes, gscales, y=None, y_bf16=None, residual=None):
-        """y (f32) or y_bf16 [m, n] = x (f16 [m, k]) @ W (+ residual)."""
-        self._check(self.lib.qm_q4_gemm(self.h, self.stream, m, k, n, _addr(x), _addr(codes), _addr(gscales),
-                                        _addr(residual), _addr(y), _addr(y_bf16)))
+    def q4_gemm(self, m, k, n, x, codes, gscales, y=None, y_bf16=None, residual=None, x_dtype=QM_F16):
+        """y (f32) or y_bf16 [m, n] = x (f16 or bf16 [m, k]) @ W (+ residual)."""
+        self._check(self.lib.qm_q4_gemm(self.h, self.stream, m, k, n, _addr(x), x_dtype, _addr(codes),
+                                        _addr(gscales), _addr(residual), _addr(y), _addr(y_bf16)))
+
+    def q4_gemm_gate_up(self, m, k, n, x, gate_codes, gate_gscales, up_codes, up_gscales, out_f16,
+                        x_dtype=QM_F16):
+        """out_f16 [m, n] = f16(silu(x @ Wg) * (x @ Wu)), x f16 or bf16 [m, k]."""
+        self._check(self.lib.qm_q4_gemm_gate_up(self.h, self.stream, m, k, n, _addr(x), x_dtype,
+                                                _addr(gate_codes), _addr(gate_gscales), _addr(up_codes),
+                                                _addr(up_gscales), _addr(out_f16)))
 
     def q4_gate_up(self, k, n, x, norm_w, gate_codes, gate_gscales, up_codes, up_gscales, out):
         """out[n] = silu(xn @ Wg) * (xn @ Wu), xn = rms_norm(x, norm_w) or x."""

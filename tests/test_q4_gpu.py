@@ -235,6 +235,64 @@ def test_q4_gemm(ctx, name, m, mode):
     assert np.all(np.abs(got - ref) <= bound)
 
 
+def test_q4_gemm_bf16_input(ctx):
+    """out_proj on a mixer prefill output (bf16 [T][4096]) with the residual
+    added in place (gemv.rs:1222-1223): bf16 x is rounded to f16 as it is
+    staged, so the result equals the f16-input GEMM on f16(x) bit for bit,
+    and meets the GEMM bar against the oracle on the bf16 values."""
+    k, n = W.Q4_PROJ_SHAPES["out_proj"]
+    m = 77
+    rng = np.random.default_rng(61)
+    packed, scales = W.q4_random_weight(k, n, rng)
+    codes, gsc = repack(ctx, packed, scales)
+    xb = W.bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
+    xv = W.bf16_value(xb)
+    res = rng.standard_normal((m, n)).astype(np.float32)
+    print("case: q4 gemm bf16 input, out_proj m=77 residual in place", flush=True)
+    y = ctx.upload(res)
+    ctx.q4_gemm(m, k, n, ctx.upload(xb), codes, gsc, y=y, residual=y, x_dtype=M.QM_BF16)
+    got = ctx.download(y, (m, n), np.float32)
+    y16 = ctx.upload(res)
+    ctx.q4_gemm(m, k, n, ctx.upload(W.f16_bits(xv)), codes, gsc, y=y16, residual=y16)
+    assert np.array_equal(got, ctx.download(y16, (m, n), np.float32))
+    ref = O.q4_gemm(xv, packed, scales).astype(np.float64) + res
+    bound = 1e-3 * (_mag(xv, packed, scales) + np.abs(res)) + 1e-30
+    print(f"max|d|/bound {(np.abs(got - ref) / bound).max():.3e}")
+    assert np.all(np.abs(got - ref) <= bound)
+
+
+@pytest.mark.parametrize("n,m,x_dtype", [(9216, 64, "f16"), (2592, 130, "f16"), (2592, 37, "bf16")])
+def test_q4_gemm_gate_up(ctx, n, m, x_dtype):
+    """The prefill MLP's gate/up GEMMs and silu(g) * u (gemv.rs:1231-1237)
+    in one launch, written as f16.  Bar: the GEMM bar carried through
+    silu(g) * u, plus the f16 rounding of the output.  n = 2592 ends in a
+    partial 128-column tile of the 8-column device layout."""
+    k = 2560
+    rng = np.random.default_rng(n + m)
+    (gp, gs), (up, us) = W.q4_random_weight(k, n, rng), W.q4_random_weight(k, n, rng)
+    (gc, gg), (uc, ug) = repack(ctx, gp, gs), repack(ctx, up, us)
+    xf = rng.standard_normal((m, k)).astype(np.float32)
+    if x_dtype == "bf16":
+        xbits, dt = W.bf16_bits(xf), M.QM_BF16
+        xv = W.bf16_value(xbits)
+    else:
+        xbits, dt = W.f16_bits(xf), M.QM_F16
+        xv = W.f16_value(xbits)
+    out = ctx.alloc(m * n * 2)
+    print(f"case: q4 gemm gate/up n={n} m={m} x {x_dtype}", flush=True)
+    ctx.q4_gemm_gate_up(m, k, n, ctx.upload(xbits), gc, gg, uc, ug, out, x_dtype=dt)
+    got = W.f16_value(ctx.download(out, (m, n), np.uint16)).astype(np.float64)
+    g = O.q4_gemm(xv, gp, gs)
+    u = O.q4_gemm(xv, up, us)
+    one = np.float32(1.0)
+    ref = ((g / (one + np.exp(-g))) * u).astype(np.float64)
+    g, u = g.astype(np.float64), u.astype(np.float64)
+    bound = (1e-3 * (1.2 * _mag(xv, gp, gs) * np.abs(u) + 1.1 * np.abs(g) * _mag(xv, up, us))
+             + np.abs(ref) * 2.0 ** -11 + 1e-7)
+    print(f"max|d|/bound {(np.abs(got - ref) / bound).max():.3e}")
+    assert np.all(np.abs(got - ref) <= bound)
+
+
 def test_q4_gemm_errors(ctx):
     w = W.q4_gemv_workload(48, 64, seed=3)
     codes, gsc = repack(ctx, w["packed"], w["scales"])
@@ -246,3 +304,9 @@ def test_q4_gemm_errors(ctx):
     with pytest.raises(M.MixerError) as e:             # both outputs given
         ctx.q4_gemm(4, 32, 64, x, codes, gsc, y=y, y_bf16=y)
     assert e.value.code == 3
+    with pytest.raises(M.MixerError) as e:             # x must be f16 or bf16
+        ctx.q4_gemm(4, 32, 64, x, codes, gsc, y=y, x_dtype=M.QM_F32)
+    assert e.value.code == 3
+    with pytest.raises(M.MixerError) as e:             # gate/up: k not a multiple of 32
+        ctx.q4_gemm_gate_up(4, 48, 64, x, codes, gsc, codes, gsc, y)
+    assert e.value.code == 4
