@@ -585,6 +585,57 @@ def run_q4_gemm(args, ctx):
     }
 
 
+LM_VOCAB, LM_HIDDEN = 248320, 2560
+
+
+def lm_head_bytes(vocab=LM_VOCAB, hidden=LM_HIDDEN):
+    """Codes + scales of every row, x and the final-norm weights read, logits written."""
+    return vocab * (hidden // 2 + (hidden // 32) * 2) + hidden * (4 + 2) + vocab * 4
+
+
+def run_lm_head(args, ctx):
+    """The decode step's lm_head: final RMSNorm + 248,320 Q4 embedding rows
+    (tied weights, vocab-major) dotted with one hidden state."""
+    K, Wm = args.steps, args.warmup
+    vocab, hidden = LM_VOCAB, LM_HIDDEN
+    packed = ctx.alloc(vocab * hidden // 2)
+    ctx.fill_normal(packed, M.QM_F16, vocab * hidden // 4, 0.0, 1.0, 5001)   # any byte is a code pair
+    scales = ctx.alloc(vocab * (hidden // 32) * 2)
+    ctx.fill_normal(scales, M.QM_F16, vocab * (hidden // 32), 0.02, 0.004, 5002)
+    x = ctx.alloc(hidden * 4)
+    ctx.fill_normal(x, M.QM_F32, hidden, 0.0, 1.0, 5003)
+    gamma = ctx.alloc(hidden * 2)
+    ctx.fill_normal(gamma, M.QM_F16, hidden, 0.0, 0.1, 5004)
+    logits = ctx.alloc(vocab * 4)
+    tm = Timer(ctx)
+
+    def step():
+        ctx.q4_lm_head(vocab, hidden, x, gamma, packed, scales, logits)
+
+    for _ in range(Wm):
+        step()
+    ctx.sync()
+    t0, t1 = ctx.event(), ctx.event()
+    wall0 = time.perf_counter()
+    t0.record()
+    for _ in range(K):
+        tm.wrap(step)
+    t1.record()
+    ctx.sync()
+    wall = time.perf_counter() - wall0
+    k_ms = tm.mean_ms()
+    nbytes = lm_head_bytes()
+    return {
+        "tokens": K, "total_ms": t0.elapsed_ms(t1), "wall_s": wall,
+        "dominant": "qm_q4_lm_head (248320 x 2560, final RMSNorm fused)",
+        "roofline": {"bound": "hbm", "achieved": nbytes / (k_ms * 1e-3), "peak": HBM_PEAK,
+                     "kernel_ms": k_ms, "bytes_per_launch": nbytes},
+        "config": {"workload": "lm_head of one decode token: final RMSNorm + 248320 x 2560 Q4 embedding "
+                               "(tied, vocab-major) -> f32 logits",
+                   "batch": 1, "seq_len": 1, "global_batch": 1, "parallelism": "single GPU"},
+    }
+
+
 def _repeat_for(fn, min_s=CPU_SAMPLE_S, max_iters=10 ** 6):
     """Call fn() until min_s seconds have elapsed; returns (calls, seconds)."""
     n, t0 = 0, time.perf_counter()
@@ -677,6 +728,15 @@ def cpu_baseline(workload: str) -> dict:
         return {"value": 8 * n / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
                 "sample": f"{n} calls of gemm_q4 on 8 rows (scalar gemv_q4_inner restatement, one thread, "
                           f"{dt:.1f} s)"}
+    if workload == "lm_head":
+        rng = np.random.default_rng(10)
+        packed, scales = W.q4_random_weight(LM_VOCAB, LM_HIDDEN, rng, scale=0.02)
+        x = rng.standard_normal(LM_HIDDEN, dtype=np.float32)
+        gam = W.f16_bits(0.1 * rng.standard_normal(LM_HIDDEN, dtype=np.float32))
+        n, dt = _repeat_for(lambda: O.q4_lm_head(O.rms_norm(x, gam), packed, scales, nthreads=att_threads))
+        return {"value": n / dt, "unit": "tokens/s", "cores": att_threads, "kind": "port",
+                "sample": f"{n} full lm_heads (rms_norm + 248320 x 2560 Q4 rows, lm_head_parallel restatement, "
+                          f"rows over {att_threads} threads, {dt:.1f} s)"}
     if workload == "gqa_decode":
         pos = 4096
         w = W.gqa_decode_workload(pos, 1, seed=1)
@@ -738,7 +798,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="stack",
                     choices=["stack", "dn_decode", "gqa_decode", "dn_prefill", "gqa_prefill", "q4_proj",
-                             "q4_gemm"])
+                             "q4_gemm", "lm_head"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
                     help="skip the graph-replayed timing (rocprofv3's kernel tracer crashes in "
@@ -754,7 +814,8 @@ def main():
               "(sharding is a design note, not a launched path); run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     defaults = {"stack": (32, 4), "dn_decode": (256, 16), "gqa_decode": (200, 20),
-                "dn_prefill": (20, 3), "gqa_prefill": (10, 2), "q4_proj": (50, 5), "q4_gemm": (20, 3)}[args.workload]
+                "dn_prefill": (20, 3), "gqa_prefill": (10, 2), "q4_proj": (50, 5), "q4_gemm": (20, 3),
+                "lm_head": (100, 10)}[args.workload]
     args.steps = args.steps or defaults[0]
     args.warmup = defaults[1] if args.warmup is None else args.warmup
 
@@ -770,7 +831,7 @@ def main():
         dst.close()
     run = {"stack": run_stack, "dn_decode": run_dn_decode, "gqa_decode": run_gqa_decode,
            "dn_prefill": run_dn_prefill, "gqa_prefill": run_gqa_prefill,
-           "q4_proj": run_q4_proj, "q4_gemm": run_q4_gemm}[args.workload]
+           "q4_proj": run_q4_proj, "q4_gemm": run_q4_gemm, "lm_head": run_lm_head}[args.workload]
     r = run(args, ctx)
     ctx.sync()
     ctx.close()
@@ -792,13 +853,15 @@ def main():
                    "dn_prefill": "mixer tokens/s (prefill) on 1x MI355X",
                    "gqa_prefill": "mixer tokens/s (prefill) on 1x MI355X",
                    "q4_proj": "Q4 projection tokens/s (decode) on 1x MI355X",
-                   "q4_gemm": "Q4 projection tokens/s (prefill) on 1x MI355X"}.get(
+                   "q4_gemm": "Q4 projection tokens/s (prefill) on 1x MI355X",
+                   "lm_head": "lm_head tokens/s (decode) on 1x MI355X"}.get(
                        args.workload, "mixer tokens/s (decode) on 1x MI355X"),
         "value": value, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": r["total_ms"] / args.steps,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": {"dn_prefill": "bf16", "gqa_prefill": "bf16", "q4_gemm": "f16"}.get(args.workload, "f32"),
-        "data": ("synthetic (seeded random Q4 codes, f16 scales and normal inputs)" if args.workload.startswith("q4")
+        "data": ("synthetic (seeded random Q4 codes, f16 scales and normal inputs)"
+                 if args.workload.startswith("q4") or args.workload == "lm_head"
                  else "synthetic (seeded normal inputs, random-init state and f16 KV cache)"),
         "config": r["config"],
         "roofline": rl,

@@ -343,6 +343,32 @@ int32_t qm_q4_gemm_gate_up(qm_context* ctx, qm_stream stream, int32_t m, int32_t
                            const uint8_t* up_codes_dev, const uint16_t* up_gscales_dev,
                            uint16_t* out_f16_dev);
 
+/* ---- vocabulary side of a step: embedding lookup and lm_head ---------- */
+/* The embedding (tied to lm_head) stays in the reference layout, a
+ * Q4Weight with k = vocab rows and n = hidden columns
+ * (write_embedding_weight, convert.rs:390-415): packed_dev u8
+ * [vocab][hidden/2], scales_dev f16 [vocab][hidden/32]. */
+
+/* logits_dev f32 [vocab] = rms_norm(x, final_norm) . row v for every v:
+ * replaces the final rms_norm + lm_head_parallel (Q4 arm, gemv.rs:678-708;
+ * called at gemv.rs:1074-1076, 1280-1282), which the reference's wgpu path
+ * keeps on the CPU (lm_head_cpu, gpu_inference.rs:425-427,818-842).
+ * x_dev f32 [hidden] (hidden % 512 == 0, at most 8192, else QM_ERR_SHAPE);
+ * norm_w_dev f16 [hidden], the (1 + gamma) final norm, or NULL for none.
+ * fp32 throughout: within 1e-5 of sum_j |xn_j W_vj| of the reference. */
+int32_t qm_q4_lm_head(qm_context* ctx, qm_stream stream, int32_t vocab, int32_t hidden,
+                      const float* x_dev, const uint16_t* norm_w_dev,
+                      const uint8_t* packed_dev, const uint16_t* scales_dev,
+                      float* logits_dev);
+
+/* out_dev f32 [count][hidden] = the embedding rows of ids_dev [count]
+ * (embed_lookup_q4, gemv.rs:544-563; used at gemv.rs:1040,1063,1260):
+ * bit-identical to the reference's rows.  An id outside [0, vocab), a
+ * slice-index panic in the reference, yields a row of NaN. */
+int32_t qm_q4_embed(qm_context* ctx, qm_stream stream, int32_t count, int32_t vocab,
+                    int32_t hidden, const int32_t* ids_dev, const uint8_t* packed_dev,
+                    const uint16_t* scales_dev, float* out_dev);
+
 #ifdef __cplusplus
 }
 #endif

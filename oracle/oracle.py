@@ -63,6 +63,8 @@ _SIG = {
     "or_q4_gemv": ([_P, _P, _P, _I32, _I32, _P], None),
     "or_q4_gemm": ([_P, _I32, _P, _P, _I32, _I32, _P, _I32], None),
     "or_q4_gate_up": ([_P, _P, _P, _P, _P, _I32, _I32, _P], None),
+    "or_q4_lm_head": ([_P, _P, _P, _I32, _I32, _P, _I32], None),
+    "or_q4_embed": ([_P, _P, _I32, _I32, _P], None),
 }
 
 _lib = None
@@ -308,4 +310,30 @@ def q4_gate_up(x, g_packed, g_scales, u_packed, u_scales):
     out = np.empty(n, np.float32)
     lib().or_q4_gate_up(x.ctypes.data, gp.ctypes.data, gs.ctypes.data, up.ctypes.data,
                         us.ctypes.data, k, n, out.ctypes.data)
+    return out
+
+
+# ---- vocabulary side ---------------------------------------------------------
+def q4_lm_head(x, packed, scales, nthreads=8):
+    """gemv.rs:678-708: logits[v] = x . row v of the vocab-major Q4 embedding
+    (packed [vocab, hidden/2], scales [vocab, hidden/32])."""
+    x = _f32(x)
+    packed = np.ascontiguousarray(packed, np.uint8)
+    scales = np.ascontiguousarray(scales, np.uint16)
+    vocab, hidden = packed.shape[0], packed.shape[1] * 2
+    assert x.size == hidden
+    out = np.empty(vocab, np.float32)
+    lib().or_q4_lm_head(x.ctypes.data, packed.ctypes.data, scales.ctypes.data, vocab, hidden,
+                        out.ctypes.data, nthreads)
+    return out
+
+
+def q4_embed(packed, scales, token_id):
+    """gemv.rs:544-563: the dequantized embedding row of token_id."""
+    packed = np.ascontiguousarray(packed, np.uint8)
+    scales = np.ascontiguousarray(scales, np.uint16)
+    vocab, hidden = packed.shape[0], packed.shape[1] * 2
+    assert 0 <= token_id < vocab
+    out = np.empty(hidden, np.float32)
+    lib().or_q4_embed(packed.ctypes.data, scales.ctypes.data, hidden, int(token_id), out.ctypes.data)
     return out

@@ -626,3 +626,46 @@ void or_q4_gate_up(const float* x, const uint8_t* g_packed,
     free(g);
     free(u);
 }
+
+/* gemv.rs:678-708: rows in parallel (rayon chunks of 256 rows there), each
+ * row's dot product sequential over its groups and bytes */
+void or_q4_lm_head(const float* x, const uint8_t* packed, const uint16_t* scales,
+                   int32_t vocab, int32_t hidden, float* out, int32_t nthreads) {
+    const int32_t gpr = hidden / 32, ppg = 16, ppr = gpr * ppg;
+    if (nthreads < 1) nthreads = 1;
+    #pragma omp parallel for num_threads(nthreads) schedule(static, 256)
+    for (int32_t v = 0; v < vocab; ++v) {
+        float dot = 0.0f;
+        const size_t sb = (size_t)v * gpr, pb = (size_t)v * ppr;
+        for (int32_t g = 0; g < gpr; ++g) {
+            const float scale = or_f16_to_f32(scales[sb + g]);
+            if (scale == 0.0f) continue;
+            const size_t po = pb + (size_t)g * ppg;
+            const int32_t io = g * 32;
+            float lut[16];
+            for (int q = 0; q < 16; ++q) lut[q] = scale * (float)(q - 8);
+            for (int32_t j = 0; j < ppg; ++j) {
+                const uint8_t byte = packed[po + j];
+                dot += x[io + j * 2] * lut[byte & 0x0F];
+                dot += x[io + j * 2 + 1] * lut[byte >> 4];
+            }
+        }
+        out[v] = dot;
+    }
+}
+
+/* gemv.rs:544-563 */
+void or_q4_embed(const uint8_t* packed, const uint16_t* scales, int32_t hidden,
+                 int32_t id, float* out) {
+    const int32_t gpr = hidden / 32;
+    const size_t sb = (size_t)id * gpr, pb = (size_t)id * gpr * 16;
+    for (int32_t g = 0; g < gpr; ++g) {
+        const float scale = or_f16_to_f32(scales[sb + g]);
+        const size_t po = pb + (size_t)g * 16;
+        for (int32_t j = 0; j < 16; ++j) {
+            const uint8_t byte = packed[po + j];
+            out[g * 32 + j * 2] = scale * (float)((int32_t)(byte & 0x0F) - 8);
+            out[g * 32 + j * 2 + 1] = scale * (float)((int32_t)((byte >> 4) & 0x0F) - 8);
+        }
+    }
+}

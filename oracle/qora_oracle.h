@@ -174,6 +174,18 @@ void or_q4_gate_up(const float* x, const uint8_t* g_packed,
                    const uint16_t* g_scales, const uint8_t* u_packed,
                    const uint16_t* u_scales, int32_t k, int32_t n, float* out);
 
+/* --- vocabulary side: embedding lookup and lm_head ------------------- */
+/* The embedding is a Q4Weight with k = vocab rows, n = hidden columns
+ * (convert.rs:390-415): packed [vocab][hidden/2], scales [vocab][hidden/32]. */
+/* lm_head_parallel, Q4 arm, gemv.rs:678-708: out[v] = x . row v, per row
+ * a 16-entry lut of scale * (q - 8) per group, groups with scale 0
+ * skipped, products summed in column order.                              */
+void or_q4_lm_head(const float* x, const uint8_t* packed, const uint16_t* scales,
+                   int32_t vocab, int32_t hidden, float* out, int32_t nthreads);
+/* embed_lookup_q4, gemv.rs:544-563: out[hidden] = row id dequantized.    */
+void or_q4_embed(const uint8_t* packed, const uint16_t* scales, int32_t hidden,
+                 int32_t id, float* out);
+
 #ifdef __cplusplus
 }
 #endif

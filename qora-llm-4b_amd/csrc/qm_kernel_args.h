@@ -171,6 +171,27 @@ struct Q4GemmArgs {
     int32_t tile;            // QM_Q4_TILE(n)
 };
 
+// lm_head on the vocab-major Q4 embedding: logits[v] = (rms_norm(x) or x) . row v.
+struct LmHeadArgs {
+    const float* x;          // f32 [k]
+    const uint16_t* norm_w;  // null or f16 [k] (1 + gamma)
+    const uint8_t* codes;    // [vocab][k/2]
+    const uint16_t* scales;  // f16 [vocab][k/32]
+    float* logits;           // f32 [vocab]
+    int32_t vocab;
+    int32_t k;               // % 512 == 0, <= 8192
+};
+
+// Embedding rows of count token ids, dequantized to f32.
+struct EmbedArgs {
+    const int32_t* ids;      // [count]
+    const uint8_t* codes;    // [vocab][k/2]
+    const uint16_t* scales;  // f16 [vocab][k/32]
+    float* out;              // f32 [count][k]
+    int32_t vocab;
+    int32_t k;               // % 32 == 0
+};
+
 // Per-row RMSNorm (or plain conversion) of f32 [m][k] into f16.
 struct RmsNormArgs {
     const float* x;          // [m][k]

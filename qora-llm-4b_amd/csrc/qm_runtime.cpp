@@ -49,6 +49,10 @@ struct qm_context {
     hipFunction_t f_q4_gate_up = nullptr;
     hipFunction_t f_q4_gemm[2][2] = {};  // [x bf16][gate/up form]
     hipFunction_t f_rms_f16 = nullptr;
+    hipFunction_t f_lm_head = nullptr;
+    hipFunction_t f_embed = nullptr;
+    int lm_head_hidden = 0;              // the hidden size lm_head_wg_per_cu was computed for
+    int lm_head_wg_per_cu = 1;
     int q4_threads = 0;            // the Q4 kernels' workgroup sizes (their launch bounds)
     int q4_gu_threads = 0;
     void* ws = nullptr;            // general workspace
@@ -254,9 +258,10 @@ int32_t qm_create(qm_context** out, const qm_config* cfg, const char* code_objec
         c->num_cu = 256;
     std::string dir = code_object_dir ? code_object_dir : library_dir();
     const char* files[] = {"qm_dn_decode.hsaco", "qm_gqa_decode.hsaco", "qm_util.hsaco",
-                           "qm_dn_prefill.hsaco", "qm_gqa_prefill.hsaco", "qm_q4_proj.hsaco"};
-    constexpr int kModules = 6;
-    hipModule_t mods[kModules] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+                           "qm_dn_prefill.hsaco", "qm_gqa_prefill.hsaco", "qm_q4_proj.hsaco",
+                           "qm_q4_vocab.hsaco"};
+    constexpr int kModules = 7;
+    hipModule_t mods[kModules] = {};
     for (int i = 0; i < kModules; ++i) {
         std::string path = dir + "/" + files[i];
         hipError_t e = hipModuleLoad(&mods[i], path.c_str());
@@ -288,6 +293,8 @@ int32_t qm_create(qm_context** out, const qm_config* cfg, const char* code_objec
     if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemm_gu", &c->f_q4_gemm[0][1]);
     if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemm_gu_xbf16", &c->f_q4_gemm[1][1]);
     if (st == QM_OK) st = load_function(c, mods[5], "qm_rms_norm_f16", &c->f_rms_f16);
+    if (st == QM_OK) st = load_function(c, mods[6], "qm_q4_lm_head", &c->f_lm_head);
+    if (st == QM_OK) st = load_function(c, mods[6], "qm_q4_embed", &c->f_embed);
     if (st == QM_OK &&
         (hipFuncGetAttribute(&c->q4_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, c->f_q4_gemv) != hipSuccess ||
          hipFuncGetAttribute(&c->q4_gu_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, c->f_q4_gate_up) !=
@@ -779,6 +786,46 @@ int32_t qm_rms_norm_f16(qm_context* c, qm_stream stream, int32_t m, int32_t k, c
         return fail(c, QM_ERR_INVALID_ARG, "qm_rms_norm_f16: device pointers must be 16-byte aligned");
     RmsNormArgs ra{x, norm_w, out, m, k};
     return launch(c, c->f_rms_f16, static_cast<uint32_t>(m), 256, ra, pick(c, stream), "qm_rms_norm_f16");
+}
+
+int32_t qm_q4_lm_head(qm_context* c, qm_stream stream, int32_t vocab, int32_t hidden, const float* x,
+                      const uint16_t* norm_w, const uint8_t* packed, const uint16_t* scales, float* logits) {
+    if (!c) return QM_ERR_INVALID_ARG;
+    if (vocab <= 0 || hidden <= 0 || hidden % 512 != 0 || hidden > 8192)
+        return fail(c, QM_ERR_SHAPE, "qm_q4_lm_head: vocab %d, hidden %d (hidden a multiple of 512, at most 8192)",
+                    vocab, hidden);
+    if (!x || !packed || !scales || !logits) return fail(c, QM_ERR_INVALID_ARG, "qm_q4_lm_head: null pointer");
+    if (!all_aligned16({x, norm_w, packed, scales, logits}))
+        return fail(c, QM_ERR_INVALID_ARG, "qm_q4_lm_head: device pointers must be 16-byte aligned");
+    const int block = hidden / 8;                         // 4 rows x hidden / 32 groups
+    if (c->lm_head_hidden != hidden) {
+        int n = 0;
+        if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, c->f_lm_head, block, 0) != hipSuccess || n <= 0)
+            n = 1;
+        c->lm_head_hidden = hidden;
+        c->lm_head_wg_per_cu = n;
+    }
+    // super-batches of 32 rows, spread evenly over at most one resident wave of workgroups
+    const int64_t nsb = (static_cast<int64_t>(vocab) + 31) / 32;
+    const int64_t slots = static_cast<int64_t>(c->num_cu) * c->lm_head_wg_per_cu;
+    const int64_t per = (nsb + slots - 1) / slots;
+    const int64_t grid = (nsb + per - 1) / per;
+    LmHeadArgs la{x, norm_w, packed, scales, logits, vocab, hidden};
+    return launch(c, c->f_lm_head, static_cast<uint32_t>(grid), static_cast<uint32_t>(block), la, pick(c, stream),
+                  "qm_q4_lm_head");
+}
+
+int32_t qm_q4_embed(qm_context* c, qm_stream stream, int32_t count, int32_t vocab, int32_t hidden,
+                    const int32_t* ids, const uint8_t* packed, const uint16_t* scales, float* out) {
+    if (!c) return QM_ERR_INVALID_ARG;
+    if (count <= 0 || vocab <= 0 || hidden <= 0 || hidden % 32 != 0)
+        return fail(c, QM_ERR_SHAPE, "qm_q4_embed: count %d, vocab %d, hidden %d (a multiple of 32)", count, vocab,
+                    hidden);
+    if (!ids || !packed || !scales || !out) return fail(c, QM_ERR_INVALID_ARG, "qm_q4_embed: null pointer");
+    if (!all_aligned16({ids, packed, scales, out}))
+        return fail(c, QM_ERR_INVALID_ARG, "qm_q4_embed: device pointers must be 16-byte aligned");
+    EmbedArgs ea{ids, packed, scales, out, vocab, hidden};
+    return launch(c, c->f_embed, static_cast<uint32_t>(count), 64, ea, pick(c, stream), "qm_q4_embed");
 }
 
 namespace {

@@ -97,6 +97,8 @@ _SIGNATURES = {
     "qm_rms_norm_f16": [_P, _P, _I32, _I32, _P, _P, _P],
     "qm_q4_gemm": [_P, _P, _I32, _I32, _I32, _P, _I32, _P, _P, _P, _P, _P],
     "qm_q4_gemm_gate_up": [_P, _P, _I32, _I32, _I32, _P, _I32, _P, _P, _P, _P, _P],
+    "qm_q4_lm_head": [_P, _P, _I32, _I32, _P, _P, _P, _P, _P],
+    "qm_q4_embed": [_P, _P, _I32, _I32, _I32, _P, _P, _P, _P],
 }
 _RESTYPES = {"qm_default_config": None, "qm_status_string": C.c_char_p, "qm_last_error": C.c_char_p}
 
@@ -339,6 +341,17 @@ class Context:
         self._check(self.lib.qm_q4_gate_up(self.h, self.stream, k, n, _addr(x), _addr(norm_w),
                                            _addr(gate_codes), _addr(gate_gscales), _addr(up_codes),
                                            _addr(up_gscales), _addr(out)))
+
+
+    def q4_lm_head(self, vocab, hidden, x, norm_w, packed, scales, logits):
+        """logits [vocab] = (rms_norm(x, norm_w) or x) . each row of the Q4 embedding."""
+        self._check(self.lib.qm_q4_lm_head(self.h, self.stream, vocab, hidden, _addr(x), _addr(norm_w),
+                                           _addr(packed), _addr(scales), _addr(logits)))
+
+    def q4_embed(self, count, vocab, hidden, ids, packed, scales, out):
+        """out [count, hidden] = the dequantized embedding rows of ids (int32 [count])."""
+        self._check(self.lib.qm_q4_embed(self.h, self.stream, count, vocab, hidden, _addr(ids), _addr(packed),
+                                         _addr(scales), _addr(out)))
 
 
 class Event:

@@ -85,3 +85,52 @@ def test_gemm_rows_and_gate_up():
     u = x[0].astype(np.float64) @ W.q4_dequant(up_p, up_s).astype(np.float64)
     ref = g / (1.0 + np.exp(-g)) * u
     assert np.all(np.abs(out - ref) <= 1e-5 * np.abs(ref).max())
+
+
+# ---- vocabulary side: lm_head_parallel (gemv.rs:678-708), embed_lookup_q4 (:544-563)
+def _embed(vocab, hidden, seed):
+    rng = np.random.default_rng(seed)
+    packed, scales = W.q4_random_weight(vocab, hidden, rng, scale=0.02)
+    return rng, packed, scales
+
+
+def test_embed_known_answer_and_rows():
+    """A hand-worked row (low nibble = even column, value s * (q - 8)), then
+    every row equals the independent numpy dequantization bit for bit."""
+    packed = np.full((2, 32), 0x88, np.uint8)
+    scales = np.zeros((2, 2), np.uint16)
+    packed[1, 0] = 0xF1                   # columns 0, 1: codes 1, 15 -> -7 s, 7 s
+    packed[1, 17] = 0x0C                  # columns 34, 35: codes 12, 0 -> 4 s', -8 s'
+    scales[1] = [0x3C00, 0x3800]          # s = 1, s' = 0.5
+    row = O.q4_embed(packed, scales, 1)
+    want = np.zeros(64, np.float32)
+    want[:2] = [-7.0, 7.0]
+    want[34:36] = [2.0, -4.0]
+    assert np.array_equal(row, want)
+    assert np.array_equal(O.q4_embed(packed, scales, 0), np.zeros(64, np.float32))
+    _, packed, scales = _embed(300, 2560, 71)
+    E = W.q4_dequant(packed, scales)
+    for v in (0, 1, 157, 299):
+        assert np.array_equal(O.q4_embed(packed, scales, v), E[v])
+
+
+def test_lm_head_vs_float64_and_one_hot():
+    """logits = E x within fp32 summation error of float64; a one-hot x
+    reads one column of E exactly; a zero-scale group is skipped (an
+    infinite x in it leaves that row finite, gemv.rs:685)."""
+    rng, packed, scales = _embed(1000, 2560, 72)
+    E = W.q4_dequant(packed, scales).astype(np.float64)
+    x = rng.standard_normal(2560).astype(np.float32)
+    got = O.q4_lm_head(x, packed, scales)
+    ref = E @ x.astype(np.float64)
+    mag = np.abs(E) @ np.abs(x).astype(np.float64)
+    assert np.all(np.abs(got - ref) <= 1e-5 * mag)
+    oh = np.zeros(2560, np.float32)
+    oh[1234] = 1.0
+    assert np.array_equal(O.q4_lm_head(oh, packed, scales), E[:, 1234].astype(np.float32))
+    scales = scales.copy()
+    scales[5, 3] = 0
+    xi = x.copy()
+    xi[3 * 32 + 7] = np.inf
+    out = O.q4_lm_head(xi, packed, scales)
+    assert np.isfinite(out[5]) and not np.isfinite(out[6])
