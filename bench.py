@@ -636,6 +636,50 @@ def run_lm_head(args, ctx):
     }
 
 
+SAMPLE_GEN = 1000
+
+
+def run_sample(args, ctx):
+    """Next-token sampling over the 248,320 logits of one decode step with
+    the reference's defaults (temperature 1, top_p 0.95, top_k 20, presence
+    penalty 1.5 over 1000 generated ids), logits resident in HBM."""
+    K, Wm = args.steps, args.warmup
+    V = LM_VOCAB
+    logits = ctx.alloc(V * 4)
+    ctx.fill_normal(logits, M.QM_F32, V, 0.0, 3.0, 6001)
+    gen = ctx.upload(np.random.default_rng(6002).integers(0, V, SAMPLE_GEN).astype(np.int32))
+    state = ctx.upload(np.array([0x9E3779B97F4A7C15], np.uint64))
+    tok = ctx.alloc(4)
+    ctx.reserve(1, 0, 0)
+
+    def step():
+        ctx.sample(V, logits, gen, SAMPLE_GEN, state, tok, temperature=1.0, top_p=0.95, top_k=20,
+                   presence_penalty=1.5)
+
+    for _ in range(Wm):
+        step()
+    ctx.sync()
+    t0, t1 = ctx.event(), ctx.event()
+    wall0 = time.perf_counter()
+    t0.record()
+    for _ in range(K):
+        step()
+    t1.record()
+    ctx.sync()
+    wall = time.perf_counter() - wall0
+    ms = t0.elapsed_ms(t1) / K
+    nbytes = V * 4 * 2 + SAMPLE_GEN * 4       # logits read by the penalty pass and the selection
+    return {
+        "tokens": K, "total_ms": t0.elapsed_ms(t1), "wall_s": wall,
+        "dominant": "qm_sample (penalties + select + merge/draw, 3 launches)",
+        "roofline": {"bound": "hbm", "achieved": nbytes / (ms * 1e-3), "peak": HBM_PEAK,
+                     "kernel_ms": ms, "bytes_per_launch": nbytes},
+        "config": {"workload": "next-token sampling over 248320 logits: presence penalty (1000 ids), top_k 20, "
+                               "top_p 0.95, temperature 1",
+                   "batch": 1, "seq_len": 1, "global_batch": 1, "parallelism": "single GPU"},
+    }
+
+
 def _repeat_for(fn, min_s=CPU_SAMPLE_S, max_iters=10 ** 6):
     """Call fn() until min_s seconds have elapsed; returns (calls, seconds)."""
     n, t0 = 0, time.perf_counter()
@@ -728,6 +772,15 @@ def cpu_baseline(workload: str) -> dict:
         return {"value": 8 * n / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
                 "sample": f"{n} calls of gemm_q4 on 8 rows (scalar gemv_q4_inner restatement, one thread, "
                           f"{dt:.1f} s)"}
+    if workload == "sample":
+        rng = np.random.default_rng(11)
+        x = (3.0 * rng.standard_normal(LM_VOCAB)).astype(np.float32)
+        gen = rng.integers(0, LM_VOCAB, SAMPLE_GEN).astype(np.int32)
+        st = np.array([12345], np.uint64)
+        n, dt = _repeat_for(lambda: O.sample_top_k(O.apply_penalties(x, gen, 1.0, 1.5), 1.0, 0.95, 20, st))
+        return {"value": n / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
+                "sample": f"{n} samplings (presence penalty, full stable sort of 248320 logits, softmax, top-p, "
+                          f"draw; generate.rs restatement, one thread, {dt:.1f} s)"}
     if workload == "lm_head":
         rng = np.random.default_rng(10)
         packed, scales = W.q4_random_weight(LM_VOCAB, LM_HIDDEN, rng, scale=0.02)
@@ -798,7 +851,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="stack",
                     choices=["stack", "dn_decode", "gqa_decode", "dn_prefill", "gqa_prefill", "q4_proj",
-                             "q4_gemm", "lm_head"])
+                             "q4_gemm", "lm_head", "sample"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
                     help="skip the graph-replayed timing (rocprofv3's kernel tracer crashes in "
@@ -815,7 +868,7 @@ def main():
         sys.exit(2)
     defaults = {"stack": (32, 4), "dn_decode": (256, 16), "gqa_decode": (200, 20),
                 "dn_prefill": (20, 3), "gqa_prefill": (10, 2), "q4_proj": (50, 5), "q4_gemm": (20, 3),
-                "lm_head": (100, 10)}[args.workload]
+                "lm_head": (100, 10), "sample": (200, 10)}[args.workload]
     args.steps = args.steps or defaults[0]
     args.warmup = defaults[1] if args.warmup is None else args.warmup
 
@@ -831,7 +884,8 @@ def main():
         dst.close()
     run = {"stack": run_stack, "dn_decode": run_dn_decode, "gqa_decode": run_gqa_decode,
            "dn_prefill": run_dn_prefill, "gqa_prefill": run_gqa_prefill,
-           "q4_proj": run_q4_proj, "q4_gemm": run_q4_gemm, "lm_head": run_lm_head}[args.workload]
+           "q4_proj": run_q4_proj, "q4_gemm": run_q4_gemm, "lm_head": run_lm_head,
+           "sample": run_sample}[args.workload]
     r = run(args, ctx)
     ctx.sync()
     ctx.close()
@@ -854,13 +908,15 @@ def main():
                    "gqa_prefill": "mixer tokens/s (prefill) on 1x MI355X",
                    "q4_proj": "Q4 projection tokens/s (decode) on 1x MI355X",
                    "q4_gemm": "Q4 projection tokens/s (prefill) on 1x MI355X",
-                   "lm_head": "lm_head tokens/s (decode) on 1x MI355X"}.get(
+                   "lm_head": "lm_head tokens/s (decode) on 1x MI355X",
+                   "sample": "sampled tokens/s (decode) on 1x MI355X"}.get(
                        args.workload, "mixer tokens/s (decode) on 1x MI355X"),
         "value": value, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": r["total_ms"] / args.steps,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": {"dn_prefill": "bf16", "gqa_prefill": "bf16", "q4_gemm": "f16"}.get(args.workload, "f32"),
-        "data": ("synthetic (seeded random Q4 codes, f16 scales and normal inputs)"
+        "data": ("synthetic (seeded normal logits, random generated ids)" if args.workload == "sample" else
+                 "synthetic (seeded random Q4 codes, f16 scales and normal inputs)"
                  if args.workload.startswith("q4") or args.workload == "lm_head"
                  else "synthetic (seeded normal inputs, random-init state and f16 KV cache)"),
         "config": r["config"],

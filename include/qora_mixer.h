@@ -369,6 +369,45 @@ int32_t qm_q4_embed(qm_context* ctx, qm_stream stream, int32_t count, int32_t vo
                     int32_t hidden, const int32_t* ids_dev, const uint8_t* packed_dev,
                     const uint16_t* scales_dev, float* out_dev);
 
+/* ---- next-token sampling ------------------------------------------------ */
+/* The sampling settings of GenerateParams (generate.rs:9-21) plus the
+ * per-step choices of the decode loop (generate.rs:185-198). */
+enum { QM_SAMPLE_WGPU = 1 };  /* follow the wgpu path's sample_token_top_k,
+                                 gpu_inference.rs:867-906: probabilities
+                                 divided by the sum, no zero-sum exits,
+                                 greedy keeps the last of equal maxima */
+typedef struct qm_sample_params {
+    float temperature;         /* <= 0: greedy (the top_k etc. are unused) */
+    float top_p;
+    int32_t top_k;             /* 1 .. 1024 when sampling */
+    float repetition_penalty;  /* applied when > 1 (last 64 ids) */
+    float presence_penalty;    /* applied when > 0, once per distinct id */
+    int32_t banned_id;         /* set to -inf after the penalties, or -1
+                                  (the EOS ban inside a think block,
+                                  generate.rs:191) */
+    int32_t flags;             /* 0 or QM_SAMPLE_WGPU */
+} qm_sample_params;
+
+/* Next token from logits_dev f32 [vocab], on the device: replaces
+ * apply_repetition_penalty + apply_presence_penalty (generate.rs:58-82,
+ * applied in place to logits_dev as the reference mutates its logits) and
+ * sample_token_top_k (generate.rs:334-384), so the logits need not be
+ * copied to the host.  generated_dev int32 [n_generated] (oldest first);
+ * rng_state_dev the Rng's xorshift64 state (generate.rs:41-55), advanced
+ * exactly when the reference draws.  token_out_dev int32 [1].  Optional
+ * top_ids_dev int32 [k] / top_probs_dev f32 [k] receive the sorted top-k
+ * ids and their probabilities.  Given the same logits and state, the token
+ * and the new state equal the reference's (the one difference: exp is the
+ * correctly rounded one, libm's expf can differ by one ulp in rare cases).
+ * Logits must not be NaN (the reference's sort has no defined order for
+ * them).  top_k = 0 (all logits) is not supported: QM_ERR_INVALID_ARG;
+ * vocab at most 262144 (QM_ERR_SHAPE).  Uses 64 KB of the context's
+ * workspace (reserved by qm_reserve). */
+int32_t qm_sample(qm_context* ctx, qm_stream stream, int32_t vocab, float* logits_dev,
+                  const int32_t* generated_dev, int32_t n_generated,
+                  const qm_sample_params* params, uint64_t* rng_state_dev,
+                  int32_t* token_out_dev, int32_t* top_ids_dev, float* top_probs_dev);
+
 #ifdef __cplusplus
 }
 #endif

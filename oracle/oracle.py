@@ -65,6 +65,10 @@ _SIG = {
     "or_q4_gate_up": ([_P, _P, _P, _P, _P, _I32, _I32, _P], None),
     "or_q4_lm_head": ([_P, _P, _P, _I32, _I32, _P, _I32], None),
     "or_q4_embed": ([_P, _P, _I32, _I32, _P], None),
+    "or_rng_next_f32": ([_P], C.c_float),
+    "or_apply_repetition_penalty": ([_P, _I32, _P, _I32, C.c_float], None),
+    "or_apply_presence_penalty": ([_P, _I32, _P, _I32, C.c_float], None),
+    "or_sample_top_k": ([_P, _I32, C.c_float, C.c_float, _I32, _P, _I32, _P, _P], _I32),
 }
 
 _lib = None
@@ -337,3 +341,32 @@ def q4_embed(packed, scales, token_id):
     out = np.empty(hidden, np.float32)
     lib().or_q4_embed(packed.ctypes.data, scales.ctypes.data, hidden, int(token_id), out.ctypes.data)
     return out
+
+
+# ---- sampling ----------------------------------------------------------------
+def rng_next_f32(state: np.ndarray) -> float:
+    """generate.rs:46-54; state is a uint64 array of one element, advanced in place."""
+    assert state.dtype == np.uint64 and state.size == 1
+    return lib().or_rng_next_f32(state.ctypes.data)
+
+
+def apply_penalties(logits, generated, repetition_penalty, presence_penalty):
+    """generate.rs:58-82, repetition then presence (generate.rs:194-195); returns a copy."""
+    out = _f32(logits).copy()
+    g = np.ascontiguousarray(generated, np.int32)
+    lib().or_apply_repetition_penalty(out.ctypes.data, out.size, g.ctypes.data, g.size, repetition_penalty)
+    lib().or_apply_presence_penalty(out.ctypes.data, out.size, g.ctypes.data, g.size, presence_penalty)
+    return out
+
+
+def sample_top_k(logits, temperature, top_p, top_k, state, wgpu=False):
+    """sample_token_top_k (generate.rs:334-384, or gpu_inference.rs:867-906 with
+    wgpu): returns (token, sorted top-k ids, their probabilities); state (uint64
+    array of one element) is advanced in place when a draw is made."""
+    x = _f32(logits)
+    k = 1 if temperature <= 0 else (min(top_k, x.size) if top_k > 0 else x.size)
+    ids = np.zeros(k, np.int32)
+    probs = np.zeros(k, np.float32)
+    tok = lib().or_sample_top_k(x.ctypes.data, x.size, temperature, top_p, top_k, state.ctypes.data,
+                                int(wgpu), ids.ctypes.data, probs.ctypes.data)
+    return tok, ids, probs

@@ -669,3 +669,123 @@ void or_q4_embed(const uint8_t* packed, const uint16_t* scales, int32_t hidden,
         }
     }
 }
+
+/* ---- sampling ---------------------------------------------------------- */
+/* generate.rs:46-54 */
+float or_rng_next_f32(uint64_t* state) {
+    uint64_t s = *state;
+    s ^= s << 13;
+    s ^= s >> 7;
+    s ^= s << 17;
+    *state = s;
+    return (float)(s >> 40) / 16777216.0f;
+}
+
+/* generate.rs:58-69 */
+void or_apply_repetition_penalty(float* logits, int32_t vocab, const int32_t* generated,
+                                 int32_t n, float penalty) {
+    if (penalty <= 1.0f) return;
+    const int32_t window = n < 64 ? n : 64;
+    for (int32_t i = n - window; i < n; ++i) {
+        const int32_t idx = generated[i];
+        if (idx >= 0 && idx < vocab) {
+            if (logits[idx] > 0.0f) logits[idx] /= penalty;
+            else logits[idx] *= penalty;
+        }
+    }
+}
+
+/* generate.rs:72-82 */
+void or_apply_presence_penalty(float* logits, int32_t vocab, const int32_t* generated,
+                               int32_t n, float penalty) {
+    if (penalty <= 0.0f || n == 0) return;
+    unsigned char* seen = (unsigned char*)calloc((size_t)vocab, 1);
+    for (int32_t i = 0; i < n; ++i)
+        if (generated[i] >= 0 && generated[i] < vocab) seen[generated[i]] = 1;
+    for (int32_t i = 0; i < vocab; ++i)
+        if (seen[i]) logits[i] -= penalty;
+    free(seen);
+}
+
+typedef struct { uint32_t id; float v; } or_idx_logit;
+
+/* the stable descending sort_by of generate.rs:350 / gpu_inference.rs:879:
+ * equal logits keep index order */
+static int or_cmp_desc(const void* a, const void* b) {
+    const or_idx_logit* x = (const or_idx_logit*)a;
+    const or_idx_logit* y = (const or_idx_logit*)b;
+    if (x->v > y->v) return -1;
+    if (x->v < y->v) return 1;
+    return x->id < y->id ? -1 : (x->id > y->id);
+}
+
+int32_t or_sample_top_k(const float* logits, int32_t vocab, float temperature, float top_p,
+                        int32_t top_k, uint64_t* rng_state, int32_t wgpu,
+                        int32_t* out_ids, float* out_probs) {
+    if (temperature <= 0.0f) {
+        int32_t best = 0;
+        if (!wgpu) {                       /* generate.rs:336-341: first maximum */
+            float max_val = -INFINITY;
+            for (int32_t i = 0; i < vocab; ++i)
+                if (logits[i] > max_val) { max_val = logits[i]; best = i; }
+        } else {                           /* max_by: the last maximum */
+            for (int32_t i = 1; i < vocab; ++i)
+                if (!(logits[i] < logits[best])) best = i;
+        }
+        if (out_ids) out_ids[0] = best;
+        return best;
+    }
+    const float inv_temp = 1.0f / temperature;
+    or_idx_logit* ix = (or_idx_logit*)malloc(sizeof(or_idx_logit) * (size_t)vocab);
+    float max_logit = -INFINITY;
+    for (int32_t i = 0; i < vocab; ++i) {
+        ix[i].id = (uint32_t)i;
+        ix[i].v = logits[i];
+        if (logits[i] > max_logit) max_logit = logits[i];     /* f32::max fold */
+    }
+    qsort(ix, (size_t)vocab, sizeof(or_idx_logit), or_cmp_desc);
+    const int32_t k = top_k > 0 ? (top_k < vocab ? top_k : vocab) : vocab;
+    if (wgpu) max_logit = ix[0].v;
+    float* p = (float*)malloc(sizeof(float) * (size_t)k);
+    for (int32_t i = 0; i < k; ++i) p[i] = expf((ix[i].v - max_logit) * inv_temp);
+    float sum = 0.0f;
+    for (int32_t i = 0; i < k; ++i) sum += p[i];
+    int32_t tok;
+    if (!wgpu && sum <= 0.0f) {
+        tok = (int32_t)ix[0].id;
+        goto done;
+    }
+    if (wgpu) {
+        for (int32_t i = 0; i < k; ++i) p[i] /= sum;
+    } else {
+        const float inv = 1.0f / sum;
+        for (int32_t i = 0; i < k; ++i) p[i] *= inv;
+    }
+    {
+        float cumsum = 0.0f;
+        int32_t cutoff = k;
+        for (int32_t i = 0; i < k; ++i) {
+            cumsum += p[i];
+            if (cumsum >= top_p) { cutoff = i + 1; break; }
+        }
+        float total = 0.0f;
+        for (int32_t i = 0; i < cutoff; ++i) total += p[i];
+        if (!wgpu && total <= 0.0f) {
+            tok = (int32_t)ix[0].id;
+            goto done;
+        }
+        const float rand_val = or_rng_next_f32(rng_state) * total;
+        float accum = 0.0f;
+        tok = (int32_t)ix[0].id;
+        for (int32_t i = 0; i < cutoff; ++i) {
+            accum += p[i];
+            if (accum >= rand_val) { tok = (int32_t)ix[i].id; break; }
+        }
+    }
+done:
+    if (out_ids) for (int32_t i = 0; i < k; ++i) out_ids[i] = (int32_t)ix[i].id;
+    if (out_probs) for (int32_t i = 0; i < k; ++i) out_probs[i] = p[i];
+    free(p);
+    free(ix);
+    return tok;
+}

@@ -186,6 +186,23 @@ void or_q4_lm_head(const float* x, const uint8_t* packed, const uint16_t* scales
 void or_q4_embed(const uint8_t* packed, const uint16_t* scales, int32_t hidden,
                  int32_t id, float* out);
 
+/* --- sampling (generate.rs:41-82,334-384; wgpu twin gpu_inference.rs:
+ * 855-931) -------------------------------------------------------------- */
+/* Rng::next_f32, generate.rs:46-54 (xorshift64 13/7/17, top 24 bits).    */
+float or_rng_next_f32(uint64_t* state);
+/* apply_repetition_penalty / apply_presence_penalty, generate.rs:58-82.  */
+void or_apply_repetition_penalty(float* logits, int32_t vocab, const int32_t* generated,
+                                 int32_t n, float penalty);
+void or_apply_presence_penalty(float* logits, int32_t vocab, const int32_t* generated,
+                               int32_t n, float penalty);
+/* sample_token_top_k: wgpu = 0 follows generate.rs:334-384, wgpu = 1
+ * gpu_inference.rs:867-906.  top_k = 0 means all logits (generate.rs only).
+ * If out_ids / out_probs are non-null they receive the first k sorted ids
+ * and (when sampling) their normalized probabilities.                    */
+int32_t or_sample_top_k(const float* logits, int32_t vocab, float temperature, float top_p,
+                        int32_t top_k, uint64_t* rng_state, int32_t wgpu,
+                        int32_t* out_ids, float* out_probs);
+
 #ifdef __cplusplus
 }
 #endif

@@ -32,7 +32,7 @@ HIPCC_FLAGS = [
     "-Wall", "-Wno-unused-parameter",
 ]
 
-KERNELS = ["dn_decode", "gqa_decode", "util", "dn_prefill", "gqa_prefill", "q4_proj", "q4_vocab"]
+KERNELS = ["dn_decode", "gqa_decode", "util", "dn_prefill", "gqa_prefill", "q4_proj", "q4_vocab", "sample"]
 
 
 def _run(cmd: list[str]) -> None:

@@ -192,6 +192,29 @@ struct EmbedArgs {
     int32_t k;               // % 32 == 0
 };
 
+// Next-token sampling (one workgroup per kernel).
+#define QMK_SAMPLE_WGPU 1          // follow gpu_inference.rs:867-906 instead of generate.rs:334-384
+struct SampleArgs {
+    float* logits;            // [vocab]; the penalties are applied in place
+    const int32_t* generated; // [n_generated] ids generated so far, oldest first
+    uint64_t* rng_state;      // xorshift64 state, advanced when a draw is made
+    int32_t* token_out;       // [1]
+    int32_t* top_ids;         // null, or [k] the sorted top-k ids
+    float* top_probs;         // null, or [k] their probabilities after the softmax
+    int32_t vocab;
+    int32_t n_generated;
+    int32_t top_k;            // 1 .. 1024 (ignored when greedy)
+    int32_t banned;           // id set to -inf after the penalties, or -1
+    int32_t flags;
+    float temperature;        // <= 0: greedy
+    float top_p;
+    float repetition_penalty; // applied when > 1
+    float presence_penalty;   // applied when > 0
+    uint64_t* cand;           // workspace: [n_cand] stage-1 candidates
+    int32_t chunk;            // vocabulary slice per stage-1 workgroup (multiple of 256)
+    int32_t n_cand;           // slices x k (<= 8192)
+};
+
 // Per-row RMSNorm (or plain conversion) of f32 [m][k] into f16.
 struct RmsNormArgs {
     const float* x;          // [m][k]

@@ -51,6 +51,9 @@ struct qm_context {
     hipFunction_t f_rms_f16 = nullptr;
     hipFunction_t f_lm_head = nullptr;
     hipFunction_t f_embed = nullptr;
+    hipFunction_t f_sample_pen = nullptr;
+    hipFunction_t f_sample = nullptr;
+    hipFunction_t f_sample_select = nullptr;
     int lm_head_hidden = 0;              // the hidden size lm_head_wg_per_cu was computed for
     int lm_head_wg_per_cu = 1;
     int q4_threads = 0;            // the Q4 kernels' workgroup sizes (their launch bounds)
@@ -91,6 +94,11 @@ bool all_aligned16(std::initializer_list<const void*> ptrs) {
         if (p && (reinterpret_cast<uintptr_t>(p) & 15u) != 0) return false;
     return true;
 }
+
+bool aligned_to(const void* p, uintptr_t a) { return !p || (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+constexpr int32_t kSampleMaxVocab = 262144;      // the presence bitmap of qm_sample_penalties (LDS)
+constexpr size_t kSampleWsBytes = 8192 * sizeof(uint64_t);   // stage-1 sampling candidates
 
 #define QM_HIP(c, call)                                                              \
     do {                                                                             \
@@ -259,8 +267,8 @@ int32_t qm_create(qm_context** out, const qm_config* cfg, const char* code_objec
     std::string dir = code_object_dir ? code_object_dir : library_dir();
     const char* files[] = {"qm_dn_decode.hsaco", "qm_gqa_decode.hsaco", "qm_util.hsaco",
                            "qm_dn_prefill.hsaco", "qm_gqa_prefill.hsaco", "qm_q4_proj.hsaco",
-                           "qm_q4_vocab.hsaco"};
-    constexpr int kModules = 7;
+                           "qm_q4_vocab.hsaco", "qm_sample.hsaco"};
+    constexpr int kModules = 8;
     hipModule_t mods[kModules] = {};
     for (int i = 0; i < kModules; ++i) {
         std::string path = dir + "/" + files[i];
@@ -295,6 +303,9 @@ int32_t qm_create(qm_context** out, const qm_config* cfg, const char* code_objec
     if (st == QM_OK) st = load_function(c, mods[5], "qm_rms_norm_f16", &c->f_rms_f16);
     if (st == QM_OK) st = load_function(c, mods[6], "qm_q4_lm_head", &c->f_lm_head);
     if (st == QM_OK) st = load_function(c, mods[6], "qm_q4_embed", &c->f_embed);
+    if (st == QM_OK) st = load_function(c, mods[7], "qm_sample_penalties", &c->f_sample_pen);
+    if (st == QM_OK) st = load_function(c, mods[7], "qm_sample_top_k", &c->f_sample);
+    if (st == QM_OK) st = load_function(c, mods[7], "qm_sample_select", &c->f_sample_select);
     if (st == QM_OK &&
         (hipFuncGetAttribute(&c->q4_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, c->f_q4_gemv) != hipSuccess ||
          hipFuncGetAttribute(&c->q4_gu_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, c->f_q4_gate_up) !=
@@ -615,6 +626,7 @@ int32_t qm_reserve(qm_context* c, int32_t max_batch, int32_t max_kv_len, int32_t
         const size_t s_pad = (static_cast<size_t>(max_prefill_tokens) + 63) / 64 * 64;
         ws = std::max(ws, gqa_prefill_vt_bytes(s_pad) + 256);
     }
+    ws = std::max(ws, kSampleWsBytes);
     return ensure(c, c->stream, ws);
 }
 
@@ -826,6 +838,51 @@ int32_t qm_q4_embed(qm_context* c, qm_stream stream, int32_t count, int32_t voca
         return fail(c, QM_ERR_INVALID_ARG, "qm_q4_embed: device pointers must be 16-byte aligned");
     EmbedArgs ea{ids, packed, scales, out, vocab, hidden};
     return launch(c, c->f_embed, static_cast<uint32_t>(count), 64, ea, pick(c, stream), "qm_q4_embed");
+}
+
+static_assert(QM_SAMPLE_WGPU == QMK_SAMPLE_WGPU, "sampling flag values");
+
+int32_t qm_sample(qm_context* c, qm_stream stream, int32_t vocab, float* logits, const int32_t* generated,
+                  int32_t n_generated, const qm_sample_params* p, uint64_t* rng_state, int32_t* token_out,
+                  int32_t* top_ids, float* top_probs) {
+    if (!c) return QM_ERR_INVALID_ARG;
+    if (!p || !logits || !token_out || vocab <= 0 || n_generated < 0 || (n_generated > 0 && !generated))
+        return fail(c, QM_ERR_INVALID_ARG, "qm_sample: null pointer or negative size");
+    if (vocab > kSampleMaxVocab)
+        return fail(c, QM_ERR_SHAPE, "qm_sample: vocab %d (at most %d)", vocab, kSampleMaxVocab);
+    if ((p->flags & ~QM_SAMPLE_WGPU) != 0) return fail(c, QM_ERR_INVALID_ARG, "qm_sample: unknown flags 0x%x", p->flags);
+    const bool greedy = !(p->temperature > 0.0f);
+    if (!greedy) {
+        // generate.rs:353 takes every logit for top_k = 0; this build sorts at most 1024 in one workgroup
+        if (p->top_k < 1 || p->top_k > 1024)
+            return fail(c, QM_ERR_INVALID_ARG, "qm_sample: top_k %d (1 .. 1024 when temperature > 0)", p->top_k);
+        if ((p->flags & QM_SAMPLE_WGPU) && vocab < p->top_k)
+            return fail(c, QM_ERR_INVALID_ARG, "qm_sample: top_k %d exceeds vocab %d", p->top_k, vocab);
+        if (!rng_state) return fail(c, QM_ERR_INVALID_ARG, "qm_sample: null rng state");
+    }
+    if (!aligned_to(logits, 4) || !aligned_to(generated, 4) || !aligned_to(token_out, 4) ||
+        !aligned_to(top_ids, 4) || !aligned_to(top_probs, 4) || !aligned_to(rng_state, 8))
+        return fail(c, QM_ERR_INVALID_ARG, "qm_sample: misaligned device pointer");
+    hipStream_t s = pick(c, stream);
+    int32_t st = ensure(c, s, kSampleWsBytes);
+    if (st != QM_OK) return st;
+    // stage 1 slices: 1024 m logits each, so that slices x k candidates fit
+    // the stage-2 sort (8192)
+    const int64_t k = greedy ? 1 : std::min(p->top_k, vocab);
+    int64_t m = 1;
+    while ((vocab + 1024 * m - 1) / (1024 * m) * k > 8192) ++m;
+    const int64_t chunk = 1024 * m, nw = (vocab + chunk - 1) / chunk;
+    SampleArgs sa{logits,     generated,     rng_state,      token_out,  top_ids,
+                  top_probs,  vocab,         n_generated,    p->top_k,   p->banned_id,
+                  p->flags,   p->temperature, p->top_p,      p->repetition_penalty, p->presence_penalty,
+                  static_cast<uint64_t*>(c->ws), static_cast<int32_t>(chunk), static_cast<int32_t>(nw * k)};
+    if (p->repetition_penalty > 1.0f || (p->presence_penalty > 0.0f && n_generated > 0) || p->banned_id >= 0) {
+        st = launch(c, c->f_sample_pen, 1, 1024, sa, s, "qm_sample_penalties");
+        if (st != QM_OK) return st;
+    }
+    st = launch(c, c->f_sample_select, static_cast<uint32_t>(nw), 256, sa, s, "qm_sample_select");
+    if (st != QM_OK) return st;
+    return launch(c, c->f_sample, 1, 1024, sa, s, "qm_sample_top_k");
 }
 
 namespace {

@@ -42,6 +42,15 @@ class QmQ4Out(C.Structure):
                 ("y_dev", C.c_void_p), ("residual_dev", C.c_void_p)]
 
 
+QM_SAMPLE_WGPU = 1
+
+
+class QmSampleParams(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_p", C.c_float), ("top_k", C.c_int32),
+                ("repetition_penalty", C.c_float), ("presence_penalty", C.c_float),
+                ("banned_id", C.c_int32), ("flags", C.c_int32)]
+
+
 class QmConfig(C.Structure):
     _fields_ = [(n, C.c_int32) for n in (
         "num_qk_heads", "num_v_heads", "dn_head_dim", "conv_kernel",
@@ -99,6 +108,7 @@ _SIGNATURES = {
     "qm_q4_gemm_gate_up": [_P, _P, _I32, _I32, _I32, _P, _I32, _P, _P, _P, _P, _P],
     "qm_q4_lm_head": [_P, _P, _I32, _I32, _P, _P, _P, _P, _P],
     "qm_q4_embed": [_P, _P, _I32, _I32, _I32, _P, _P, _P, _P],
+    "qm_sample": [_P, _P, _I32, _P, _P, _I32, C.POINTER(QmSampleParams), _P, _P, _P, _P],
 }
 _RESTYPES = {"qm_default_config": None, "qm_status_string": C.c_char_p, "qm_last_error": C.c_char_p}
 
@@ -352,6 +362,17 @@ class Context:
         """out [count, hidden] = the dequantized embedding rows of ids (int32 [count])."""
         self._check(self.lib.qm_q4_embed(self.h, self.stream, count, vocab, hidden, _addr(ids), _addr(packed),
                                          _addr(scales), _addr(out)))
+
+
+    def sample(self, vocab, logits, generated, n_generated, rng_state, token_out, temperature=1.0, top_p=0.95,
+               top_k=20, repetition_penalty=1.0, presence_penalty=0.0, banned_id=-1, flags=0,
+               top_ids=None, top_probs=None):
+        """Penalties (in place on logits) and the next token into token_out (int32 [1]);
+        rng_state is the device uint64 xorshift64 state."""
+        p = QmSampleParams(temperature, top_p, top_k, repetition_penalty, presence_penalty, banned_id, flags)
+        self._check(self.lib.qm_sample(self.h, self.stream, vocab, _addr(logits), _addr(generated), n_generated,
+                                       C.byref(p), _addr(rng_state), _addr(token_out), _addr(top_ids),
+                                       _addr(top_probs)))
 
 
 class Event:
