@@ -70,10 +70,18 @@ def build_host_test() -> None:
     """tests/cpp/host_mirror_test.cpp: the C++ mirror driven against the oracle
     (test infrastructure; needs the library and the oracle built)."""
     _run(["g++", "-O2", "-std=c++17", "-Wall", "-Wextra", "-I", str(ROOT / "include"),
-          "-I", str(PKG / "host"), "-I", str(ROOT / "oracle"),
+          "-I", str(PKG / "host"), "-I", str(ROOT / "oracle"), "-I", str(ROOT / "tests" / "cpp"),
           str(ROOT / "tests" / "cpp" / "host_mirror_test.cpp"), "-o", str(LIB / "host_mirror_test"),
           f"-L{LIB}", "-lqora_mixer", f"-L{ROOT / 'oracle'}", "-loracle",
           "-Wl,-rpath,$ORIGIN", "-Wl,-rpath,$ORIGIN/../../oracle"])
+
+
+
+def build_file_test() -> None:
+    """tests/cpp/qor4b_file_test.cpp: the .qor4b parser on the CPU (g++ only,
+    no device code; test infrastructure)."""
+    _run(["g++", "-O2", "-std=c++17", "-Wall", "-Wextra", "-I", str(PKG / "host"), "-I", str(ROOT / "tests" / "cpp"),
+          str(ROOT / "tests" / "cpp" / "qor4b_file_test.cpp"), "-o", str(LIB / "qor4b_file_test")])
 
 
 if __name__ == "__main__":
@@ -81,4 +89,5 @@ if __name__ == "__main__":
     if "--no-oracle" not in sys.argv:
         build_oracle()
         build_host_test()
+        build_file_test()
     print("built:", ", ".join(sorted(p.name for p in LIB.iterdir())))

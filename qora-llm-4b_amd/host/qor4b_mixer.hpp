@@ -253,8 +253,8 @@ struct GpuQ4Weight {
     DeviceBuffer codes, gscales;
     std::size_t k = 0, n = 0;
 
-    static GpuQ4Weight upload(Context& ctx, const uint8_t* packed, const uint16_t* scales, std::size_t k,
-                              std::size_t n) {
+    // packed / scales are host bytes in any alignment (a file map, say)
+    static GpuQ4Weight upload(Context& ctx, const void* packed, const void* scales, std::size_t k, std::size_t n) {
         const std::size_t pb = k * n / 2, sb = k * (n / 32) * 2;
         DeviceBuffer p(ctx, pb), s(ctx, sb < 16 ? 16 : sb);
         p.upload(packed, pb);

@@ -1,0 +1,230 @@
+// qor4b_model.hpp -- a .qor4b model resident on the device and one decode
+// step through it, over the C ABI (include/qora_mixer.h):
+//   load_gpu_model      load_model (save.rs:247-396) + the device upload of
+//                       load_gpu_model (gpu_loader.rs:69-140): every Q4
+//                       projection repacked (qm_q4_repack), norms, conv and
+//                       gate parameters, the vocab-major embedding and the
+//                       RoPE tables copied as they are
+//   GpuHybridCache      HybridCache / GpuHybridCache (gemv.rs:171-186,
+//                       gpu_inference.rs:44-60): per-layer DeltaNet state or
+//                       f16 KV cache of a fixed capacity
+//   forward_decode_gpu  forward_decode (gemv.rs:1059-1077): embedding row,
+//                       the 32 layer-forwards (gemv.rs:719-900, 907-1025)
+//                       with their projections, final norm and lm_head, all
+//                       on the device; the token id is read from device
+//                       memory, so sampling (qm_sample) can feed it directly
+// The model must have the mixer's shape (Qor4bConfig::default_4b) and Q4
+// weights; other files raise MixerError(QM_ERR_SHAPE).
+#pragma once
+
+#include "qor4b_file.hpp"
+#include "qor4b_mixer.hpp"
+
+#include <algorithm>
+#include <vector>
+
+namespace qor4b {
+
+struct GpuDeltaNetLayerWeights {
+    GpuQ4Weight in_proj_qkv, in_proj_a, in_proj_b, in_proj_z, out_proj, gate_proj, up_proj, down_proj;
+    GpuDeltaNetLayer mixer;
+    DeviceBuffer input_norm, post_attn_norm;   // f16 [hidden], (1 + gamma)
+};
+
+struct GpuFullAttnLayerWeights {
+    GpuQ4Weight q_proj, k_proj, v_proj, o_proj, gate_proj, up_proj, down_proj;
+    GpuFullAttnLayer mixer;
+    DeviceBuffer input_norm, post_attn_norm;
+};
+
+struct GpuEmbedding {
+    DeviceBuffer packed, scales;               // [vocab][hidden/2], f16 [vocab][hidden/32]
+    std::size_t vocab = 0, hidden = 0;
+};
+
+struct GpuModel {
+    FileConfig config;
+    std::vector<GpuDeltaNetLayerWeights> dn;   // the DeltaNet layers, in order
+    std::vector<GpuFullAttnLayerWeights> fa;   // the attention layers, in order
+    std::vector<std::size_t> slot;             // layer i -> its index in dn or fa
+    GpuEmbedding embed;
+    DeviceBuffer final_norm;                   // f16 [hidden]
+    DeviceBuffer rope_cos, rope_sin;           // f32 [rope_len][rope_dim / 2]
+    int32_t rope_len = 0;
+};
+
+namespace detail {
+
+inline GpuQ4Weight upload_q4(Context& ctx, const WeightView& w, uint64_t k, uint64_t n, const char* what) {
+    if (w.fmt != 1)
+        throw MixerError(QM_ERR_SHAPE, std::string(what) + ": F16 weights are not supported (Q4 only)");
+    if (w.k != k || w.n != n || w.packed.len != k * n / 2 || w.scales.len != k * (n / 32))
+        throw MixerError(QM_ERR_SHAPE, std::string(what) + ": " + std::to_string(w.k) + " x " + std::to_string(w.n) +
+                                           ", expected " + std::to_string(k) + " x " + std::to_string(n));
+    return GpuQ4Weight::upload(ctx, w.packed.data, w.scales.data, k, n);
+}
+
+inline DeviceBuffer upload_array(Context& ctx, const ArrayView& a, uint64_t len, const char* what) {
+    if (a.len != len)
+        throw MixerError(QM_ERR_SHAPE, std::string(what) + ": " + std::to_string(a.len) + " elements, expected " +
+                                           std::to_string(len));
+    DeviceBuffer b(ctx, a.bytes() < 16 ? 16 : a.bytes());
+    b.upload(a.data, a.bytes());
+    return b;
+}
+
+}  // namespace detail
+
+inline GpuModel load_gpu_model(Context& ctx, const ModelView& m) {
+    const Qor4bConfig mc = Qor4bConfig::default_4b();
+    const FileConfig& c = m.config;
+    if (c.num_attn_heads != mc.num_attn_heads || c.num_kv_heads != mc.num_kv_heads ||
+        c.attn_head_dim != mc.attn_head_dim || c.num_qk_heads != mc.num_qk_heads ||
+        c.num_v_heads != mc.num_v_heads || c.deltanet_head_dim != mc.deltanet_head_dim ||
+        c.conv_kernel_size != mc.conv_kernel_size || c.hidden_size % 512 != 0)
+        throw MixerError(QM_ERR_SHAPE, "load_gpu_model: the file's layer shapes are not the 4B mixer's");
+    const uint64_t H = c.hidden_size, I = c.intermediate_size;
+    const uint64_t qkv = mc.deltanet_qkv_dim(), vd = mc.deltanet_v_dim(), nv = mc.num_v_heads;
+    const uint64_t qd = mc.attn_q_dim(), kvd = mc.attn_kv_dim();
+    GpuModel g;
+    g.config = c;
+    for (const LayerView& l : m.layers) {
+        if (l.deltanet) {
+            const DeltaNetLayerView& d = l.dn;
+            GpuDeltaNetLayerWeights w;
+            w.in_proj_qkv = detail::upload_q4(ctx, d.in_proj_qkv, H, qkv, "in_proj_qkv");
+            w.in_proj_a = detail::upload_q4(ctx, d.in_proj_a, H, nv, "in_proj_a");
+            w.in_proj_b = detail::upload_q4(ctx, d.in_proj_b, H, nv, "in_proj_b");
+            w.in_proj_z = detail::upload_q4(ctx, d.in_proj_z, H, vd, "in_proj_z");
+            w.out_proj = detail::upload_q4(ctx, d.out_proj, vd, H, "out_proj");
+            w.mixer.conv1d_weight = detail::upload_array(ctx, d.conv1d_weight, qkv * mc.conv_kernel_size, "conv1d_weight");
+            w.mixer.a_log = detail::upload_array(ctx, d.a_log, nv, "a_log");
+            w.mixer.dt_bias = detail::upload_array(ctx, d.dt_bias, nv, "dt_bias");
+            w.mixer.attn_norm_weight = detail::upload_array(ctx, d.attn_norm_weight, mc.deltanet_head_dim, "attn_norm");
+            w.gate_proj = detail::upload_q4(ctx, d.gate_proj, H, I, "gate_proj");
+            w.up_proj = detail::upload_q4(ctx, d.up_proj, H, I, "up_proj");
+            w.down_proj = detail::upload_q4(ctx, d.down_proj, I, H, "down_proj");
+            w.input_norm = detail::upload_array(ctx, d.input_norm, H, "input_norm");
+            w.post_attn_norm = detail::upload_array(ctx, d.post_attn_norm, H, "post_attn_norm");
+            g.slot.push_back(g.dn.size());
+            g.dn.push_back(std::move(w));
+        } else {
+            const FullAttnLayerView& a = l.fa;
+            GpuFullAttnLayerWeights w;
+            w.q_proj = detail::upload_q4(ctx, a.q_proj, H, 2 * qd, "q_proj");
+            w.k_proj = detail::upload_q4(ctx, a.k_proj, H, kvd, "k_proj");
+            w.v_proj = detail::upload_q4(ctx, a.v_proj, H, kvd, "v_proj");
+            w.o_proj = detail::upload_q4(ctx, a.o_proj, qd, H, "o_proj");
+            w.mixer.q_norm = detail::upload_array(ctx, a.q_norm, mc.attn_head_dim, "q_norm");
+            w.mixer.k_norm = detail::upload_array(ctx, a.k_norm, mc.attn_head_dim, "k_norm");
+            w.gate_proj = detail::upload_q4(ctx, a.gate_proj, H, I, "gate_proj");
+            w.up_proj = detail::upload_q4(ctx, a.up_proj, H, I, "up_proj");
+            w.down_proj = detail::upload_q4(ctx, a.down_proj, I, H, "down_proj");
+            w.input_norm = detail::upload_array(ctx, a.input_norm, H, "input_norm");
+            w.post_attn_norm = detail::upload_array(ctx, a.post_attn_norm, H, "post_attn_norm");
+            g.slot.push_back(g.fa.size());
+            g.fa.push_back(std::move(w));
+        }
+    }
+    // the embedding is used as stored (vocab-major, tied to lm_head)
+    const WeightView& e = m.embed;
+    if (e.fmt != 1 || e.n != H || e.packed.len != e.k * H / 2 || e.scales.len != e.k * (H / 32))
+        throw MixerError(QM_ERR_SHAPE, "embed: a Q4 [vocab][hidden] weight is required");
+    g.embed.vocab = e.k;
+    g.embed.hidden = H;
+    g.embed.packed = detail::upload_array(ctx, e.packed, e.packed.len, "embed");
+    g.embed.scales = detail::upload_array(ctx, e.scales, e.scales.len, "embed scales");
+    g.final_norm = detail::upload_array(ctx, m.final_norm, H, "final_norm");
+    const uint64_t half = mc.rope_dim() / 2;
+    if (m.rope_cos.len % half != 0 || m.rope_sin.len != m.rope_cos.len)
+        throw MixerError(QM_ERR_SHAPE, "rope tables: not [positions][rope_dim / 2]");
+    g.rope_len = static_cast<int32_t>(m.rope_cos.len / half);
+    g.rope_cos = detail::upload_array(ctx, m.rope_cos, m.rope_cos.len, "rope_cos");
+    g.rope_sin = detail::upload_array(ctx, m.rope_sin, m.rope_sin.len, "rope_sin");
+    ctx.sync();
+    return g;
+}
+
+// HybridCache::new (gemv.rs:175-186): zero DeltaNet states, empty KV caches
+// of kv_capacity positions.
+struct GpuHybridCache {
+    std::vector<GpuDeltaNetState> dn;
+    std::vector<GpuKvCacheEntry> kv;
+
+    static GpuHybridCache create(Context& ctx, const GpuModel& m, std::size_t kv_capacity) {
+        const Qor4bConfig cfg = Qor4bConfig::default_4b();
+        GpuHybridCache c;
+        for (std::size_t i = 0; i < m.dn.size(); ++i) c.dn.push_back(GpuDeltaNetState::zeros(ctx, cfg));
+        for (std::size_t i = 0; i < m.fa.size(); ++i)
+            c.kv.push_back(GpuKvCacheEntry::with_capacity(ctx, cfg, kv_capacity));
+        return c;
+    }
+};
+
+// Device buffers one decode step works in.
+struct DecodeScratch {
+    DeviceBuffer x, proj, a, b, z, k, v, mix, inter;
+
+    static DecodeScratch create(Context& ctx, const GpuModel& m) {
+        const Qor4bConfig cfg = Qor4bConfig::default_4b();
+        DecodeScratch s;
+        s.x = DeviceBuffer(ctx, m.config.hidden_size * 4);
+        s.proj = DeviceBuffer(ctx, std::max(cfg.deltanet_qkv_dim(), 2 * cfg.attn_q_dim()) * 4);
+        s.a = DeviceBuffer(ctx, 64 * 4);
+        s.b = DeviceBuffer(ctx, 64 * 4);
+        s.z = DeviceBuffer(ctx, cfg.deltanet_v_dim() * 4);
+        s.k = DeviceBuffer(ctx, cfg.attn_kv_dim() * 4);
+        s.v = DeviceBuffer(ctx, cfg.attn_kv_dim() * 4);
+        s.mix = DeviceBuffer(ctx, std::max(cfg.deltanet_v_dim(), cfg.attn_q_dim()) * 4);
+        s.inter = DeviceBuffer(ctx, m.config.intermediate_size * 4);
+        return s;
+    }
+};
+
+// forward_decode (gemv.rs:1059-1077): logits [vocab] for the token whose id
+// is at token_dev (device int32), with every layer's state / KV cache
+// advanced by one position.
+inline void forward_decode_gpu(Context& ctx, const GpuModel& m, GpuHybridCache& cache, DecodeScratch& s,
+                               const int32_t* token_dev, float* logits_dev, qm_stream stream = nullptr) {
+    const Qor4bConfig cfg = Qor4bConfig::default_4b();
+    const int32_t H = static_cast<int32_t>(m.config.hidden_size);
+    const int32_t V = static_cast<int32_t>(m.embed.vocab);
+    float* x = s.x.as<float>();
+    ctx.check(qm_q4_embed(ctx.get(), stream, 1, V, H, token_dev, m.embed.packed.as<uint8_t>(),
+                          m.embed.scales.as<uint16_t>(), x));
+    std::size_t di = 0, ai = 0;
+    for (std::size_t i = 0; i < m.slot.size(); ++i) {
+        if (m.config.layer_types[i] == 0) {
+            // forward_deltanet_decode, gemv.rs:719-900
+            const GpuDeltaNetLayerWeights& w = m.dn[m.slot[i]];
+            rms_norm_gemv_gpu(ctx, x, w.input_norm.as<uint16_t>(),
+                              {{&w.in_proj_qkv, s.proj.as<float>()}, {&w.in_proj_z, s.z.as<float>()},
+                               {&w.in_proj_a, s.a.as<float>()}, {&w.in_proj_b, s.b.as<float>()}},
+                              stream);
+            forward_deltanet_decode_gpu(ctx, s.proj.as<float>(), s.a.as<float>(), s.b.as<float>(), s.z.as<float>(),
+                                        w.mixer, cache.dn[di++], cfg, s.mix.as<float>(), stream);
+            gemv_residual_gpu(ctx, s.mix.as<float>(), w.out_proj, x, stream);
+            rms_norm_fused_gate_up_gpu(ctx, x, w.post_attn_norm.as<uint16_t>(), w.gate_proj, w.up_proj,
+                                       s.inter.as<float>(), stream);
+            gemv_residual_gpu(ctx, s.inter.as<float>(), w.down_proj, x, stream);
+        } else {
+            // forward_attn_decode, gemv.rs:907-1025
+            const GpuFullAttnLayerWeights& w = m.fa[m.slot[i]];
+            rms_norm_gemv_gpu(ctx, x, w.input_norm.as<uint16_t>(),
+                              {{&w.q_proj, s.proj.as<float>()}, {&w.k_proj, s.k.as<float>()},
+                               {&w.v_proj, s.v.as<float>()}},
+                              stream);
+            forward_attn_decode_gpu(ctx, s.proj.as<float>(), s.k.as<float>(), s.v.as<float>(), w.mixer,
+                                    cache.kv[ai++], cfg, m.rope_cos.as<float>(), m.rope_sin.as<float>(),
+                                    m.rope_len, s.mix.as<float>(), stream);
+            gemv_residual_gpu(ctx, s.mix.as<float>(), w.o_proj, x, stream);
+            rms_norm_fused_gate_up_gpu(ctx, x, w.post_attn_norm.as<uint16_t>(), w.gate_proj, w.up_proj,
+                                       s.inter.as<float>(), stream);
+            gemv_residual_gpu(ctx, s.inter.as<float>(), w.down_proj, x, stream);
+        }
+    }
+    ctx.check(qm_q4_lm_head(ctx.get(), stream, V, H, x, m.final_norm.as<uint16_t>(), m.embed.packed.as<uint8_t>(),
+                            m.embed.scales.as<uint16_t>(), logits_dev));
+}
+
+}  // namespace qor4b

@@ -4,12 +4,16 @@
 // from prefill into decode as generate.rs does (prefill at :243, decode
 // loop at :126).  Every output is checked against the CPU oracle
 // (test infrastructure, linked only here).  Exit status 0 = all checks pass.
-#include "qor4b_mixer.hpp"
+#include "qor4b_model.hpp"
+#include "qor4b_writer.hpp"
 #include "qora_oracle.h"
 
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <string>
+#include <unistd.h>
 #include <vector>
 
 using namespace qor4b;
@@ -278,6 +282,186 @@ void q4_layer_flow(Context& ctx) {
     expect(e <= 1e-5, "q4 down_proj + residual (rel)", e, 1e-5);
 }
 
+// A two-layer model of the 4B's shapes (one DeltaNet layer, one attention
+// layer, a 4096-token vocabulary) written as a .qor4b file, loaded onto the
+// device (load_gpu_model) and decoded for a few tokens with forward_decode_gpu
+// and greedy qm_sample, the sampled id feeding the next step on the device.
+// Each step's logits are checked against the oracle's forward_decode
+// (gemv.rs:1059-1077) composed from its restatements.
+void model_flow(Context& ctx, const Qor4bConfig& cfg) {
+    using namespace qor4b_test;
+    Rng r(31);
+    const uint32_t H = 2560, I = 9216, V = 4096;
+    auto q4w = [&](uint64_t k, uint64_t n) {
+        W w;
+        w.k = k;
+        w.n = n;
+        w.packed.resize(k * n / 2);
+        w.scales.resize(k * (n / 32));
+        for (std::size_t i = 0; i < w.packed.size(); i += 8) {
+            const uint64_t b = r.next();
+            std::memcpy(&w.packed[i], &b, std::min<std::size_t>(8, w.packed.size() - i));
+        }
+        for (auto& x : w.scales) x = or_f32_to_f16(0.006f * (1.0f + 0.2f * r.normal()));
+        return w;
+    };
+    auto f16v = [&](std::size_t n, float mean, float sd) {
+        std::vector<uint16_t> v(n);
+        for (auto& x : v) x = or_f32_to_f16(mean + sd * r.normal());
+        return v;
+    };
+    Model m;
+    m.vocab = V;
+    m.hidden = H;
+    m.intermediate = I;
+    m.layer_types = {0, 1};
+    DnLayer d;
+    d.in_proj_qkv = q4w(H, cfg.deltanet_qkv_dim());
+    d.in_proj_a = q4w(H, cfg.num_v_heads);
+    d.in_proj_b = q4w(H, cfg.num_v_heads);
+    d.in_proj_z = q4w(H, cfg.deltanet_v_dim());
+    d.out_proj = q4w(cfg.deltanet_v_dim(), H);
+    d.conv1d_weight = normals(r, cfg.deltanet_qkv_dim() * 4, 0.5f);
+    d.a_log.resize(cfg.num_v_heads);
+    for (auto& x : d.a_log) x = std::log(0.01f + 0.09f * (float)r.uniform());
+    d.dt_bias.assign(cfg.num_v_heads, 0.0f);
+    d.attn_norm_weight = f16v(cfg.deltanet_head_dim, 1.0f, 0.1f);
+    d.gate_proj = q4w(H, I);
+    d.up_proj = q4w(H, I);
+    d.down_proj = q4w(I, H);
+    d.input_norm = f16v(H, 0.0f, 0.1f);
+    d.post_attn_norm = f16v(H, 0.0f, 0.1f);
+    m.dn.push_back(std::move(d));
+    FaLayer a;
+    a.q_proj = q4w(H, 2 * cfg.attn_q_dim());
+    a.k_proj = q4w(H, cfg.attn_kv_dim());
+    a.v_proj = q4w(H, cfg.attn_kv_dim());
+    a.o_proj = q4w(cfg.attn_q_dim(), H);
+    a.q_norm = f16v(cfg.attn_head_dim, 0.0f, 0.1f);
+    a.k_norm = f16v(cfg.attn_head_dim, 0.0f, 0.1f);
+    a.gate_proj = q4w(H, I);
+    a.up_proj = q4w(H, I);
+    a.down_proj = q4w(I, H);
+    a.input_norm = f16v(H, 0.0f, 0.1f);
+    a.post_attn_norm = f16v(H, 0.0f, 0.1f);
+    m.fa.push_back(std::move(a));
+    m.embed = q4w(V, H);
+    for (auto& x : m.embed.scales) x = or_f32_to_f16(0.02f * (1.0f + 0.2f * r.normal()));
+    m.final_norm = f16v(H, 0.0f, 0.1f);
+    const int32_t rope_len = 8192, half = (int32_t)cfg.rope_dim() / 2;
+    m.rope_cos.resize((std::size_t)rope_len * half);
+    m.rope_sin.resize((std::size_t)rope_len * half);
+    or_rope_table(m.rope_theta, (int32_t)cfg.rope_dim(), rope_len, m.rope_cos.data(), m.rope_sin.data());
+
+    const char* tmp = std::getenv("TMPDIR");
+    std::string path = std::string(tmp && *tmp ? tmp : "/tmp") + "/qor4b_model_flow_XXXXXX";
+    std::vector<char> pbuf(path.begin(), path.end());
+    pbuf.push_back('\0');
+    const int fd = mkstemp(pbuf.data());
+    if (fd < 0) throw std::runtime_error("model_flow: no temporary file");
+    close(fd);
+    path = pbuf.data();
+    const bool written = write_file(path, serialize(m));
+    expect(written, "model file written (failed = 1)", written ? 0 : 1, 0.5);
+    GpuModel gm;
+    {
+        MappedFile f(path);
+        gm = load_gpu_model(ctx, parse_qor4b(f.data(), f.size()));
+    }
+    unlink(path.c_str());
+    GpuHybridCache cache = GpuHybridCache::create(ctx, gm, 64);
+    DecodeScratch scratch = DecodeScratch::create(ctx, gm);
+    DeviceBuffer tok(ctx, 16), logits(ctx, V * 4);
+    const int32_t first = 1234;
+    tok.upload(&first, 4);
+
+    // the oracle's forward_decode over the same weights
+    const or_config oc = oracle_cfg(cfg);
+    const DnLayer& od = m.dn[0];
+    const FaLayer& oa = m.fa[0];
+    std::vector<float> S(cfg.num_v_heads * cfg.deltanet_head_dim * cfg.deltanet_head_dim, 0.0f);
+    std::vector<float> buf(cfg.deltanet_qkv_dim() * 3, 0.0f);
+    std::vector<float> Kc, Vc;
+    auto gemv = [](const std::vector<float>& x, const W& w) {
+        std::vector<float> y(w.n);
+        or_q4_gemv(x.data(), w.packed.data(), w.scales.data(), (int32_t)w.k, (int32_t)w.n, y.data());
+        return y;
+    };
+    auto rms = [](const std::vector<float>& x, const std::vector<uint16_t>& g) {
+        std::vector<float> y(x.size());
+        or_rms_norm(x.data(), (int32_t)x.size(), g.data(), y.data());
+        return y;
+    };
+    auto mlp = [&](std::vector<float>& x, const std::vector<uint16_t>& norm, const W& g, const W& u, const W& dw) {
+        const std::vector<float> xn = rms(x, norm);
+        std::vector<float> inter(I);
+        or_q4_gate_up(xn.data(), g.packed.data(), g.scales.data(), u.packed.data(), u.scales.data(), (int32_t)H,
+                      (int32_t)I, inter.data());
+        const std::vector<float> y = gemv(inter, dw);
+        for (uint32_t j = 0; j < H; ++j) x[j] += y[j];
+    };
+    double worst = 0;
+    int32_t id = first;
+    bool greedy_ok = true;
+    const int steps = 4;
+    for (int step = 0; step < steps; ++step) {
+        forward_decode_gpu(ctx, gm, cache, scratch, tok.as<int32_t>(), logits.as<float>());
+        std::vector<float> got(V);
+        logits.download(got.data(), V * 4);
+
+        std::vector<float> x(H);
+        or_q4_embed(m.embed.packed.data(), m.embed.scales.data(), (int32_t)H, id, x.data());
+        {   // forward_deltanet_decode
+            const std::vector<float> xn = rms(x, od.input_norm);
+            const std::vector<float> qkv = gemv(xn, od.in_proj_qkv), av = gemv(xn, od.in_proj_a),
+                                     bv = gemv(xn, od.in_proj_b), zv = gemv(xn, od.in_proj_z);
+            std::vector<float> out(cfg.deltanet_v_dim());
+            or_deltanet_decode_step(&oc, qkv.data(), 1, buf.data(), od.conv1d_weight.data(), av.data(), bv.data(),
+                                    od.a_log.data(), od.dt_bias.data(), zv.data(), od.attn_norm_weight.data(),
+                                    S.data(), out.data(), OR_UPDATE_AUTO);
+            const std::vector<float> h = gemv(out, od.out_proj);
+            for (uint32_t j = 0; j < H; ++j) x[j] += h[j];
+            mlp(x, od.post_attn_norm, od.gate_proj, od.up_proj, od.down_proj);
+        }
+        {   // forward_attn_decode
+            const std::vector<float> xn = rms(x, oa.input_norm);
+            const std::vector<float> qg = gemv(xn, oa.q_proj), kn = gemv(xn, oa.k_proj), vn = gemv(xn, oa.v_proj);
+            Kc.resize((std::size_t)(step + 1) * cfg.attn_kv_dim());
+            Vc.resize((std::size_t)(step + 1) * cfg.attn_kv_dim());
+            std::vector<float> out(cfg.attn_q_dim());
+            or_attn_decode_step(&oc, qg.data(), kn.data(), vn.data(), oa.q_norm.data(), oa.k_norm.data(),
+                                m.rope_cos.data(), m.rope_sin.data(), rope_len, Kc.data(), Vc.data(), step, 1,
+                                out.data(), 4);
+            const std::vector<float> h = gemv(out, oa.o_proj);
+            for (uint32_t j = 0; j < H; ++j) x[j] += h[j];
+            mlp(x, oa.post_attn_norm, oa.gate_proj, oa.up_proj, oa.down_proj);
+        }
+        const std::vector<float> xf = rms(x, m.final_norm);
+        std::vector<float> ref(V);
+        or_q4_lm_head(xf.data(), m.embed.packed.data(), m.embed.scales.data(), (int32_t)V, (int32_t)H, ref.data(), 4);
+        worst = std::fmax(worst, rel_err(got.data(), ref.data(), V));
+
+        // greedy next token on the device, fed back through tok
+        qm_sample_params sp{0.0f, 1.0f, 1, 1.0f, 0.0f, -1, 0};
+        ctx.check(qm_sample(ctx.get(), nullptr, (int32_t)V, logits.as<float>(), nullptr, 0, &sp, nullptr,
+                            tok.as<int32_t>(), nullptr, nullptr));
+        int32_t next = 0;
+        tok.download(&next, 4);
+        std::size_t best = 0, second = 1;
+        if (ref[second] > ref[best]) std::swap(best, second);
+        for (std::size_t i = 2; i < V; ++i) {
+            if (ref[i] > ref[best]) { second = best; best = i; }
+            else if (ref[i] > ref[second]) second = i;
+        }
+        if (ref[best] - ref[second] > 1e-3 * std::fabs(ref[best]) && (std::size_t)next != best) greedy_ok = false;
+        id = next;
+    }
+    expect(worst <= 2e-3, "qor4b file -> device model, 4 decode steps: logits rel", worst, 2e-3);
+    expect(greedy_ok, "greedy qm_sample = oracle argmax (mismatch = 1)", greedy_ok ? 0 : 1, 0.5);
+    expect(cache.kv[0].seq_len == (std::size_t)steps && cache.dn[0].conv_pos == (std::size_t)steps,
+           "cache positions advanced (error = 1)", 0, 0.5);
+}
+
 }  // namespace
 
 int main() {
@@ -287,6 +471,7 @@ int main() {
         deltanet_flow(ctx, cfg);
         attention_flow(ctx, cfg);
         q4_layer_flow(ctx);
+        model_flow(ctx, cfg);
     } catch (const std::exception& e) {
         std::printf("exception: %s\n", e.what());
         return 2;
