@@ -637,6 +637,140 @@ def run_lm_head(args, ctx):
 
 
 SAMPLE_GEN = 1000
+MODEL_POS = 4096          # decode position of the whole-model step
+FA_LAYER_PROJ = {"q_proj": (2560, 8192), "k_proj": (2560, 1024), "v_proj": (2560, 1024), "o_proj": (4096, 2560),
+                 "gate_proj": (2560, 9216), "up_proj": (2560, 9216), "down_proj": (9216, 2560)}
+
+
+def run_decode_model(args, ctx):
+    """One decode token through the whole 4B model at batch 1, position 4096:
+    embedding row, 24 DeltaNet and 8 GQA layers (input RMSNorm + projections,
+    mixer, out/o_proj residual, RMSNorm + gate/up MLP, down residual), final
+    RMSNorm + lm_head over 248,320 rows, and top-k sampling whose token feeds
+    the next step's embedding on the device (forward_decode, gemv.rs:1059-1077,
+    then sample_token_top_k).  Random weights of the real shapes (2.3 GB
+    resident), captured once as a HIP graph and replayed."""
+    K, Wm = args.steps, args.warmup
+    seed = [7000]
+    V, H, P = LM_VOCAB, LM_HIDDEN, MODEL_POS
+    cap = P + 1
+
+    def fill(buf, dtype, count, std, mean=0.0):
+        ctx.fill_normal(buf, dtype, count, mean, std, seed[0])
+        seed[0] += 1
+
+    def weight(k, n):
+        codes = ctx.alloc(k * n // 2)
+        fill(codes, M.QM_F16, k * n // 4, 1.0)
+        gscales = ctx.alloc(max(16, k * (n // 32) * 2))
+        fill(gscales, M.QM_F16, k * (n // 32), 0.0012, 0.006)
+        return codes, gscales
+
+    def f16vec(n, mean, std):
+        b = ctx.alloc(max(16, n * 2))
+        fill(b, M.QM_F16, n, std, mean)
+        return b
+
+    rng = np.random.default_rng(8)
+    layers = []
+    for layer in range(32):
+        if layer % 4 != 3:
+            p = W.dn_params(rng)
+            L = {"dn": True, **{nm: weight(*W.Q4_PROJ_SHAPES[nm]) for nm in Q4_LAYER_PROJ},
+                 "conv_w": ctx.upload(p["conv_w"]), "a_log": ctx.upload(p["a_log"]),
+                 "dt_bias": ctx.upload(p["dt_bias"]), "attn_norm": ctx.upload(p["norm_w"]),
+                 "state": ctx.alloc(32 * 128 * 128 * 4), "conv_buf": ctx.alloc(8192 * 3 * 4)}
+            fill(L["state"], M.QM_F32, 32 * 128 * 128, 0.02)
+            fill(L["conv_buf"], M.QM_F32, 8192 * 3, 1.0)
+        else:
+            L = {"dn": False, **{nm: weight(*sh) for nm, sh in FA_LAYER_PROJ.items()},
+                 "q_norm": f16vec(256, 0.0, 0.1), "k_norm": f16vec(256, 0.0, 0.1),
+                 "kc": ctx.alloc(4 * cap * 256 * 2), "vc": ctx.alloc(4 * cap * 256 * 2)}
+            fill(L["kc"], M.QM_F16, 4 * cap * 256, 1.0)
+            fill(L["vc"], M.QM_F16, 4 * cap * 256, 1.0)
+        L["in_norm"], L["post_norm"] = f16vec(H, 0.0, 0.1), f16vec(H, 0.0, 0.1)
+        layers.append(L)
+    emb_codes = ctx.alloc(V * H // 2)
+    fill(emb_codes, M.QM_F16, V * H // 4, 1.0)
+    emb_scales = ctx.alloc(V * (H // 32) * 2)
+    fill(emb_scales, M.QM_F16, V * (H // 32), 0.004, 0.02)
+    final_norm = f16vec(H, 0.0, 0.1)
+    cos, sin = M.rope_table(cap + 1)
+    rc, rs = ctx.upload(cos), ctx.upload(sin)
+    tok = ctx.upload(np.array([1234, 0, 0, 0], np.int32))
+    rng_state = ctx.upload(np.array([0x9E3779B97F4A7C15], np.uint64))
+    x, proj, z = ctx.alloc(H * 4), ctx.alloc(8192 * 4), ctx.alloc(4096 * 4)
+    a, b, kn, vn = ctx.alloc(32 * 4), ctx.alloc(32 * 4), ctx.alloc(1024 * 4), ctx.alloc(1024 * 4)
+    mix, inter, logits = ctx.alloc(4096 * 4), ctx.alloc(9216 * 4), ctx.alloc(V * 4)
+    ctx.reserve(max_batch=1, max_kv_len=cap)
+    ctx.sync()
+
+    def step():
+        ctx.q4_embed(1, V, H, tok, emb_codes, emb_scales, x)
+        for L in layers:
+            if L["dn"]:
+                ctx.q4_gemv_multi(H, x, [(8192, *L["in_proj_qkv"], proj), (4096, *L["in_proj_z"], z),
+                                         (32, *L["in_proj_a"], a), (32, *L["in_proj_b"], b)], norm_w=L["in_norm"])
+                ctx.deltanet_decode(1, M.QM_DN_PREACT, proj, L["conv_buf"], L["conv_w"], a, b, L["a_log"],
+                                    L["dt_bias"], z, L["attn_norm"], L["state"], mix)
+                ctx.q4_gemv_multi(4096, mix, [(H, *L["out_proj"], x, x)])
+            else:
+                ctx.q4_gemv_multi(H, x, [(8192, *L["q_proj"], proj), (1024, *L["k_proj"], kn),
+                                         (1024, *L["v_proj"], vn)], norm_w=L["in_norm"])
+                ctx.gqa_decode(1, proj, kn, vn, L["q_norm"], L["k_norm"], rc, rs, cap + 1, None, P,
+                               L["kc"], L["vc"], cap, mix)
+                ctx.q4_gemv_multi(4096, mix, [(H, *L["o_proj"], x, x)])
+            ctx.q4_gate_up(H, 9216, x, L["post_norm"], *L["gate_proj"], *L["up_proj"], inter)
+            ctx.q4_gemv_multi(9216, inter, [(H, *L["down_proj"], x, x)])
+        ctx.q4_lm_head(V, H, x, final_norm, emb_codes, emb_scales, logits)
+        ctx.sample(V, logits, None, 0, rng_state, tok, temperature=1.0, top_p=0.95, top_k=20)
+
+    for _ in range(Wm):
+        step()
+    ctx.sync()
+    t0, t1 = ctx.event(), ctx.event()
+    wall0 = time.perf_counter()
+    t0.record()
+    for _ in range(K):
+        step()
+    t1.record()
+    ctx.sync()
+    eager_ms = t0.elapsed_ms(t1) / K
+    total_ms, wall = t0.elapsed_ms(t1), time.perf_counter() - wall0
+    graph_ms = float("nan")
+    if not args.no_graph:
+        ctx.graph_begin()
+        step()
+        g = ctx.graph_end()
+        g.launch()
+        ctx.sync()
+        g0, g1 = ctx.event(), ctx.event()
+        wall0 = time.perf_counter()
+        g0.record()
+        for _ in range(K):
+            g.launch()
+        g1.record()
+        ctx.sync()
+        wall = time.perf_counter() - wall0
+        total_ms = g0.elapsed_ms(g1)
+        graph_ms = total_ms / K
+    wbytes = (24 * sum(q4_weight_bytes(*W.Q4_PROJ_SHAPES[nm]) for nm in Q4_LAYER_PROJ)
+              + 8 * sum(q4_weight_bytes(*sh) for sh in FA_LAYER_PROJ.values()))
+    nbytes = (wbytes + lm_head_bytes() + 24 * 2 * 32 * 128 * 128 * 4    # weights, lm_head, state read + write
+              + 8 * 2 * 4 * cap * 256 * 2)                              # K and V read
+    ms = total_ms / K
+    return {
+        "tokens": K, "total_ms": total_ms, "wall_s": wall,
+        "dominant": "whole decode step (embedding, 32 layers, lm_head, sampling)" +
+                    (" as one HIP graph" if not args.no_graph else ", eager"),
+        "roofline": {"bound": "hbm", "achieved": nbytes / (ms * 1e-3), "peak": HBM_PEAK,
+                     "kernel_ms": ms, "bytes_per_launch": nbytes},
+        "eager_ms_per_step": eager_ms, "graph_ms_per_step": graph_ms,
+        "config": {"workload": "whole-model decode, batch 1, position 4096: embedding, 24 DeltaNet + 8 GQA layers "
+                               "with Q4 projections and MLPs, final RMSNorm + lm_head (248320 x 2560), top-k 20 "
+                               "sampling feeding the next token on the device",
+                   "batch": 1, "seq_len": P, "global_batch": 1, "parallelism": "single GPU"},
+    }
 
 
 def run_sample(args, ctx):
@@ -772,6 +906,50 @@ def cpu_baseline(workload: str) -> dict:
         return {"value": 8 * n / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
                 "sample": f"{n} calls of gemm_q4 on 8 rows (scalar gemv_q4_inner restatement, one thread, "
                           f"{dt:.1f} s)"}
+    if workload == "decode_model":
+        # one DeltaNet and one GQA layer (projections, mixer, MLP) and the
+        # lm_head, timed separately; tokens/s = 1 / (24 t_dn + 8 t_gqa + t_head)
+        rng = np.random.default_rng(12)
+        dw = {nm: W.q4_random_weight(*W.Q4_PROJ_SHAPES[nm], rng) for nm in Q4_LAYER_PROJ}
+        fw = {nm: W.q4_random_weight(*sh, rng) for nm, sh in FA_LAYER_PROJ.items()}
+        p = W.dn_params(rng)
+        gam = W.f16_bits(0.1 * rng.standard_normal(2560, dtype=np.float32))
+        qn = W.f16_bits(0.1 * rng.standard_normal(256, dtype=np.float32))
+        x = rng.standard_normal(2560, dtype=np.float32)
+        S = 0.02 * rng.standard_normal((32, 128, 128), dtype=np.float32)
+        cbuf = rng.standard_normal((8192, 3), dtype=np.float32)
+        cos, sin = O.rope_table(MODEL_POS + 1)
+        Kc = W.f16_value(W.f16_bits(rng.standard_normal((MODEL_POS + 1, 4, 256), dtype=np.float32)))
+        Vc = W.f16_value(W.f16_bits(rng.standard_normal((MODEL_POS + 1, 4, 256), dtype=np.float32)))
+
+        def mlp(h):
+            inter = O.q4_gate_up(O.rms_norm(h, gam), *dw["gate_proj"], *dw["up_proj"])
+            return h + O.q4_gemv(inter, *dw["down_proj"])
+
+        def dn_layer():
+            xn = O.rms_norm(x, gam)
+            qkv, z = O.q4_gemv(xn, *dw["in_proj_qkv"]), O.q4_gemv(xn, *dw["in_proj_z"])
+            av, bv = O.q4_gemv(xn, *dw["in_proj_a"]), O.q4_gemv(xn, *dw["in_proj_b"])
+            out = O.deltanet_decode_step(cfg, qkv, av, bv, z, p["conv_w"], p["a_log"], p["dt_bias"], p["norm_w"],
+                                         S, conv_buf=cbuf, preact=True)
+            return mlp(x + O.q4_gemv(out, *dw["out_proj"]))
+
+        def gqa_layer():
+            xn = O.rms_norm(x, gam)
+            qg, kk, vv = (O.q4_gemv(xn, *fw[nm]) for nm in ("q_proj", "k_proj", "v_proj"))
+            out = O.attn_decode_step(cfg, qg, kk, vv, qn, qn, cos, sin, Kc, Vc, MODEL_POS, nthreads=att_threads)
+            return mlp(x + O.q4_gemv(out, *fw["o_proj"]))
+
+        ep, es = W.q4_random_weight(LM_VOCAB, LM_HIDDEN, rng, scale=0.02)
+        n1, t_dn = _repeat_for(dn_layer, min_s=4.0)
+        n2, t_fa = _repeat_for(gqa_layer, min_s=4.0)
+        n3, t_hd = _repeat_for(lambda: O.q4_lm_head(O.rms_norm(x, gam), ep, es, nthreads=att_threads), min_s=2.0)
+        per_token = 24 * t_dn / n1 + 8 * t_fa / n2 + t_hd / n3
+        return {"value": 1.0 / per_token, "unit": "tokens/s", "cores": att_threads, "kind": "port",
+                "sample": f"{n1} DeltaNet layers, {n2} GQA layers (position 4096, heads over {att_threads} "
+                          f"threads) and {n3} lm_heads timed separately (projections by the scalar gemv_q4_inner "
+                          f"restatement, one thread); tokens/s = 1 / (24 t_dn + 8 t_gqa + t_head); "
+                          f"{per_token:.2f} s per token"}
     if workload == "sample":
         rng = np.random.default_rng(11)
         x = (3.0 * rng.standard_normal(LM_VOCAB)).astype(np.float32)
@@ -851,7 +1029,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="stack",
                     choices=["stack", "dn_decode", "gqa_decode", "dn_prefill", "gqa_prefill", "q4_proj",
-                             "q4_gemm", "lm_head", "sample"])
+                             "q4_gemm", "lm_head", "sample", "decode_model"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
                     help="skip the graph-replayed timing (rocprofv3's kernel tracer crashes in "
@@ -868,7 +1046,7 @@ def main():
         sys.exit(2)
     defaults = {"stack": (32, 4), "dn_decode": (256, 16), "gqa_decode": (200, 20),
                 "dn_prefill": (20, 3), "gqa_prefill": (10, 2), "q4_proj": (50, 5), "q4_gemm": (20, 3),
-                "lm_head": (100, 10), "sample": (200, 10)}[args.workload]
+                "lm_head": (100, 10), "sample": (200, 10), "decode_model": (30, 3)}[args.workload]
     args.steps = args.steps or defaults[0]
     args.warmup = defaults[1] if args.warmup is None else args.warmup
 
@@ -885,7 +1063,7 @@ def main():
     run = {"stack": run_stack, "dn_decode": run_dn_decode, "gqa_decode": run_gqa_decode,
            "dn_prefill": run_dn_prefill, "gqa_prefill": run_gqa_prefill,
            "q4_proj": run_q4_proj, "q4_gemm": run_q4_gemm, "lm_head": run_lm_head,
-           "sample": run_sample}[args.workload]
+           "sample": run_sample, "decode_model": run_decode_model}[args.workload]
     r = run(args, ctx)
     ctx.sync()
     ctx.close()
@@ -909,7 +1087,8 @@ def main():
                    "q4_proj": "Q4 projection tokens/s (decode) on 1x MI355X",
                    "q4_gemm": "Q4 projection tokens/s (prefill) on 1x MI355X",
                    "lm_head": "lm_head tokens/s (decode) on 1x MI355X",
-                   "sample": "sampled tokens/s (decode) on 1x MI355X"}.get(
+                   "sample": "sampled tokens/s (decode) on 1x MI355X",
+                   "decode_model": "whole-model decode tokens/s (batch 1) on 1x MI355X"}.get(
                        args.workload, "mixer tokens/s (decode) on 1x MI355X"),
         "value": value, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": r["total_ms"] / args.steps,
@@ -917,7 +1096,7 @@ def main():
         "dtype": {"dn_prefill": "bf16", "gqa_prefill": "bf16", "q4_gemm": "f16"}.get(args.workload, "f32"),
         "data": ("synthetic (seeded normal logits, random generated ids)" if args.workload == "sample" else
                  "synthetic (seeded random Q4 codes, f16 scales and normal inputs)"
-                 if args.workload.startswith("q4") or args.workload == "lm_head"
+                 if args.workload.startswith("q4") or args.workload in ("lm_head", "decode_model")
                  else "synthetic (seeded normal inputs, random-init state and f16 KV cache)"),
         "config": r["config"],
         "roofline": rl,
@@ -926,7 +1105,7 @@ def main():
         tf = ROOT / "profiles" / "traffic_stack_gqa_decode.json"
         if tf.exists():   # measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (see the profile summary)
             line["roofline"]["traffic"] = json.loads(tf.read_text())["traffic_bytes_per_launch"]
-    for k in ("kernels", "step_frac_hbm", "graph_ms_per_step", "graph_step_frac_hbm"):
+    for k in ("kernels", "step_frac_hbm", "graph_ms_per_step", "graph_step_frac_hbm", "eager_ms_per_step"):
         if k in r:
             line[k] = r[k]
     if not args.no_cpu_baseline:
