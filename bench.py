@@ -709,9 +709,11 @@ def run_decode_model(args, ctx):
         ctx.q4_embed(1, V, H, tok, emb_codes, emb_scales, x)
         for L in layers:
             if L["dn"]:
+                # the conv1d step + SiLU ride on the in_proj_qkv launch
                 ctx.q4_gemv_multi(H, x, [(8192, *L["in_proj_qkv"], proj), (4096, *L["in_proj_z"], z),
-                                         (32, *L["in_proj_a"], a), (32, *L["in_proj_b"], b)], norm_w=L["in_norm"])
-                ctx.deltanet_decode(1, M.QM_DN_PREACT, proj, L["conv_buf"], L["conv_w"], a, b, L["a_log"],
+                                         (32, *L["in_proj_a"], a), (32, *L["in_proj_b"], b)], norm_w=L["in_norm"],
+                                  conv_buf=L["conv_buf"], conv_w=L["conv_w"])
+                ctx.deltanet_decode(1, M.QM_DN_POSTACT, proj, None, None, a, b, L["a_log"],
                                     L["dt_bias"], z, L["attn_norm"], L["state"], mix)
                 ctx.q4_gemv_multi(4096, mix, [(H, *L["out_proj"], x, x)])
             else:

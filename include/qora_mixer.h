@@ -296,6 +296,18 @@ int32_t qm_q4_gemv_multi(qm_context* ctx, qm_stream stream, int32_t k,
                          const float* x_dev, const uint16_t* norm_w_dev,
                          int32_t count, const qm_q4_out* outs);
 
+/* qm_q4_gemv_multi with the DeltaNet decode's conv1d step + SiLU fused
+ * onto outs[0], the in_proj_qkv output (gemv.rs:744-772): y_0 =
+ * silu(sum_{j<3} buf[c][j] w[c][j] + v w[c][3]) with v = (x W_0)[c], and
+ * the buffer shifted in place (buf[c] <- {buf[c][1], buf[c][2], v}).
+ * conv_buf_dev f32 [n_0][3] (oldest .. newest), conv_w_dev f32 [n_0][4];
+ * outs[0] takes no residual.  qm_deltanet_decode then runs with
+ * QM_DN_POSTACT (conv skipped), one launch fewer per layer than
+ * QM_DN_PREACT. */
+int32_t qm_q4_gemv_multi_conv(qm_context* ctx, qm_stream stream, int32_t k, const float* x_dev,
+                              const uint16_t* norm_w_dev, int32_t count, const qm_q4_out* outs,
+                              float* conv_buf_dev, const float* conv_w_dev);
+
 /* The MLP's first half: out = silu(xn Wg) * (xn Wu) with xn = x, or
  * rms_norm(x, norm_w) when norm_w_dev is not NULL (replaces rms_norm +
  * fused_gate_up_q4, gemv.rs:893-894 and :469-526).  Both weights k x n,

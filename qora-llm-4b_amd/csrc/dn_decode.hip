@@ -31,13 +31,7 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_conv_silu(DnConvArgs A) 
     const float4 w = ld4(A.conv_w + ch * 4);
     const float x = A.qkv[idx];
     const float b0 = buf[0], b1 = buf[1], b2 = buf[2];
-    // Same operation order as the reference, without FMA contraction.
-    float s = 0.0f;
-    s = __fadd_rn(s, __fmul_rn(b0, w.x));
-    s = __fadd_rn(s, __fmul_rn(b1, w.y));
-    s = __fadd_rn(s, __fmul_rn(b2, w.z));
-    s = __fadd_rn(s, __fmul_rn(x, w.w));
-    A.act[idx] = silu_f(s);
+    A.act[idx] = silu_f(conv_taps4(b0, b1, b2, x, w));
     buf[0] = b1;
     buf[1] = b2;
     buf[2] = x;

@@ -23,7 +23,9 @@
 //   - y <- residual + x W (the residual adds after out_proj / o_proj and
 //     down_proj, gemv.rs:889-890,896);
 //   - qm_q4_gate_up: silu(x Wg) * (x Wu) for one tile of both weights per
-//     workgroup (fused_gate_up_q4, gemv.rs:469-526).
+//     workgroup (fused_gate_up_q4, gemv.rs:469-526);
+//   - on the first weight, the DeltaNet conv1d step + SiLU (gemv.rs:744-772)
+//     of the in_proj_qkv output, with its conv buffer shifted in place.
 // One workgroup owns one column tile and all k rows, so the result needs
 // no second pass: lane t takes rows t, t + 512, ..., and loads its 8 rows'
 // codes, scales, x (and norm weights) before any arithmetic, at clamped
@@ -161,7 +163,21 @@ QM_DEV void q4_tile(const Q4GemvArgs& A, int p, int tile, float (*red)[17], floa
         if (tid < T) A.y[0][T * (size_t)tile + tid] = (y / (1.0f + expf(-y))) * u;
     } else if (tid < T) {
         const size_t c = T * (size_t)tile + tid;
-        A.y[p][c] = A.residual[p] ? A.residual[p][c] + y : y;
+        float v = A.residual[p] ? A.residual[p][c] + y : y;
+        if (p == 0 && A.conv_buf) {
+            // gemv.rs:744-772 on the in_proj_qkv output: causal depthwise
+            // conv over the buffer (oldest .. newest) and v, buffer shift,
+            // SiLU
+            float* buf = A.conv_buf + c * 3;
+            const float4 w = *reinterpret_cast<const float4*>(A.conv_w + c * 4);
+            const float b0 = buf[0], b1 = buf[1], b2 = buf[2];
+            const float s = conv_taps4(b0, b1, b2, v, w);
+            buf[0] = b1;
+            buf[1] = b2;
+            buf[2] = v;
+            v = silu_f(s);
+        }
+        A.y[p][c] = v;
     }
 }
 

@@ -78,6 +78,21 @@ QM_DEV uint16_t f32_to_bf16(float f) {   // round to nearest even
 
 // ---- scalar math (gemv.rs:631-659 semantics) -----------------------------
 QM_DEV float silu_f(float x) { return x / (1.0f + expf(-x)); }
+
+// The causal conv1d tap sum of gemv.rs:750-756 (and :1137-1142):
+// ((b0 w0 + b1 w1) + b2 w2) + x w3 from zero, every product and sum rounded
+// on its own as the reference's f32 arithmetic is.  The pragma is what keeps
+// the compiler from contracting the pairs into FMAs (the __fmul_rn /
+// __fadd_rn spellings do not).
+QM_DEV float conv_taps4(float b0, float b1, float b2, float x, float4 w) {
+#pragma clang fp contract(off)
+    float s = 0.0f;
+    s = s + b0 * w.x;
+    s = s + b1 * w.y;
+    s = s + b2 * w.z;
+    s = s + x * w.w;
+    return s;
+}
 // x * sigmoid(x) from v_exp_f32 (exp(-x) = 2^(-x log2 e)) and v_rcp_f32, a few
 // ulp from silu_f; for the prefill paths, whose bar is bf16-level.
 QM_DEV float silu_fast(float x) {

@@ -138,6 +138,8 @@ struct Q4GemvArgs {
     int32_t wstart[QM_Q4_MAX_OUT + 1];
     int32_t k;
     int32_t count;
+    float* conv_buf;                       // null, or f32 [n_0][3]: y_0 <- silu(conv1d(y_0)), buffer shifted
+    const float* conv_w;                   // f32 [n_0][4]
 };
 
 // Reference Q4Weight layout -> tile-major device layout.

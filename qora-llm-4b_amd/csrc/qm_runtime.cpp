@@ -721,8 +721,9 @@ int32_t qm_q4_repack(qm_context* c, qm_stream stream, int32_t k, int32_t n, cons
     return launch(c, c->f_q4_repack, grid, 256, ra, pick(c, stream), "qm_q4_repack");
 }
 
-int32_t qm_q4_gemv_multi(qm_context* c, qm_stream stream, int32_t k, const float* x, const uint16_t* norm_w,
-                         int32_t count, const qm_q4_out* outs) {
+namespace {
+int32_t q4_gemv_multi_impl(qm_context* c, qm_stream stream, int32_t k, const float* x, const uint16_t* norm_w,
+                           int32_t count, const qm_q4_out* outs, float* conv_buf, const float* conv_w) {
     if (!c) return QM_ERR_INVALID_ARG;
     if (count < 1 || count > QM_Q4_MAX_OUT || !outs || !x)
         return fail(c, QM_ERR_INVALID_ARG, "qm_q4_gemv_multi: %d outputs (1..%d) or null pointer", count,
@@ -753,8 +754,28 @@ int32_t qm_q4_gemv_multi(qm_context* c, qm_stream stream, int32_t k, const float
     }
     for (int32_t i = count; i < QM_Q4_MAX_OUT; ++i) qa.tile[i] = 16;
     for (int32_t i = count; i <= QM_Q4_MAX_OUT; ++i) qa.wstart[i] = tiles;
+    qa.conv_buf = conv_buf;
+    qa.conv_w = conv_w;
     return launch(c, c->f_q4_gemv, static_cast<uint32_t>(tiles), static_cast<uint32_t>(c->q4_threads), qa,
                   pick(c, stream), "qm_q4_gemv");
+}
+}  // namespace
+
+int32_t qm_q4_gemv_multi(qm_context* c, qm_stream stream, int32_t k, const float* x, const uint16_t* norm_w,
+                         int32_t count, const qm_q4_out* outs) {
+    return q4_gemv_multi_impl(c, stream, k, x, norm_w, count, outs, nullptr, nullptr);
+}
+
+int32_t qm_q4_gemv_multi_conv(qm_context* c, qm_stream stream, int32_t k, const float* x, const uint16_t* norm_w,
+                              int32_t count, const qm_q4_out* outs, float* conv_buf, const float* conv_w) {
+    if (!c) return QM_ERR_INVALID_ARG;
+    if (!conv_buf || !conv_w || !outs || count < 1)
+        return fail(c, QM_ERR_INVALID_ARG, "qm_q4_gemv_multi_conv: null conv buffer, weights or outputs");
+    if (outs[0].residual_dev)
+        return fail(c, QM_ERR_INVALID_ARG, "qm_q4_gemv_multi_conv: the conv output takes no residual");
+    if (!all_aligned16({conv_buf, conv_w}))
+        return fail(c, QM_ERR_INVALID_ARG, "qm_q4_gemv_multi_conv: device pointers must be 16-byte aligned");
+    return q4_gemv_multi_impl(c, stream, k, x, norm_w, count, outs, conv_buf, conv_w);
 }
 
 int32_t qm_q4_gemv(qm_context* c, qm_stream stream, int32_t k, int32_t n, const float* x,

@@ -197,12 +197,22 @@ inline void forward_decode_gpu(Context& ctx, const GpuModel& m, GpuHybridCache& 
         if (m.config.layer_types[i] == 0) {
             // forward_deltanet_decode, gemv.rs:719-900
             const GpuDeltaNetLayerWeights& w = m.dn[m.slot[i]];
-            rms_norm_gemv_gpu(ctx, x, w.input_norm.as<uint16_t>(),
-                              {{&w.in_proj_qkv, s.proj.as<float>()}, {&w.in_proj_z, s.z.as<float>()},
-                               {&w.in_proj_a, s.a.as<float>()}, {&w.in_proj_b, s.b.as<float>()}},
-                              stream);
-            forward_deltanet_decode_gpu(ctx, s.proj.as<float>(), s.a.as<float>(), s.b.as<float>(), s.z.as<float>(),
-                                        w.mixer, cache.dn[di++], cfg, s.mix.as<float>(), stream);
+            GpuDeltaNetState& st = cache.dn[di++];
+            // input norm + the four projections, with the conv1d step + SiLU
+            // on in_proj_qkv (its buffer shifted there), then the mixer on
+            // the activated stream
+            const qm_q4_out outs[4] = {w.in_proj_qkv.out(s.proj.as<float>()), w.in_proj_z.out(s.z.as<float>()),
+                                       w.in_proj_a.out(s.a.as<float>()), w.in_proj_b.out(s.b.as<float>())};
+            ctx.check(qm_q4_gemv_multi_conv(ctx.get(), stream, H, x, w.input_norm.as<uint16_t>(), 4, outs,
+                                            st.conv_buf.as<float>(), w.mixer.conv1d_weight.as<float>()));
+            ctx.check(qm_deltanet_decode(ctx.get(), stream, 1, QM_DN_POSTACT, s.proj.as<float>(), nullptr, nullptr,
+                                         s.a.as<float>(), s.b.as<float>(), w.mixer.a_log.as<float>(),
+                                         w.mixer.dt_bias.as<float>(), s.z.as<float>(),
+                                         w.mixer.attn_norm_weight.as<uint16_t>(), st.s.as<float>(),
+                                         static_cast<int64_t>(cfg.num_v_heads * cfg.deltanet_head_dim *
+                                                              cfg.deltanet_head_dim),
+                                         s.mix.as<float>()));
+            st.conv_pos += 1;
             gemv_residual_gpu(ctx, s.mix.as<float>(), w.out_proj, x, stream);
             rms_norm_fused_gate_up_gpu(ctx, x, w.post_attn_norm.as<uint16_t>(), w.gate_proj, w.up_proj,
                                        s.inter.as<float>(), stream);

@@ -102,6 +102,7 @@ _SIGNATURES = {
     "qm_q4_repack": [_P, _P, _I32, _I32, _P, _P, _P, _P],
     "qm_q4_gemv": [_P, _P, _I32, _I32, _P, _P, _P, _P],
     "qm_q4_gemv_multi": [_P, _P, _I32, _P, _P, _I32, _P],
+    "qm_q4_gemv_multi_conv": [_P, _P, _I32, _P, _P, _I32, _P, _P, _P],
     "qm_q4_gate_up": [_P, _P, _I32, _I32, _P, _P, _P, _P, _P, _P, _P],
     "qm_rms_norm_f16": [_P, _P, _I32, _I32, _P, _P, _P],
     "qm_q4_gemm": [_P, _P, _I32, _I32, _I32, _P, _I32, _P, _P, _P, _P, _P],
@@ -322,13 +323,18 @@ class Context:
         self._check(self.lib.qm_q4_gemv(self.h, self.stream, k, n, _addr(x), _addr(codes),
                                         _addr(gscales), _addr(y)))
 
-    def q4_gemv_multi(self, k, x, outs, norm_w=None):
+    def q4_gemv_multi(self, k, x, outs, norm_w=None, conv_buf=None, conv_w=None):
         """outs: [(n, codes, gscales, y) or (n, codes, gscales, y, residual), ...]
-        (1..4 weights sharing x); norm_w: optional f16 [k] RMSNorm weight."""
+        (1..4 weights sharing x); norm_w: optional f16 [k] RMSNorm weight.  With
+        conv_buf / conv_w, outs[0] gets the DeltaNet conv1d step + SiLU."""
         arr = (QmQ4Out * len(outs))(*[
             QmQ4Out(o[0], _addr(o[1]), _addr(o[2]), _addr(o[3]), _addr(o[4]) if len(o) > 4 else None)
             for o in outs])
-        self._check(self.lib.qm_q4_gemv_multi(self.h, self.stream, k, _addr(x), _addr(norm_w), len(outs), arr))
+        if conv_buf is None and conv_w is None:
+            self._check(self.lib.qm_q4_gemv_multi(self.h, self.stream, k, _addr(x), _addr(norm_w), len(outs), arr))
+        else:
+            self._check(self.lib.qm_q4_gemv_multi_conv(self.h, self.stream, k, _addr(x), _addr(norm_w), len(outs),
+                                                       arr, _addr(conv_buf), _addr(conv_w)))
 
     def rms_norm_f16(self, m, k, x, norm_w, out):
         """out f16 [m, k] = rms_norm(x, norm_w) per row (or plain f16 if norm_w is None)."""

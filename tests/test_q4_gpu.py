@@ -161,6 +161,48 @@ def test_q4_gemv_multi_norm_and_residual(ctx):
     assert np.array_equal(ctx.download(dx, (k,), np.float32), x)       # x itself is not written
 
 
+def test_q4_gemv_conv_fused(ctx):
+    """The DeltaNet decode's input projections with the conv1d step + SiLU
+    fused onto in_proj_qkv (gemv.rs:740-742,744-772,788-789,865): the
+    shifted conv buffer holds the unfused projection bit for bit, and the
+    activation matches the oracle's conv1d step + silu on it; the other
+    outputs equal the unfused launch."""
+    rng = np.random.default_rng(47)
+    k = 2560
+    x = rng.standard_normal(k).astype(np.float32)
+    gamma = W.f16_bits(0.1 * rng.standard_normal(k).astype(np.float32))
+    names = ("in_proj_qkv", "in_proj_z", "in_proj_a", "in_proj_b")
+    ws = {nm: W.q4_random_weight(*W.Q4_PROJ_SHAPES[nm], rng) for nm in names}
+    dev = {nm: repack(ctx, *ws[nm]) for nm in names}
+    conv_w = (0.5 * rng.standard_normal((8192, 4))).astype(np.float32)
+    buf0 = rng.standard_normal((8192, 3)).astype(np.float32)
+    dx, dg, dw = ctx.upload(x), ctx.upload(gamma), ctx.upload(conv_w)
+    plain = {nm: ctx.alloc(W.Q4_PROJ_SHAPES[nm][1] * 4) for nm in names}
+    fused = {nm: ctx.alloc(W.Q4_PROJ_SHAPES[nm][1] * 4) for nm in names}
+    print("case: q4 gemv + conv1d + silu fused", flush=True)
+    ctx.q4_gemv_multi(k, dx, [(W.Q4_PROJ_SHAPES[nm][1], *dev[nm], plain[nm]) for nm in names], norm_w=dg)
+    dbuf = ctx.upload(buf0)
+    ctx.q4_gemv_multi(k, dx, [(W.Q4_PROJ_SHAPES[nm][1], *dev[nm], fused[nm]) for nm in names], norm_w=dg,
+                      conv_buf=dbuf, conv_w=dw)
+    v = ctx.download(plain["in_proj_qkv"], (8192,), np.float32)
+    buf = ctx.download(dbuf, (8192, 3), np.float32)
+    assert np.array_equal(buf[:, :2], buf0[:, 1:]) and np.array_equal(buf[:, 2], v)
+    ref_buf = buf0.copy()
+    conv = O.conv1d_step(ref_buf, conv_w, v)
+    ref = np.array([O.silu(float(c)) for c in conv], np.float32)
+    got = ctx.download(fused["in_proj_qkv"], (8192,), np.float32)
+    # silu's expf on the device and in libm differ by an ulp or so
+    ulps = np.abs(got - ref) / np.spacing(np.abs(ref))
+    print(f"silu: max {ulps.max():.1f} ulp")
+    assert np.all(np.abs(got - ref) <= 4 * np.spacing(np.abs(ref)) + 1e-30)
+    for nm in names[1:]:
+        n = W.Q4_PROJ_SHAPES[nm][1]
+        assert np.array_equal(ctx.download(fused[nm], (n,), np.float32), ctx.download(plain[nm], (n,), np.float32))
+    with pytest.raises(M.MixerError):                   # no residual on the conv output
+        ctx.q4_gemv_multi(k, dx, [(8192, *dev["in_proj_qkv"], fused["in_proj_qkv"], fused["in_proj_qkv"])],
+                          conv_buf=dbuf, conv_w=dw)
+
+
 @pytest.mark.parametrize("norm", [False, True])
 def test_q4_gate_up(ctx, norm):
     """silu(xn Wg) * (xn Wu) (fused_gate_up_q4, gemv.rs:469-526) for the
