@@ -22,7 +22,7 @@
 //      sorted lists up to k elements; then the reference's sequential f32
 //      arithmetic on one thread: the softmax sum, the top-p cutoff, the
 //      total and the cumulative draw, in the reference's order and rounding
-//      (no contraction).  exp is taken in double and rounded to f32 (the
+//      (contraction off in these kernels).  exp is taken in double and rounded to f32 (the
 //      reference calls libm expf, correctly rounded but for rare half-way
 //      cases).
 // Greedy (temperature <= 0) is the same selection with k = 1.
@@ -48,6 +48,7 @@ QM_DEV float key_logit(uint32_t k) {
 }
 
 extern "C" __global__ __launch_bounds__(SMP_THREADS) void qm_sample_penalties(SampleArgs A) {
+#pragma clang fp contract(off)
     __shared__ uint32_t seen[(SMP_MAX_VOCAB + 31) / 32];
     const int tid = threadIdx.x;
     const int n = A.n_generated;
@@ -228,6 +229,7 @@ extern "C" __global__ __launch_bounds__(256) void qm_sample_select(SampleArgs A)
 // of the global order (wave 0 repeatedly takes the largest list head), and
 // draw.
 extern "C" __global__ __launch_bounds__(SMP_THREADS) void qm_sample_top_k(SampleArgs A) {
+#pragma clang fp contract(off)
     __shared__ uint64_t cand[SMP_MAX_CAND];
     __shared__ uint64_t top[SMP_MAX_K];
     __shared__ float prob[SMP_MAX_K];
