@@ -8,6 +8,9 @@
 //   GpuHybridCache      HybridCache / GpuHybridCache (gemv.rs:171-186,
 //                       gpu_inference.rs:44-60): per-layer DeltaNet state or
 //                       f16 KV cache of a fixed capacity
+//   forward_prefill_gpu prefill (gemv.rs:1243-1283): the prompt through
+//                       every layer on MFMA GEMMs and the chunked mixers,
+//                       logits of the last token
 //   forward_decode_gpu  forward_decode (gemv.rs:1059-1077): embedding row,
 //                       the 32 layer-forwards (gemv.rs:719-900, 907-1025)
 //                       with their projections, final norm and lm_head, all
@@ -235,6 +238,96 @@ inline void forward_decode_gpu(Context& ctx, const GpuModel& m, GpuHybridCache& 
     }
     ctx.check(qm_q4_lm_head(ctx.get(), stream, V, H, x, m.final_norm.as<uint16_t>(), m.embed.packed.as<uint8_t>(),
                             m.embed.scales.as<uint16_t>(), logits_dev));
+}
+
+// Device buffers a prefill of up to max_tokens works in.
+struct PrefillScratch {
+    DeviceBuffer x, xn16, proj16, z16, a, b, k16, v16, mix16, inter16;
+    std::size_t max_tokens = 0;
+
+    static PrefillScratch create(Context& ctx, const GpuModel& m, std::size_t max_tokens) {
+        const Qor4bConfig cfg = Qor4bConfig::default_4b();
+        const std::size_t T = max_tokens, H = m.config.hidden_size;
+        PrefillScratch s;
+        s.max_tokens = T;
+        s.x = DeviceBuffer(ctx, T * H * 4);
+        s.xn16 = DeviceBuffer(ctx, T * H * 2);
+        s.proj16 = DeviceBuffer(ctx, T * std::max(cfg.deltanet_qkv_dim(), 2 * cfg.attn_q_dim()) * 2);
+        s.z16 = DeviceBuffer(ctx, T * cfg.deltanet_v_dim() * 2);
+        s.a = DeviceBuffer(ctx, T * cfg.num_v_heads * 4);
+        s.b = DeviceBuffer(ctx, T * cfg.num_v_heads * 4);
+        s.k16 = DeviceBuffer(ctx, T * cfg.attn_kv_dim() * 2);
+        s.v16 = DeviceBuffer(ctx, T * cfg.attn_kv_dim() * 2);
+        s.mix16 = DeviceBuffer(ctx, T * std::max(cfg.deltanet_v_dim(), cfg.attn_q_dim()) * 2);
+        s.inter16 = DeviceBuffer(ctx, T * m.config.intermediate_size * 2);
+        return s;
+    }
+};
+
+// prefill (gemv.rs:1243-1283): the tokens_dev [T] prompt through every
+// layer on MFMA (prefill_deltanet_layer, gemv.rs:1086-1240;
+// prefill_attn_layer, :1339-1470), each projection one qm_q4_gemm over all
+// T rows (f16 inputs from qm_rms_norm_f16, bf16 mixer inputs and outputs,
+// the hidden state f32 with the residuals added in the GEMM epilogues),
+// the MLP's gate/up as one launch; then the final norm and lm_head of the
+// last token into logits_dev.  DeltaNet states and conv buffers continue
+// from where they are; KV caches are replaced by positions 0 .. T-1.
+inline void forward_prefill_gpu(Context& ctx, const GpuModel& m, GpuHybridCache& cache, PrefillScratch& s,
+                                const int32_t* tokens_dev, int32_t T, float* logits_dev, qm_stream stream = nullptr) {
+    if (T < 1 || static_cast<std::size_t>(T) > s.max_tokens)
+        throw MixerError(QM_ERR_INVALID_ARG, "forward_prefill_gpu: " + std::to_string(T) + " tokens, scratch holds " +
+                                                 std::to_string(s.max_tokens));
+    const Qor4bConfig cfg = Qor4bConfig::default_4b();
+    const int32_t H = static_cast<int32_t>(m.config.hidden_size), I = static_cast<int32_t>(m.config.intermediate_size);
+    const int32_t V = static_cast<int32_t>(m.embed.vocab);
+    float* x = s.x.as<float>();
+    uint16_t* xn = s.xn16.as<uint16_t>();
+    auto gemm = [&](const uint16_t* in, int32_t x_dtype, const GpuQ4Weight& w, float* y, uint16_t* y_bf16,
+                    const float* residual) {
+        ctx.check(qm_q4_gemm(ctx.get(), stream, T, static_cast<int32_t>(w.k), static_cast<int32_t>(w.n), in, x_dtype,
+                             w.codes.as<uint8_t>(), w.gscales.as<uint16_t>(), residual, y, y_bf16));
+    };
+    auto mlp = [&](const DeviceBuffer& post_norm, const GpuQ4Weight& gate, const GpuQ4Weight& up,
+                   const GpuQ4Weight& down) {
+        ctx.check(qm_rms_norm_f16(ctx.get(), stream, T, H, x, post_norm.as<uint16_t>(), xn));
+        ctx.check(qm_q4_gemm_gate_up(ctx.get(), stream, T, H, I, xn, QM_F16, gate.codes.as<uint8_t>(),
+                                     gate.gscales.as<uint16_t>(), up.codes.as<uint8_t>(), up.gscales.as<uint16_t>(),
+                                     s.inter16.as<uint16_t>()));
+        gemm(s.inter16.as<uint16_t>(), QM_F16, down, x, nullptr, x);
+    };
+    ctx.check(qm_q4_embed(ctx.get(), stream, T, V, H, tokens_dev, m.embed.packed.as<uint8_t>(),
+                          m.embed.scales.as<uint16_t>(), x));
+    std::size_t di = 0, ai = 0;
+    for (std::size_t i = 0; i < m.slot.size(); ++i) {
+        if (m.config.layer_types[i] == 0) {
+            const GpuDeltaNetLayerWeights& w = m.dn[m.slot[i]];
+            GpuDeltaNetState& st = cache.dn[di++];
+            ctx.check(qm_rms_norm_f16(ctx.get(), stream, T, H, x, w.input_norm.as<uint16_t>(), xn));
+            gemm(xn, QM_F16, w.in_proj_qkv, nullptr, s.proj16.as<uint16_t>(), nullptr);
+            gemm(xn, QM_F16, w.in_proj_z, nullptr, s.z16.as<uint16_t>(), nullptr);
+            gemm(xn, QM_F16, w.in_proj_a, s.a.as<float>(), nullptr, nullptr);
+            gemm(xn, QM_F16, w.in_proj_b, s.b.as<float>(), nullptr, nullptr);
+            prefill_deltanet_layer_gpu(ctx, static_cast<std::size_t>(T), s.proj16.as<uint16_t>(), s.a.as<float>(),
+                                       s.b.as<float>(), s.z16.as<uint16_t>(), w.mixer, st, cfg,
+                                       s.mix16.as<uint16_t>(), stream);
+            gemm(s.mix16.as<uint16_t>(), QM_BF16, w.out_proj, x, nullptr, x);
+            mlp(w.post_attn_norm, w.gate_proj, w.up_proj, w.down_proj);
+        } else {
+            const GpuFullAttnLayerWeights& w = m.fa[m.slot[i]];
+            ctx.check(qm_rms_norm_f16(ctx.get(), stream, T, H, x, w.input_norm.as<uint16_t>(), xn));
+            gemm(xn, QM_F16, w.q_proj, nullptr, s.proj16.as<uint16_t>(), nullptr);
+            gemm(xn, QM_F16, w.k_proj, nullptr, s.k16.as<uint16_t>(), nullptr);
+            gemm(xn, QM_F16, w.v_proj, nullptr, s.v16.as<uint16_t>(), nullptr);
+            prefill_attn_layer_gpu(ctx, static_cast<std::size_t>(T), s.proj16.as<uint16_t>(), s.k16.as<uint16_t>(),
+                                   s.v16.as<uint16_t>(), w.mixer, cache.kv[ai++], cfg, m.rope_cos.as<float>(),
+                                   m.rope_sin.as<float>(), m.rope_len, s.mix16.as<uint16_t>(), stream);
+            gemm(s.mix16.as<uint16_t>(), QM_BF16, w.o_proj, x, nullptr, x);
+            mlp(w.post_attn_norm, w.gate_proj, w.up_proj, w.down_proj);
+        }
+    }
+    ctx.check(qm_q4_lm_head(ctx.get(), stream, V, H, x + static_cast<std::size_t>(T - 1) * H,
+                            m.final_norm.as<uint16_t>(), m.embed.packed.as<uint8_t>(), m.embed.scales.as<uint16_t>(),
+                            logits_dev));
 }
 
 }  // namespace qor4b

@@ -457,6 +457,117 @@ void model_flow(Context& ctx, const Qor4bConfig& cfg) {
         id = next;
     }
     expect(worst <= 2e-3, "qor4b file -> device model, 4 decode steps: logits rel", worst, 2e-3);
+
+    // prefill (gemv.rs:1243-1283) of a 37-token prompt on a fresh cache, on
+    // MFMA with f16 / bf16 activations, against the oracle's f32 prefill
+    // composed from its restatements; then one decode step continuing from
+    // the prefilled state, conv buffer and KV cache
+    {
+        const int32_t T = 37;
+        std::vector<int32_t> ids(T);
+        for (auto& v : ids) v = static_cast<int32_t>(r.next() % V);
+        DeviceBuffer dids = upload(ctx, ids);
+        GpuHybridCache pc = GpuHybridCache::create(ctx, gm, 64);
+        PrefillScratch ps = PrefillScratch::create(ctx, gm, T);
+        forward_prefill_gpu(ctx, gm, pc, ps, dids.as<int32_t>(), T, logits.as<float>());
+        std::vector<float> got(V);
+        logits.download(got.data(), V * 4);
+
+        auto gemm_rows = [&](const std::vector<float>& X, const W& w) {
+            std::vector<float> Y((std::size_t)T * w.n);
+            or_q4_gemm(X.data(), T, w.packed.data(), w.scales.data(), (int32_t)w.k, (int32_t)w.n, Y.data(), 8);
+            return Y;
+        };
+        auto rms_rows = [&](const std::vector<float>& X, const std::vector<uint16_t>& g) {
+            std::vector<float> Y(X.size());
+            for (int32_t t = 0; t < T; ++t) or_rms_norm(&X[(std::size_t)t * H], (int32_t)H, g.data(), &Y[(std::size_t)t * H]);
+            return Y;
+        };
+        auto add = [](std::vector<float>& X, const std::vector<float>& D) {
+            for (std::size_t i = 0; i < X.size(); ++i) X[i] += D[i];
+        };
+        auto mlp_rows = [&](std::vector<float>& X, const std::vector<uint16_t>& norm, const W& g, const W& u,
+                            const W& dw) {
+            const std::vector<float> XN = rms_rows(X, norm);
+            std::vector<float> G = gemm_rows(XN, g);
+            const std::vector<float> U = gemm_rows(XN, u);
+            for (std::size_t i = 0; i < G.size(); ++i) G[i] = (G[i] / (1.0f + std::exp(-G[i]))) * U[i];   // gemv.rs:1235
+            add(X, gemm_rows(G, dw));
+        };
+        std::vector<float> X((std::size_t)T * H);
+        for (int32_t t = 0; t < T; ++t)
+            or_q4_embed(m.embed.packed.data(), m.embed.scales.data(), (int32_t)H, ids[t], &X[(std::size_t)t * H]);
+        std::vector<float> S2(S.size(), 0.0f), buf2(buf.size(), 0.0f);
+        {   // prefill_deltanet_layer
+            const std::vector<float> XN = rms_rows(X, od.input_norm);
+            const std::vector<float> qkv = gemm_rows(XN, od.in_proj_qkv), z = gemm_rows(XN, od.in_proj_z),
+                                     av = gemm_rows(XN, od.in_proj_a), bv = gemm_rows(XN, od.in_proj_b);
+            std::vector<float> out((std::size_t)T * cfg.deltanet_v_dim());
+            or_deltanet_prefill(&oc, T, qkv.data(), av.data(), bv.data(), z.data(), buf2.data(),
+                                od.conv1d_weight.data(), od.a_log.data(), od.dt_bias.data(), od.attn_norm_weight.data(),
+                                S2.data(), out.data());
+            add(X, gemm_rows(out, od.out_proj));
+            mlp_rows(X, od.post_attn_norm, od.gate_proj, od.up_proj, od.down_proj);
+        }
+        std::vector<float> Kp((std::size_t)(T + 1) * cfg.attn_kv_dim()), Vp(Kp.size());
+        {   // prefill_attn_layer
+            const std::vector<float> XN = rms_rows(X, oa.input_norm);
+            const std::vector<float> qg = gemm_rows(XN, oa.q_proj), kk = gemm_rows(XN, oa.k_proj),
+                                     vv = gemm_rows(XN, oa.v_proj);
+            std::vector<float> out((std::size_t)T * cfg.attn_q_dim());
+            or_attn_prefill(&oc, T, qg.data(), kk.data(), vv.data(), oa.q_norm.data(), oa.k_norm.data(),
+                            m.rope_cos.data(), m.rope_sin.data(), rope_len, Kp.data(), Vp.data(), out.data(),
+                            nullptr, 0, 4);
+            add(X, gemm_rows(out, oa.o_proj));
+            mlp_rows(X, oa.post_attn_norm, oa.gate_proj, oa.up_proj, oa.down_proj);
+        }
+        std::vector<float> xl(X.end() - H, X.end()), xf(H), ref(V);
+        or_rms_norm(xl.data(), (int32_t)H, m.final_norm.data(), xf.data());
+        or_q4_lm_head(xf.data(), m.embed.packed.data(), m.embed.scales.data(), (int32_t)V, (int32_t)H, ref.data(), 4);
+        double e = rel_err(got.data(), ref.data(), V);
+        expect(e <= 2e-2, "device prefill T=37 (MFMA, f16/bf16 activations): logits rel", e, 2e-2);
+        std::vector<float> Sg(S2.size());
+        pc.dn[0].s.download(Sg.data(), Sg.size() * 4);
+        e = rel_err(Sg.data(), S2.data(), S2.size());
+        expect(e <= 2e-2, "device prefill: DeltaNet state rel", e, 2e-2);
+        expect(pc.kv[0].seq_len == (std::size_t)T && pc.dn[0].conv_pos == (std::size_t)T,
+               "prefill cache positions (error = 1)", 0, 0.5);
+
+        // one decode step continuing from the prefill
+        const int32_t nid = 77;
+        tok.upload(&nid, 4);
+        forward_decode_gpu(ctx, gm, pc, scratch, tok.as<int32_t>(), logits.as<float>());
+        logits.download(got.data(), V * 4);
+        std::vector<float> x(H);
+        or_q4_embed(m.embed.packed.data(), m.embed.scales.data(), (int32_t)H, nid, x.data());
+        {
+            const std::vector<float> xn = rms(x, od.input_norm);
+            const std::vector<float> qkv = gemv(xn, od.in_proj_qkv), av = gemv(xn, od.in_proj_a),
+                                     bv = gemv(xn, od.in_proj_b), zv = gemv(xn, od.in_proj_z);
+            std::vector<float> out(cfg.deltanet_v_dim());
+            or_deltanet_decode_step(&oc, qkv.data(), 1, buf2.data(), od.conv1d_weight.data(), av.data(), bv.data(),
+                                    od.a_log.data(), od.dt_bias.data(), zv.data(), od.attn_norm_weight.data(),
+                                    S2.data(), out.data(), OR_UPDATE_AUTO);
+            const std::vector<float> h = gemv(out, od.out_proj);
+            for (uint32_t j = 0; j < H; ++j) x[j] += h[j];
+            mlp(x, od.post_attn_norm, od.gate_proj, od.up_proj, od.down_proj);
+        }
+        {
+            const std::vector<float> xn = rms(x, oa.input_norm);
+            const std::vector<float> qg = gemv(xn, oa.q_proj), kn = gemv(xn, oa.k_proj), vn = gemv(xn, oa.v_proj);
+            std::vector<float> out(cfg.attn_q_dim());
+            or_attn_decode_step(&oc, qg.data(), kn.data(), vn.data(), oa.q_norm.data(), oa.k_norm.data(),
+                                m.rope_cos.data(), m.rope_sin.data(), rope_len, Kp.data(), Vp.data(), T, 1,
+                                out.data(), 4);
+            const std::vector<float> h = gemv(out, oa.o_proj);
+            for (uint32_t j = 0; j < H; ++j) x[j] += h[j];
+            mlp(x, oa.post_attn_norm, oa.gate_proj, oa.up_proj, oa.down_proj);
+        }
+        or_rms_norm(x.data(), (int32_t)H, m.final_norm.data(), xf.data());
+        or_q4_lm_head(xf.data(), m.embed.packed.data(), m.embed.scales.data(), (int32_t)V, (int32_t)H, ref.data(), 4);
+        e = rel_err(got.data(), ref.data(), V);
+        expect(e <= 2e-2, "decode step after the device prefill: logits rel", e, 2e-2);
+    }
     expect(greedy_ok, "greedy qm_sample = oracle argmax (mismatch = 1)", greedy_ok ? 0 : 1, 0.5);
     expect(cache.kv[0].seq_len == (std::size_t)steps && cache.dn[0].conv_pos == (std::size_t)steps,
            "cache positions advanced (error = 1)", 0, 0.5);
