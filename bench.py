@@ -642,18 +642,13 @@ FA_LAYER_PROJ = {"q_proj": (2560, 8192), "k_proj": (2560, 1024), "v_proj": (2560
                  "gate_proj": (2560, 9216), "up_proj": (2560, 9216), "down_proj": (9216, 2560)}
 
 
-def run_decode_model(args, ctx):
-    """One decode token through the whole 4B model at batch 1, position 4096:
-    embedding row, 24 DeltaNet and 8 GQA layers (input RMSNorm + projections,
-    mixer, out/o_proj residual, RMSNorm + gate/up MLP, down residual), final
-    RMSNorm + lm_head over 248,320 rows, and top-k sampling whose token feeds
-    the next step's embedding on the device (forward_decode, gemv.rs:1059-1077,
-    then sample_token_top_k).  Random weights of the real shapes (2.3 GB
-    resident), captured once as a HIP graph and replayed."""
-    K, Wm = args.steps, args.warmup
+def _model_on_device(ctx, cap):
+    """Random weights of the 4B's real shapes in the device layouts (2.3 GB):
+    24 DeltaNet and 8 GQA layers with their Q4 projections, mixer
+    parameters, DeltaNet states and f16 KV caches of cap positions, the
+    vocab-major Q4 embedding, final norm and RoPE tables."""
     seed = [7000]
-    V, H, P = LM_VOCAB, LM_HIDDEN, MODEL_POS
-    cap = P + 1
+    V, H = LM_VOCAB, LM_HIDDEN
 
     def fill(buf, dtype, count, std, mean=0.0):
         ctx.fill_normal(buf, dtype, count, mean, std, seed[0])
@@ -694,9 +689,105 @@ def run_decode_model(args, ctx):
     fill(emb_codes, M.QM_F16, V * H // 4, 1.0)
     emb_scales = ctx.alloc(V * (H // 32) * 2)
     fill(emb_scales, M.QM_F16, V * (H // 32), 0.004, 0.02)
-    final_norm = f16vec(H, 0.0, 0.1)
     cos, sin = M.rope_table(cap + 1)
-    rc, rs = ctx.upload(cos), ctx.upload(sin)
+    return {"layers": layers, "emb": (emb_codes, emb_scales), "final_norm": f16vec(H, 0.0, 0.1),
+            "rope": (ctx.upload(cos), ctx.upload(sin), cap + 1)}
+
+
+PREFILL_T = 4096
+
+
+def model_gemm_flops_per_token():
+    """2 k n over every projection of the 32 layers (the MLP's gate and up included)."""
+    dn = sum(k * n for k, n in (W.Q4_PROJ_SHAPES[nm] for nm in Q4_LAYER_PROJ))
+    fa = sum(k * n for k, n in FA_LAYER_PROJ.values())
+    return 2 * (24 * dn + 8 * fa)
+
+
+def run_prefill_model(args, ctx):
+    """A 4096-token prompt through the whole 4B model (prefill, gemv.rs:1243-1283):
+    embedding rows; per layer RMSNorm to f16, the projections as Q4 GEMMs on
+    MFMA (bf16 mixer inputs), the chunked DeltaNet or causal GQA prefill, the
+    out/o_proj GEMM on the bf16 mixer output with the residual, RMSNorm, the
+    fused gate/up GEMM and the down GEMM with the residual; then the final
+    norm and lm_head of the last token.  Random weights of the real shapes."""
+    K, Wm = args.steps, args.warmup
+    V, H, T = LM_VOCAB, LM_HIDDEN, PREFILL_T
+    mdl = _model_on_device(ctx, T)
+    layers, (emb_codes, emb_scales), final_norm = mdl["layers"], mdl["emb"], mdl["final_norm"]
+    rc, rs, rope_len = mdl["rope"]
+    ids = ctx.upload(np.random.default_rng(9).integers(0, V, T).astype(np.int32))
+    x, xn = ctx.alloc(T * H * 4), ctx.alloc(T * H * 2)
+    proj, z16, mix16 = ctx.alloc(T * 8192 * 2), ctx.alloc(T * 4096 * 2), ctx.alloc(T * 4096 * 2)
+    a, b, k16, v16 = ctx.alloc(T * 32 * 4), ctx.alloc(T * 32 * 4), ctx.alloc(T * 1024 * 2), ctx.alloc(T * 1024 * 2)
+    inter16, logits = ctx.alloc(T * 9216 * 2), ctx.alloc(V * 4)
+    ctx.reserve(max_batch=1, max_kv_len=T, max_prefill_tokens=T)
+    ctx.sync()
+    gemm_timer = Timer(ctx)
+
+    def step():
+        ctx.q4_embed(T, V, H, ids, emb_codes, emb_scales, x)
+        for L in layers:
+            ctx.rms_norm_f16(T, H, x, L["in_norm"], xn)
+            if L["dn"]:
+                ctx.q4_gemm(T, H, 8192, xn, *L["in_proj_qkv"], y_bf16=proj)
+                ctx.q4_gemm(T, H, 4096, xn, *L["in_proj_z"], y_bf16=z16)
+                ctx.q4_gemm(T, H, 32, xn, *L["in_proj_a"], y=a)
+                ctx.q4_gemm(T, H, 32, xn, *L["in_proj_b"], y=b)
+                ctx.deltanet_prefill(T, proj, L["conv_buf"], L["conv_w"], a, b, L["a_log"], L["dt_bias"], z16,
+                                     L["attn_norm"], L["state"], mix16)
+                ctx.q4_gemm(T, 4096, H, mix16, *L["out_proj"], y=x, residual=x, x_dtype=M.QM_BF16)
+            else:
+                ctx.q4_gemm(T, H, 8192, xn, *L["q_proj"], y_bf16=proj)
+                ctx.q4_gemm(T, H, 1024, xn, *L["k_proj"], y_bf16=k16)
+                ctx.q4_gemm(T, H, 1024, xn, *L["v_proj"], y_bf16=v16)
+                ctx.gqa_prefill(T, proj, k16, v16, L["q_norm"], L["k_norm"], rc, rs, rope_len, L["kc"], L["vc"], T,
+                                mix16)
+                ctx.q4_gemm(T, 4096, H, mix16, *L["o_proj"], y=x, residual=x, x_dtype=M.QM_BF16)
+            ctx.rms_norm_f16(T, H, x, L["post_norm"], xn)
+            ctx.q4_gemm_gate_up(T, H, 9216, xn, *L["gate_proj"], *L["up_proj"], inter16)
+            ctx.q4_gemm(T, 9216, H, inter16, *L["down_proj"], y=x, residual=x)
+        ctx.q4_lm_head(V, H, x.offset((T - 1) * H * 4), final_norm, emb_codes, emb_scales, logits)
+
+    for _ in range(Wm):
+        step()
+    ctx.sync()
+    t0, t1 = ctx.event(), ctx.event()
+    wall0 = time.perf_counter()
+    t0.record()
+    for _ in range(K):
+        step()
+    t1.record()
+    ctx.sync()
+    wall = time.perf_counter() - wall0
+    ms = t0.elapsed_ms(t1) / K
+    flops = model_gemm_flops_per_token() * T
+    return {
+        "tokens": K * T, "total_ms": t0.elapsed_ms(t1), "wall_s": wall,
+        "dominant": "whole prefill (embedding, 32 layers of Q4 GEMMs + chunked mixers, lm_head)",
+        "roofline": {"bound": "mfma", "achieved": flops / (ms * 1e-3), "peak": MFMA_BF16_PEAK,
+                     "kernel_ms": ms, "flops_per_launch": flops},
+        "config": {"workload": "whole-model prefill of a 4096-token prompt: embedding, 24 DeltaNet + 8 GQA layers "
+                               "(Q4 projection GEMMs on MFMA with f16/bf16 activations, chunked DeltaNet and causal "
+                               "GQA prefill), lm_head of the last token; roofline over the projection GEMM flops",
+                   "batch": 1, "seq_len": T, "global_batch": 1, "parallelism": "single GPU"},
+    }
+
+
+def run_decode_model(args, ctx):
+    """One decode token through the whole 4B model at batch 1, position 4096:
+    embedding row, 24 DeltaNet and 8 GQA layers (input RMSNorm + projections,
+    mixer, out/o_proj residual, RMSNorm + gate/up MLP, down residual), final
+    RMSNorm + lm_head over 248,320 rows, and top-k sampling whose token feeds
+    the next step's embedding on the device (forward_decode, gemv.rs:1059-1077,
+    then sample_token_top_k).  Random weights of the real shapes (2.3 GB
+    resident), captured once as a HIP graph and replayed."""
+    K, Wm = args.steps, args.warmup
+    V, H, P = LM_VOCAB, LM_HIDDEN, MODEL_POS
+    cap = P + 1
+    mdl = _model_on_device(ctx, cap)
+    layers, (emb_codes, emb_scales), final_norm = mdl["layers"], mdl["emb"], mdl["final_norm"]
+    rc, rs, _ = mdl["rope"]
     tok = ctx.upload(np.array([1234, 0, 0, 0], np.int32))
     rng_state = ctx.upload(np.array([0x9E3779B97F4A7C15], np.uint64))
     x, proj, z = ctx.alloc(H * 4), ctx.alloc(8192 * 4), ctx.alloc(4096 * 4)
@@ -952,6 +1043,49 @@ def cpu_baseline(workload: str) -> dict:
                           f"threads) and {n3} lm_heads timed separately (projections by the scalar gemv_q4_inner "
                           f"restatement, one thread); tokens/s = 1 / (24 t_dn + 8 t_gqa + t_head); "
                           f"{per_token:.2f} s per token"}
+    if workload == "prefill_model":
+        # one DeltaNet and one GQA layer prefilled over an 8-token prompt
+        # (gemm_q4 = 8 row gemvs, the sequential DeltaNet prefill, causal
+        # attention), scaled linearly to 24 + 8 layers
+        rng = np.random.default_rng(13)
+        Tc = 8
+        dw = {nm: W.q4_random_weight(*W.Q4_PROJ_SHAPES[nm], rng) for nm in Q4_LAYER_PROJ}
+        fw = {nm: W.q4_random_weight(*sh, rng) for nm, sh in FA_LAYER_PROJ.items()}
+        p = W.dn_params(rng)
+        gam = W.f16_bits(0.1 * rng.standard_normal(2560, dtype=np.float32))
+        qn = W.f16_bits(0.1 * rng.standard_normal(256, dtype=np.float32))
+        X = rng.standard_normal((Tc, 2560), dtype=np.float32)
+        cos, sin = O.rope_table(Tc + 1)
+
+        def rows(f, A):
+            return np.stack([f(r) for r in A])
+
+        def mlp(h, ws):
+            hn = rows(lambda r: O.rms_norm(r, gam), h)
+            g, u = O.q4_gemm(hn, *ws["gate_proj"], nthreads=1), O.q4_gemm(hn, *ws["up_proj"], nthreads=1)
+            return h + O.q4_gemm((g / (1.0 + np.exp(-g)) * u).astype(np.float32), *ws["down_proj"], nthreads=1)
+
+        def dn_layer():
+            xn = rows(lambda r: O.rms_norm(r, gam), X)
+            qkv, z = O.q4_gemm(xn, *dw["in_proj_qkv"], nthreads=1), O.q4_gemm(xn, *dw["in_proj_z"], nthreads=1)
+            av, bv = O.q4_gemm(xn, *dw["in_proj_a"], nthreads=1), O.q4_gemm(xn, *dw["in_proj_b"], nthreads=1)
+            out = O.deltanet_prefill(cfg, qkv, av, bv, z, p["conv_w"], p["a_log"], p["dt_bias"], p["norm_w"],
+                                     np.zeros((32, 128, 128), np.float32), np.zeros((8192, 3), np.float32))
+            return mlp(X + O.q4_gemm(out, *dw["out_proj"], nthreads=1), dw)
+
+        def gqa_layer():
+            xn = rows(lambda r: O.rms_norm(r, gam), X)
+            qg, kk, vv = (O.q4_gemm(xn, *fw[nm], nthreads=1) for nm in ("q_proj", "k_proj", "v_proj"))
+            out = O.attn_prefill(cfg, qg, kk, vv, qn, qn, cos, sin, nthreads=att_threads)[0]
+            return mlp(X + O.q4_gemm(out, *fw["o_proj"], nthreads=1), fw)
+
+        n1, t_dn = _repeat_for(dn_layer, min_s=4.0)
+        n2, t_fa = _repeat_for(gqa_layer, min_s=4.0)
+        per_prompt = 24 * t_dn / n1 + 8 * t_fa / n2
+        return {"value": Tc / per_prompt, "unit": "tokens/s", "cores": 1, "kind": "port",
+                "sample": f"{n1} DeltaNet and {n2} GQA layer prefills of an {Tc}-token prompt timed separately "
+                          f"(gemm_q4 as row gemvs, the sequential DeltaNet prefill, one thread), scaled to "
+                          f"24 + 8 layers: tokens/s = {Tc} / (24 t_dn + 8 t_gqa)"}
     if workload == "sample":
         rng = np.random.default_rng(11)
         x = (3.0 * rng.standard_normal(LM_VOCAB)).astype(np.float32)
@@ -1031,7 +1165,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="stack",
                     choices=["stack", "dn_decode", "gqa_decode", "dn_prefill", "gqa_prefill", "q4_proj",
-                             "q4_gemm", "lm_head", "sample", "decode_model"])
+                             "q4_gemm", "lm_head", "sample", "decode_model", "prefill_model"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
                     help="skip the graph-replayed timing (rocprofv3's kernel tracer crashes in "
@@ -1048,7 +1182,8 @@ def main():
         sys.exit(2)
     defaults = {"stack": (32, 4), "dn_decode": (256, 16), "gqa_decode": (200, 20),
                 "dn_prefill": (20, 3), "gqa_prefill": (10, 2), "q4_proj": (50, 5), "q4_gemm": (20, 3),
-                "lm_head": (100, 10), "sample": (200, 10), "decode_model": (30, 3)}[args.workload]
+                "lm_head": (100, 10), "sample": (200, 10), "decode_model": (30, 3),
+                "prefill_model": (5, 1)}[args.workload]
     args.steps = args.steps or defaults[0]
     args.warmup = defaults[1] if args.warmup is None else args.warmup
 
@@ -1065,7 +1200,8 @@ def main():
     run = {"stack": run_stack, "dn_decode": run_dn_decode, "gqa_decode": run_gqa_decode,
            "dn_prefill": run_dn_prefill, "gqa_prefill": run_gqa_prefill,
            "q4_proj": run_q4_proj, "q4_gemm": run_q4_gemm, "lm_head": run_lm_head,
-           "sample": run_sample, "decode_model": run_decode_model}[args.workload]
+           "sample": run_sample, "decode_model": run_decode_model,
+           "prefill_model": run_prefill_model}[args.workload]
     r = run(args, ctx)
     ctx.sync()
     ctx.close()
@@ -1090,15 +1226,17 @@ def main():
                    "q4_gemm": "Q4 projection tokens/s (prefill) on 1x MI355X",
                    "lm_head": "lm_head tokens/s (decode) on 1x MI355X",
                    "sample": "sampled tokens/s (decode) on 1x MI355X",
-                   "decode_model": "whole-model decode tokens/s (batch 1) on 1x MI355X"}.get(
+                   "decode_model": "whole-model decode tokens/s (batch 1) on 1x MI355X",
+                   "prefill_model": "whole-model prefill tokens/s on 1x MI355X"}.get(
                        args.workload, "mixer tokens/s (decode) on 1x MI355X"),
         "value": value, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": r["total_ms"] / args.steps,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": {"dn_prefill": "bf16", "gqa_prefill": "bf16", "q4_gemm": "f16"}.get(args.workload, "f32"),
+        "dtype": {"dn_prefill": "bf16", "gqa_prefill": "bf16", "q4_gemm": "f16",
+                  "prefill_model": "f16"}.get(args.workload, "f32"),
         "data": ("synthetic (seeded normal logits, random generated ids)" if args.workload == "sample" else
                  "synthetic (seeded random Q4 codes, f16 scales and normal inputs)"
-                 if args.workload.startswith("q4") or args.workload in ("lm_head", "decode_model")
+                 if args.workload.startswith("q4") or args.workload in ("lm_head", "decode_model", "prefill_model")
                  else "synthetic (seeded normal inputs, random-init state and f16 KV cache)"),
         "config": r["config"],
         "roofline": rl,

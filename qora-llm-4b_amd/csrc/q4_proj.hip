@@ -288,24 +288,33 @@ __device__ __forceinline__ uint4 bf16x8_to_f16x8(uint4 v) {
 // and up weights alternately, over 128 output columns, so a wave's fragments
 // j (gate) and j + 1 (up) hold the same outputs and the epilogue writes
 // silu(g) * u as f16.
-template <bool XBF16, bool GU>
+// Workgroup tiles TM x TN: 128 x 256, four waves of 64 x 128 (2 x 2); for
+// narrow outputs whose 128 x 256 tiles would leave CUs idle (n = 2560: 10
+// column tiles), 128 x 128 (2 x 2 waves of 64 x 64), twice the workgroups;
+// its W tile is staged by threads 0 .. 127.  (64 x 256 tiles, four waves of
+// 64 x 64 side by side, measured 2% slower on the 4096-token prefill.)
+template <bool XBF16, bool GU, int TM, int TN>
 __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
-    __shared__ __attribute__((aligned(16))) _Float16 sA[2][GM_TM][GM_LDK];
-    __shared__ __attribute__((aligned(16))) _Float16 sB[2][GM_TN][GM_LDK];
+    static_assert((TM == 128 && TN == 256) || (!GU && ((TM == 64 && TN == 256) || (TM == 128 && TN == 128))),
+                  "tile");
+    constexpr int NJ = TN / (16 * (TM == 128 ? 2 : 4));  // 16-column fragments per wave
+    __shared__ __attribute__((aligned(16))) _Float16 sA[2][TM][GM_LDK];
+    __shared__ __attribute__((aligned(16))) _Float16 sB[2][TN][GM_LDK];
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-    constexpr int NCOLS = GU ? GM_TN / 2 : GM_TN;       // output columns per workgroup
+    constexpr int NCOLS = GU ? TN / 2 : TN;              // output columns per workgroup
     const int nbn = (A.n + NCOLS - 1) / NCOLS;
     // consecutive workgroups walk n within one row block: the row block's X
-    // (k x 128 f16) is reused from L2 across its column tiles
+    // (k x TM f16) is reused from L2 across its column tiles
     const int bm = (int)blockIdx.x / nbn, bn = (int)blockIdx.x % nbn;
-    const int m0 = bm * GM_TM, n0 = bn * NCOLS;
-    const int wm = w >> 1, wn = w & 1;
+    const int m0 = bm * TM, n0 = bn * NCOLS;
+    const int wm = TM == 128 ? w >> 1 : 0, wn = TM == 128 ? w & 1 : w;
     const int T = A.tile, K = A.k;
     const int nk = K / GM_TK;
 
-    // X staging: thread -> row tid / 2, 16 k at 16 (tid & 1)
-    const int ar = tid >> 1, ah = tid & 1;
-    const uint16_t* xrow = A.x + (size_t)min(m0 + ar, A.m - 1) * K + 16 * ah;
+    // X staging: thread -> row tid / (256 / TM), TM / 8 halves of k
+    constexpr int XH = TM / 8;                           // 16 or 8 halves per thread
+    const int ar = tid / (32 / XH), ah = tid % (32 / XH);
+    const uint16_t* xrow = A.x + (size_t)min(m0 + ar, A.m - 1) * K + XH * ah;
     // W staging: thread -> 8-column block c8 = tid / 8 of the tile, rows
     // 4 rq .. 4 rq + 3 of the step (rq = tid % 8); a block is 4 code bytes
     // of one row (T = 16: half of a tile row, T = 8: a whole one)
@@ -327,10 +336,12 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
     do {                                                                               \
         const int k0_ = (kt) * GM_TK;                                                  \
         ra0 = *reinterpret_cast<const uint4*>(xrow + k0_);                            \
-        ra1 = *reinterpret_cast<const uint4*>(xrow + k0_ + 8);                        \
-        _Pragma("unroll") for (int i_ = 0; i_ < 4; ++i_)                               \
-            rb[i_] = *reinterpret_cast<const uint32_t*>(bcodes + (size_t)(k0_ + i_) * cstride); \
-        rs = *reinterpret_cast<const uint2*>(bsc + k0_);                              \
+        if (XH == 16) ra1 = *reinterpret_cast<const uint4*>(xrow + k0_ + 8);          \
+        if (TN == 256 || tid < TN) {                                                   \
+            _Pragma("unroll") for (int i_ = 0; i_ < 4; ++i_)                           \
+                rb[i_] = *reinterpret_cast<const uint32_t*>(bcodes + (size_t)(k0_ + i_) * cstride); \
+            rs = *reinterpret_cast<const uint2*>(bsc + k0_);                          \
+        }                                                                              \
     } while (0)
     // Columns 2b, 2b + 1 of a row pair come from byte b of each row's block.
     // v_perm_b32 puts the first row's byte at bits 0-7 and the second's at
@@ -340,10 +351,11 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
     // fp32).  Column n's four rows are one 8-byte store.
 #define GM_LSTORE(buf)                                                                 \
     do {                                                                               \
-        *reinterpret_cast<uint4*>(&sA[buf][ar][16 * ah]) = XBF16 ? bf16x8_to_f16x8(ra0) : ra0; \
-        *reinterpret_cast<uint4*>(&sA[buf][ar][16 * ah + 8]) = XBF16 ? bf16x8_to_f16x8(ra1) : ra1; \
+        *reinterpret_cast<uint4*>(&sA[buf][ar][XH * ah]) = XBF16 ? bf16x8_to_f16x8(ra0) : ra0; \
+        if (XH == 16)                                                                  \
+            *reinterpret_cast<uint4*>(&sA[buf][ar][XH * ah + 8]) = XBF16 ? bf16x8_to_f16x8(ra1) : ra1; \
         const half2 s01 = __builtin_bit_cast(half2, rs.x), s23 = __builtin_bit_cast(half2, rs.y); \
-        _Pragma("unroll") for (int b_ = 0; b_ < 4; ++b_) {                            \
+        if (TN == 256 || tid < TN) _Pragma("unroll") for (int b_ = 0; b_ < 4; ++b_) {  \
             const uint32_t sel = 0x0c040c00u + 0x00010001u * b_;                       \
             const uint32_t p01 = __builtin_amdgcn_perm(rb[1], rb[0], sel);             \
             const uint32_t p23 = __builtin_amdgcn_perm(rb[3], rb[2], sel);             \
@@ -359,11 +371,11 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
         }                                                                              \
     } while (0)
 
-    floatx4 acc[4][8];
+    floatx4 acc[4][NJ];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < NJ; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
     GM_GLOAD(0);
     GM_LSTORE(0);
@@ -376,8 +388,8 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const half8*>(&sA[b][64 * wm + 16 * i + fr][fk]);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const half8 bf = *reinterpret_cast<const half8*>(&sB[b][128 * wn + 16 * j + fr][fk]);
+        for (int j = 0; j < NJ; ++j) {
+            const half8 bf = *reinterpret_cast<const half8*>(&sB[b][16 * NJ * wn + 16 * j + fr][fk]);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf, acc[i][j], 0, 0, 0);
@@ -392,7 +404,7 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
     // C fragment: lane (n = lane & 15, mg = lane >> 4) holds rows 4 mg .. +3
     if constexpr (GU) {
 #pragma unroll
-        for (int j = 0; j < 8; j += 2) {
+        for (int j = 0; j < NJ; j += 2) {
             const int col = n0 + 64 * wn + 8 * j + fr;
             if (col >= A.n) continue;
 #pragma unroll
@@ -408,8 +420,8 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
         return;
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int col = n0 + 128 * wn + 16 * j + fr;
+    for (int j = 0; j < NJ; ++j) {
+        const int col = n0 + 16 * NJ * wn + 16 * j + fr;
         if (col >= A.n) continue;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -426,10 +438,12 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
     }
 }
 
-extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm(Q4GemmArgs A) { q4_gemm_body<false, false>(A); }
-extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm_xbf16(Q4GemmArgs A) { q4_gemm_body<true, false>(A); }
-extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm_gu(Q4GemmArgs A) { q4_gemm_body<false, true>(A); }
-extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm_gu_xbf16(Q4GemmArgs A) { q4_gemm_body<true, true>(A); }
+extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm(Q4GemmArgs A) { q4_gemm_body<false, false, 128, 256>(A); }
+extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm_xbf16(Q4GemmArgs A) { q4_gemm_body<true, false, 128, 256>(A); }
+extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm_gu(Q4GemmArgs A) { q4_gemm_body<false, true, 128, 256>(A); }
+extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm_gu_xbf16(Q4GemmArgs A) { q4_gemm_body<true, true, 128, 256>(A); }
+extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm_n128(Q4GemmArgs A) { q4_gemm_body<false, false, 128, 128>(A); }
+extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm_xbf16_n128(Q4GemmArgs A) { q4_gemm_body<true, false, 128, 128>(A); }
 
 // rms_norm (1 + gamma, eps 1e-6; gemv.rs:571-579) of each of m rows of f32
 // x [m][k], written as the f16 input of qm_q4_gemm; without a norm weight,

@@ -48,6 +48,7 @@ struct qm_context {
     hipFunction_t f_q4_repack = nullptr;
     hipFunction_t f_q4_gate_up = nullptr;
     hipFunction_t f_q4_gemm[2][2] = {};  // [x bf16][gate/up form]
+    hipFunction_t f_q4_gemm_n128[2] = {}; // [x bf16]: 128 x 128 tiles for narrow outputs
     hipFunction_t f_rms_f16 = nullptr;
     hipFunction_t f_lm_head = nullptr;
     hipFunction_t f_embed = nullptr;
@@ -300,6 +301,8 @@ int32_t qm_create(qm_context** out, const qm_config* cfg, const char* code_objec
     if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemm_xbf16", &c->f_q4_gemm[1][0]);
     if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemm_gu", &c->f_q4_gemm[0][1]);
     if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemm_gu_xbf16", &c->f_q4_gemm[1][1]);
+    if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemm_n128", &c->f_q4_gemm_n128[0]);
+    if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemm_xbf16_n128", &c->f_q4_gemm_n128[1]);
     if (st == QM_OK) st = load_function(c, mods[5], "qm_rms_norm_f16", &c->f_rms_f16);
     if (st == QM_OK) st = load_function(c, mods[6], "qm_q4_lm_head", &c->f_lm_head);
     if (st == QM_OK) st = load_function(c, mods[6], "qm_q4_embed", &c->f_embed);
@@ -929,8 +932,15 @@ int32_t qm_q4_gemm(qm_context* c, qm_stream stream, int32_t m, int32_t k, int32_
     if (!all_aligned16({x, codes, gscales, residual, y, y_bf16}))
         return fail(c, QM_ERR_INVALID_ARG, "qm_q4_gemm: device pointers must be 16-byte aligned");
     Q4GemmArgs ga{x, codes, gscales, nullptr, nullptr, y, y_bf16, nullptr, residual, m, k, n, QM_Q4_TILE(n)};
-    const uint32_t grid = static_cast<uint32_t>((m + 127) / 128) * static_cast<uint32_t>((n + 255) / 256);
-    return launch(c, c->f_q4_gemm[x_dtype == QM_BF16][0], grid, 256, ga, pick(c, stream), "qm_q4_gemm");
+    const int64_t ncol = (n + 255) / 256;
+    const int64_t tiles128 = (m + 127) / 128 * ncol;
+    // too few 128 x 256 tiles for two workgroups per CU (e.g. n = 2560): 128 x 128 tiles
+    if (tiles128 < 2 * static_cast<int64_t>(c->num_cu) && m > 64) {
+        const uint32_t grid = static_cast<uint32_t>((m + 127) / 128 * ((n + 127) / 128));
+        return launch(c, c->f_q4_gemm_n128[x_dtype == QM_BF16], grid, 256, ga, pick(c, stream), "qm_q4_gemm");
+    }
+    return launch(c, c->f_q4_gemm[x_dtype == QM_BF16][0], static_cast<uint32_t>(tiles128), 256, ga, pick(c, stream),
+                  "qm_q4_gemm");
 }
 
 int32_t qm_q4_gemm_gate_up(qm_context* c, qm_stream stream, int32_t m, int32_t k, int32_t n, const uint16_t* x,

@@ -244,9 +244,12 @@ def test_rms_norm_f16(ctx):
     assert np.array_equal(ctx.download(out, (m, k), np.uint16), W.f16_bits(x))
 
 
+# m > 64 with fewer than two 128 x 256 tiles per CU takes the 128 x 128
+# kernel; m = 1930 on the 8192-wide weight (512 tiles) the 128 x 256 one.
 @pytest.mark.parametrize("name,m,mode", [("in_proj_qkv", 200, "bf16"), ("in_proj_z", 37, "bf16"),
                                          ("out_proj", 64, "residual"), ("in_proj_a", 130, "f32"),
-                                         ("down_proj", 129, "residual"), ("k_proj", 1, "f32")])
+                                         ("down_proj", 129, "residual"), ("k_proj", 1, "f32"),
+                                         ("in_proj_qkv", 1930, "bf16")])
 def test_q4_gemm(ctx, name, m, mode):
     """gemm_q4 (gemv.rs:529-542) on MFMA: y = x W (+ residual), x f16; bar
     |y - y_ref| <= 1e-3 * sum_k |x_k W_kj| per element (W rounded to f16 per
