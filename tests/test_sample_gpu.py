@@ -108,3 +108,31 @@ def test_sample_errors(ctx):
     with pytest.raises(M.MixerError) as e:             # wgpu twin: top_k above the vocabulary
         ctx.sample(16, dx, None, 0, dst, tok, temperature=1.0, top_k=20, flags=M.QM_SAMPLE_WGPU)
     assert e.value.code == 3
+
+
+def test_sample_in_graph_replays(ctx):
+    """The penalties, top-k select and draw captured once as a HIP graph and
+    replayed five times, with eager work on the same logits buffer between
+    replays (a fresh upload each time): every replay's token and xorshift64
+    state equal the oracle's sequence, as eager calls do."""
+    rng = np.random.default_rng(91)
+    ctx.reserve(1, 0, 0)
+    dx = ctx.alloc(VOCAB * 4)
+    gen = rng.integers(0, VOCAB, 200).astype(np.int32)
+    dg, dst, tok = ctx.upload(gen), ctx.upload(np.array([2024], np.uint64)), ctx.alloc(16)
+    st = np.array([2024], np.uint64)
+    kw = dict(temperature=0.9, top_p=0.9, top_k=40, repetition_penalty=1.2, presence_penalty=1.0)
+    ctx.sync()
+    ctx.graph_begin()
+    ctx.sample(VOCAB, dx, dg, len(gen), dst, tok, **kw)
+    g = ctx.graph_end()
+    print("case: sample graph replays", flush=True)
+    for rep in range(5):
+        x = _logits(rng, rep % 2 == 1)
+        ctx.upload(x, dx)                                  # eager work between replays
+        g.launch()
+        ctx.sync()
+        want = O.sample_top_k(O.apply_penalties(x, gen, 1.2, 1.0), 0.9, 0.9, 40, st)[0]
+        got = int(ctx.download(tok, (1,), np.int32)[0])
+        assert (got, int(ctx.download(dst, (1,), np.uint64)[0])) == (want, int(st[0])), f"replay {rep}"
+    g.close()
