@@ -3,7 +3,7 @@
  *
  * TEST INFRASTRUCTURE ONLY.  This is a plain-C restatement of the
  * reference CPU path (Rust crate qor4b, src/gemv.rs, src/simd.rs,
- * src/convert.rs), written from reading that source.  It is the checker
+ * src/convert.rs), written from reading that source.  It is the oracle
  * that the HIP kernels are compared against and the CPU baseline that the
  * benchmark times.  Only tests/, __graft_entry__.smoke() and bench.py's
  * cpu_baseline leg may load it; the product library never links it.

@@ -877,7 +877,7 @@ int32_t qm_sample(qm_context* c, qm_stream stream, int32_t vocab, float* logits,
     if ((p->flags & ~QM_SAMPLE_WGPU) != 0) return fail(c, QM_ERR_INVALID_ARG, "qm_sample: unknown flags 0x%x", p->flags);
     const bool greedy = !(p->temperature > 0.0f);
     if (!greedy) {
-        // generate.rs:353 takes every logit for top_k = 0; this build sorts at most 1024 in one workgroup
+        // generate.rs:353 takes every logit for top_k = 0; the top-k kernel sorts at most 1024 in one workgroup
         if (p->top_k < 1 || p->top_k > 1024)
             return fail(c, QM_ERR_INVALID_ARG, "qm_sample: top_k %d (1 .. 1024 when temperature > 0)", p->top_k);
         if ((p->flags & QM_SAMPLE_WGPU) && vocab < p->top_k)
