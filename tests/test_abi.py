@@ -40,7 +40,8 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_code_objects_are_gfx950_bundles():
-    for name in ["qm_dn_decode", "qm_gqa_decode", "qm_util", "qm_dn_prefill", "qm_gqa_prefill", "qm_q4_proj"]:
+    for name in ["qm_dn_decode", "qm_gqa_decode", "qm_util", "qm_dn_prefill", "qm_gqa_prefill", "qm_q4_proj",
+                 "qm_q4_vocab", "qm_sample"]:
         p = M.LIB_DIR / f"{name}.hsaco"
         assert p.exists(), p
         data = p.read_bytes()
