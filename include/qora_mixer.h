@@ -108,6 +108,12 @@ enum {
 int32_t     qm_set_option(qm_context* ctx, int32_t option, int64_t value);
 
 /* ---- device memory, streams, events, graphs (caller plumbing) ----- */
+/* The reference's GPU path gets its device from the wgpu backend
+ * (gpu_inference.rs:987-991) and allocates through tensor constructors
+ * (GpuHybridCache::new, gpu_inference.rs:45-70); these entries are the
+ * explicit HIP equivalents a caller uses to own state, KV caches and
+ * streams.  qm_create / qm_reserve above play the part of that device
+ * set-up. */
 int32_t qm_alloc(qm_context* ctx, uint64_t bytes, void** dev);
 int32_t qm_free(qm_context* ctx, void* dev);
 int32_t qm_memcpy_h2d(qm_context* ctx, void* dst_dev, const void* src_host,
