@@ -100,3 +100,15 @@ def test_workload_generators_are_seeded(workloads):
     assert np.all((rate >= 0.01) & (rate <= 0.1))
     bits = workloads.bf16_bits(np.array([1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -2.0], np.float32))
     assert bits.tolist() == [0x3F80, 0x3F82, 0xC000]
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """The bench measures one GPU; a request for more exits with a message
+    before any device work."""
+    import subprocess
+    import sys
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120, cwd=str(ROOT))
+    assert r.returncode == 2
+    assert "--gpus 1" in (r.stdout + r.stderr)
+    assert not r.stdout.strip().startswith("{")
