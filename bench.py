@@ -35,6 +35,8 @@ ROOT = Path(__file__).resolve().parent
 HBM_PEAK = 8.0e12          # MI355X HBM3E, bytes/s
 MFMA_BF16_PEAK = 2.5e15    # MI355X dense bf16/f16 MFMA, flop/s
 N_DN, N_GQA = 24, 8        # 3x DeltaNet + 1x GQA, repeated 8 times (config.rs:44-50)
+# the sources of the GQA decode kernels whose rocprofv3 traffic is stored
+GQA_DECODE_SOURCES = ("qora-llm-4b_amd/csrc/gqa_decode.hip", "qora-llm-4b_amd/csrc/qm_gqa_common.h")
 
 
 def _load(name, path):
@@ -1158,6 +1160,86 @@ def cpu_baseline(workload: str) -> dict:
                       f"DeltaNet heads serial ({avx} update) ({dt:.1f} s)"}
 
 
+# The per-config sub-results of the default line: each single-layer workload
+# of the metric at its own default step counts, with its CPU baseline on a
+# shorter sample than the headline's.
+SUB_CONFIGS = (("dn_decode_b1", "dn_decode"), ("gqa_decode_b1_pos4096", "gqa_decode"),
+               ("dn_prefill_seq4096", "dn_prefill"), ("gqa_prefill_seq8192", "gqa_prefill"))
+SUB_CPU_SAMPLE_S = 5.0
+DEFAULT_STEPS = {"stack": (32, 4), "dn_decode": (256, 16), "gqa_decode": (200, 20),
+                 "dn_prefill": (20, 3), "gqa_prefill": (10, 2), "q4_proj": (50, 5), "q4_gemm": (20, 3),
+                 "lm_head": (100, 10), "sample": (200, 10), "decode_model": (30, 3),
+                 "prefill_model": (5, 1)}
+RUNNERS = {"stack": "run_stack", "dn_decode": "run_dn_decode", "gqa_decode": "run_gqa_decode",
+           "dn_prefill": "run_dn_prefill", "gqa_prefill": "run_gqa_prefill", "q4_proj": "run_q4_proj",
+           "q4_gemm": "run_q4_gemm", "lm_head": "run_lm_head", "sample": "run_sample",
+           "decode_model": "run_decode_model", "prefill_model": "run_prefill_model"}
+
+
+def roofline_of(r: dict) -> dict:
+    roof = r["roofline"]
+    if roof["bound"] == "mfma":
+        return {"bound": "mfma", "achieved": roof["achieved"] / 1e12, "peak": roof["peak"] / 1e12,
+                "unit": "TFLOP/s", "frac": roof["achieved"] / roof["peak"], "traffic": None,
+                "kernel": r["dominant"], "kernel_avg_ms": roof["kernel_ms"],
+                "flops_per_launch": roof["flops_per_launch"]}
+    return {"bound": roof["bound"], "achieved": roof["achieved"] / 1e9, "peak": roof["peak"] / 1e9,
+            "unit": "GB/s", "frac": roof["achieved"] / roof["peak"], "traffic": None,
+            "kernel": r["dominant"], "kernel_avg_ms": roof["kernel_ms"],
+            "bytes_per_launch": roof["bytes_per_launch"]}
+
+
+def code_hash(sources):
+    """sha256 over the sources with comments and blank space removed (so a
+    comment edit does not invalidate a measurement of the code)."""
+    import hashlib
+    import re
+    h = hashlib.sha256()
+    for src in sources:
+        text = (ROOT / src).read_text()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        text = re.sub(r"//[^\n]*", "", text)
+        h.update(re.sub(r"\s+", " ", text).strip().encode())
+    return h
+
+
+def stored_traffic(kernel_sources) -> dict:
+    """HBM bytes per launch of the stack's GQA decode from the committed
+    rocprofv3 --pmc calibration, used only while the kernel sources it was
+    measured on are unchanged (their sha256 is stored beside the figure)."""
+    tf = ROOT / "profiles" / "traffic_stack_gqa_decode.json"
+    if not tf.exists():
+        return {"traffic": None, "traffic_source": "no stored rocprofv3 calibration"}
+    rec = json.loads(tf.read_text())
+    h = code_hash(kernel_sources)
+    if rec.get("sources_sha256") != h.hexdigest():
+        return {"traffic": None,
+                "traffic_source": "stored rocprofv3 calibration is stale (kernel sources changed since)"}
+    return {"traffic": rec["traffic_bytes_per_launch"],
+            "traffic_source": "stored: rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE of this workload, scaled by a "
+                              "1 GiB copy (profiles/traffic_stack_gqa_decode.json), valid for the unchanged "
+                              "kernel sources (sha256 " + h.hexdigest()[:16] + ")"}
+
+
+def sub_config(name: str, workload: str, ctx, with_cpu: bool) -> dict:
+    ns = argparse.Namespace(steps=DEFAULT_STEPS[workload][0], warmup=DEFAULT_STEPS[workload][1],
+                            no_graph=False)
+    r = globals()[RUNNERS[workload]](ns, ctx)
+    ctx.sync()
+    rl = roofline_of(r)
+    out = {"workload": r["config"]["workload"], "steps": ns.steps, "warmup": ns.warmup,
+           "ms": rl["kernel_avg_ms"], "tokens_per_s": r["tokens"] / (r["total_ms"] * 1e-3),
+           "roofline": {k: rl[k] for k in ("bound", "achieved", "peak", "unit", "frac", "kernel")}}
+    if with_cpu:
+        global CPU_SAMPLE_S
+        saved, CPU_SAMPLE_S = CPU_SAMPLE_S, SUB_CPU_SAMPLE_S
+        try:
+            out["cpu_baseline"] = cpu_baseline(workload)
+        finally:
+            CPU_SAMPLE_S = saved
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -1167,6 +1249,9 @@ def main():
                     choices=["stack", "dn_decode", "gqa_decode", "dn_prefill", "gqa_prefill", "q4_proj",
                              "q4_gemm", "lm_head", "sample", "decode_model", "prefill_model"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-sub-configs", action="store_true",
+                    help="stack only: skip the single-layer sub-results (DeltaNet / GQA decode at batch 1, "
+                         "DeltaNet prefill of 4096 tokens, GQA prefill of 8192 tokens)")
     ap.add_argument("--no-graph", action="store_true",
                     help="skip the graph-replayed timing (rocprofv3's kernel tracer crashes in "
                          "hipGraphLaunch of a captured q4_proj step)")
@@ -1175,15 +1260,18 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="before timing, copy 1 GiB device-to-device once (a dispatch of known "
                          "traffic for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--code-hash", action="store_true",
+                    help="print the comment-insensitive sha256 of the GQA decode sources (stored beside a "
+                         "traffic measurement) and exit")
     args = ap.parse_args()
+    if args.code_hash:
+        print(code_hash(GQA_DECODE_SOURCES).hexdigest())
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the mixer path here is a single-GPU build "
               "(sharding is a design note, not a launched path); run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
-    defaults = {"stack": (32, 4), "dn_decode": (256, 16), "gqa_decode": (200, 20),
-                "dn_prefill": (20, 3), "gqa_prefill": (10, 2), "q4_proj": (50, 5), "q4_gemm": (20, 3),
-                "lm_head": (100, 10), "sample": (200, 10), "decode_model": (30, 3),
-                "prefill_model": (5, 1)}[args.workload]
+    defaults = DEFAULT_STEPS[args.workload]
     args.steps = args.steps or defaults[0]
     args.warmup = defaults[1] if args.warmup is None else args.warmup
 
@@ -1197,27 +1285,20 @@ def main():
         ctx.sync()
         src.close()
         dst.close()
-    run = {"stack": run_stack, "dn_decode": run_dn_decode, "gqa_decode": run_gqa_decode,
-           "dn_prefill": run_dn_prefill, "gqa_prefill": run_gqa_prefill,
-           "q4_proj": run_q4_proj, "q4_gemm": run_q4_gemm, "lm_head": run_lm_head,
-           "sample": run_sample, "decode_model": run_decode_model,
-           "prefill_model": run_prefill_model}[args.workload]
-    r = run(args, ctx)
+    r = globals()[RUNNERS[args.workload]](args, ctx)
     ctx.sync()
+    subs = None
+    if args.workload == "stack" and not args.no_sub_configs:
+        import gc
+        gc.collect()                      # the stack's 72 GB of buffers
+        subs = {}
+        for name, wl in SUB_CONFIGS:
+            subs[name] = sub_config(name, wl, ctx, with_cpu=not args.no_cpu_baseline)
+            gc.collect()
     ctx.close()
 
     value = r["tokens"] / (r["total_ms"] * 1e-3)
-    roof = r["roofline"]
-    if roof["bound"] == "mfma":
-        rl = {"bound": "mfma", "achieved": roof["achieved"] / 1e12, "peak": roof["peak"] / 1e12,
-              "unit": "TFLOP/s", "frac": roof["achieved"] / roof["peak"], "traffic": None,
-              "kernel": r["dominant"], "kernel_avg_ms": roof["kernel_ms"],
-              "flops_per_launch": roof["flops_per_launch"]}
-    else:
-        rl = {"bound": roof["bound"], "achieved": roof["achieved"] / 1e9, "peak": roof["peak"] / 1e9,
-              "unit": "GB/s", "frac": roof["achieved"] / roof["peak"], "traffic": None,
-              "kernel": r["dominant"], "kernel_avg_ms": roof["kernel_ms"],
-              "bytes_per_launch": roof["bytes_per_launch"]}
+    rl = roofline_of(r)
     line = {
         "metric": {"stack": "mixer tokens/s (decode, 32-layer hybrid stack) on 1x MI355X",
                    "dn_prefill": "mixer tokens/s (prefill) on 1x MI355X",
@@ -1242,14 +1323,14 @@ def main():
         "roofline": rl,
     }
     if args.workload == "stack":
-        tf = ROOT / "profiles" / "traffic_stack_gqa_decode.json"
-        if tf.exists():   # measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (see the profile summary)
-            line["roofline"]["traffic"] = json.loads(tf.read_text())["traffic_bytes_per_launch"]
+        line["roofline"].update(stored_traffic(GQA_DECODE_SOURCES))
     for k in ("kernels", "step_frac_hbm", "graph_ms_per_step", "graph_step_frac_hbm", "eager_ms_per_step"):
         if k in r:
             line[k] = r[k]
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.workload)
+    if subs is not None:
+        line["configs"] = subs
     print(json.dumps(line), flush=True)
 
 

@@ -6,10 +6,13 @@
  *   - Gated DeltaNet: recurrent decode step and chunked prefill;
  *   - full-attention GQA: decode step over an f16 KV cache and causal
  *     prefill that writes that cache.
- * Projections (in_proj_*, q/k/v/o_proj, out_proj), the MLP, lm_head and
- * sampling stay with the caller.  Each mixer entry replaces the middle of
- * one reference layer-forward (cited per entry); the surrounding
- * projection calls are unchanged.
+ * Each mixer entry replaces the middle of one reference layer-forward
+ * (cited per entry).  Around the mixer the library also exports the
+ * neighbouring steps of a decode or prefill layer, each a separate entry
+ * the caller may use or not: the Q4 projections (GEMV for decode with the
+ * RMSNorm, residual, SiLU gate/up and DeltaNet conv fused; an MFMA GEMM for
+ * prefill), lm_head and the embedding lookup, and next-token sampling.
+ * F16 projections stay with the caller.
  *
  * Conventions
  *   - Every entry returns int32_t status (QM_OK == 0); qm_status_string()
@@ -32,6 +35,11 @@
  *     the workspace for the largest batch / KV length the caller will use;
  *     without it the first larger call grows the workspace (not allowed
  *     while the stream is being captured into a graph: QM_ERR_WORKSPACE).
+ *     A grown-out-of workspace is kept, not freed, until qm_destroy: a graph
+ *     captured before the growth still holds its address and stays valid
+ *     to replay.  Graphs and eager calls of one context share the current
+ *     workspace, so they must not run concurrently (one stream at a time,
+ *     as above).
  *   - f16 / bf16 values are passed as uint16_t bit patterns.
  *
  * Shapes are those of Qor4bConfig::default_4b (config.rs:42-79):

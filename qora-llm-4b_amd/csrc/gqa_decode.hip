@@ -20,9 +20,12 @@
 // computed (a scheduling barrier keeps the compiler from sinking them), so
 // 16-32 KB per wave stay in flight.
 //   QK^T: MFMA v_mfma_f32_16x16x32_f16.  q is fp32 in the reference, so it
-//         enters as an exact two-term f16 split q = q_hi + q_lo (A rows 0..3
-//         hi, rows 4..7 lo); K comes straight from the f16 cache as the B
-//         operand; products are exact in the fp32 accumulator.
+//         enters as a two-term f16 split q ~ q_hi + q_lo (A rows 0..3 hi,
+//         rows 4..7 lo).  The pair carries about 22 of fp32's 24 mantissa
+//         bits (fewer when q_lo falls in the f16 subnormal range, i.e. for
+//         |q| below ~2^-4); each f16 x f16 product is exact in the fp32
+//         accumulator, so the score error is that split's residue, ~2^-22
+//         relative.  K comes straight from the f16 cache as the B operand.
 //   PV:   VALU; each lane owns 4 of the 256 dims of all four heads; the 64
 //         probabilities of a round are broadcast through LDS.
 #include "qm_device.h"

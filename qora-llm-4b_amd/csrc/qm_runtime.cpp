@@ -61,6 +61,10 @@ struct qm_context {
     int q4_gu_threads = 0;
     void* ws = nullptr;            // general workspace
     size_t ws_bytes = 0;
+    // Workspaces replaced by a larger one.  A graph captured earlier holds
+    // their addresses in its kernel arguments, so they stay allocated until
+    // qm_destroy.
+    std::vector<void*> retired_ws;
     std::string err;
     int64_t opt_dn_threads = 0;
     int64_t opt_gqa_chunk = 0;
@@ -117,20 +121,25 @@ bool capturing(hipStream_t s) {
     return st != hipStreamCaptureStatusNone;
 }
 
-// Grow the workspace.  Growth synchronises the device and is refused while
-// the stream is being captured.
+// Grow the workspace.  Growth is refused while the stream is being captured.
+// The old buffer is retired, not freed: graphs captured from earlier calls
+// keep its address in their kernel arguments and may be replayed later.
+// Growth is geometric (at least 1.5x) so that callers who never call
+// qm_reserve retire O(log) buffers, not one per KV-length step.
 int32_t ensure(qm_context* c, hipStream_t s, size_t ws_bytes) {
     if (ws_bytes <= c->ws_bytes) return QM_OK;
     if (capturing(s))
         return fail(c, QM_ERR_WORKSPACE,
                     "workspace must grow to %zu bytes during graph capture; "
                     "call qm_reserve() before capturing", ws_bytes);
-    QM_HIP(c, hipDeviceSynchronize());
-    if (c->ws) QM_HIP(c, hipFree(c->ws));
-    c->ws = nullptr;
-    c->ws_bytes = 0;
-    QM_HIP(c, hipMalloc(&c->ws, ws_bytes));
-    c->ws_bytes = ws_bytes;
+    size_t want = ws_bytes;
+    if (c->ws_bytes > 0) want = std::max(want, c->ws_bytes + c->ws_bytes / 2);
+    want = (want + 4095) & ~static_cast<size_t>(4095);
+    void* fresh = nullptr;
+    QM_HIP(c, hipMalloc(&fresh, want));
+    if (c->ws) c->retired_ws.push_back(c->ws);
+    c->ws = fresh;
+    c->ws_bytes = want;
     return QM_OK;
 }
 
@@ -330,6 +339,7 @@ int32_t qm_destroy(qm_context* c) {
     hipSetDevice(c->device);
     hipDeviceSynchronize();
     if (c->ws) hipFree(c->ws);
+    for (void* p : c->retired_ws) hipFree(p);
     if (c->stream) hipStreamDestroy(c->stream);
     for (hipModule_t m : c->modules) hipModuleUnload(m);
     delete c;

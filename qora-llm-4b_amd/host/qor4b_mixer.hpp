@@ -99,6 +99,11 @@ public:
         if (st != QM_OK) throw MixerError(st, qm_last_error(h_));
     }
     void sync(qm_stream s = nullptr) const { check(qm_sync(h_, s)); }
+    // Size the context's workspace once (qm_reserve), so that no later mixer
+    // call allocates or synchronises to grow it.
+    void reserve(int32_t max_batch, int32_t max_kv_len, int32_t max_prefill_tokens) const {
+        check(qm_reserve(h_, max_batch, max_kv_len, max_prefill_tokens));
+    }
 
 private:
     qm_context* h_ = nullptr;

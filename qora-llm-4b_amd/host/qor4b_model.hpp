@@ -16,6 +16,11 @@
 //                       with their projections, final norm and lm_head, all
 //                       on the device; the token id is read from device
 //                       memory, so sampling (qm_sample) can feed it directly
+//   forward_decode_no_logits_gpu
+//                       forward_decode_no_logits (gemv.rs:1033-1053): the
+//                       same layers, no final norm and no lm_head, for a
+//                       token that is already known (the forced THINK_END
+//                       of generate.rs:182)
 // The model must have the mixer's shape (Qor4bConfig::default_4b) and Q4
 // weights; other files raise MixerError(QM_ERR_SHAPE).
 #pragma once
@@ -156,6 +161,11 @@ struct GpuHybridCache {
 
     static GpuHybridCache create(Context& ctx, const GpuModel& m, std::size_t kv_capacity) {
         const Qor4bConfig cfg = Qor4bConfig::default_4b();
+        if (kv_capacity < 1 || kv_capacity > 0x7fffffffu)
+            throw MixerError(QM_ERR_INVALID_ARG, "GpuHybridCache: kv_capacity " + std::to_string(kv_capacity));
+        // decode at any position up to the capacity: the split-K partials'
+        // workspace is sized once here, not grown every 128 positions
+        ctx.reserve(1, static_cast<int32_t>(kv_capacity), 0);
         GpuHybridCache c;
         for (std::size_t i = 0; i < m.dn.size(); ++i) c.dn.push_back(GpuDeltaNetState::zeros(ctx, cfg));
         for (std::size_t i = 0; i < m.fa.size(); ++i)
@@ -184,11 +194,12 @@ struct DecodeScratch {
     }
 };
 
-// forward_decode (gemv.rs:1059-1077): logits [vocab] for the token whose id
-// is at token_dev (device int32), with every layer's state / KV cache
-// advanced by one position.
-inline void forward_decode_gpu(Context& ctx, const GpuModel& m, GpuHybridCache& cache, DecodeScratch& s,
-                               const int32_t* token_dev, float* logits_dev, qm_stream stream = nullptr) {
+namespace detail {
+
+// The embedding row and the 32 layer-forwards of one decode token; the
+// hidden state is left in s.x.
+inline void decode_layers_gpu(Context& ctx, const GpuModel& m, GpuHybridCache& cache, DecodeScratch& s,
+                              const int32_t* token_dev, qm_stream stream) {
     const Qor4bConfig cfg = Qor4bConfig::default_4b();
     const int32_t H = static_cast<int32_t>(m.config.hidden_size);
     const int32_t V = static_cast<int32_t>(m.embed.vocab);
@@ -236,8 +247,29 @@ inline void forward_decode_gpu(Context& ctx, const GpuModel& m, GpuHybridCache& 
             gemv_residual_gpu(ctx, s.inter.as<float>(), w.down_proj, x, stream);
         }
     }
-    ctx.check(qm_q4_lm_head(ctx.get(), stream, V, H, x, m.final_norm.as<uint16_t>(), m.embed.packed.as<uint8_t>(),
-                            m.embed.scales.as<uint16_t>(), logits_dev));
+}
+
+}  // namespace detail
+
+// forward_decode (gemv.rs:1059-1077): logits [vocab] for the token whose id
+// is at token_dev (device int32), with every layer's state / KV cache
+// advanced by one position.
+inline void forward_decode_gpu(Context& ctx, const GpuModel& m, GpuHybridCache& cache, DecodeScratch& s,
+                               const int32_t* token_dev, float* logits_dev, qm_stream stream = nullptr) {
+    if (!logits_dev) throw MixerError(QM_ERR_INVALID_ARG, "forward_decode_gpu: null logits");
+    detail::decode_layers_gpu(ctx, m, cache, s, token_dev, stream);
+    const int32_t H = static_cast<int32_t>(m.config.hidden_size);
+    const int32_t V = static_cast<int32_t>(m.embed.vocab);
+    ctx.check(qm_q4_lm_head(ctx.get(), stream, V, H, s.x.as<float>(), m.final_norm.as<uint16_t>(),
+                            m.embed.packed.as<uint8_t>(), m.embed.scales.as<uint16_t>(), logits_dev));
+}
+
+// forward_decode_no_logits (gemv.rs:1033-1053): every layer's state / KV
+// cache advanced by the token at token_dev, without the final norm and the
+// 248,320-row lm_head (the caller already knows the next token).
+inline void forward_decode_no_logits_gpu(Context& ctx, const GpuModel& m, GpuHybridCache& cache,
+                                         DecodeScratch& s, const int32_t* token_dev, qm_stream stream = nullptr) {
+    detail::decode_layers_gpu(ctx, m, cache, s, token_dev, stream);
 }
 
 // Device buffers a prefill of up to max_tokens works in.
@@ -248,6 +280,9 @@ struct PrefillScratch {
     static PrefillScratch create(Context& ctx, const GpuModel& m, std::size_t max_tokens) {
         const Qor4bConfig cfg = Qor4bConfig::default_4b();
         const std::size_t T = max_tokens, H = m.config.hidden_size;
+        if (T < 1 || T > 0x7fffffffu)
+            throw MixerError(QM_ERR_INVALID_ARG, "PrefillScratch: max_tokens " + std::to_string(T));
+        ctx.reserve(1, 0, static_cast<int32_t>(T));   // the chunked mixers' workspace
         PrefillScratch s;
         s.max_tokens = T;
         s.x = DeviceBuffer(ctx, T * H * 4);

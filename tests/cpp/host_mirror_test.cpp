@@ -458,6 +458,32 @@ void model_flow(Context& ctx, const Qor4bConfig& cfg) {
     }
     expect(worst <= 2e-3, "qor4b file -> device model, 4 decode steps: logits rel", worst, 2e-3);
 
+    // forward_decode_no_logits (gemv.rs:1033-1053): a forced token advances
+    // every state and cache exactly as a full decode step does, so the next
+    // step's logits are bit-identical either way
+    {
+        GpuHybridCache ca = GpuHybridCache::create(ctx, gm, 64), cb = GpuHybridCache::create(ctx, gm, 64);
+        DeviceBuffer la(ctx, V * 4), lb(ctx, V * 4);
+        const int32_t forced = 77, after = 4321;
+        tok.upload(&forced, 4);
+        forward_decode_gpu(ctx, gm, ca, scratch, tok.as<int32_t>(), la.as<float>());
+        forward_decode_no_logits_gpu(ctx, gm, cb, scratch, tok.as<int32_t>());
+        tok.upload(&after, 4);
+        forward_decode_gpu(ctx, gm, ca, scratch, tok.as<int32_t>(), la.as<float>());
+        forward_decode_gpu(ctx, gm, cb, scratch, tok.as<int32_t>(), lb.as<float>());
+        std::vector<float> ga(V), gb(V);
+        la.download(ga.data(), V * 4);
+        lb.download(gb.data(), V * 4);
+        const std::size_t ns = cfg.num_v_heads * cfg.deltanet_head_dim * cfg.deltanet_head_dim;
+        std::vector<float> sa(ns), sb(ns);
+        ca.dn[0].s.download(sa.data(), ns * 4);
+        cb.dn[0].s.download(sb.data(), ns * 4);
+        const bool same = std::memcmp(ga.data(), gb.data(), V * 4) == 0 &&
+                          std::memcmp(sa.data(), sb.data(), ns * 4) == 0;
+        expect(same, "forward_decode_no_logits then a decode step == two decode steps (bit-identical; 1 = differs)",
+               same ? 0 : 1, 0.5);
+    }
+
     // prefill (gemv.rs:1243-1283) of a 37-token prompt on a fresh cache, on
     // MFMA with f16 / bf16 activations, against the oracle's f32 prefill
     // composed from its restatements; then one decode step continuing from

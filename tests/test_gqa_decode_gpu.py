@@ -158,3 +158,38 @@ def test_decode_graph_replay_matches_eager(ctx):
         assert np.array_equal(ctx.download(out_g, (2, 16 * 256), np.float32), ref)
         step(out_e)                                                           # eager work in between
         ctx.sync()
+
+
+def test_graph_survives_workspace_growth():
+    """A graph captured on a context whose workspace later grows (an eager call
+    at a longer KV length, no qm_reserve) still replays to the same result:
+    the grown-out-of workspace stays allocated while the context lives."""
+    pos_small, pos_big = 300, 4000
+    w = W.gqa_decode_workload(pos_big, 2, seed=12)
+    cos, sin = M.rope_table(pos_big + 1)
+    with M.Context(0) as c:                    # fresh context: workspace starts empty
+        d = {k: c.upload(w[k]) for k in ["q_gate", "k_new", "v_new", "q_norm", "k_norm", "k_cache", "v_cache"]}
+        rc, rs = c.upload(cos), c.upload(sin)
+        out_e, out_g = c.alloc(2 * 16 * 256 * 4), c.alloc(2 * 16 * 256 * 4)
+        c.set_option(M.QM_OPT_GQA_DECODE_CHUNK, 64)   # many splits: the partials grow with the length
+
+        def step(pos, out):
+            c.gqa_decode(2, d["q_gate"], d["k_new"], d["v_new"], d["q_norm"], d["k_norm"], rc, rs, pos_big + 1,
+                         None, pos, d["k_cache"], d["v_cache"], w["cap"], out)
+
+        print("case: gqa decode graph, then workspace growth", flush=True)
+        step(pos_small, out_e)                  # sizes the workspace for pos 300
+        ref = c.download(out_e, (2, 16 * 256), np.float32)
+        c.graph_begin()
+        step(pos_small, out_g)
+        g = c.graph_end()
+        step(pos_big, out_e)                    # grows the workspace (79 splits vs 5)
+        c.sync()
+        for rep in range(3):
+            c.fill_normal(out_g, M.QM_F32, 2 * 16 * 256, 0.0, 1.0, seed=rep)
+            g.launch()
+            c.sync()
+            assert np.array_equal(c.download(out_g, (2, 16 * 256), np.float32), ref)
+            step(pos_big, out_e)
+            c.sync()
+        g.close()
