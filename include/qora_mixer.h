@@ -239,6 +239,27 @@ int32_t qm_gqa_decode(qm_context* ctx, qm_stream stream, int32_t batch,
                       uint16_t* k_cache_dev, uint16_t* v_cache_dev,
                       int64_t cache_capacity, float* out_dev);
 
+/* qm_gqa_decode without any device allocation: no counterpart in the
+ * reference.  For callers that cannot allocate device memory at call time
+ * (code under HIP graph capture without a prior qm_reserve, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments, kernels, launch
+ * shapes and results as qm_gqa_decode, bit for bit; the split partials go to
+ * a fixed 32 MiB scratch array each GPU holds for the life of the process
+ * (batch x 4 x splits <= 8065, i.e. e.g. batch 64 up to ~63K positions at
+ * the automatic split size), and a call that needs more is refused with
+ * QM_ERR_WORKSPACE before anything is enqueued.  Every call on a GPU, from
+ * any context, shares that GPU's array: calls that overlap in time on one
+ * GPU (other streams, other contexts or threads) race and must be ordered
+ * by the caller. */
+int32_t qm_gqa_decode_noalloc(qm_context* ctx, qm_stream stream, int32_t batch,
+                              const float* q_gate_dev, const float* k_new_dev,
+                              const float* v_new_dev, const uint16_t* q_norm_dev,
+                              const uint16_t* k_norm_dev, const float* rope_cos_dev,
+                              const float* rope_sin_dev, int32_t rope_len,
+                              const int32_t* pos_dev, int32_t max_pos,
+                              uint16_t* k_cache_dev, uint16_t* v_cache_dev,
+                              int64_t cache_capacity, float* out_dev);
+
 /* ---- GQA causal prefill ---------------------------------------------- */
 /* Replaces the mixer slice of prefill_attn_layer, gemv.rs:1364-1444
  * (wgpu twin prefill_attn_layer_gpu, gpu_inference.rs:679-766): per-token

@@ -46,20 +46,30 @@ def hip_cmd(name: str) -> list[str]:
             str(CSRC / f"{name}.hip"), "-o", str(LIB / f"qm_{name}.hsaco")]
 
 
+def noalloc_cmd() -> list[str]:
+    """csrc/qm_noalloc.hip, the fixed device scratch of the allocation-free
+    entry point, compiled into an object of the host library itself (its
+    device array lives in the library's own gfx950 fat binary)."""
+    flags = [f for f in HIPCC_FLAGS if f != "--genco"]
+    return [str(ROCM / "bin" / "hipcc"), *flags, "-fPIC", "-c", "-I", str(CSRC),
+            str(CSRC / "qm_noalloc.hip"), "-o", str(LIB / "qm_noalloc.o")]
+
+
 def host_cmd() -> list[str]:
     return ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off",
             "-Wall", "-Wextra", "-Wno-unused-result", "-D__HIP_PLATFORM_AMD__",
             "-I", str(ROOT / "include"), "-I", str(CSRC), "-I", str(ROCM / "include"),
-            str(CSRC / "qm_runtime.cpp"), "-o", str(LIB / "libqora_mixer.so"),
+            str(CSRC / "qm_runtime.cpp"), str(LIB / "qm_noalloc.o"), "-o", str(LIB / "libqora_mixer.so"),
             f"-L{ROCM / 'lib'}", "-lamdhip64", f"-Wl,-rpath,{ROCM / 'lib'}", "-ldl"]
 
 
 def build(jobs: int = 8) -> None:
     LIB.mkdir(exist_ok=True)
-    cmds = [hip_cmd(k) for k in KERNELS] + [host_cmd()]
+    cmds = [hip_cmd(k) for k in KERNELS] + [noalloc_cmd()]
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         for f in [ex.submit(_run, c) for c in cmds]:
             f.result()
+    _run(host_cmd())
 
 
 def build_oracle() -> None:

@@ -10,6 +10,7 @@
 // outside stream capture.
 #include "qora_mixer.h"
 #include "qm_kernel_args.h"
+#include "qm_noalloc.h"
 
 #include <hip/hip_runtime_api.h>
 #include <dlfcn.h>
@@ -69,6 +70,10 @@ struct qm_context {
     int64_t opt_dn_threads = 0;
     int64_t opt_gqa_chunk = 0;
     int num_cu = 0;                // compute units of the device
+    // this device's copy of the fixed scratch array of the allocation-free
+    // entry point (qm_noalloc.hip), resolved at qm_create; null if that failed
+    void* noalloc_scratch = nullptr;
+    std::string noalloc_err;
 };
 
 struct qm_graph {
@@ -325,6 +330,16 @@ int32_t qm_create(qm_context** out, const qm_config* cfg, const char* code_objec
         st = fail(c, QM_ERR_CODE_OBJECT, "qm_q4_gemv: cannot read its workgroup size");
     if (st == QM_OK && hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess)
         st = fail(c, QM_ERR_HIP, "hipStreamCreate failed");
+    if (st == QM_OK) {
+        // once per device, with the device current (set above): the address
+        // of its copy of the no-alloc scratch array
+        const int e = qm_noalloc_scratch(device, &c->noalloc_scratch);
+        if (e != 0) {
+            c->noalloc_scratch = nullptr;
+            c->noalloc_err = std::string("hipGetSymbolAddress(scratch): ") +
+                             hipGetErrorString(static_cast<hipError_t>(e));
+        }
+    }
     if (st != QM_OK) {
         g_create_error = c->err;
         qm_destroy(c);
@@ -580,11 +595,17 @@ static int64_t gqa_auto_chunk(int64_t len, int32_t batch) {
     return std::max<int64_t>(128, std::min<int64_t>(ch, 2048));
 }
 
-int32_t qm_gqa_decode(qm_context* c, qm_stream stream, int32_t batch, const float* q_gate,
-                      const float* k_new, const float* v_new, const uint16_t* q_norm,
-                      const uint16_t* k_norm, const float* rope_cos, const float* rope_sin,
-                      int32_t rope_len, const int32_t* pos, int32_t max_pos, uint16_t* k_cache,
-                      uint16_t* v_cache, int64_t cap, float* out) {
+}  // extern "C"
+
+namespace {
+// qm_gqa_decode and qm_gqa_decode_noalloc: the same checks, launch shapes and
+// kernels; the split partials go to the context's workspace (grown if
+// needed) or to the device's fixed scratch array (never allocated here).
+int32_t gqa_decode_impl(qm_context* c, qm_stream stream, int32_t batch, const float* q_gate,
+                        const float* k_new, const float* v_new, const uint16_t* q_norm,
+                        const uint16_t* k_norm, const float* rope_cos, const float* rope_sin,
+                        int32_t rope_len, const int32_t* pos, int32_t max_pos, uint16_t* k_cache,
+                        uint16_t* v_cache, int64_t cap, float* out, bool noalloc) {
     if (!c) return QM_ERR_INVALID_ARG;
     if (batch <= 0) return fail(c, QM_ERR_INVALID_ARG, "qm_gqa_decode: batch %d", batch);
     if (!q_gate || !k_new || !v_new || !q_norm || !k_norm || !rope_cos || !rope_sin || !k_cache ||
@@ -605,15 +626,51 @@ int32_t qm_gqa_decode(qm_context* c, qm_stream stream, int32_t batch, const floa
     const uint64_t grid = static_cast<uint64_t>(batch) * QM_GQA_KV_HEADS * nsplit;
     if (grid > 0x7fffffffull) return fail(c, QM_ERR_INVALID_ARG, "qm_gqa_decode: grid too large");
     const size_t part_bytes = nsplit > 1 ? static_cast<size_t>(grid) * 4 * 260 * sizeof(float) : 0;
-    int32_t st = ensure(c, s, part_bytes);
-    if (st != QM_OK) return st;
+    float* partials = nullptr;
+    if (noalloc) {
+        if (!c->noalloc_scratch)
+            return fail(c, QM_ERR_HIP, "qm_gqa_decode_noalloc: the device scratch is unavailable (%s)",
+                        c->noalloc_err.c_str());
+        if (part_bytes > QM_NOALLOC_SCRATCH_BYTES)
+            return fail(c, QM_ERR_WORKSPACE,
+                        "qm_gqa_decode_noalloc: %lld splits of %lld keys for batch %d need %zu bytes of "
+                        "partials; the fixed scratch holds %u (batch x 4 x splits <= %u)",
+                        static_cast<long long>(nsplit), static_cast<long long>(chunk), batch, part_bytes,
+                        QM_NOALLOC_SCRATCH_BYTES, QM_NOALLOC_SCRATCH_BYTES / (4 * 260 * 4));
+        partials = static_cast<float*>(c->noalloc_scratch);
+    } else {
+        const int32_t st = ensure(c, s, part_bytes);
+        if (st != QM_OK) return st;
+        partials = static_cast<float*>(c->ws);
+    }
     GqaDecodeArgs ga{q_gate, k_new, v_new, q_norm, k_norm, rope_cos, rope_sin, pos, k_cache, v_cache,
-                     out, static_cast<float*>(c->ws), cap, max_pos,
+                     out, partials, cap, max_pos,
                      static_cast<int32_t>(chunk), static_cast<int32_t>(nsplit), batch};
-    st = launch(c, c->f_gqa_split, static_cast<uint32_t>(grid), 256, ga, s, "qm_gqa_decode_split");
+    int32_t st = launch(c, c->f_gqa_split, static_cast<uint32_t>(grid), 256, ga, s, "qm_gqa_decode_split");
     if (st != QM_OK || nsplit == 1) return st;
     return launch(c, c->f_gqa_merge, static_cast<uint32_t>(batch) * QM_GQA_KV_HEADS * 4, 1024, ga, s,
                   "qm_gqa_decode_merge");
+}
+}  // namespace
+
+extern "C" {
+
+int32_t qm_gqa_decode(qm_context* c, qm_stream stream, int32_t batch, const float* q_gate,
+                      const float* k_new, const float* v_new, const uint16_t* q_norm,
+                      const uint16_t* k_norm, const float* rope_cos, const float* rope_sin,
+                      int32_t rope_len, const int32_t* pos, int32_t max_pos, uint16_t* k_cache,
+                      uint16_t* v_cache, int64_t cap, float* out) {
+    return gqa_decode_impl(c, stream, batch, q_gate, k_new, v_new, q_norm, k_norm, rope_cos, rope_sin, rope_len,
+                           pos, max_pos, k_cache, v_cache, cap, out, false);
+}
+
+int32_t qm_gqa_decode_noalloc(qm_context* c, qm_stream stream, int32_t batch, const float* q_gate,
+                              const float* k_new, const float* v_new, const uint16_t* q_norm,
+                              const uint16_t* k_norm, const float* rope_cos, const float* rope_sin,
+                              int32_t rope_len, const int32_t* pos, int32_t max_pos, uint16_t* k_cache,
+                              uint16_t* v_cache, int64_t cap, float* out) {
+    return gqa_decode_impl(c, stream, batch, q_gate, k_new, v_new, q_norm, k_norm, rope_cos, rope_sin, rope_len,
+                           pos, max_pos, k_cache, v_cache, cap, out, true);
 }
 
 int32_t qm_reserve(qm_context* c, int32_t max_batch, int32_t max_kv_len, int32_t max_prefill_tokens) {

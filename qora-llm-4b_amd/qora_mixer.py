@@ -98,6 +98,7 @@ _SIGNATURES = {
     "qm_deltanet_decode": [_P, _P, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P],
     "qm_deltanet_prefill": [_P, _P, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P],
     "qm_gqa_decode": [_P, _P, _I32, _P, _P, _P, _P, _P, _P, _P, _I32, _P, _I32, _P, _P, _I64, _P],
+    "qm_gqa_decode_noalloc": [_P, _P, _I32, _P, _P, _P, _P, _P, _P, _P, _I32, _P, _I32, _P, _P, _I64, _P],
     "qm_gqa_prefill": [_P, _P, _I32, _P, _P, _P, _P, _P, _P, _P, _I32, _P, _P, _I64, _P],
     "qm_q4_repack": [_P, _P, _I32, _I32, _P, _P, _P, _P],
     "qm_q4_gemv": [_P, _P, _I32, _I32, _P, _P, _P, _P],
@@ -301,6 +302,14 @@ class Context:
     def gqa_decode(self, batch, q_gate, k_new, v_new, q_norm, k_norm, rope_cos, rope_sin,
                    rope_len, pos, max_pos, k_cache, v_cache, cap, out):
         self._check(self.lib.qm_gqa_decode(
+            self.h, self.stream, batch, _addr(q_gate), _addr(k_new), _addr(v_new), _addr(q_norm),
+            _addr(k_norm), _addr(rope_cos), _addr(rope_sin), rope_len, _addr(pos), max_pos,
+            _addr(k_cache), _addr(v_cache), cap, _addr(out)))
+
+    def gqa_decode_noalloc(self, batch, q_gate, k_new, v_new, q_norm, k_norm, rope_cos, rope_sin,
+                           rope_len, pos, max_pos, k_cache, v_cache, cap, out):
+        """qm_gqa_decode with its partials in the device's fixed scratch array (no allocation)."""
+        self._check(self.lib.qm_gqa_decode_noalloc(
             self.h, self.stream, batch, _addr(q_gate), _addr(k_new), _addr(v_new), _addr(q_norm),
             _addr(k_norm), _addr(rope_cos), _addr(rope_sin), rope_len, _addr(pos), max_pos,
             _addr(k_cache), _addr(v_cache), cap, _addr(out)))
