@@ -909,8 +909,10 @@ def run_sample(args, ctx):
     }
 
 
-def _repeat_for(fn, min_s=CPU_SAMPLE_S, max_iters=10 ** 6):
-    """Call fn() until min_s seconds have elapsed; returns (calls, seconds)."""
+def _repeat_for(fn, min_s=None, max_iters=10 ** 6):
+    """Call fn() until min_s (default CPU_SAMPLE_S) seconds have elapsed;
+    returns (calls, seconds)."""
+    min_s = CPU_SAMPLE_S if min_s is None else min_s
     n, t0 = 0, time.perf_counter()
     while True:
         fn()

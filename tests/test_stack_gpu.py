@@ -39,8 +39,18 @@ def test_stack_b64_ctx32k_two_steps():
     dn_par = [W.dn_params(rng) for _ in range(N_DN)]
     gqa_par = [{"q_norm": W.f16_bits(0.1 * rng.standard_normal(256, dtype=np.float32)),
                 "k_norm": W.f16_bits(0.1 * rng.standard_normal(256, dtype=np.float32))} for _ in range(N_GQA)]
+    # per (step, layer): inputs of the 64 sequences, dn_in[s, l, b] = qkv | a | b | z of sequence b
     dn_in = rng.standard_normal((STEPS, N_DN, B, DN_IN), dtype=np.float32)
     gqa_in = rng.standard_normal((STEPS, N_GQA, B, GQA_IN), dtype=np.float32)
+
+    def device_blocks(x, widths):
+        # the entry points take each input as its own [64][width] array: per
+        # (step, layer) the blocks [qkv 64 x 8192 | a 64 x 32 | ...] one after another
+        out, o = [], 0
+        for wd in widths:
+            out.append(x[..., o:o + wd].reshape(x.shape[0], x.shape[1], -1))
+            o += wd
+        return np.ascontiguousarray(np.concatenate(out, axis=2))
     rope_rows = CAP
     cos, sin = M.rope_table(rope_rows)
 
@@ -66,7 +76,8 @@ def test_stack_b64_ctx32k_two_steps():
                 c.fill_normal(s, M.QM_F32, B * S_SEQ, 0.0, 0.02, seed=7000 + i)
             for i, buf in enumerate(kcs + vcs):
                 c.fill_normal(buf, M.QM_F16, B * KV_SEQ, 0.0, 1.0, seed=8000 + i)
-            din, gin = c.upload(dn_in), c.upload(gqa_in)
+            din = c.upload(device_blocks(dn_in, (8192, 32, 32, 4096)))
+            gin = c.upload(device_blocks(gqa_in, (16 * 512, 4 * 256, 4 * 256)))
             bufs += [din, gin]
             dn_out = alloc(STEPS * N_DN * B * 4096 * 4)
             gqa_out = alloc(STEPS * N_GQA * B * 4096 * 4)
