@@ -1255,8 +1255,9 @@ def main():
                     help="stack only: skip the single-layer sub-results (DeltaNet / GQA decode at batch 1, "
                          "DeltaNet prefill of 4096 tokens, GQA prefill of 8192 tokens)")
     ap.add_argument("--no-graph", action="store_true",
-                    help="skip the graph-replayed timing (rocprofv3's kernel tracer crashes in "
-                         "hipGraphLaunch of a captured q4_proj step)")
+                    help="skip the graph-replayed timing, e.g. to profile the q4_proj workload from eager "
+                         "launches (a traced replay of its captured step once ended in a host-side SIGSEGV "
+                         "inside the tracer's hipGraphLaunch callback)")
     ap.add_argument("--gqa-chunk", type=int, default=0,
                     help="keys per GQA decode split workgroup (multiple of 64; 0 = the library's choice)")
     ap.add_argument("--calibrate-copy", action="store_true",
