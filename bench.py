@@ -722,7 +722,7 @@ def run_prefill_model(args, ctx):
     x, xn = ctx.alloc(T * H * 4), ctx.alloc(T * H * 2)
     proj, z16, mix16 = ctx.alloc(T * 8192 * 2), ctx.alloc(T * 4096 * 2), ctx.alloc(T * 4096 * 2)
     a, b, k16, v16 = ctx.alloc(T * 32 * 4), ctx.alloc(T * 32 * 4), ctx.alloc(T * 1024 * 2), ctx.alloc(T * 1024 * 2)
-    inter16, logits = ctx.alloc(T * 9216 * 2), ctx.alloc(V * 4)
+    inter_bf16, logits = ctx.alloc(T * 9216 * 2), ctx.alloc(V * 4)
     ctx.reserve(max_batch=1, max_kv_len=T, max_prefill_tokens=T)
     ctx.sync()
     gemm_timer = Timer(ctx)
@@ -747,8 +747,8 @@ def run_prefill_model(args, ctx):
                                 mix16)
                 ctx.q4_gemm(T, 4096, H, mix16, *L["o_proj"], y=x, residual=x, x_dtype=M.QM_BF16)
             ctx.rms_norm_f16(T, H, x, L["post_norm"], xn)
-            ctx.q4_gemm_gate_up(T, H, 9216, xn, *L["gate_proj"], *L["up_proj"], inter16)
-            ctx.q4_gemm(T, 9216, H, inter16, *L["down_proj"], y=x, residual=x)
+            ctx.q4_gemm_gate_up(T, H, 9216, xn, *L["gate_proj"], *L["up_proj"], inter_bf16)
+            ctx.q4_gemm(T, 9216, H, inter_bf16, *L["down_proj"], y=x, residual=x, x_dtype=M.QM_BF16)
         ctx.q4_lm_head(V, H, x.offset((T - 1) * H * 4), final_norm, emb_codes, emb_scales, logits)
 
     for _ in range(Wm):

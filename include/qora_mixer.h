@@ -372,7 +372,11 @@ int32_t qm_rms_norm_f16(qm_context* ctx, qm_stream stream, int32_t m, int32_t k,
  * e.g. the in_proj_qkv / in_proj_z outputs that qm_deltanet_prefill reads)
  * is non-NULL.  W is dequantized to f16 per element (s * (q - 8), one
  * rounding) and x is f16: a bf16-path result, within 1e-3 of
- * sum_k |x_k W_kj| of the fp32 reference per element. */
+ * sum_k |x_k W_kj| of the fp32 reference per element.  A bf16 input keeps
+ * bf16's range: a row whose values in a 32-wide k step pass f16's range is
+ * staged times a power of two 2^-s and its fp32 accumulators rescaled by
+ * 2^s, so outliers up to bf16's range give finite results at the same
+ * relative precision. */
 int32_t qm_q4_gemm(qm_context* ctx, qm_stream stream, int32_t m, int32_t k, int32_t n,
                    const uint16_t* x_dev, int32_t x_dtype, const uint8_t* codes_dev,
                    const uint16_t* gscales_dev, const float* residual_dev,
@@ -380,15 +384,17 @@ int32_t qm_q4_gemm(qm_context* ctx, qm_stream stream, int32_t m, int32_t k, int3
 
 /* The prefill MLP's gate and up projections and their SiLU product
  * (gemv.rs:1231-1237: gemm(gate_proj), gemm(up_proj), then
- * silu(g) * u per element) in one launch: out_f16_dev [m][n] =
- * f16(silu(x Wg) * (x Wu)), the input of the down_proj qm_q4_gemm.  Both
- * weights are k x n in the device layout; x as for qm_q4_gemm.  Values of
- * the product beyond the f16 range become +-inf. */
+ * silu(g) * u per element) in one launch: out_dev bf16 [m][n] =
+ * bf16(silu(x Wg) * (x Wu)), the input of the down_proj qm_q4_gemm
+ * (x_dtype QM_BF16).  bf16 holds any product of the fp32 accumulators (the
+ * reference keeps this intermediate in f32, gemv.rs:469-526), so outlier
+ * activations stay finite.  Both weights are k x n in the device layout; x
+ * as for qm_q4_gemm. */
 int32_t qm_q4_gemm_gate_up(qm_context* ctx, qm_stream stream, int32_t m, int32_t k, int32_t n,
                            const uint16_t* x_dev, int32_t x_dtype,
                            const uint8_t* gate_codes_dev, const uint16_t* gate_gscales_dev,
                            const uint8_t* up_codes_dev, const uint16_t* up_gscales_dev,
-                           uint16_t* out_f16_dev);
+                           uint16_t* out_dev);
 
 /* ---- vocabulary side of a step: embedding lookup and lm_head ---------- */
 /* The embedding (tied to lm_head) stays in the reference layout, a

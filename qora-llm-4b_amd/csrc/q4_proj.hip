@@ -272,22 +272,50 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2 __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-// Two bf16 values (one 32-bit word) as two f16, each rounded to nearest even.
-__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t v) {
-    const half2 h = half2{(_Float16)__builtin_bit_cast(float, v << 16),
-                          (_Float16)__builtin_bit_cast(float, v & 0xffff0000u)};
+// Two bf16 values (one 32-bit word) times 2^-s as two f16, each rounded to
+// nearest even (the power-of-two factor is exact in fp32).
+__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t v, int s) {
+    const float lo = __builtin_amdgcn_ldexpf(__builtin_bit_cast(float, v << 16), -s);
+    const float hi = __builtin_amdgcn_ldexpf(__builtin_bit_cast(float, v & 0xffff0000u), -s);
+    const half2 h = half2{(_Float16)lo, (_Float16)hi};
     return __builtin_bit_cast(uint32_t, h);
 }
 
-__device__ __forceinline__ uint4 bf16x8_to_f16x8(uint4 v) {
-    return make_uint4(bf16x2_to_f16x2(v.x), bf16x2_to_f16x2(v.y), bf16x2_to_f16x2(v.z), bf16x2_to_f16x2(v.w));
+__device__ __forceinline__ uint4 bf16x8_to_f16x8(uint4 v, int s) {
+    return make_uint4(bf16x2_to_f16x2(v.x, s), bf16x2_to_f16x2(v.y, s), bf16x2_to_f16x2(v.z, s),
+                      bf16x2_to_f16x2(v.w, s));
 }
 
-// XBF16: x is bf16, converted to f16 as it is staged.  GU: the gate/up form.
-// The workgroup's 256 W rows of LDS are then 16-column fragments of the gate
-// and up weights alternately, over 128 output columns, so a wave's fragments
-// j (gate) and j + 1 (up) hold the same outputs and the epilogue writes
-// silu(g) * u as f16.
+// Largest |x| of eight bf16 values, as the 15-bit magnitude pattern (ordered
+// like the values themselves).
+__device__ __forceinline__ uint32_t bf16x8_maxmag(uint4 v) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) m = max(m, max(w[i] & 0x7fffu, (w[i] >> 16) & 0x7fffu));
+    return m;
+}
+
+// The power of two s >= 0 that brings a row whose largest bf16 magnitude is
+// mag below 2^15: 0 for every value f16 holds (mag <= 0x477f, 65280), else
+// the biased exponent minus 141.
+__device__ __forceinline__ int f16_range_shift(uint32_t mag) {
+    return mag <= 0x477fu ? 0 : (int)(mag >> 7) - 141;
+}
+
+// XBF16: x is bf16, converted to f16 as it is staged.  bf16 has fp32's range
+// and f16 does not, so a row of a k step whose bf16 values reach past f16's
+// range (|x| > 65280) is staged times 2^-s (s from its largest value, so the
+// row stays below 2^15) and its accumulators are multiplied by 2^-s before
+// that step's products and by 2^s after them: exact powers of two, so such
+// a row is accumulated at the same relative precision as any other.  Rows
+// of ordinary range (s = 0: every row of every k step in practice) take the
+// plain path; the check costs one LDS read and a ballot per k step.
+// GU: the gate/up form.  The workgroup's 256 W rows of LDS are then
+// 16-column fragments of the gate and up weights alternately, over 128
+// output columns, so a wave's fragments j (gate) and j + 1 (up) hold the
+// same outputs and the epilogue writes silu(g) * u as bf16 (whose range,
+// unlike f16's, holds any product of the fp32 accumulators).
 // Workgroup tiles TM x TN: 128 x 256, four waves of 64 x 128 (2 x 2); for
 // narrow outputs whose 128 x 256 tiles would leave CUs idle (n = 2560: 10
 // column tiles), 128 x 128 (2 x 2 waves of 64 x 64), twice the workgroups;
@@ -300,6 +328,7 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
     constexpr int NJ = TN / (16 * (TM == 128 ? 2 : 4));  // 16-column fragments per wave
     __shared__ __attribute__((aligned(16))) _Float16 sA[2][TM][GM_LDK];
     __shared__ __attribute__((aligned(16))) _Float16 sB[2][TN][GM_LDK];
+    __shared__ int sShift[2][XBF16 ? TM : 1];            // per row: the k step's 2^-s staging factor
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     constexpr int NCOLS = GU ? TN / 2 : TN;              // output columns per workgroup
     const int nbn = (A.n + NCOLS - 1) / NCOLS;
@@ -351,9 +380,20 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
     // fp32).  Column n's four rows are one 8-byte store.
 #define GM_LSTORE(buf)                                                                 \
     do {                                                                               \
-        *reinterpret_cast<uint4*>(&sA[buf][ar][XH * ah]) = XBF16 ? bf16x8_to_f16x8(ra0) : ra0; \
-        if (XH == 16)                                                                  \
-            *reinterpret_cast<uint4*>(&sA[buf][ar][XH * ah + 8]) = XBF16 ? bf16x8_to_f16x8(ra1) : ra1; \
+        if constexpr (XBF16) {                                                         \
+            /* the 32 / XH threads of a row are adjacent lanes */                      \
+            uint32_t mag_ = bf16x8_maxmag(ra0);                                        \
+            if (XH == 16) mag_ = max(mag_, bf16x8_maxmag(ra1));                        \
+            _Pragma("unroll") for (int o_ = 1; o_ < 32 / XH; o_ <<= 1)                 \
+                mag_ = max(mag_, (uint32_t)__shfl_xor((int)mag_, o_));                 \
+            const int sh_ = f16_range_shift(mag_);                                     \
+            if (ah == 0) sShift[buf][ar] = sh_;                                        \
+            *reinterpret_cast<uint4*>(&sA[buf][ar][XH * ah]) = bf16x8_to_f16x8(ra0, sh_); \
+            if (XH == 16) *reinterpret_cast<uint4*>(&sA[buf][ar][XH * ah + 8]) = bf16x8_to_f16x8(ra1, sh_); \
+        } else {                                                                       \
+            *reinterpret_cast<uint4*>(&sA[buf][ar][XH * ah]) = ra0;                    \
+            if (XH == 16) *reinterpret_cast<uint4*>(&sA[buf][ar][XH * ah + 8]) = ra1;  \
+        }                                                                              \
         const half2 s01 = __builtin_bit_cast(half2, rs.x), s23 = __builtin_bit_cast(half2, rs.y); \
         if (TN == 256 || tid < TN) _Pragma("unroll") for (int b_ = 0; b_ < 4; ++b_) {  \
             const uint32_t sel = 0x0c040c00u + 0x00010001u * b_;                       \
@@ -387,6 +427,26 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
         half8 af[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const half8*>(&sA[b][64 * wm + 16 * i + fr][fk]);
+        // rows of this step staged times 2^-s (bf16 input past f16's range):
+        // lane l holds the shift of wave row l; a C fragment row 16 i + 4 q + e
+        // takes it by a lane shuffle
+        int rsh = 0;
+        bool scaled = false;
+        if constexpr (XBF16) {
+            rsh = sShift[b][64 * wm + lane];
+            scaled = __builtin_amdgcn_ballot_w64(rsh != 0) != 0;     // wave-uniform
+        }
+        auto rescale = [&](int sign) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int sh = sign * __shfl(rsh, 16 * i + 4 * (lane >> 4) + e);
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j) acc[i][j][e] = __builtin_amdgcn_ldexpf(acc[i][j][e], sh);
+                }
+        };
+        if (scaled) rescale(-1);
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
             const half8 bf = *reinterpret_cast<const half8*>(&sB[b][16 * NJ * wn + 16 * j + fr][fk]);
@@ -394,6 +454,7 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
             for (int i = 0; i < 4; ++i)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf, acc[i][j], 0, 0, 0);
         }
+        if (scaled) rescale(1);
         // the other buffer was last read in step kt - 1, before the barrier
         if (kt + 1 < nk) GM_LSTORE(b ^ 1);
         __syncthreads();
@@ -414,7 +475,7 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
                     const int row = m0 + 64 * wm + 16 * i + 4 * (lane >> 4) + e;
                     if (row >= A.m) continue;
                     const float g = acc[i][j][e], u = acc[i][j + 1][e];
-                    A.y_f16[(size_t)row * A.n + col] = __builtin_bit_cast(uint16_t, (_Float16)(g / (1.0f + expf(-g)) * u));
+                    A.y_bf16[(size_t)row * A.n + col] = f32_to_bf16(g / (1.0f + expf(-g)) * u);
                 }
         }
         return;

@@ -156,7 +156,7 @@ struct Q4RepackArgs {
 // Q4 prefill GEMM: y[m][n] = x[m][k] W (+ residual), x f16 or bf16, W in
 // the device layout; output f32 (y) or bf16 (y_bf16 non-null).  The gate/up
 // form reads two weights (codes/gscales the gate, codes2/gscales2 the up
-// weight) and writes y_f16 = silu(x Wg) * (x Wu).  k % 32 == 0.
+// weight) and writes y_bf16 = silu(x Wg) * (x Wu).  k % 32 == 0.
 struct Q4GemmArgs {
     const uint16_t* x;       // f16 or bf16 [m][k]
     const uint8_t* codes;    // [n/T][k][T/2]
@@ -164,8 +164,7 @@ struct Q4GemmArgs {
     const uint8_t* codes2;   // gate/up form: the up weight
     const uint16_t* gscales2;
     float* y;                // f32 [m][n]
-    uint16_t* y_bf16;        // or bf16 [m][n]
-    uint16_t* y_f16;         // gate/up form: f16 [m][n]
+    uint16_t* y_bf16;        // or bf16 [m][n] (the gate/up form's output)
     const float* residual;   // null, or f32 [m][n]
     int32_t m;
     int32_t k;

@@ -998,7 +998,7 @@ int32_t qm_q4_gemm(qm_context* c, qm_stream stream, int32_t m, int32_t k, int32_
         return fail(c, QM_ERR_INVALID_ARG, "qm_q4_gemm: null pointer, or not exactly one of y / y_bf16");
     if (!all_aligned16({x, codes, gscales, residual, y, y_bf16}))
         return fail(c, QM_ERR_INVALID_ARG, "qm_q4_gemm: device pointers must be 16-byte aligned");
-    Q4GemmArgs ga{x, codes, gscales, nullptr, nullptr, y, y_bf16, nullptr, residual, m, k, n, QM_Q4_TILE(n)};
+    Q4GemmArgs ga{x, codes, gscales, nullptr, nullptr, y, y_bf16, residual, m, k, n, QM_Q4_TILE(n)};
     const int64_t ncol = (n + 255) / 256;
     const int64_t tiles128 = (m + 127) / 128 * ncol;
     // too few 128 x 256 tiles for two workgroups per CU (e.g. n = 2560): 128 x 128 tiles
@@ -1012,16 +1012,16 @@ int32_t qm_q4_gemm(qm_context* c, qm_stream stream, int32_t m, int32_t k, int32_
 
 int32_t qm_q4_gemm_gate_up(qm_context* c, qm_stream stream, int32_t m, int32_t k, int32_t n, const uint16_t* x,
                            int32_t x_dtype, const uint8_t* gate_codes, const uint16_t* gate_gscales,
-                           const uint8_t* up_codes, const uint16_t* up_gscales, uint16_t* out_f16) {
+                           const uint8_t* up_codes, const uint16_t* up_gscales, uint16_t* out_bf16) {
     if (!c) return QM_ERR_INVALID_ARG;
     int32_t st = q4_gemm_check(c, "qm_q4_gemm_gate_up", m, k, n, x_dtype);
     if (st != QM_OK) return st;
-    if (!x || !gate_codes || !gate_gscales || !up_codes || !up_gscales || !out_f16)
+    if (!x || !gate_codes || !gate_gscales || !up_codes || !up_gscales || !out_bf16)
         return fail(c, QM_ERR_INVALID_ARG, "qm_q4_gemm_gate_up: null pointer");
-    if (!all_aligned16({x, gate_codes, gate_gscales, up_codes, up_gscales, out_f16}))
+    if (!all_aligned16({x, gate_codes, gate_gscales, up_codes, up_gscales, out_bf16}))
         return fail(c, QM_ERR_INVALID_ARG, "qm_q4_gemm_gate_up: device pointers must be 16-byte aligned");
-    Q4GemmArgs ga{x,       gate_codes, gate_gscales, up_codes, up_gscales, nullptr, nullptr, out_f16,
-                  nullptr, m,          k,            n,        QM_Q4_TILE(n)};
+    Q4GemmArgs ga{x, gate_codes, gate_gscales, up_codes, up_gscales, nullptr, out_bf16, nullptr, m, k, n,
+                  QM_Q4_TILE(n)};
     const uint32_t grid = static_cast<uint32_t>((m + 127) / 128) * static_cast<uint32_t>((n + 127) / 128);
     return launch(c, c->f_q4_gemm[x_dtype == QM_BF16][1], grid, 256, ga, pick(c, stream), "qm_q4_gemm_gate_up");
 }

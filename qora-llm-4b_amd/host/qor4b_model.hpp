@@ -274,7 +274,7 @@ inline void forward_decode_no_logits_gpu(Context& ctx, const GpuModel& m, GpuHyb
 
 // Device buffers a prefill of up to max_tokens works in.
 struct PrefillScratch {
-    DeviceBuffer x, xn16, proj16, z16, a, b, k16, v16, mix16, inter16;
+    DeviceBuffer x, xn16, proj16, z16, a, b, k16, v16, mix16, inter_bf16;
     std::size_t max_tokens = 0;
 
     static PrefillScratch create(Context& ctx, const GpuModel& m, std::size_t max_tokens) {
@@ -294,7 +294,7 @@ struct PrefillScratch {
         s.k16 = DeviceBuffer(ctx, T * cfg.attn_kv_dim() * 2);
         s.v16 = DeviceBuffer(ctx, T * cfg.attn_kv_dim() * 2);
         s.mix16 = DeviceBuffer(ctx, T * std::max(cfg.deltanet_v_dim(), cfg.attn_q_dim()) * 2);
-        s.inter16 = DeviceBuffer(ctx, T * m.config.intermediate_size * 2);
+        s.inter_bf16 = DeviceBuffer(ctx, T * m.config.intermediate_size * 2);
         return s;
     }
 };
@@ -302,7 +302,8 @@ struct PrefillScratch {
 // prefill (gemv.rs:1243-1283): the tokens_dev [T] prompt through every
 // layer on MFMA (prefill_deltanet_layer, gemv.rs:1086-1240;
 // prefill_attn_layer, :1339-1470), each projection one qm_q4_gemm over all
-// T rows (f16 inputs from qm_rms_norm_f16, bf16 mixer inputs and outputs,
+// T rows (f16 inputs from qm_rms_norm_f16, bf16 mixer inputs and outputs
+// and MLP intermediate,
 // the hidden state f32 with the residuals added in the GEMM epilogues),
 // the MLP's gate/up as one launch; then the final norm and lm_head of the
 // last token into logits_dev.  DeltaNet states and conv buffers continue
@@ -327,8 +328,8 @@ inline void forward_prefill_gpu(Context& ctx, const GpuModel& m, GpuHybridCache&
         ctx.check(qm_rms_norm_f16(ctx.get(), stream, T, H, x, post_norm.as<uint16_t>(), xn));
         ctx.check(qm_q4_gemm_gate_up(ctx.get(), stream, T, H, I, xn, QM_F16, gate.codes.as<uint8_t>(),
                                      gate.gscales.as<uint16_t>(), up.codes.as<uint8_t>(), up.gscales.as<uint16_t>(),
-                                     s.inter16.as<uint16_t>()));
-        gemm(s.inter16.as<uint16_t>(), QM_F16, down, x, nullptr, x);
+                                     s.inter_bf16.as<uint16_t>()));
+        gemm(s.inter_bf16.as<uint16_t>(), QM_BF16, down, x, nullptr, x);
     };
     ctx.check(qm_q4_embed(ctx.get(), stream, T, V, H, tokens_dev, m.embed.packed.as<uint8_t>(),
                           m.embed.scales.as<uint16_t>(), x));

@@ -354,12 +354,12 @@ class Context:
         self._check(self.lib.qm_q4_gemm(self.h, self.stream, m, k, n, _addr(x), x_dtype, _addr(codes),
                                         _addr(gscales), _addr(residual), _addr(y), _addr(y_bf16)))
 
-    def q4_gemm_gate_up(self, m, k, n, x, gate_codes, gate_gscales, up_codes, up_gscales, out_f16,
+    def q4_gemm_gate_up(self, m, k, n, x, gate_codes, gate_gscales, up_codes, up_gscales, out_bf16,
                         x_dtype=QM_F16):
-        """out_f16 [m, n] = f16(silu(x @ Wg) * (x @ Wu)), x f16 or bf16 [m, k]."""
+        """out_bf16 [m, n] = bf16(silu(x @ Wg) * (x @ Wu)), x f16 or bf16 [m, k]."""
         self._check(self.lib.qm_q4_gemm_gate_up(self.h, self.stream, m, k, n, _addr(x), x_dtype,
                                                 _addr(gate_codes), _addr(gate_gscales), _addr(up_codes),
-                                                _addr(up_gscales), _addr(out_f16)))
+                                                _addr(up_gscales), _addr(out_bf16)))
 
     def q4_gate_up(self, k, n, x, norm_w, gate_codes, gate_gscales, up_codes, up_gscales, out):
         """out[n] = silu(xn @ Wg) * (xn @ Wu), xn = rms_norm(x, norm_w) or x."""
