@@ -1,5 +1,7 @@
 """CPU check of the chunked (WY/UT) DeltaNet prefill algebra used by the
-qm_dn_prefill_{chunk,scan,out} kernels.
+qm_dn_prefill_{chunk,scan,out} kernels, and of the segment form of a
+sequence split (a segment maps S_in to S_in M + B; segments compose), the
+algebra behind a prefill split across GPUs or segments.
 
 The kernels evaluate, per chunk of C tokens with state S0 entering,
   A = strictly-lower(beta_i gamma_i/gamma_j k_i.k_j), T = (I + A)^-1,
@@ -84,6 +86,38 @@ def chunked_prefill(q, k, v, g, beta, S0, C):
     return Y[:Tn], S
 
 
+def segmented_prefill(q, k, v, g, beta, S0, C, seg_chunks):
+    """The two-pass segment form of a sequence split: the sequence is cut
+    into segments of seg_chunks chunks; pass 1 runs every segment but the
+    last from a zero state (B_s, the state rows) and from the identity with
+    V = 0 (M_s, rows of the linear map), so that S_out = S_in M_s + B_s;
+    the combine chains S_entry(s + 1) = S_entry(s) M_s + B_s from S0; pass
+    3 reruns each segment from its entry state with the outputs."""
+    Tn, H, d = q.shape
+    nc = -(-Tn // C)
+    NS = -(-nc // seg_chunks)
+
+    def seg(s, S_in, vv):
+        lo, hi = s * seg_chunks * C, min((s + 1) * seg_chunks * C, Tn)
+        return chunked_prefill(q[lo:hi], k[lo:hi], vv[lo:hi], g[lo:hi], beta[lo:hi], S_in, C)
+
+    Ms, Bs = [], []
+    for s in range(NS - 1):
+        _, B = seg(s, np.zeros_like(S0), v)
+        _, Mt = seg(s, np.broadcast_to(np.eye(d), (H, d, d)).copy(), np.zeros_like(v))
+        Ms.append(Mt)
+        Bs.append(B)
+    ent = [S0.copy()]
+    for s in range(NS - 1):
+        ent.append(np.einsum("hvr,hrk->hvk", ent[s], Ms[s]) + Bs[s])
+    Y = np.zeros((Tn, H, d))
+    for s in range(NS):
+        Ys, S_last = seg(s, ent[s], v)
+        lo = s * seg_chunks * C
+        Y[lo:lo + Ys.shape[0]] = Ys
+    return Y, S_last
+
+
 def gated_norm(y, z, gw):
     inv = 1.0 / np.sqrt(np.mean(y ** 2, axis=-1, keepdims=True) + 1e-6)
     return y * inv * gw * z / (1.0 + np.exp(-z))
@@ -126,6 +160,39 @@ def test_chunked_algebra_matches_sequential_oracle(Tn, C):
     assert np.abs(out - ref).max() < 2e-4
     assert np.abs(S - S_or).max() < 2e-5
     assert np.array_equal(buf, qkv[-3:].T)
+    # the segment form (pass 1 maps, combine, pass 3) gives the same outputs and state
+    for seg_chunks in (1, 2, 3):
+        Ys, Ss = segmented_prefill(q, k, v, g, beta, S0.astype(np.float64), C, seg_chunks)
+        assert np.abs(Ys - Y).max() < 1e-9 and np.abs(Ss - S).max() < 1e-9
+
+
+def test_segment_maps_compose():
+    """S_out = S_in M + B over a segment holds for any entering state, and
+    two segments compose as (M1 M2, B1 M2 + B2)."""
+    r = np.random.default_rng(5)
+    Tn, H, d, C = 96, 2, 8, 16
+    q = r.standard_normal((Tn, H, d)); q /= np.linalg.norm(q, axis=-1, keepdims=True)
+    k = r.standard_normal((Tn, H, d)); k /= np.linalg.norm(k, axis=-1, keepdims=True)
+    v = r.standard_normal((Tn, H, d))
+    g = -r.uniform(0.0, 0.2, (Tn, H))
+    beta = r.uniform(0.0, 1.0, (Tn, H))
+    eye = np.broadcast_to(np.eye(d), (H, d, d)).copy()
+    zero = np.zeros((H, d, d))
+    half = Tn // 2
+    _, M1 = chunked_prefill(q[:half], k[:half], 0 * v[:half], g[:half], beta[:half], eye, C)
+    _, B1 = chunked_prefill(q[:half], k[:half], v[:half], g[:half], beta[:half], zero, C)
+    _, M2 = chunked_prefill(q[half:], k[half:], 0 * v[half:], g[half:], beta[half:], eye, C)
+    _, B2 = chunked_prefill(q[half:], k[half:], v[half:], g[half:], beta[half:], zero, C)
+    S_in = r.standard_normal((H, d, d))
+    _, S_direct = chunked_prefill(q, k, v, g, beta, S_in, C)
+    S_two = np.einsum("hvr,hrk->hvk", np.einsum("hvr,hrk->hvk", S_in, M1) + B1, M2) + B2
+    S_composed = np.einsum("hvr,hrk->hvk", S_in, np.einsum("hvr,hrk->hvk", M1, M2)) + \
+        np.einsum("hvr,hrk->hvk", B1, M2) + B2
+    assert np.abs(S_two - S_direct).max() < 1e-10
+    assert np.abs(S_composed - S_direct).max() < 1e-10
+    # M does not depend on V, and is not the identity (the map really acts)
+    _, M1b = chunked_prefill(q[:half], k[:half], 0 * v[:half] + 0, g[:half], beta[:half], eye, C)
+    assert np.array_equal(M1, M1b) and np.abs(M1 - eye).max() > 1e-2
 
 
 def test_blocked_inverse_is_the_inverse():
