@@ -269,7 +269,7 @@ def run_dn_decode(args, ctx):
     ctx.sync()
     nbytes = dn_decode_bytes(1)
     return {
-        "tokens": K, "total_ms": total_ms, "wall_s": wall, "dominant": "qm_dn_decode_t1024",
+        "tokens": K, "total_ms": total_ms, "wall_s": wall, "dominant": "qm_dn_decode_t512",
         "roofline": {"bound": "hbm", "achieved": nbytes / (k_ms * 1e-3), "peak": HBM_PEAK,
                      "unit": "GB/s", "kernel_ms": k_ms, "bytes_per_launch": nbytes},
         "eager_event_ms_per_launch": tm.mean_ms(),

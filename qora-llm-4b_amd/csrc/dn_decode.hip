@@ -48,17 +48,26 @@ QM_DEV float dot8(float4 a0, float4 a1, float4 b0, float4 b1) {
 QM_DEV float4 scale4(float4 a, float s) { return make_float4(a.x * s, a.y * s, a.z * s, a.w * s); }
 
 // gemv.rs:643-649 + :780-785: x /= ||x|| when ||x|| > 1e-12 (per head of 128,
-// the 16 lanes of a DPP row hold the whole head).
-QM_DEV void l2norm_row(float4& x0, float4& x1) {
+// the 16 lanes of a DPP row hold the whole head), times `scale`.
+// 1/||x|| from v_rsq_f32 (1 ulp).
+QM_DEV void l2norm_row(float4& x0, float4& x1, float scale) {
     float ss = x0.x * x0.x + x0.y * x0.y + x0.z * x0.z + x0.w * x0.w
              + x1.x * x1.x + x1.y * x1.y + x1.z * x1.z + x1.w * x1.w;
     ss = row_sum16(ss);
-    const float norm = sqrtf(ss);
-    if (norm > 1e-12f) {
-        const float inv = 1.0f / norm;
-        x0 = scale4(x0, inv);
-        x1 = scale4(x1, inv);
-    }
+    const float inv = (ss > 1e-24f ? __builtin_amdgcn_rsqf(ss) : 1.0f) * scale;
+    x0 = scale4(x0, inv);
+    x1 = scale4(x1, inv);
+}
+
+// The gates on the hardware transcendentals (v_exp_f32 / v_log_f32 / v_rcp_f32,
+// a few ulp from libm): every thread of a workgroup evaluates them, and on a
+// 16-lane SIMD each wave64 VALU instruction takes 4 cycles, so libm's
+// expansions were a large part of a batch-1 step.  gemv.rs:788-800:
+// alpha = exp(-exp(A_log) softplus(a + dt_bias)), softplus(x) = x above 20,
+// else ln(1 + e^x); beta = sigmoid(b).
+QM_DEV float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+QM_DEV float softplus_fast(float x) {
+    return x > 20.0f ? x : __builtin_amdgcn_logf(1.0f + exp_fast(x)) * 0.6931471805599453f;
 }
 
 template <int RPG>
@@ -91,25 +100,21 @@ QM_DEV void dn_decode_body(const DnDecodeArgs& A) {
     for (int i = 0; i < RPG; ++i) vr[i] = act[2 * 2048 + vh * QM_DN_HD + g + GROUPS * i];
     // The epilogue's inputs (norm weight, z gate) do not depend on the
     // update: fetch them with the state so the norm costs no extra round trip.
-    float gz = 0.0f;
+    float zz = 0.0f, nw = 0.0f;
     if (tid < QM_DN_HD) {
-        const float zz = A.z[(size_t)b * QM_DN_V_DIM + vh * QM_DN_HD + tid];
-        gz = f16_to_f32(A.norm_w[tid]) * silu_f(zz);
+        zz = A.z[(size_t)b * QM_DN_V_DIM + vh * QM_DN_HD + tid];
+        nw = f16_to_f32(A.norm_w[tid]);
     }
+    const float a_in = A.a[b * QM_DN_V_HEADS + vh], b_in = A.b[b * QM_DN_V_HEADS + vh];
+    const float a_log = A.a_log[vh], dt_bias = A.dt_bias[vh];
 
     float4 q0 = ld4(act + qkh * QM_DN_HD + 4 * l), q1 = ld4(act + qkh * QM_DN_HD + 64 + 4 * l);
     float4 k0 = ld4(act + 2048 + qkh * QM_DN_HD + 4 * l), k1 = ld4(act + 2048 + qkh * QM_DN_HD + 64 + 4 * l);
-    l2norm_row(q0, q1);
-    l2norm_row(k0, k1);
-    const float qscale = 1.0f / sqrtf((float)QM_DN_HD);
-    q0 = scale4(q0, qscale);
-    q1 = scale4(q1, qscale);
+    l2norm_row(q0, q1, 0.08838834764831845f);    // q *= 1/sqrt(128)
+    l2norm_row(k0, k1, 1.0f);
 
-    // gemv.rs:788-800
-    const float a_exp = expf(A.a_log[vh]);
-    const float spl = softplus_f(A.a[b * QM_DN_V_HEADS + vh] + A.dt_bias[vh]);
-    const float alpha = expf(-a_exp * spl);
-    const float beta = 1.0f / (1.0f + expf(-A.b[b * QM_DN_V_HEADS + vh]));
+    const float alpha = exp_fast(-exp_fast(a_log) * softplus_fast(a_in + dt_bias));
+    const float beta = sigmoid_fast(b_in);
 
 #pragma unroll
     for (int i = 0; i < RPG; ++i) {
@@ -137,8 +142,8 @@ QM_DEV void dn_decode_body(const DnDecodeArgs& A) {
         const int ln = tid & 63;
         const float y0 = ys[ln], y1 = ys[64 + ln];
         const float ss = wave_sum64(fmaf(y1, y1, y0 * y0));
-        const float inv_rms = 1.0f / sqrtf(ss / (float)QM_DN_HD + 1e-6f);
-        A.out[(size_t)b * QM_DN_V_DIM + vh * QM_DN_HD + tid] = ys[tid] * inv_rms * gz;
+        const float inv_rms = __builtin_amdgcn_rsqf(ss * (1.0f / (float)QM_DN_HD) + 1e-6f);
+        A.out[(size_t)b * QM_DN_V_DIM + vh * QM_DN_HD + tid] = ys[tid] * inv_rms * (nw * silu_fast(zz));
     }
 }
 

@@ -61,7 +61,12 @@ struct WaveState {
     float m[4], l[4], acc[4][4];
 };
 
-// One 16-key round: scores on MFMA, online softmax, PV on VALU.
+// One 16-key round: scores on MFMA, online softmax, PV on VALU.  The
+// softmax runs in base 2: scores are scaled by log2(e)/16 and exponentiated
+// with v_exp_f32 (2^x, 1 ulp), so the running max m and the partials'
+// maxima are in log2 units; libm's expf per head and round was most of a
+// batch-1 step's VALU time (each wave64 VALU op takes 4 cycles on a
+// 16-lane SIMD, and at batch 1 one wave per SIMD does the whole round).
 QM_DEV void compute_round(WaveState& st, const RoundBuf& rb, const half8 (&afr)[8], int t0,
                           int t_end, int lane, float4* pw /* LDS [16] of this wave */) {
     floatx4 c = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -70,7 +75,7 @@ QM_DEV void compute_round(WaveState& st, const RoundBuf& rb, const half8 (&afr)[
     // D[i][j] sits in lane j + 16*(i/4), element i%4: lanes 0..15 carry the
     // hi rows, lanes 16..31 the lo rows of key j = lane & 15.
     const bool valid = (lane < 16) && (t0 + (lane & 15) < t_end);
-    const float scale = 1.0f / sqrtf((float)QM_GQA_HD);
+    const float scale = 1.4426950408889634f / 16.0f;   // log2(e) / sqrt(256)
     float p[4], corr[4];
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
@@ -78,8 +83,8 @@ QM_DEV void compute_round(WaveState& st, const RoundBuf& rb, const half8 (&afr)[
         const float x = valid ? sc : -INFINITY;
         const float mt = readlane_f32(row_max16(x), 0);
         const float m_new = fmaxf(st.m[h], mt);
-        corr[h] = (st.m[h] == -INFINITY) ? 0.0f : expf(st.m[h] - m_new);
-        p[h] = valid ? expf(sc - m_new) : 0.0f;
+        corr[h] = (st.m[h] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(st.m[h] - m_new);
+        p[h] = valid ? __builtin_amdgcn_exp2f(sc - m_new) : 0.0f;
         const float ps = readlane_f32(row_sum16(p[h]), 0);
         st.l[h] = st.l[h] * corr[h] + ps;
         st.m[h] = m_new;
@@ -118,15 +123,16 @@ QM_DEV float4 gqa_gate(const GqaDecodeArgs& A, int b, int qh, int lane) {
     return ld4(A.q_gate + ((size_t)b * QM_GQA_HEADS + qh) * (2 * QM_GQA_HD) + QM_GQA_HD + 4 * lane);
 }
 
-// Gate and store one head's output: out = (acc / l) * sigmoid(gate).
+// Gate and store one head's output: out = (acc / l) * sigmoid(gate)
+// (v_rcp_f32 / v_exp_f32, about 1 ulp each).
 QM_DEV void gqa_store_out(const GqaDecodeArgs& A, int b, int qh, int lane, float4 o, float Ls,
                           float4 gv) {
-    const float inv = 1.0f / Ls;
+    const float inv = __builtin_amdgcn_rcpf(Ls);
     float4 r;
-    r.x = (o.x * inv) * sigmoid_f(gv.x);
-    r.y = (o.y * inv) * sigmoid_f(gv.y);
-    r.z = (o.z * inv) * sigmoid_f(gv.z);
-    r.w = (o.w * inv) * sigmoid_f(gv.w);
+    r.x = (o.x * inv) * sigmoid_fast(gv.x);
+    r.y = (o.y * inv) * sigmoid_fast(gv.y);
+    r.z = (o.z * inv) * sigmoid_fast(gv.z);
+    r.w = (o.w * inv) * sigmoid_fast(gv.w);
     st4(A.out + ((size_t)b * QM_GQA_HEADS + qh) * QM_GQA_HD + 4 * lane, r);
 }
 
@@ -272,7 +278,7 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_decode_split(GqaDecodeA
         float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
         for (int ww = 0; ww < 4; ++ww) {
-            const float f = (wm[ww][h] == -INFINITY) ? 0.0f : expf(wm[ww][h] - M);
+            const float f = (wm[ww][h] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(wm[ww][h] - M);
             Ls += wl[ww][h] * f;
             const float4 a = *reinterpret_cast<const float4*>(&wacc[ww][h][4 * lane]);
             o.x += a.x * f; o.y += a.y * f; o.z += a.z * f; o.w += a.w * f;
@@ -322,12 +328,12 @@ extern "C" __global__ __launch_bounds__(1024) void qm_gqa_decode_merge(GqaDecode
         // empty splits (sequence shorter than max_pos) carry m = -inf
         const float nm = fmaxf(mw, fmaxf(fmaxf(ms[0], ms[1]), fmaxf(ms[2], ms[3])));
         if (nm == -INFINITY) continue;                   // wave-uniform
-        const float c = expf(mw - nm);                   // 0 while mw = -inf
+        const float c = __builtin_amdgcn_exp2f(mw - nm); // 0 while mw = -inf (log2 units)
         lw *= c;
         ow.x *= c; ow.y *= c; ow.z *= c; ow.w *= c;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const float f = (ms[j] == -INFINITY) ? 0.0f : expf(ms[j] - nm);
+            const float f = (ms[j] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(ms[j] - nm);
             lw = fmaf(ls[j], f, lw);
             ow.x = fmaf(a[j].x, f, ow.x);
             ow.y = fmaf(a[j].y, f, ow.y);
@@ -347,7 +353,7 @@ extern "C" __global__ __launch_bounds__(1024) void qm_gqa_decode_merge(GqaDecode
         float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
         for (int ww = 0; ww < 16; ++ww) {
-            const float f = (wm[ww] == -INFINITY) ? 0.0f : expf(wm[ww] - M);
+            const float f = (wm[ww] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(wm[ww] - M);
             const float4 x = wo[ww][lane];
             Ls = fmaf(wl[ww], f, Ls);
             o.x = fmaf(x.x, f, o.x); o.y = fmaf(x.y, f, o.y);

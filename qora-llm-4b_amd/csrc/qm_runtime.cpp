@@ -538,13 +538,15 @@ int32_t qm_fill_normal(qm_context* c, void* dst, int32_t dtype, uint64_t count, 
 }
 
 // ---- DeltaNet decode ---------------------------------------------------------------
-// Threads per (sequence, v-head) workgroup.  Small batches leave most CUs idle,
-// so they take wider workgroups (more loads in flight per head).
+// Threads per (sequence, v-head) workgroup.  Small batches leave most CUs
+// idle, so they take wider workgroups (more loads in flight per head), up
+// to 512: with 1024 (4 waves per SIMD) the per-wave fixed VALU work (gates,
+// q/k norms) is paid four times per SIMD, and batch 1 measured 3.68 us per
+// step against 3.54 us with 512.
 static int dn_auto_threads(int32_t batch) {
     const int64_t heads = static_cast<int64_t>(batch) * QM_DN_V_HEADS;
     if (heads >= 512) return 256;
-    if (heads >= 128) return 512;
-    return 1024;
+    return 512;
 }
 
 int32_t qm_deltanet_decode(qm_context* c, qm_stream stream, int32_t batch, int32_t flags,
