@@ -588,13 +588,15 @@ int32_t qm_deltanet_decode(qm_context* c, qm_stream stream, int32_t batch, int32
 }
 
 // ---- GQA decode --------------------------------------------------------------------
-// Keys per split workgroup: about 2048 workgroups per launch (8 per CU) with
-// at least 128 keys each (two 16-key rounds per wave, both in flight at
-// once), at most 2048.
+// Keys per split workgroup, a multiple of 16 (one wave round): enough that
+// a launch has at most about 2048 workgroups (8 per CU) and the merge folds
+// at most 64 splits per head in one pass, at most 2048.  Small batches thus
+// get the shortest chunks that still fit (batch 1 at position 4096: 80 keys,
+// 208 workgroups), since each wave's rounds run one after another.
 static int64_t gqa_auto_chunk(int64_t len, int32_t batch) {
-    int64_t want = (len * batch * QM_GQA_KV_HEADS + 2047) / 2048;
-    int64_t ch = ((want + 63) / 64) * 64;
-    return std::max<int64_t>(128, std::min<int64_t>(ch, 2048));
+    const int64_t want = std::max<int64_t>((len + 63) / 64, (len * batch * QM_GQA_KV_HEADS + 2047) / 2048);
+    const int64_t ch = ((want + 15) / 16) * 16;
+    return std::max<int64_t>(16, std::min<int64_t>(ch, 2048));
 }
 
 }  // extern "C"
@@ -682,14 +684,16 @@ int32_t qm_reserve(qm_context* c, int32_t max_batch, int32_t max_kv_len, int32_t
     if (max_kv_len > 0) {
         // Bound on batch * nsplit over every batch <= max_batch and length
         // <= max_kv_len.  Automatic chunks: below the 2048 cap a chunk holds
-        // at least len*batch/512 keys, so nsplit <= ceil(512/batch); at the
-        // cap nsplit = ceil(len/2048); and always nsplit <= ceil(len/128).
+        // at least len*batch/512 keys, so nsplit <= ceil(512/batch), and at
+        // least len/64, so nsplit <= 64; at the cap nsplit = ceil(len/2048);
+        // and always nsplit <= ceil(len/16).
         const int64_t L = max_kv_len, B = max_batch;
         int64_t bn;
         if (c->opt_gqa_chunk) {
             bn = B * ((L + c->opt_gqa_chunk - 1) / c->opt_gqa_chunk);
         } else {
-            bn = std::min<int64_t>(B * ((L + 127) / 128), std::max<int64_t>(512 + B, B * ((L + 2047) / 2048)));
+            const int64_t per_seq = std::min<int64_t>((L + 15) / 16, std::max<int64_t>(64, (L + 2047) / 2048));
+            bn = std::min<int64_t>(B * per_seq, std::max<int64_t>(512 + B, B * ((L + 2047) / 2048)));
         }
         ws = std::max(ws, static_cast<size_t>(bn) * QM_GQA_KV_HEADS * 4 * 260 * sizeof(float));
     }
