@@ -82,6 +82,25 @@ def test_decode_ragged_positions(ctx):
     assert np.abs(got - ref).max() <= TOL
 
 
+@pytest.mark.parametrize("chunk", [0, 64, 192])
+def test_decode_rows_past_the_end_never_reach_the_output(ctx, chunk):
+    """Cache rows past a sequence's position may never have been written:
+    here they hold f16 NaN and Inf (K and V), in the same rounds as valid keys
+    and in whole rounds and splits past the end.  The outputs stay finite and
+    equal the oracle's, which reads rows 0..pos only."""
+    positions = [37, 1500, 64, 911]
+    w = W.gqa_decode_workload(1500, 4, cap=1600, seed=21)
+    for b, p in enumerate(positions):
+        w["k_cache"][b, :, p + 1:] = np.uint16(0x7E00)            # NaN
+        w["v_cache"][b, :, p + 1:] = np.uint16(0x7C00 if b % 2 else 0x7E00)   # +Inf / NaN
+    print(f"case: gqa decode NaN/Inf past the end chunk={chunk}", positions, flush=True)
+    got, _, _ = run_gpu(ctx, w, positions, 1501, chunk=chunk)
+    ref, _, _ = run_oracle(w, positions, 1501)
+    assert np.isfinite(got).all()
+    print(f"max|dout|={np.abs(got - ref).max():.3e}")
+    assert np.abs(got - ref).max() <= TOL
+
+
 @pytest.mark.parametrize("chunk", [64, 192, 1024, 4160])  # 4160: one split, no merge kernel
 def test_decode_chunk_invariance(ctx, chunk):
     w = W.gqa_decode_workload(3000, 2, seed=3)
