@@ -96,3 +96,55 @@ def test_prefill_4096_vs_oracle_and_recurrent_decode(ctx):
     print(f"vs recurrent decode: rel out {e1:.3e} rel state {e2:.3e}")
     assert e1 <= RTOL and e2 <= RTOL
     assert np.array_equal(ctx.download(buf, (8192, 3), np.float32), cb)
+
+
+@pytest.mark.parametrize("T", [1500, 2500, 8292])
+def test_prefill_long_warm(ctx, T):
+    """Longer sequences from a nonzero entering state and conv history: 24,
+    40 and 130 chunks (8292: more than one 64-chunk window of the scan's
+    gamma loads, and a partial last chunk)."""
+    w = W.dn_prefill_workload(T, seed=7 + T)
+    r = np.random.default_rng(T)
+    w["state0"] = (0.02 * r.standard_normal((32, 128, 128))).astype(np.float32)
+    w["conv_buf0"] = r.standard_normal((8192, 3)).astype(np.float32)
+    print(f"case: dn prefill warm T={T}", flush=True)
+    o, S, cb = run_prefill(ctx, w, T)
+    ro, rS, rcb = run_oracle(w, T)
+    eo, es = rel(o, ro), rel(S, rS)
+    print(f"rel out {eo:.3e} rel state {es:.3e}")
+    assert eo <= RTOL and es <= RTOL
+    assert np.array_equal(cb, rcb)
+
+
+def test_prefill_graph_replay_matches_eager(ctx):
+    """The prefill captured in a graph replays to the eager result, bit for
+    bit, three times (state and conv buffer reset between replays)."""
+    T = 2500
+    w = W.dn_prefill_workload(T, seed=31)
+    up = ctx.upload
+    d = {k: up(w[k]) for k in ["qkv", "conv_w", "a", "b", "a_log", "dt_bias", "z", "norm_w"]}
+    state, buf = up(w["state0"]), up(w["conv_buf0"])
+    out = ctx.alloc(T * 4096 * 2)
+
+    def call():
+        ctx.deltanet_prefill(T, d["qkv"], buf, d["conv_w"], d["a"], d["b"], d["a_log"], d["dt_bias"],
+                             d["z"], d["norm_w"], state, out)
+
+    print("case: dn prefill graph replay T=2500", flush=True)
+    ctx.reserve(max_batch=1, max_prefill_tokens=T)
+    call()
+    ctx.sync()
+    ref_o = ctx.download(out, (T, 4096), np.uint16)
+    ref_S = ctx.download(state, (32, 128, 128), np.float32)
+    ctx.graph_begin()
+    call()
+    g = ctx.graph_end()
+    for rep in range(3):
+        up(w["state0"], state)
+        up(w["conv_buf0"], buf)
+        ctx.memset(out, 0, T * 4096 * 2)
+        ctx.sync()
+        g.launch()
+        ctx.sync()
+        assert np.array_equal(ctx.download(out, (T, 4096), np.uint16), ref_o), rep
+        assert np.array_equal(ctx.download(state, (32, 128, 128), np.float32), ref_S), rep
