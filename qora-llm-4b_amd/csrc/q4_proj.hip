@@ -30,8 +30,9 @@
 // no second pass: lane t takes rows t, t + 512, ..., and loads its 8 rows'
 // codes, scales, x (and norm weights) before any arithmetic, at clamped
 // rows so that no load waits behind a branch.  The T partial sums of every
-// lane are reduced through LDS in a fixed order (bit-reproducible run to
-// run).  Dequantization costs ~2.4 VALU ops per weight: the codes are split
+// lane are reduced across the wave in registers (a transpose-reduce over
+// lane swaps), then across the waves through LDS behind one barrier, in a
+// fixed order (bit-reproducible run to run).  Dequantization costs ~2.4 VALU ops per weight: the codes are split
 // into low and high nibble bytes by two masks, each byte converts with one
 // v_cvt_f32_ubyteN, and the fma uses q itself, the -8 offset being applied
 // once per lane through sum(scale * x).  The RMSNorm is applied by
@@ -61,43 +62,65 @@ QM_DEV void q4_word(float* acc, uint32_t w, float sx) {  // 8 codes: columns 0..
 QM_DEV void q4_accumulate(float (&acc)[16], uint2 c, float sx) { q4_word(acc, c.x, sx); q4_word(acc + 8, c.y, sx); }
 QM_DEV void q4_accumulate(float (&acc)[8], uint32_t c, float sx) { q4_word(acc, c, sx); }
 
-// Sum over the workgroup's lanes of each of the T columns (valid in threads
-// < T): THREADS / T parts of T lanes, then the parts, in a fixed order.
-template <int T, int THREADS>
-QM_DEV float q4_reduce(float (*red)[17], float (*red2)[16], const float (&acc)[T], float bias, int tid) {
-#pragma unroll
-    for (int j = 0; j < T; ++j) red[tid][j] = fmaf(-8.0f, bias, acc[j]);
-    __syncthreads();
-    {
-        const int j = tid % T, p = tid / T;
-        float sum = 0.0f;
-#pragma unroll
-        for (int l = 0; l < T; ++l) sum += red[T * p + l][j];
-        red2[p / (16 / T) % (THREADS / 16)][j + T * (p % (16 / T))] = sum;
-    }
-    __syncthreads();
-    float sum = 0.0f;
-    if (tid < T) {
-#pragma unroll
-        for (int p = 0; p < THREADS / T; ++p) sum += red2[p / (16 / T)][tid + T * (p % (16 / T))];
-    }
-    return sum;
+// Wave-level sum of each of a lane's T column partials by transpose-reduce:
+// each step pairs lane l with l ^ 32, ^16, ^8 (and ^4 for T = 16), and each
+// lane keeps the half of its columns its side of the pair owns, summed with
+// the partner's copy of them; then the remaining lane bits are summed.  At
+// the end lane l holds the wave's total of column q4_col<T>(l) (the same in
+// the 64 / T lanes that share it).  No LDS, no barrier; a fixed order, so
+// the result is reproducible run to run.
+QM_DEV float xor_swz4(float x) {            // the value of lane l ^ 4 (ds_swizzle bit mode)
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x101F));
 }
-
-// Sum of ss over the workgroup (every thread gets it).
-template <int THREADS>
-QM_DEV float q4_block_sum(float ss, float* red, int tid) {
-    ss = wave_sum64(ss);
-    if ((tid & 63) == 0) red[tid >> 6] = ss;
-    __syncthreads();
-    float t = 0.0f;
+QM_DEV void halve32(float* v, int n) {      // n values -> n/2: lanes < 32 keep 0..n/2-1
 #pragma unroll
-    for (int w = 0; w < THREADS / 64; ++w) t += red[w];
-    return t;
+    for (int j = 0; j < n / 2; ++j) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[j]), __float_as_uint(v[j + n / 2]), false, false);
+        v[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+}
+QM_DEV void halve16(float* v, int n) {      // even 16-lane rows keep 0..n/2-1
+#pragma unroll
+    for (int j = 0; j < n / 2; ++j) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[j]), __float_as_uint(v[j + n / 2]), false, false);
+        v[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+}
+template <int BIT>
+QM_DEV void halve_dpp(float* v, int n, int lane) {   // lanes with bit BIT clear keep 0..n/2-1
+    const bool hi = (lane >> BIT) & 1;
+#pragma unroll
+    for (int j = 0; j < n / 2; ++j) {
+        const float keep = hi ? v[j + n / 2] : v[j];
+        const float send = hi ? v[j] : v[j + n / 2];
+        const float got = BIT == 3 ? dpp_f32<0x128>(send) : xor_swz4(send);   // row_ror:8 = lane ^ 8
+        v[j] = keep + got;
+    }
+}
+template <int T> QM_DEV int q4_col(int lane) {
+    return T == 16 ? 8 * ((lane >> 5) & 1) + 4 * ((lane >> 4) & 1) + 2 * ((lane >> 3) & 1) + ((lane >> 2) & 1)
+                   : 4 * ((lane >> 5) & 1) + 2 * ((lane >> 4) & 1) + ((lane >> 3) & 1);
+}
+template <int T>
+QM_DEV float q4_wave_reduce(float (&v)[T], int lane) {
+    halve32(v, T);
+    halve16(v, T / 2);
+    halve_dpp<3>(v, T / 4, lane);
+    float x;
+    if (T == 16) {
+        halve_dpp<2>(v, 2, lane);
+        x = v[0];
+    } else {
+        x = v[0];
+        x += xor_swz4(x);
+    }
+    x += dpp_f32<0x4E>(x);                  // lane ^ 2
+    x += dpp_f32<0xB1>(x);                  // lane ^ 1
+    return x;
 }
 
 template <bool GATE_UP, int T, int STEPS, int THREADS>
-QM_DEV void q4_tile(const Q4GemvArgs& A, int p, int tile, float (*red)[17], float (*red2)[16]) {
+QM_DEV void q4_tile(const Q4GemvArgs& A, int p, int tile, float (*red)[33]) {
     typedef typename Q4Codes<T>::type CodeT;
     const int tid = threadIdx.x;
     const int K = A.k;
@@ -151,14 +174,41 @@ QM_DEV void q4_tile(const Q4GemvArgs& A, int p, int tile, float (*red)[17], floa
         }
     }
 
-    // gemv.rs:573: 1 / sqrt(mean(x^2) + 1e-6)
-    const float inv = A.norm_w ? 1.0f / sqrtf(q4_block_sum<THREADS>(ss, &red2[0][0], tid) / (float)K + 1e-6f)
-                               : 1.0f;
-    __syncthreads();
-    const float y = inv * q4_reduce<T, THREADS>(red, red2, acc, bsum, tid);
+    // Column sums: each wave reduces its lanes' partials in registers (the
+    // -8 code offset applied through the scale * x sums), writes one value
+    // per column, and after one barrier thread j < T adds the THREADS / 64
+    // waves' values in order.  x's sum of squares for the RMSNorm rides along.
+    const int lane = tid & 63, wv = tid >> 6;
+#pragma unroll
+    for (int j = 0; j < T; ++j) acc[j] = fmaf(-8.0f, bsum, acc[j]);
+    const float cs = q4_wave_reduce<T>(acc, lane);
+    float cs_u = 0.0f;
     if (GATE_UP) {
-        __syncthreads();
-        const float u = inv * q4_reduce<T, THREADS>(red, red2, reinterpret_cast<const float(&)[T]>(acc_u), bsum_u, tid);
+#pragma unroll
+        for (int j = 0; j < T; ++j) acc_u[j] = fmaf(-8.0f, bsum_u, acc_u[j]);
+        cs_u = q4_wave_reduce<T>(reinterpret_cast<float(&)[T]>(acc_u), lane);
+    }
+    const float ssw = A.norm_w ? wave_sum64(ss) : 0.0f;
+    if ((lane & (64 / T - 1)) == 0) {
+        red[wv][q4_col<T>(lane)] = cs;
+        if (GATE_UP) red[wv][16 + q4_col<T>(lane)] = cs_u;
+    }
+    if (lane == 0) red[wv][32] = ssw;
+    __syncthreads();
+    float y = 0.0f, u = 0.0f, sst = 0.0f;
+    if (tid < T) {
+#pragma unroll
+        for (int w = 0; w < THREADS / 64; ++w) {
+            y += red[w][tid];
+            if (GATE_UP) u += red[w][16 + tid];
+            sst += red[w][32];
+        }
+    }
+    // gemv.rs:573: 1 / sqrt(mean(x^2) + 1e-6)
+    const float inv = A.norm_w ? 1.0f / sqrtf(sst / (float)K + 1e-6f) : 1.0f;
+    y *= inv;
+    if (GATE_UP) {
+        u *= inv;
         // gemv.rs:524: (g / (1 + exp(-g))) * u
         if (tid < T) A.y[0][T * (size_t)tile + tid] = (y / (1.0f + expf(-y))) * u;
     } else if (tid < T) {
@@ -183,8 +233,7 @@ QM_DEV void q4_tile(const Q4GemvArgs& A, int p, int tile, float (*red)[17], floa
 
 template <bool GATE_UP, int STEPS, int THREADS>
 QM_DEV void q4_gemv_body(const Q4GemvArgs& A) {
-    __shared__ float red[THREADS][17];
-    __shared__ float red2[THREADS / 16][16];
+    __shared__ float red[THREADS / 64][33];   // per wave: column sums (gate, up), x's sum of squares
     // which weight: workgroups wstart[p] .. wstart[p+1]-1 are weight p's
     // tiles (gate / up: weights 0 and 1 share the tile index)
     int p = 0;
@@ -194,8 +243,8 @@ QM_DEV void q4_gemv_body(const Q4GemvArgs& A) {
             if (q < A.count && (int)blockIdx.x >= A.wstart[q]) p = q;
     }
     const int tile = (int)blockIdx.x - A.wstart[p];
-    if (A.tile[p] == 16) q4_tile<GATE_UP, 16, STEPS, THREADS>(A, p, tile, red, red2);
-    else q4_tile<GATE_UP, 8, STEPS, THREADS>(A, p, tile, red, red2);
+    if (A.tile[p] == 16) q4_tile<GATE_UP, 16, STEPS, THREADS>(A, p, tile, red);
+    else q4_tile<GATE_UP, 8, STEPS, THREADS>(A, p, tile, red);
 }
 
 extern "C" __global__ __launch_bounds__(Q4_THREADS) void qm_q4_gemv(Q4GemvArgs A) {
@@ -204,6 +253,24 @@ extern "C" __global__ __launch_bounds__(Q4_THREADS) void qm_q4_gemv(Q4GemvArgs A
 
 extern "C" __global__ __launch_bounds__(Q4_THREADS) void qm_q4_gate_up(Q4GemvArgs A) {
     q4_gemv_body<true, Q4_STEPS, Q4_THREADS>(A);
+}
+
+// Shape-fitted forms.  A launch's workgroups should all be resident at once
+// (a second dispatch round repeats the whole load -> reduce latency), and a
+// lane's rows should come in as few load rounds as possible:
+//   k <= 2560 (the hidden size): 5 rows per lane, one round; <= 64 VGPRs, so
+//     four workgroups per CU (1024 slots for the 776 tiles of the fused
+//     DeltaNet input projections);
+//   k <= 9216 (the MLP's down_proj): 9 rows per lane, two rounds instead of
+//     three, at <= 128 VGPRs (two workgroups per CU, 512 slots for 320 tiles).
+// (The gate/up form at 5 rows and <= 80 VGPRs spilled and ran slower.)
+extern "C" __global__ __launch_bounds__(Q4_THREADS) __attribute__((amdgpu_waves_per_eu(8)))
+void qm_q4_gemv_s5(Q4GemvArgs A) {
+    q4_gemv_body<false, 5, Q4_THREADS>(A);
+}
+extern "C" __global__ __launch_bounds__(Q4_THREADS) __attribute__((amdgpu_waves_per_eu(4)))
+void qm_q4_gemv_s9(Q4GemvArgs A) {
+    q4_gemv_body<false, 9, Q4_THREADS>(A);
 }
 
 // Reference layout -> tile-major.  Workgroup = 64 rows x 16 groups: each

@@ -46,6 +46,8 @@ struct qm_context {
     hipFunction_t f_gqp_kv = nullptr;
     hipFunction_t f_gqp_attn = nullptr;
     hipFunction_t f_q4_gemv = nullptr;
+    hipFunction_t f_q4_gemv_s5 = nullptr;   // k <= 2560: 5 rows per lane, four workgroups per CU
+    hipFunction_t f_q4_gemv_s9 = nullptr;   // 4096 < k <= 9216: 9 rows per lane, two load rounds
     hipFunction_t f_q4_repack = nullptr;
     hipFunction_t f_q4_gate_up = nullptr;
     hipFunction_t f_q4_gemm[2][2] = {};  // [x bf16][gate/up form]
@@ -309,6 +311,8 @@ int32_t qm_create(qm_context** out, const qm_config* cfg, const char* code_objec
     if (st == QM_OK) st = load_function(c, mods[4], "qm_gqa_prefill_kv", &c->f_gqp_kv);
     if (st == QM_OK) st = load_function(c, mods[4], "qm_gqa_prefill_attn", &c->f_gqp_attn);
     if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemv", &c->f_q4_gemv);
+    if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemv_s5", &c->f_q4_gemv_s5);
+    if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemv_s9", &c->f_q4_gemv_s9);
     if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_repack", &c->f_q4_repack);
     if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gate_up", &c->f_q4_gate_up);
     if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemm", &c->f_q4_gemm[0][0]);
@@ -832,7 +836,12 @@ int32_t q4_gemv_multi_impl(qm_context* c, qm_stream stream, int32_t k, const flo
     for (int32_t i = count; i <= QM_Q4_MAX_OUT; ++i) qa.wstart[i] = tiles;
     qa.conv_buf = conv_buf;
     qa.conv_w = conv_w;
-    return launch(c, c->f_q4_gemv, static_cast<uint32_t>(tiles), static_cast<uint32_t>(c->q4_threads), qa,
+    // the shape-fitted forms (same threads per workgroup): 5 rows per lane
+    // up to k = 2560, 9 from 4097 to 9216, else 8
+    hipFunction_t f = c->f_q4_gemv;
+    if (k <= c->q4_threads * 5) f = c->f_q4_gemv_s5;
+    else if (k > c->q4_threads * 8 && k <= c->q4_threads * 9 * 2) f = c->f_q4_gemv_s9;
+    return launch(c, f, static_cast<uint32_t>(tiles), static_cast<uint32_t>(c->q4_threads), qa,
                   pick(c, stream), "qm_q4_gemv");
 }
 }  // namespace
