@@ -251,25 +251,31 @@ extern "C" __global__ __launch_bounds__(Q4_THREADS) void qm_q4_gemv(Q4GemvArgs A
     q4_gemv_body<false, Q4_STEPS, Q4_THREADS>(A);
 }
 
-extern "C" __global__ __launch_bounds__(Q4_THREADS) void qm_q4_gate_up(Q4GemvArgs A) {
-    q4_gemv_body<true, Q4_STEPS, Q4_THREADS>(A);
+// 256 threads, 10 rows per lane: one load round at k = 2560, and at 134
+// VGPRs three workgroups per CU, so the 576 tiles of the 2560 x 9216 gate /
+// up pair are resident in one dispatch round (the 512-thread form fitted two
+// per CU and ran 3% slower per model token).
+extern "C" __global__ __launch_bounds__(256) void qm_q4_gate_up(Q4GemvArgs A) {
+    q4_gemv_body<true, 10, 256>(A);
 }
 
 // Shape-fitted forms.  A launch's workgroups should all be resident at once
 // (a second dispatch round repeats the whole load -> reduce latency), and a
 // lane's rows should come in as few load rounds as possible:
-//   k <= 2560 (the hidden size): 5 rows per lane, one round; <= 64 VGPRs, so
-//     four workgroups per CU (1024 slots for the 776 tiles of the fused
-//     DeltaNet input projections);
+//   k <= 2560 (the hidden size): 256 threads of 10 rows, one load round, 91
+//     VGPRs (five workgroups per CU, 1280 slots for the 776 tiles of the
+//     fused DeltaNet input projections);
 //   k <= 9216 (the MLP's down_proj): 9 rows per lane, two rounds instead of
 //     three, at <= 128 VGPRs (two workgroups per CU, 512 slots for 320 tiles).
-// (The gate/up form at 5 rows and <= 80 VGPRs spilled and ran slower.)
-extern "C" __global__ __launch_bounds__(Q4_THREADS) __attribute__((amdgpu_waves_per_eu(8)))
-void qm_q4_gemv_s5(Q4GemvArgs A) {
-    q4_gemv_body<false, 5, Q4_THREADS>(A);
+// (512-thread forms of 5 rows for k <= 2560, of 18 or 12 rows at 256 threads
+// for down_proj, and of 16 at 256 threads for the general case all measured
+// slower over a model token.)
+extern "C" __global__ __launch_bounds__(256)
+void qm_q4_gemv_hidden(Q4GemvArgs A) {
+    q4_gemv_body<false, 10, 256>(A);
 }
 extern "C" __global__ __launch_bounds__(Q4_THREADS) __attribute__((amdgpu_waves_per_eu(4)))
-void qm_q4_gemv_s9(Q4GemvArgs A) {
+void qm_q4_gemv_inter(Q4GemvArgs A) {
     q4_gemv_body<false, 9, Q4_THREADS>(A);
 }
 

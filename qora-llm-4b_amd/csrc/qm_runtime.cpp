@@ -46,8 +46,8 @@ struct qm_context {
     hipFunction_t f_gqp_kv = nullptr;
     hipFunction_t f_gqp_attn = nullptr;
     hipFunction_t f_q4_gemv = nullptr;
-    hipFunction_t f_q4_gemv_s5 = nullptr;   // k <= 2560: 5 rows per lane, four workgroups per CU
-    hipFunction_t f_q4_gemv_s9 = nullptr;   // 4096 < k <= 9216: 9 rows per lane, two load rounds
+    hipFunction_t f_q4_gemv_hidden = nullptr;  // k <= 2560 (the hidden size)
+    hipFunction_t f_q4_gemv_inter = nullptr;   // 4096 < k <= 9216 (the MLP's intermediate size)
     hipFunction_t f_q4_repack = nullptr;
     hipFunction_t f_q4_gate_up = nullptr;
     hipFunction_t f_q4_gemm[2][2] = {};  // [x bf16][gate/up form]
@@ -62,6 +62,7 @@ struct qm_context {
     int lm_head_wg_per_cu = 1;
     int q4_threads = 0;            // the Q4 kernels' workgroup sizes (their launch bounds)
     int q4_gu_threads = 0;
+    int q4_hidden_threads = 0, q4_inter_threads = 0;
     void* ws = nullptr;            // general workspace
     size_t ws_bytes = 0;
     // Workspaces replaced by a larger one.  A graph captured earlier holds
@@ -311,8 +312,8 @@ int32_t qm_create(qm_context** out, const qm_config* cfg, const char* code_objec
     if (st == QM_OK) st = load_function(c, mods[4], "qm_gqa_prefill_kv", &c->f_gqp_kv);
     if (st == QM_OK) st = load_function(c, mods[4], "qm_gqa_prefill_attn", &c->f_gqp_attn);
     if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemv", &c->f_q4_gemv);
-    if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemv_s5", &c->f_q4_gemv_s5);
-    if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemv_s9", &c->f_q4_gemv_s9);
+    if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemv_hidden", &c->f_q4_gemv_hidden);
+    if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemv_inter", &c->f_q4_gemv_inter);
     if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_repack", &c->f_q4_repack);
     if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gate_up", &c->f_q4_gate_up);
     if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemm", &c->f_q4_gemm[0][0]);
@@ -330,6 +331,10 @@ int32_t qm_create(qm_context** out, const qm_config* cfg, const char* code_objec
     if (st == QM_OK &&
         (hipFuncGetAttribute(&c->q4_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, c->f_q4_gemv) != hipSuccess ||
          hipFuncGetAttribute(&c->q4_gu_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, c->f_q4_gate_up) !=
+             hipSuccess ||
+         hipFuncGetAttribute(&c->q4_hidden_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, c->f_q4_gemv_hidden) !=
+             hipSuccess ||
+         hipFuncGetAttribute(&c->q4_inter_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, c->f_q4_gemv_inter) !=
              hipSuccess))
         st = fail(c, QM_ERR_CODE_OBJECT, "qm_q4_gemv: cannot read its workgroup size");
     if (st == QM_OK && hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess)
@@ -836,13 +841,19 @@ int32_t q4_gemv_multi_impl(qm_context* c, qm_stream stream, int32_t k, const flo
     for (int32_t i = count; i <= QM_Q4_MAX_OUT; ++i) qa.wstart[i] = tiles;
     qa.conv_buf = conv_buf;
     qa.conv_w = conv_w;
-    // the shape-fitted forms (same threads per workgroup): 5 rows per lane
-    // up to k = 2560, 9 from 4097 to 9216, else 8
+    // the shape-fitted forms: k up to 2560 (the hidden size) and 4097 .. 9216
+    // (the MLP's down_proj), each with its own workgroup size
     hipFunction_t f = c->f_q4_gemv;
-    if (k <= c->q4_threads * 5) f = c->f_q4_gemv_s5;
-    else if (k > c->q4_threads * 8 && k <= c->q4_threads * 9 * 2) f = c->f_q4_gemv_s9;
-    return launch(c, f, static_cast<uint32_t>(tiles), static_cast<uint32_t>(c->q4_threads), qa,
-                  pick(c, stream), "qm_q4_gemv");
+    int threads = c->q4_threads;
+    if (k <= 2560) {
+        f = c->f_q4_gemv_hidden;
+        threads = c->q4_hidden_threads;
+    } else if (k > 4096 && k <= 9216) {
+        f = c->f_q4_gemv_inter;
+        threads = c->q4_inter_threads;
+    }
+    return launch(c, f, static_cast<uint32_t>(tiles), static_cast<uint32_t>(threads), qa, pick(c, stream),
+                  "qm_q4_gemv");
 }
 }  // namespace
 
