@@ -203,14 +203,27 @@ QM_DEV uint2 pack_f16x4(float a, float b, float c, float d) {
     return o;
 }
 
-extern "C" __global__ __launch_bounds__(256) void qm_gqa_decode_split(GqaDecodeArgs A) {
+struct SplitLds {
     // q columns in f16: rows 0..3 q_hi of heads 4g..4g+3, rows 4..7 q_lo,
     // row 8 zeros (the B operand's unused columns).
-    __shared__ __attribute__((aligned(16))) uint16_t qhl[9][QM_GQA_HD];
-    __shared__ float wacc[4][4][QM_GQA_HD];     // per-wave partial PV
-    __shared__ float wm[4][4], wl[4][4];
-    __shared__ __attribute__((aligned(16))) uint16_t knew[QM_GQA_HD], vnew[QM_GQA_HD];   // appended rows
+    __attribute__((aligned(16))) uint16_t qhl[9][QM_GQA_HD];
+    float wacc[4][4][QM_GQA_HD];                // per-wave partial PV
+    float wm[4][4], wl[4][4];
+    __attribute__((aligned(16))) uint16_t knew[QM_GQA_HD], vnew[QM_GQA_HD];   // appended rows
+};
 
+// POS_ARG: no per-sequence positions (every sequence at max_pos, as at batch
+// 1), so the RoPE rows and the append's inputs are known before any load and
+// are issued with the q row, ahead of the first round; otherwise they wait
+// for pos and follow the round.
+template <bool POS_ARG>
+QM_DEV void split_body(const GqaDecodeArgs& A, SplitLds& sh) {
+    auto& qhl = sh.qhl;
+    auto& wacc = sh.wacc;
+    auto& wm = sh.wm;
+    auto& wl = sh.wl;
+    auto& knew = sh.knew;
+    auto& vnew = sh.vnew;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int bid = blockIdx.x;
     const int split = bid % A.nsplit;
@@ -223,15 +236,31 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_decode_split(GqaDecodeA
     const uint16_t* vbase = A.v_cache + kv_base;
 
     // Loads first, in the order their consumers need them: pos (scalar), the
-    // q row and its norm weight, then the first 16-key round (bounded by
-    // max_pos, since pos <= max_pos; keys past the real end are masked when
-    // the round is computed), then what depends on pos.  Each wave's vector
+    // q row and its norm weight (and, with POS_ARG, the RoPE rows and the
+    // appended k / v), then the first 16-key round (bounded by max_pos,
+    // since pos <= max_pos; keys past the real end are masked when the round
+    // is computed), then what depends on a loaded pos.  Each wave's vector
     // loads complete in issue order, so the q norm starts while the round is
     // still in flight.
-    int pos = A.pos ? A.pos[b] : A.max_pos;
+    int pos = POS_ARG ? A.max_pos : A.pos[b];
     const float* qg = A.q_gate + ((size_t)b * QM_GQA_HEADS + 4 * g + w) * (2 * QM_GQA_HD);
     const float4 qx = ld4(qg + 4 * lane);
     const uint2 gq = *reinterpret_cast<const uint2*>(A.q_norm + 4 * lane);
+    float4 rc, rs;
+    float4 ax = make_float4(0.0f, 0.0f, 0.0f, 0.0f);     // new k (wave 0) or v (wave 1)
+    uint2 gk = make_uint2(0, 0);
+    auto pos_loads = [&](int p, bool app) {
+        rope_row_loads(A.rope_cos + (size_t)p * (QM_GQA_ROT / 2), A.rope_sin + (size_t)p * (QM_GQA_ROT / 2), lane, rc, rs);
+        if (app && w < 2) {
+            const float* src = (w == 0 ? A.k_new : A.v_new) + ((size_t)b * QM_GQA_KV_HEADS + g) * QM_GQA_HD;
+            ax = ld4(src + 4 * lane);
+            gk = *reinterpret_cast<const uint2*>(A.k_norm + 4 * lane);
+        }
+    };
+    if (POS_ARG) {
+        const int t_end = min(t_begin + A.chunk, pos + 1);
+        pos_loads(pos, t_begin <= pos && pos < t_end);
+    }
     __builtin_amdgcn_sched_barrier(0);
     // 4a. Wave w takes rounds t_begin + 64*r + 16*w (r = 0 .. nr-1).
     RoundBuf ra, rb;
@@ -243,21 +272,11 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_decode_split(GqaDecodeA
     pos = pos < 0 ? 0 : (pos > A.max_pos ? A.max_pos : pos);
     const int L = pos + 1;
     const int t_end = min(t_begin + A.chunk, L);
-    const float* cos_row = A.rope_cos + (size_t)pos * (QM_GQA_ROT / 2);
-    const float* sin_row = A.rope_sin + (size_t)pos * (QM_GQA_ROT / 2);
     const bool appends = (t_begin <= pos && pos < t_end);
     const int span = t_end - t_begin - 16 * w;
     const int nr = __builtin_amdgcn_readfirstlane(span > 0 ? (span + 63) / 64 : 0);
     const int t_last = t_end - 1;
-    float4 rc, rs;
-    rope_row_loads(cos_row, sin_row, lane, rc, rs);
-    float4 ax = make_float4(0.0f, 0.0f, 0.0f, 0.0f);     // new k (wave 0) or v (wave 1)
-    uint2 gk = make_uint2(0, 0);
-    if (appends && w < 2) {
-        const float* src = (w == 0 ? A.k_new : A.v_new) + ((size_t)b * QM_GQA_KV_HEADS + g) * QM_GQA_HD;
-        ax = ld4(src + 4 * lane);
-        gk = *reinterpret_cast<const uint2*>(A.k_norm + 4 * lane);
-    }
+    if (!POS_ARG) pos_loads(pos, appends);
     float4 gv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (A.nsplit == 1) gv = gqa_gate(A, b, 4 * g + w, lane);
 
@@ -371,72 +390,56 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_decode_split(GqaDecodeA
     }
 }
 
+extern "C" __global__ __launch_bounds__(256) void qm_gqa_decode_split(GqaDecodeArgs A) {
+    __shared__ SplitLds sh;
+    if (A.pos) split_body<false>(A, sh);
+    else split_body<true>(A, sh);
+}
+
 // Merge the split partials of query head 4g+h of sequence b and apply the
-// gate.  Workgroup (b, g, h) has 16 waves; wave w folds splits w, w+16,
-// w+32, w+48 (then the next 64, ...) with all four partials' loads in
-// flight, so up to 64 splits cost one memory round trip, and the 16 wave
-// results combine through LDS.  Lane l owns dims 4l .. 4l+3.
-extern "C" __global__ __launch_bounds__(1024) void qm_gqa_decode_merge(GqaDecodeArgs A) {
-    __shared__ float4 wo[16][64];
-    __shared__ float wm[16], wl[16];
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-    const int h = blockIdx.x & 3;
-    const int g = (blockIdx.x >> 2) % QM_GQA_KV_HEADS;
-    const int b = blockIdx.x / (4 * QM_GQA_KV_HEADS);
+// gate.  One wave per (b, g, h, quarter of the dims): lane l owns dim
+// 64 q + l.  The splits are folded 56 at a time with every load of a batch in
+// flight at once (a wave can have 63 vector loads outstanding): each lane
+// loads its dim of the batch's partials and one split's (max, sum) pair; the
+// batch maximum and the sum of the rescaled sums are wave reductions, and
+// split j's factor is read from lane j.  So up to 56 splits cost one memory
+// round trip, and the merge needs no LDS or barrier.  (Two waves splitting
+// the splits, with an LDS combine, measured no faster at batch 1.)
+#define MERGE_BATCH 56
+QM_DEV float wave_max64(float x) {
+    return max_xor32(max_xor16(row_max16(x)));
+}
+extern "C" __global__ __launch_bounds__(64) void qm_gqa_decode_merge(GqaDecodeArgs A) {
+    const int lane = threadIdx.x;
+    const int q = blockIdx.x & 3;
+    const int h = (blockIdx.x >> 2) & 3;
+    const int g = (blockIdx.x >> 4) % QM_GQA_KV_HEADS;
+    const int b = blockIdx.x / (16 * QM_GQA_KV_HEADS);
     const int nsplit = A.nsplit;
-    float4 gv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (w == 0) gv = gqa_gate(A, b, 4 * g + h, lane);
+    const int d = 64 * q + lane;
+    const float gate = A.q_gate[((size_t)b * QM_GQA_HEADS + 4 * g + h) * (2 * QM_GQA_HD) + QM_GQA_HD + d];
     const float* P0 = A.partial + (((size_t)b * QM_GQA_KV_HEADS + g) * nsplit * 4 + h) * GQA_PART_STRIDE;
     const size_t step = 4 * GQA_PART_STRIDE;
-
-    float mw = -INFINITY, lw = 0.0f;
-    float4 ow = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int s0 = w; s0 < nsplit; s0 += 64) {
-        float4 a[4];
-        float ms[4], ls[4];
+    float M = -INFINITY, Ls = 0.0f, o = 0.0f;
+    for (int s0 = 0; s0 < nsplit; s0 += MERGE_BATCH) {        // uniform
+        float a[MERGE_BATCH];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int s = s0 + 16 * j;
-            const bool ok = s < nsplit;                  // wave-uniform
-            const float* P = P0 + (size_t)(ok ? s : s0) * step;
-            a[j] = ld4(P + 4 * lane);
-            ms[j] = ok ? P[256] : -INFINITY;
-            ls[j] = P[257];
-        }
+        for (int j = 0; j < MERGE_BATCH; ++j) a[j] = P0[(size_t)min(s0 + j, nsplit - 1) * step + d];
+        const bool mine = lane < MERGE_BATCH && s0 + lane < nsplit;       // lane's split s0 + lane
+        const float2 ml = *reinterpret_cast<const float2*>(P0 + (size_t)min(s0 + lane, nsplit - 1) * step + 256);
         // empty splits (sequence shorter than max_pos) carry m = -inf
-        const float nm = fmaxf(mw, fmaxf(fmaxf(ms[0], ms[1]), fmaxf(ms[2], ms[3])));
-        if (nm == -INFINITY) continue;                   // wave-uniform
-        const float c = __builtin_amdgcn_exp2f(mw - nm); // 0 while mw = -inf (log2 units)
-        lw *= c;
-        ow.x *= c; ow.y *= c; ow.z *= c; ow.w *= c;
+        const float mj = mine ? ml.x : -INFINITY;
+        const float mb = fmaxf(M, wave_max64(mj));
+        if (mb == -INFINITY) continue;                         // uniform
+        const float c = __builtin_amdgcn_exp2f(M - mb);         // 0 while M = -inf (log2 units)
+        const float fj = (mj == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mj - mb);
+        Ls = Ls * c + wave_sum64(mine ? ml.y * fj : 0.0f);
+        float op[4] = {o * c, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float f = (ms[j] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(ms[j] - nm);
-            lw = fmaf(ls[j], f, lw);
-            ow.x = fmaf(a[j].x, f, ow.x);
-            ow.y = fmaf(a[j].y, f, ow.y);
-            ow.z = fmaf(a[j].z, f, ow.z);
-            ow.w = fmaf(a[j].w, f, ow.w);
-        }
-        mw = nm;
+        for (int j = 0; j < MERGE_BATCH; ++j) op[j & 3] = fmaf(a[j], readlane_f32(fj, j), op[j & 3]);
+        o = (op[0] + op[1]) + (op[2] + op[3]);
+        M = mb;
     }
-    if (lane == 0) { wm[w] = mw; wl[w] = lw; }
-    wo[w][lane] = ow;
-    __syncthreads();
-    if (w == 0) {
-        float M = -INFINITY;
-#pragma unroll
-        for (int ww = 0; ww < 16; ++ww) M = fmaxf(M, wm[ww]);
-        float Ls = 0.0f;
-        float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll
-        for (int ww = 0; ww < 16; ++ww) {
-            const float f = (wm[ww] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(wm[ww] - M);
-            const float4 x = wo[ww][lane];
-            Ls = fmaf(wl[ww], f, Ls);
-            o.x = fmaf(x.x, f, o.x); o.y = fmaf(x.y, f, o.y);
-            o.z = fmaf(x.z, f, o.z); o.w = fmaf(x.w, f, o.w);
-        }
-        gqa_store_out(A, b, 4 * g + h, lane, o, Ls, gv);
-    }
+    // gemv.rs:1008-1011: out = (o / l) * sigmoid(gate)
+    A.out[((size_t)b * QM_GQA_HEADS + 4 * g + h) * QM_GQA_HD + d] = (o * __builtin_amdgcn_rcpf(Ls)) * sigmoid_fast(gate);
 }

@@ -599,7 +599,8 @@ int32_t qm_deltanet_decode(qm_context* c, qm_stream stream, int32_t batch, int32
 // ---- GQA decode --------------------------------------------------------------------
 // Keys per split workgroup, a multiple of 16 (one wave round): enough that
 // a launch has at most about 2048 workgroups (8 per CU) and the merge folds
-// at most 64 splits per head in one pass, at most 2048.  Small batches thus
+// at most 64 splits per head in one pass (at most 56 per memory round
+// trip), at most 2048.  Small batches thus
 // get the shortest chunks that still fit (batch 1 at position 4096: 80 keys,
 // 208 workgroups), since each wave's rounds run one after another.
 static int64_t gqa_auto_chunk(int64_t len, int32_t batch) {
@@ -661,7 +662,7 @@ int32_t gqa_decode_impl(qm_context* c, qm_stream stream, int32_t batch, const fl
                      static_cast<int32_t>(chunk), static_cast<int32_t>(nsplit), batch};
     int32_t st = launch(c, c->f_gqa_split, static_cast<uint32_t>(grid), 256, ga, s, "qm_gqa_decode_split");
     if (st != QM_OK || nsplit == 1) return st;
-    return launch(c, c->f_gqa_merge, static_cast<uint32_t>(batch) * QM_GQA_KV_HEADS * 4, 1024, ga, s,
+    return launch(c, c->f_gqa_merge, static_cast<uint32_t>(batch) * QM_GQA_KV_HEADS * 16, 64, ga, s,
                   "qm_gqa_decode_merge");
 }
 }  // namespace
