@@ -365,18 +365,16 @@ int32_t qm_rms_norm_f16(qm_context* ctx, qm_stream stream, int32_t m, int32_t k,
  * gemv.rs:529-542 (gemm() on a Q4 weight, :295-300), which the prefill
  * layers call for every projection (gemv.rs:1114-1117,1222,1231-1239,
  * 1366-1385,1447-1467).  x_dev [m][k] (k % 32 == 0, else QM_ERR_SHAPE) of
- * x_dtype QM_F16 (from qm_rms_norm_f16) or QM_BF16 (a mixer prefill output,
- * rounded to f16 as it is read); codes_dev/gscales_dev a weight in the
- * device layout (qm_q4_repack); residual_dev NULL or f32 [m][n] (may alias
- * y_dev); exactly one of y_dev (f32 [m][n]) and y_bf16_dev (bf16 [m][n],
- * e.g. the in_proj_qkv / in_proj_z outputs that qm_deltanet_prefill reads)
- * is non-NULL.  W is dequantized to f16 per element (s * (q - 8), one
- * rounding) and x is f16: a bf16-path result, within 1e-3 of
- * sum_k |x_k W_kj| of the fp32 reference per element.  A bf16 input keeps
- * bf16's range: a row whose values in a 32-wide k step pass f16's range is
- * staged times a power of two 2^-s and its fp32 accumulators rescaled by
- * 2^s, so outliers up to bf16's range give finite results at the same
- * relative precision. */
+ * x_dtype QM_F16 (from qm_rms_norm_f16) or QM_BF16 (a mixer prefill output
+ * or the MLP's silu(g) * u); codes_dev/gscales_dev a weight in the device
+ * layout (qm_q4_repack); residual_dev NULL or f32 [m][n] (may alias y_dev);
+ * exactly one of y_dev (f32 [m][n]) and y_bf16_dev (bf16 [m][n], e.g. the
+ * in_proj_qkv / in_proj_z outputs that qm_deltanet_prefill reads) is
+ * non-NULL.  Products accumulate in fp32.  An f16 x multiplies W rounded to
+ * f16 per element (s * (q - 8), one rounding): within 1e-3 of
+ * sum_k |x_k W_kj| of the fp32 reference per element.  A bf16 x is used as
+ * it is (bf16's range: outliers stay finite) and multiplies W rounded on to
+ * bf16: within 2^-8 + 2^-11 (+ the fp32 accumulation) of that sum. */
 int32_t qm_q4_gemm(qm_context* ctx, qm_stream stream, int32_t m, int32_t k, int32_t n,
                    const uint16_t* x_dev, int32_t x_dtype, const uint8_t* codes_dev,
                    const uint16_t* gscales_dev, const float* residual_dev,

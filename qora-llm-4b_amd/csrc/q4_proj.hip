@@ -325,15 +325,16 @@ extern "C" __global__ __launch_bounds__(256) void qm_q4_repack(Q4RepackArgs A) {
 // ---------------------------------------------------------------------------
 // Prefill: C[m][n] = X[m][k] W on MFMA (gemm_q4, gemv.rs:529-542, for
 // seq_len > 1).  X is f16 (qm_rms_norm_f16 produces it from the f32 hidden
-// state, fusing the layer's RMSNorm); W stays Q4 in HBM and is dequantized
-// to f16 on its way into LDS, s * (q - 8) rounded once to f16.
-// Workgroup tile 128 x 256, four waves of 64 x 128 (4 x 8 tiles of
-// v_mfma_f32_16x16x32_f16: 12 fragment reads feed 32 MFMAs), k steps of 32
-// double-buffered in LDS with one barrier per step: step t + 1's X rows and
-// codes are loaded into registers before step t's MFMAs and stored to the
-// other buffer after them.  LDS rows are k-contiguous, X as [m][k] and W as
-// [n][k], padded to 40 f16 (80 bytes) so the 16 rows of a fragment read land
-// in 16 distinct bank slots; a lane's A operand (row m, k 8kg .. +7) and B
+// state, fusing the layer's RMSNorm) or bf16 (the mixer outputs and the
+// MLP's silu(g) * u).  W stays Q4 in HBM and is dequantized on its way into
+// LDS: s * (q - 8) rounded once to f16 and, for a bf16 X, on to bf16.  An
+// f16 X runs v_mfma_f32_16x16x32_f16; a bf16 X is staged as it is and runs
+// v_mfma_f32_16x16x32_bf16, so it keeps fp32's range.
+// Workgroup tile 128 x 256, four waves of 64 x 128 (4 x 8 MFMA tiles: 12
+// fragment reads feed 32 MFMAs), k steps of 32 in two LDS stages with one
+// barrier per step.  LDS rows are k-contiguous, X as [m][k] and W as [n][k],
+// padded to 40 halves (80 bytes) so the 16 rows of a fragment read land in
+// 16 distinct bank slots; a lane's A operand (row m, k 8kg .. +7) and B
 // operand (column n, k 8kg .. +7) are then one 16-byte read each.
 // ---------------------------------------------------------------------------
 #define GM_TM 128
@@ -343,47 +344,18 @@ extern "C" __global__ __launch_bounds__(256) void qm_q4_repack(Q4RepackArgs A) {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-// Two bf16 values (one 32-bit word) times 2^-s as two f16, each rounded to
-// nearest even (the power-of-two factor is exact in fp32).
-__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t v, int s) {
-    const float lo = __builtin_amdgcn_ldexpf(__builtin_bit_cast(float, v << 16), -s);
-    const float hi = __builtin_amdgcn_ldexpf(__builtin_bit_cast(float, v & 0xffff0000u), -s);
-    const half2 h = half2{(_Float16)lo, (_Float16)hi};
-    return __builtin_bit_cast(uint32_t, h);
+// An f16 pair as a bf16 pair, each rounded to nearest even (the f16 values
+// are exact in fp32, so this is one rounding of each).
+__device__ __forceinline__ uint32_t f16x2_to_bf16x2(half2 h) {
+    const bf16x2 b = bf16x2{(__bf16)(float)h[0], (__bf16)(float)h[1]};
+    return __builtin_bit_cast(uint32_t, b);
 }
 
-__device__ __forceinline__ uint4 bf16x8_to_f16x8(uint4 v, int s) {
-    return make_uint4(bf16x2_to_f16x2(v.x, s), bf16x2_to_f16x2(v.y, s), bf16x2_to_f16x2(v.z, s),
-                      bf16x2_to_f16x2(v.w, s));
-}
-
-// Largest |x| of eight bf16 values, as the 15-bit magnitude pattern (ordered
-// like the values themselves).
-__device__ __forceinline__ uint32_t bf16x8_maxmag(uint4 v) {
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-    uint32_t m = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) m = max(m, max(w[i] & 0x7fffu, (w[i] >> 16) & 0x7fffu));
-    return m;
-}
-
-// The power of two s >= 0 that brings a row whose largest bf16 magnitude is
-// mag below 2^15: 0 for every value f16 holds (mag <= 0x477f, 65280), else
-// the biased exponent minus 141.
-__device__ __forceinline__ int f16_range_shift(uint32_t mag) {
-    return mag <= 0x477fu ? 0 : (int)(mag >> 7) - 141;
-}
-
-// XBF16: x is bf16, converted to f16 as it is staged.  bf16 has fp32's range
-// and f16 does not, so a row of a k step whose bf16 values reach past f16's
-// range (|x| > 65280) is staged times 2^-s (s from its largest value, so the
-// row stays below 2^15) and its accumulators are multiplied by 2^-s before
-// that step's products and by 2^s after them: exact powers of two, so such
-// a row is accumulated at the same relative precision as any other.  Rows
-// of ordinary range (s = 0: every row of every k step in practice) take the
-// plain path; the check costs one LDS read and a ballot per k step.
+// XBF16: x is bf16 and W is rounded on to bf16 (bf16 MFMA); else both f16.
 // GU: the gate/up form.  The workgroup's 256 W rows of LDS are then
 // 16-column fragments of the gate and up weights alternately, over 128
 // output columns, so a wave's fragments j (gate) and j + 1 (up) hold the
@@ -401,12 +373,11 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
     constexpr int NJ = TN / (16 * (TM == 128 ? 2 : 4));  // 16-column fragments per wave
     __shared__ __attribute__((aligned(16))) _Float16 sA[2][TM][GM_LDK];
     __shared__ __attribute__((aligned(16))) _Float16 sB[2][TN][GM_LDK];
-    __shared__ int sShift[2][XBF16 ? TM : 1];            // per row: the k step's 2^-s staging factor
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     constexpr int NCOLS = GU ? TN / 2 : TN;              // output columns per workgroup
     const int nbn = (A.n + NCOLS - 1) / NCOLS;
     // consecutive workgroups walk n within one row block: the row block's X
-    // (k x TM f16) is reused from L2 across its column tiles
+    // (k x TM halves) is reused from L2 across its column tiles
     const int bm = (int)blockIdx.x / nbn, bn = (int)blockIdx.x % nbn;
     const int m0 = bm * TM, n0 = bn * NCOLS;
     const int wm = TM == 128 ? w >> 1 : 0, wn = TM == 128 ? w & 1 : w;
@@ -451,22 +422,11 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
     // (1024 + q), and packed f16 ops make it s * (q - 8): exact, then one
     // rounding of the product (the same bits as rounding s * (q - 8) from
     // fp32).  Column n's four rows are one 8-byte store.
+#define GM_BPAIR(v) (XBF16 ? f16x2_to_bf16x2(v) : __builtin_bit_cast(uint32_t, v))
 #define GM_LSTORE(buf)                                                                 \
     do {                                                                               \
-        if constexpr (XBF16) {                                                         \
-            /* the 32 / XH threads of a row are adjacent lanes */                      \
-            uint32_t mag_ = bf16x8_maxmag(ra0);                                        \
-            if (XH == 16) mag_ = max(mag_, bf16x8_maxmag(ra1));                        \
-            _Pragma("unroll") for (int o_ = 1; o_ < 32 / XH; o_ <<= 1)                 \
-                mag_ = max(mag_, (uint32_t)__shfl_xor((int)mag_, o_));                 \
-            const int sh_ = f16_range_shift(mag_);                                     \
-            if (ah == 0) sShift[buf][ar] = sh_;                                        \
-            *reinterpret_cast<uint4*>(&sA[buf][ar][XH * ah]) = bf16x8_to_f16x8(ra0, sh_); \
-            if (XH == 16) *reinterpret_cast<uint4*>(&sA[buf][ar][XH * ah + 8]) = bf16x8_to_f16x8(ra1, sh_); \
-        } else {                                                                       \
-            *reinterpret_cast<uint4*>(&sA[buf][ar][XH * ah]) = ra0;                    \
-            if (XH == 16) *reinterpret_cast<uint4*>(&sA[buf][ar][XH * ah + 8]) = ra1;  \
-        }                                                                              \
+        *reinterpret_cast<uint4*>(&sA[buf][ar][XH * ah]) = ra0;                        \
+        if (XH == 16) *reinterpret_cast<uint4*>(&sA[buf][ar][XH * ah + 8]) = ra1;      \
         const half2 s01 = __builtin_bit_cast(half2, rs.x), s23 = __builtin_bit_cast(half2, rs.y); \
         if (TN == 256 || tid < TN) _Pragma("unroll") for (int b_ = 0; b_ < 4; ++b_) {  \
             const uint32_t sel = 0x0c040c00u + 0x00010001u * b_;                       \
@@ -477,10 +437,8 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
             const half2 h01 = (__builtin_bit_cast(half2, ((p01 >> 4) & 0x000f000fu) | 0x64006400u) - k1032) * s01; \
             const half2 l23 = (__builtin_bit_cast(half2, (p23 & 0x000f000fu) | 0x64006400u) - k1032) * s23; \
             const half2 h23 = (__builtin_bit_cast(half2, ((p23 >> 4) & 0x000f000fu) | 0x64006400u) - k1032) * s23; \
-            *reinterpret_cast<uint2*>(&sB[buf][8 * c8 + 2 * b_][4 * rq]) =            \
-                make_uint2(__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23)); \
-            *reinterpret_cast<uint2*>(&sB[buf][8 * c8 + 2 * b_ + 1][4 * rq]) =        \
-                make_uint2(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23)); \
+            *reinterpret_cast<uint2*>(&sB[buf][8 * c8 + 2 * b_][4 * rq]) = make_uint2(GM_BPAIR(l01), GM_BPAIR(l23)); \
+            *reinterpret_cast<uint2*>(&sB[buf][8 * c8 + 2 * b_ + 1][4 * rq]) = make_uint2(GM_BPAIR(h01), GM_BPAIR(h23)); \
         }                                                                              \
     } while (0)
 
@@ -489,51 +447,58 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < NJ; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    auto mma = [](half8 a, half8 b, floatx4 c) {
+        if constexpr (XBF16)
+            return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                           c, 0, 0, 0);
+        else
+            return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    };
 
+    // Software pipeline over k steps, two LDS stages.  Entering iteration kt
+    // a wave holds step kt's fragments in registers, LDS stage (kt+1)&1 holds
+    // step kt+1 and the staging registers hold step kt+2's global data.
+    // Iteration kt runs step kt's MFMAs with step kt+1's fragment reads
+    // between them, stores step kt+2 into stage kt&1 (whose fragments every
+    // wave read before the previous barrier) and issues step kt+3's global
+    // loads; a barrier ends it.  The body is one basic block (the last
+    // iterations load a clamped step and store it into a stage nobody reads
+    // again), so the dequantization and the stores are scheduled between
+    // the MFMAs.  The k-step order of each accumulator is unchanged.
+    const int fr = lane & 15, fk = 8 * (lane >> 4);
     GM_GLOAD(0);
     GM_LSTORE(0);
+    GM_GLOAD(min(1, nk - 1));
+    GM_LSTORE(1);
+    GM_GLOAD(min(2, nk - 1));
     __syncthreads();
-    const int fr = lane & 15, fk = 8 * (lane >> 4);
+    half8 af[4], bfr[NJ];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const half8*>(&sA[0][64 * wm + 16 * i + fr][fk]);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) bfr[j] = *reinterpret_cast<const half8*>(&sB[0][16 * NJ * wn + 16 * j + fr][fk]);
+    __syncthreads();
     for (int kt = 0; kt < nk; ++kt) {
-        const int b = kt & 1;
-        if (kt + 1 < nk) GM_GLOAD(kt + 1);
-        half8 af[4];
+        const int nb = (kt + 1) & 1;
+        half8 an[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const half8*>(&sA[b][64 * wm + 16 * i + fr][fk]);
-        // rows of this step staged times 2^-s (bf16 input past f16's range):
-        // lane l holds the shift of wave row l; a C fragment row 16 i + 4 q + e
-        // takes it by a lane shuffle
-        int rsh = 0;
-        bool scaled = false;
-        if constexpr (XBF16) {
-            rsh = sShift[b][64 * wm + lane];
-            scaled = __builtin_amdgcn_ballot_w64(rsh != 0) != 0;     // wave-uniform
-        }
-        auto rescale = [&](int sign) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int sh = sign * __shfl(rsh, 16 * i + 4 * (lane >> 4) + e);
-#pragma unroll
-                    for (int j = 0; j < NJ; ++j) acc[i][j][e] = __builtin_amdgcn_ldexpf(acc[i][j][e], sh);
-                }
-        };
-        if (scaled) rescale(-1);
+        for (int i = 0; i < 4; ++i) an[i] = *reinterpret_cast<const half8*>(&sA[nb][64 * wm + 16 * i + fr][fk]);
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-            const half8 bf = *reinterpret_cast<const half8*>(&sB[b][16 * NJ * wn + 16 * j + fr][fk]);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf, acc[i][j], 0, 0, 0);
+            for (int i = 0; i < 4; ++i) acc[i][j] = mma(af[i], bfr[j], acc[i][j]);
+            bfr[j] = *reinterpret_cast<const half8*>(&sB[nb][16 * NJ * wn + 16 * j + fr][fk]);
         }
-        if (scaled) rescale(1);
-        // the other buffer was last read in step kt - 1, before the barrier
-        if (kt + 1 < nk) GM_LSTORE(b ^ 1);
+        GM_LSTORE(kt & 1);
+        GM_GLOAD(min(kt + 3, nk - 1));
+        __builtin_amdgcn_iglp_opt(0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) af[i] = an[i];
         __syncthreads();
     }
 #undef GM_GLOAD
 #undef GM_LSTORE
+#undef GM_BPAIR
 
     // C fragment: lane (n = lane & 15, mg = lane >> 4) holds rows 4 mg .. +3
     if constexpr (GU) {
@@ -609,3 +574,4 @@ extern "C" __global__ __launch_bounds__(256) void qm_rms_norm_f16(RmsNormArgs A)
         *reinterpret_cast<uint2*>(out + i) = make_uint2(lo, hi);
     }
 }
+

@@ -280,11 +280,24 @@ def test_q4_gemm(ctx, name, m, mode):
     assert np.all(np.abs(got - ref) <= bound)
 
 
+# A bf16 input runs bf16 MFMA with W rounded to f16 and then to bf16: per
+# term at most 2^-8 + 2^-11 of |x w| (the input itself is exact), plus the
+# fp32 accumulation.
+BF16_W_EPS = 2.0 ** -8 + 2.0 ** -11 + 1e-4
+
+
+def _w_bf16(packed, scales):
+    """W as the bf16-input GEMM multiplies it: f16(s (q - 8)), then bf16."""
+    return W.bf16_value(W.bf16_bits(W.f16_value(W.f16_bits(W.q4_dequant(packed, scales)))))
+
+
 def test_q4_gemm_bf16_input(ctx):
     """out_proj on a mixer prefill output (bf16 [T][4096]) with the residual
-    added in place (gemv.rs:1222-1223): bf16 x is rounded to f16 as it is
-    staged, so the result equals the f16-input GEMM on f16(x) bit for bit,
-    and meets the GEMM bar against the oracle on the bf16 values."""
+    added in place (gemv.rs:1222-1223).  Against the oracle on the bf16
+    values: |y - y_ref| <= (2^-8 + 2^-11 + 1e-4) sum_k |x_k W_kj|.  Against
+    the arithmetic the kernel states (x times bf16(f16(s (q - 8))) summed in
+    fp32): within 1e-5 of max |y|, where a W rounded only to f16 would differ
+    by ~1e-3 of it."""
     k, n = W.Q4_PROJ_SHAPES["out_proj"]
     m = 77
     rng = np.random.default_rng(61)
@@ -296,14 +309,18 @@ def test_q4_gemm_bf16_input(ctx):
     print("case: q4 gemm bf16 input, out_proj m=77 residual in place", flush=True)
     y = ctx.upload(res)
     ctx.q4_gemm(m, k, n, ctx.upload(xb), codes, gsc, y=y, residual=y, x_dtype=M.QM_BF16)
-    got = ctx.download(y, (m, n), np.float32)
-    y16 = ctx.upload(res)
-    ctx.q4_gemm(m, k, n, ctx.upload(W.f16_bits(xv)), codes, gsc, y=y16, residual=y16)
-    assert np.array_equal(got, ctx.download(y16, (m, n), np.float32))
+    got = ctx.download(y, (m, n), np.float32).astype(np.float64)
     ref = O.q4_gemm(xv, packed, scales).astype(np.float64) + res
-    bound = 1e-3 * (_mag(xv, packed, scales) + np.abs(res)) + 1e-30
+    bound = BF16_W_EPS * (_mag(xv, packed, scales) + np.abs(res)) + 1e-30
     print(f"max|d|/bound {(np.abs(got - ref) / bound).max():.3e}")
     assert np.all(np.abs(got - ref) <= bound)
+    model = xv.astype(np.float64) @ _w_bf16(packed, scales).astype(np.float64) + res
+    dev = np.abs(got - model).max() / np.abs(model - res).max()
+    f16w = xv.astype(np.float64) @ W.f16_value(W.f16_bits(W.q4_dequant(packed, scales))).astype(np.float64) + res
+    print(f"vs bf16-weight arithmetic {dev:.2e}, f16-weight arithmetic differs by "
+          f"{np.abs(f16w - model).max() / np.abs(model - res).max():.2e}")
+    assert dev <= 1e-5
+    assert np.abs(f16w - model).max() / np.abs(model - res).max() > 1e-4      # the check can tell them apart
 
 
 @pytest.mark.parametrize("n,m,x_dtype", [(9216, 64, "f16"), (2592, 130, "f16"), (2592, 37, "bf16")])
@@ -332,7 +349,8 @@ def test_q4_gemm_gate_up(ctx, n, m, x_dtype):
     one = np.float32(1.0)
     ref = ((g / (one + np.exp(-g))) * u).astype(np.float64)
     g, u = g.astype(np.float64), u.astype(np.float64)
-    bound = (1e-3 * (1.2 * _mag(xv, gp, gs) * np.abs(u) + 1.1 * np.abs(g) * _mag(xv, up, us))
+    eps = BF16_W_EPS if x_dtype == "bf16" else 1e-3
+    bound = (eps * (1.2 * _mag(xv, gp, gs) * np.abs(u) + 1.1 * np.abs(g) * _mag(xv, up, us))
              + np.abs(ref) * 2.0 ** -8 + 1e-7)
     print(f"max|d|/bound {(np.abs(got - ref) / bound).max():.3e}")
     assert np.all(np.abs(got - ref) <= bound)
@@ -349,8 +367,10 @@ def _outlier_rows(rng, m, k, cols, scale):
 def test_q4_gemm_gate_up_outliers(ctx, scale):
     """Outlier input channels whose gate and up products reach past f16's
     range (|silu(g) u| up to ~1e9 here): the bf16 output stays finite and
-    within the same bar as ordinary inputs, and the down_proj GEMM that reads
-    it (bf16 input of ~1e9 in a few rows) is finite and within its bar."""
+    within the bf16-input bar, and the down_proj GEMM that reads it (bf16
+    input of ~1e9 in a few rows) is finite and within the same bar.  These
+    sums are dominated by a few outlier terms, so the bar's per-term bound
+    (W rounded to bf16) is what they are held to, without averaging."""
     k, n, m = 2560, 2592, 40
     rng = np.random.default_rng(int(scale))
     (gp, gs), (up, us) = W.q4_random_weight(k, n, rng), W.q4_random_weight(k, n, rng)
@@ -369,7 +389,7 @@ def test_q4_gemm_gate_up_outliers(ctx, scale):
     ref = ((g / (np.float32(1.0) + np.exp(-g))) * u).astype(np.float64)
     assert np.isfinite(got).all() and np.abs(ref).max() > 65504.0
     g, u = g.astype(np.float64), u.astype(np.float64)
-    bound = (1e-3 * (1.2 * _mag(xv, gp, gs) * np.abs(u) + 1.1 * np.abs(g) * _mag(xv, up, us))
+    bound = (BF16_W_EPS * (1.2 * _mag(xv, gp, gs) * np.abs(u) + 1.1 * np.abs(g) * _mag(xv, up, us))
              + np.abs(ref) * 2.0 ** -8 + 1e-7)
     print(f"gate/up: max|h| {np.abs(ref).max():.3e}, max|d|/bound {(np.abs(got - ref) / bound).max():.3e}")
     assert np.all(np.abs(got - ref) <= bound)
@@ -382,18 +402,17 @@ def test_q4_gemm_gate_up_outliers(ctx, scale):
     goty = ctx.download(y, (m, 2560), np.float32).astype(np.float64)
     hv = W.bf16_value(hbits)
     refy = O.q4_gemm(hv, dp, ds).astype(np.float64) + res
-    boundy = 1e-3 * (_mag(hv, dp, ds) + np.abs(res)) + 1e-30
+    boundy = BF16_W_EPS * (_mag(hv, dp, ds) + np.abs(res)) + 1e-30
     print(f"down: max|y| {np.abs(refy).max():.3e}, max|d|/bound {(np.abs(goty - refy) / boundy).max():.3e}")
     assert np.isfinite(goty).all()
     assert np.all(np.abs(goty - refy) <= boundy)
 
 
 def test_q4_gemm_bf16_rows_past_f16_range_match_unscaled_rows(ctx):
-    """A bf16 input row scaled by 2^20 (past f16's range in every k step)
-    gives exactly 2^20 times the unscaled row's result: the power-of-two
-    staging and accumulator rescaling commute with every rounding.  The
-    base values keep |x| >= 0.01, inside f16's normal range, so the base
-    row's own f16 staging rounds like the scaled one."""
+    """A bf16 input row scaled by 2^20 (past f16's range, inside bf16's)
+    gives exactly 2^20 times the unscaled row's result: bf16 inputs run
+    bf16 MFMA with fp32 accumulation, and a power of two commutes with
+    every rounding on that path."""
     k, n, m = 2560, 4096, 8
     rng = np.random.default_rng(77)
     packed, scales = W.q4_random_weight(k, n, rng)
@@ -410,7 +429,7 @@ def test_q4_gemm_bf16_rows_past_f16_range_match_unscaled_rows(ctx):
     assert np.isfinite(got).all()
     assert np.array_equal(got[m:], got[:m] * np.float32(2.0 ** 20))
     ref = O.q4_gemm(base, packed, scales).astype(np.float64)
-    assert np.all(np.abs(got[:m] - ref) <= 1e-3 * _mag(base, packed, scales) + 1e-30)
+    assert np.all(np.abs(got[:m] - ref) <= BF16_W_EPS * _mag(base, packed, scales) + 1e-30)
 
 
 def test_q4_gemm_errors(ctx):
