@@ -291,22 +291,23 @@ def _w_bf16(packed, scales):
     return W.bf16_value(W.bf16_bits(W.f16_value(W.f16_bits(W.q4_dequant(packed, scales)))))
 
 
-def test_q4_gemm_bf16_input(ctx):
+@pytest.mark.parametrize("name,m", [("out_proj", 77), ("in_proj_qkv", 2000)])
+def test_q4_gemm_bf16_input(ctx, name, m):
     """out_proj on a mixer prefill output (bf16 [T][4096]) with the residual
-    added in place (gemv.rs:1222-1223).  Against the oracle on the bf16
+    added in place (gemv.rs:1222-1223), and a 2000-row bf16 input on the
+    in_proj_qkv shape (several tiles per CU).  Against the oracle on the bf16
     values: |y - y_ref| <= (2^-8 + 2^-11 + 1e-4) sum_k |x_k W_kj|.  Against
     the arithmetic the kernel states (x times bf16(f16(s (q - 8))) summed in
     fp32): within 1e-5 of max |y|, where a W rounded only to f16 would differ
     by ~1e-3 of it."""
-    k, n = W.Q4_PROJ_SHAPES["out_proj"]
-    m = 77
-    rng = np.random.default_rng(61)
+    k, n = W.Q4_PROJ_SHAPES[name]
+    rng = np.random.default_rng(61 + m)
     packed, scales = W.q4_random_weight(k, n, rng)
     codes, gsc = repack(ctx, packed, scales)
     xb = W.bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
     xv = W.bf16_value(xb)
     res = rng.standard_normal((m, n)).astype(np.float32)
-    print("case: q4 gemm bf16 input, out_proj m=77 residual in place", flush=True)
+    print(f"case: q4 gemm bf16 input, {name} m={m} residual in place", flush=True)
     y = ctx.upload(res)
     ctx.q4_gemm(m, k, n, ctx.upload(xb), codes, gsc, y=y, residual=y, x_dtype=M.QM_BF16)
     got = ctx.download(y, (m, n), np.float32).astype(np.float64)
@@ -323,12 +324,14 @@ def test_q4_gemm_bf16_input(ctx):
     assert np.abs(f16w - model).max() / np.abs(model - res).max() > 1e-4      # the check can tell them apart
 
 
-@pytest.mark.parametrize("n,m,x_dtype", [(9216, 64, "f16"), (2592, 130, "f16"), (2592, 37, "bf16")])
+@pytest.mark.parametrize("n,m,x_dtype", [(9216, 64, "f16"), (2592, 130, "f16"), (2592, 37, "bf16"),
+                                         (9216, 1000, "f16"), (9216, 1000, "bf16")])
 def test_q4_gemm_gate_up(ctx, n, m, x_dtype):
     """The prefill MLP's gate/up GEMMs and silu(g) * u (gemv.rs:1231-1237)
     in one launch, written as bf16.  Bar: the GEMM bar carried through
     silu(g) * u, plus the bf16 rounding of the output.  n = 2592 ends in a
-    partial 128-column tile of the 8-column device layout."""
+    partial 128-column tile of the 8-column device layout; m = 1000 on
+    n = 9216 runs 576 workgroups, several per CU."""
     k = 2560
     rng = np.random.default_rng(n + m)
     (gp, gs), (up, us) = W.q4_random_weight(k, n, rng), W.q4_random_weight(k, n, rng)
