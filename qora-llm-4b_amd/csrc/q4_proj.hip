@@ -337,8 +337,6 @@ extern "C" __global__ __launch_bounds__(256) void qm_q4_repack(Q4RepackArgs A) {
 // 16 distinct bank slots; a lane's A operand (row m, k 8kg .. +7) and B
 // operand (column n, k 8kg .. +7) are then one 16-byte read each.
 // ---------------------------------------------------------------------------
-#define GM_TM 128
-#define GM_TN 256
 #define GM_TK 32
 #define GM_LDK 40
 
@@ -361,16 +359,19 @@ __device__ __forceinline__ uint32_t f16x2_to_bf16x2(half2 h) {
 // output columns, so a wave's fragments j (gate) and j + 1 (up) hold the
 // same outputs and the epilogue writes silu(g) * u as bf16 (whose range,
 // unlike f16's, holds any product of the fp32 accumulators).
-// Workgroup tiles TM x TN: 128 x 256, four waves of 64 x 128 (2 x 2); for
-// narrow outputs whose 128 x 256 tiles would leave CUs idle (n = 2560: 10
-// column tiles), 128 x 128 (2 x 2 waves of 64 x 64), twice the workgroups;
-// its W tile is staged by threads 0 .. 127.  (64 x 256 tiles, four waves of
-// 64 x 64 side by side, measured 2% slower on the 4096-token prefill.)
-template <bool XBF16, bool GU, int TM, int TN>
+// A workgroup is WM x WN waves; a wave computes MI x NJ MFMA tiles of
+// 16 x 16 (16 MI rows, 16 NJ columns), so the workgroup tile is TM x TN =
+// 16 MI WM x 16 NJ WN.  128 x 256 (2 x 2 waves of 64 x 128) where there are
+// tiles enough for two workgroups per CU; for narrow outputs that would
+// leave CUs idle, 128 x 128 (n = 2560: 10 column tiles of 256) or 64 x 128
+// (n = 1024), and 16 x 32 (one wave) for n = 32.  The W tile is staged by
+// threads 0 .. TN-1.  (64 x 256 tiles, four waves of 64 x 64 side by side,
+// measured 2% slower on the 4096-token prefill.)
+template <bool XBF16, bool GU, int WM, int WN, int MI, int NJ>
 __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
-    static_assert((TM == 128 && TN == 256) || (!GU && ((TM == 64 && TN == 256) || (TM == 128 && TN == 128))),
-                  "tile");
-    constexpr int NJ = TN / (16 * (TM == 128 ? 2 : 4));  // 16-column fragments per wave
+    constexpr int TM = 16 * MI * WM, TN = 16 * NJ * WN, NTH = 64 * WM * WN;
+    static_assert(!GU || (WN == 2 && NJ == 8), "the gate/up form pairs fragments j, j + 1 over 256 LDS rows");
+    static_assert(NTH >= TN && (TM * GM_TK / NTH == 8 || TM * GM_TK / NTH == 16), "staging shape");
     __shared__ __attribute__((aligned(16))) _Float16 sA[2][TM][GM_LDK];
     __shared__ __attribute__((aligned(16))) _Float16 sB[2][TN][GM_LDK];
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
@@ -380,12 +381,12 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
     // (k x TM halves) is reused from L2 across its column tiles
     const int bm = (int)blockIdx.x / nbn, bn = (int)blockIdx.x % nbn;
     const int m0 = bm * TM, n0 = bn * NCOLS;
-    const int wm = TM == 128 ? w >> 1 : 0, wn = TM == 128 ? w & 1 : w;
+    const int wm = w / WN, wn = w % WN;
     const int T = A.tile, K = A.k;
     const int nk = K / GM_TK;
 
-    // X staging: thread -> row tid / (256 / TM), TM / 8 halves of k
-    constexpr int XH = TM / 8;                           // 16 or 8 halves per thread
+    // X staging: thread -> row tid / (32 / XH), XH halves of k
+    constexpr int XH = TM * GM_TK / NTH;                 // 16 or 8 halves per thread
     const int ar = tid / (32 / XH), ah = tid % (32 / XH);
     const uint16_t* xrow = A.x + (size_t)min(m0 + ar, A.m - 1) * K + XH * ah;
     // W staging: thread -> 8-column block c8 = tid / 8 of the tile, rows
@@ -410,7 +411,7 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
         const int k0_ = (kt) * GM_TK;                                                  \
         ra0 = *reinterpret_cast<const uint4*>(xrow + k0_);                            \
         if (XH == 16) ra1 = *reinterpret_cast<const uint4*>(xrow + k0_ + 8);          \
-        if (TN == 256 || tid < TN) {                                                   \
+        if (NTH == TN || tid < TN) {                                                   \
             _Pragma("unroll") for (int i_ = 0; i_ < 4; ++i_)                           \
                 rb[i_] = *reinterpret_cast<const uint32_t*>(bcodes + (size_t)(k0_ + i_) * cstride); \
             rs = *reinterpret_cast<const uint2*>(bsc + k0_);                          \
@@ -428,7 +429,7 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
         *reinterpret_cast<uint4*>(&sA[buf][ar][XH * ah]) = ra0;                        \
         if (XH == 16) *reinterpret_cast<uint4*>(&sA[buf][ar][XH * ah + 8]) = ra1;      \
         const half2 s01 = __builtin_bit_cast(half2, rs.x), s23 = __builtin_bit_cast(half2, rs.y); \
-        if (TN == 256 || tid < TN) _Pragma("unroll") for (int b_ = 0; b_ < 4; ++b_) {  \
+        if (NTH == TN || tid < TN) _Pragma("unroll") for (int b_ = 0; b_ < 4; ++b_) {  \
             const uint32_t sel = 0x0c040c00u + 0x00010001u * b_;                       \
             const uint32_t p01 = __builtin_amdgcn_perm(rb[1], rb[0], sel);             \
             const uint32_t p23 = __builtin_amdgcn_perm(rb[3], rb[2], sel);             \
@@ -442,9 +443,9 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
         }                                                                              \
     } while (0)
 
-    floatx4 acc[4][NJ];
+    floatx4 acc[MI][NJ];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < NJ; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     auto mma = [](half8 a, half8 b, floatx4 c) {
@@ -472,28 +473,28 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
     GM_LSTORE(1);
     GM_GLOAD(min(2, nk - 1));
     __syncthreads();
-    half8 af[4], bfr[NJ];
+    half8 af[MI], bfr[NJ];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const half8*>(&sA[0][64 * wm + 16 * i + fr][fk]);
+    for (int i = 0; i < MI; ++i) af[i] = *reinterpret_cast<const half8*>(&sA[0][16 * MI * wm + 16 * i + fr][fk]);
 #pragma unroll
     for (int j = 0; j < NJ; ++j) bfr[j] = *reinterpret_cast<const half8*>(&sB[0][16 * NJ * wn + 16 * j + fr][fk]);
     __syncthreads();
     for (int kt = 0; kt < nk; ++kt) {
         const int nb = (kt + 1) & 1;
-        half8 an[4];
+        half8 an[MI];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) an[i] = *reinterpret_cast<const half8*>(&sA[nb][64 * wm + 16 * i + fr][fk]);
+        for (int i = 0; i < MI; ++i) an[i] = *reinterpret_cast<const half8*>(&sA[nb][16 * MI * wm + 16 * i + fr][fk]);
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[i][j] = mma(af[i], bfr[j], acc[i][j]);
+            for (int i = 0; i < MI; ++i) acc[i][j] = mma(af[i], bfr[j], acc[i][j]);
             bfr[j] = *reinterpret_cast<const half8*>(&sB[nb][16 * NJ * wn + 16 * j + fr][fk]);
         }
         GM_LSTORE(kt & 1);
         GM_GLOAD(min(kt + 3, nk - 1));
         __builtin_amdgcn_iglp_opt(0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) af[i] = an[i];
+        for (int i = 0; i < MI; ++i) af[i] = an[i];
         __syncthreads();
     }
 #undef GM_GLOAD
@@ -504,13 +505,13 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
     if constexpr (GU) {
 #pragma unroll
         for (int j = 0; j < NJ; j += 2) {
-            const int col = n0 + 64 * wn + 8 * j + fr;
+            const int col = n0 + 8 * NJ * wn + 8 * j + fr;
             if (col >= A.n) continue;
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const int row = m0 + 64 * wm + 16 * i + 4 * (lane >> 4) + e;
+                    const int row = m0 + 16 * MI * wm + 16 * i + 4 * (lane >> 4) + e;
                     if (row >= A.m) continue;
                     const float g = acc[i][j][e], u = acc[i][j + 1][e];
                     A.y_bf16[(size_t)row * A.n + col] = f32_to_bf16(g / (1.0f + expf(-g)) * u);
@@ -523,10 +524,10 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
         const int col = n0 + 16 * NJ * wn + 16 * j + fr;
         if (col >= A.n) continue;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < MI; ++i)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int row = m0 + 64 * wm + 16 * i + 4 * (lane >> 4) + e;
+                const int row = m0 + 16 * MI * wm + 16 * i + 4 * (lane >> 4) + e;
                 if (row >= A.m) continue;
                 const size_t o = (size_t)row * A.n + col;
                 float v = acc[i][j][e];
@@ -537,12 +538,16 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
     }
 }
 
-extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm(Q4GemmArgs A) { q4_gemm_body<false, false, 128, 256>(A); }
-extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm_xbf16(Q4GemmArgs A) { q4_gemm_body<true, false, 128, 256>(A); }
-extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm_gu(Q4GemmArgs A) { q4_gemm_body<false, true, 128, 256>(A); }
-extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm_gu_xbf16(Q4GemmArgs A) { q4_gemm_body<true, true, 128, 256>(A); }
-extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm_n128(Q4GemmArgs A) { q4_gemm_body<false, false, 128, 128>(A); }
-extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm_xbf16_n128(Q4GemmArgs A) { q4_gemm_body<true, false, 128, 128>(A); }
+extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm(Q4GemmArgs A) { q4_gemm_body<false, false, 2, 2, 4, 8>(A); }
+extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm_xbf16(Q4GemmArgs A) { q4_gemm_body<true, false, 2, 2, 4, 8>(A); }
+extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm_gu(Q4GemmArgs A) { q4_gemm_body<false, true, 2, 2, 4, 8>(A); }
+extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm_gu_xbf16(Q4GemmArgs A) { q4_gemm_body<true, true, 2, 2, 4, 8>(A); }
+extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm_n128(Q4GemmArgs A) { q4_gemm_body<false, false, 2, 2, 4, 4>(A); }
+extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm_xbf16_n128(Q4GemmArgs A) { q4_gemm_body<true, false, 2, 2, 4, 4>(A); }
+extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm_m64(Q4GemmArgs A) { q4_gemm_body<false, false, 2, 2, 2, 4>(A); }
+extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm_xbf16_m64(Q4GemmArgs A) { q4_gemm_body<true, false, 2, 2, 2, 4>(A); }
+extern "C" __global__ __launch_bounds__(64) void qm_q4_gemm_n32(Q4GemmArgs A) { q4_gemm_body<false, false, 1, 1, 1, 2>(A); }
+extern "C" __global__ __launch_bounds__(64) void qm_q4_gemm_xbf16_n32(Q4GemmArgs A) { q4_gemm_body<true, false, 1, 1, 1, 2>(A); }
 
 // rms_norm (1 + gamma, eps 1e-6; gemv.rs:571-579) of each of m rows of f32
 // x [m][k], written as the f16 input of qm_q4_gemm; without a norm weight,

@@ -52,6 +52,8 @@ struct qm_context {
     hipFunction_t f_q4_gate_up = nullptr;
     hipFunction_t f_q4_gemm[2][2] = {};  // [x bf16][gate/up form]
     hipFunction_t f_q4_gemm_n128[2] = {}; // [x bf16]: 128 x 128 tiles for narrow outputs
+    hipFunction_t f_q4_gemm_m64[2] = {};  // [x bf16]: 64 x 128 tiles
+    hipFunction_t f_q4_gemm_n32[2] = {};  // [x bf16]: 16 x 32 tiles, one wave, for n = 32
     hipFunction_t f_rms_f16 = nullptr;
     hipFunction_t f_lm_head = nullptr;
     hipFunction_t f_embed = nullptr;
@@ -322,6 +324,10 @@ int32_t qm_create(qm_context** out, const qm_config* cfg, const char* code_objec
     if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemm_gu_xbf16", &c->f_q4_gemm[1][1]);
     if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemm_n128", &c->f_q4_gemm_n128[0]);
     if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemm_xbf16_n128", &c->f_q4_gemm_n128[1]);
+    if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemm_m64", &c->f_q4_gemm_m64[0]);
+    if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemm_xbf16_m64", &c->f_q4_gemm_m64[1]);
+    if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemm_n32", &c->f_q4_gemm_n32[0]);
+    if (st == QM_OK) st = load_function(c, mods[5], "qm_q4_gemm_xbf16_n32", &c->f_q4_gemm_n32[1]);
     if (st == QM_OK) st = load_function(c, mods[5], "qm_rms_norm_f16", &c->f_rms_f16);
     if (st == QM_OK) st = load_function(c, mods[6], "qm_q4_lm_head", &c->f_lm_head);
     if (st == QM_OK) st = load_function(c, mods[6], "qm_q4_embed", &c->f_embed);
@@ -1026,14 +1032,21 @@ int32_t qm_q4_gemm(qm_context* c, qm_stream stream, int32_t m, int32_t k, int32_
     if (!all_aligned16({x, codes, gscales, residual, y, y_bf16}))
         return fail(c, QM_ERR_INVALID_ARG, "qm_q4_gemm: device pointers must be 16-byte aligned");
     Q4GemmArgs ga{x, codes, gscales, nullptr, nullptr, y, y_bf16, residual, m, k, n, QM_Q4_TILE(n)};
-    const int64_t ncol = (n + 255) / 256;
-    const int64_t tiles128 = (m + 127) / 128 * ncol;
-    // too few 128 x 256 tiles for two workgroups per CU (e.g. n = 2560): 128 x 128 tiles
-    if (tiles128 < 2 * static_cast<int64_t>(c->num_cu) && m > 64) {
-        const uint32_t grid = static_cast<uint32_t>((m + 127) / 128 * ((n + 127) / 128));
-        return launch(c, c->f_q4_gemm_n128[x_dtype == QM_BF16], grid, 256, ga, pick(c, stream), "qm_q4_gemm");
-    }
-    return launch(c, c->f_q4_gemm[x_dtype == QM_BF16][0], static_cast<uint32_t>(tiles128), 256, ga, pick(c, stream),
+    const int xb = x_dtype == QM_BF16;
+    auto tiles = [&](int64_t tm, int64_t tn) { return (m + tm - 1) / tm * ((n + tn - 1) / tn); };
+    const int64_t two_per_cu = 2 * static_cast<int64_t>(c->num_cu);
+    // the widest tile that still gives two workgroups per CU; n = 32 (the
+    // DeltaNet a/b projections) one wave per 16 rows
+    if (n <= 32)
+        return launch(c, c->f_q4_gemm_n32[xb], static_cast<uint32_t>(tiles(16, 32)), 64, ga, pick(c, stream),
+                      "qm_q4_gemm");
+    if (tiles(128, 256) >= two_per_cu)
+        return launch(c, c->f_q4_gemm[xb][0], static_cast<uint32_t>(tiles(128, 256)), 256, ga, pick(c, stream),
+                      "qm_q4_gemm");
+    if (tiles(128, 128) >= two_per_cu)
+        return launch(c, c->f_q4_gemm_n128[xb], static_cast<uint32_t>(tiles(128, 128)), 256, ga, pick(c, stream),
+                      "qm_q4_gemm");
+    return launch(c, c->f_q4_gemm_m64[xb], static_cast<uint32_t>(tiles(64, 128)), 256, ga, pick(c, stream),
                   "qm_q4_gemm");
 }
 

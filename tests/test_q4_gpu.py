@@ -244,12 +244,14 @@ def test_rms_norm_f16(ctx):
     assert np.array_equal(ctx.download(out, (m, k), np.uint16), W.f16_bits(x))
 
 
-# m > 64 with fewer than two 128 x 256 tiles per CU takes the 128 x 128
-# kernel; m = 1930 on the 8192-wide weight (512 tiles) the 128 x 256 one.
+# Tile shapes on 256 CUs: m = 1930 on the 8192-wide weight (512 tiles of
+# 128 x 256) and m = 3300 on the 2560-wide one (520 tiles of 128 x 128)
+# take the wide kernels, the smaller cases 64 x 128 tiles, and n = 32 the
+# one-wave 16 x 32 kernel.
 @pytest.mark.parametrize("name,m,mode", [("in_proj_qkv", 200, "bf16"), ("in_proj_z", 37, "bf16"),
                                          ("out_proj", 64, "residual"), ("in_proj_a", 130, "f32"),
                                          ("down_proj", 129, "residual"), ("k_proj", 1, "f32"),
-                                         ("in_proj_qkv", 1930, "bf16")])
+                                         ("in_proj_qkv", 1930, "bf16"), ("out_proj", 3300, "residual")])
 def test_q4_gemm(ctx, name, m, mode):
     """gemm_q4 (gemv.rs:529-542) on MFMA: y = x W (+ residual), x f16; bar
     |y - y_ref| <= 1e-3 * sum_k |x_k W_kj| per element (W rounded to f16 per
@@ -291,11 +293,13 @@ def _w_bf16(packed, scales):
     return W.bf16_value(W.bf16_bits(W.f16_value(W.f16_bits(W.q4_dequant(packed, scales)))))
 
 
-@pytest.mark.parametrize("name,m", [("out_proj", 77), ("in_proj_qkv", 2000)])
+@pytest.mark.parametrize("name,m", [("out_proj", 77), ("in_proj_qkv", 2000), ("down_proj", 3300),
+                                    ("in_proj_a", 300)])
 def test_q4_gemm_bf16_input(ctx, name, m):
     """out_proj on a mixer prefill output (bf16 [T][4096]) with the residual
-    added in place (gemv.rs:1222-1223), and a 2000-row bf16 input on the
-    in_proj_qkv shape (several tiles per CU).  Against the oracle on the bf16
+    added in place (gemv.rs:1222-1223), and bf16 inputs on the other tile
+    shapes (in_proj_qkv 128 x 256, down_proj 128 x 128, the 32-wide
+    in_proj_a 16 x 32).  Against the oracle on the bf16
     values: |y - y_ref| <= (2^-8 + 2^-11 + 1e-4) sum_k |x_k W_kj|.  Against
     the arithmetic the kernel states (x times bf16(f16(s (q - 8))) summed in
     fp32): within 1e-5 of max |y|, where a W rounded only to f16 would differ
