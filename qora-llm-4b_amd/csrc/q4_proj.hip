@@ -389,10 +389,13 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
     constexpr int XH = TM * GM_TK / NTH;                 // 16 or 8 halves per thread
     const int ar = tid / (32 / XH), ah = tid % (32 / XH);
     const uint16_t* xrow = A.x + (size_t)min(m0 + ar, A.m - 1) * K + XH * ah;
-    // W staging: thread -> 8-column block c8 = tid / 8 of the tile, rows
-    // 4 rq .. 4 rq + 3 of the step (rq = tid % 8); a block is 4 code bytes
-    // of one row (T = 16: half of a tile row, T = 8: a whole one)
-    const int c8 = tid >> 3, rq = tid & 7;
+    // W staging: thread -> 8-column block c8 of the tile and RQ rows
+    // RQ rq .. +RQ-1 of the step, with every thread taking a share (RQ = 4
+    // when the tile has as many columns as the workgroup threads, else 2); a
+    // block is 4 code bytes of one row (T = 16: half of a tile row, T = 8: a
+    // whole one)
+    constexpr int RQ = NTH == TN ? 4 : 2;
+    const int c8 = tid / (32 / RQ), rq = tid % (32 / RQ);
     // GU: LDS rows 8 c8 .. +7 are half of fragment c8 / 2, of the up weight
     // when that fragment is odd
     const bool up = GU && ((c8 >> 1) & 1);
@@ -400,21 +403,23 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
     const int ncl = min(n0 + ccol, A.n - 8);            // valid block for loads
     const size_t cstride = (size_t)(T / 2);
     const uint8_t* bcodes = (up ? A.codes2 : A.codes) + (size_t)(ncl / T) * K * cstride + (ncl % T) / 2 +
-                            4 * rq * cstride;
-    const uint16_t* bsc = (up ? A.gscales2 : A.gscales) + (size_t)(ncl / 32) * K + 4 * rq;
+                            RQ * rq * cstride;
+    const uint16_t* bsc = (up ? A.gscales2 : A.gscales) + (size_t)(ncl / 32) * K + RQ * rq;
+    const bool wthread = NTH * RQ == 4 * TN || tid < TN * 4 / RQ;
 
     uint4 ra0, ra1;
     uint32_t rb[4];
-    uint2 rs;                                            // 4 f16 scales of rows 4rq .. +3
+    uint2 rs;                                            // RQ f16 scales of rows RQ rq .. +RQ-1
 #define GM_GLOAD(kt)                                                                   \
     do {                                                                               \
         const int k0_ = (kt) * GM_TK;                                                  \
         ra0 = *reinterpret_cast<const uint4*>(xrow + k0_);                            \
         if (XH == 16) ra1 = *reinterpret_cast<const uint4*>(xrow + k0_ + 8);          \
-        if (NTH == TN || tid < TN) {                                                   \
-            _Pragma("unroll") for (int i_ = 0; i_ < 4; ++i_)                           \
+        if (wthread) {                                                                 \
+            _Pragma("unroll") for (int i_ = 0; i_ < RQ; ++i_)                          \
                 rb[i_] = *reinterpret_cast<const uint32_t*>(bcodes + (size_t)(k0_ + i_) * cstride); \
-            rs = *reinterpret_cast<const uint2*>(bsc + k0_);                          \
+            if (RQ == 4) rs = *reinterpret_cast<const uint2*>(bsc + k0_);             \
+            else rs.x = *reinterpret_cast<const uint32_t*>(bsc + k0_);                \
         }                                                                              \
     } while (0)
     // Columns 2b, 2b + 1 of a row pair come from byte b of each row's block.
@@ -429,17 +434,22 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
         *reinterpret_cast<uint4*>(&sA[buf][ar][XH * ah]) = ra0;                        \
         if (XH == 16) *reinterpret_cast<uint4*>(&sA[buf][ar][XH * ah + 8]) = ra1;      \
         const half2 s01 = __builtin_bit_cast(half2, rs.x), s23 = __builtin_bit_cast(half2, rs.y); \
-        if (NTH == TN || tid < TN) _Pragma("unroll") for (int b_ = 0; b_ < 4; ++b_) {  \
+        if (wthread) _Pragma("unroll") for (int b_ = 0; b_ < 4; ++b_) {                \
             const uint32_t sel = 0x0c040c00u + 0x00010001u * b_;                       \
-            const uint32_t p01 = __builtin_amdgcn_perm(rb[1], rb[0], sel);             \
-            const uint32_t p23 = __builtin_amdgcn_perm(rb[3], rb[2], sel);             \
             const half2 k1032 = half2{1032.0f16, 1032.0f16};                           \
+            const uint32_t p01 = __builtin_amdgcn_perm(rb[1], rb[0], sel);             \
             const half2 l01 = (__builtin_bit_cast(half2, (p01 & 0x000f000fu) | 0x64006400u) - k1032) * s01; \
             const half2 h01 = (__builtin_bit_cast(half2, ((p01 >> 4) & 0x000f000fu) | 0x64006400u) - k1032) * s01; \
-            const half2 l23 = (__builtin_bit_cast(half2, (p23 & 0x000f000fu) | 0x64006400u) - k1032) * s23; \
-            const half2 h23 = (__builtin_bit_cast(half2, ((p23 >> 4) & 0x000f000fu) | 0x64006400u) - k1032) * s23; \
-            *reinterpret_cast<uint2*>(&sB[buf][8 * c8 + 2 * b_][4 * rq]) = make_uint2(GM_BPAIR(l01), GM_BPAIR(l23)); \
-            *reinterpret_cast<uint2*>(&sB[buf][8 * c8 + 2 * b_ + 1][4 * rq]) = make_uint2(GM_BPAIR(h01), GM_BPAIR(h23)); \
+            if constexpr (RQ == 4) {                                                   \
+                const uint32_t p23 = __builtin_amdgcn_perm(rb[3], rb[2], sel);         \
+                const half2 l23 = (__builtin_bit_cast(half2, (p23 & 0x000f000fu) | 0x64006400u) - k1032) * s23; \
+                const half2 h23 = (__builtin_bit_cast(half2, ((p23 >> 4) & 0x000f000fu) | 0x64006400u) - k1032) * s23; \
+                *reinterpret_cast<uint2*>(&sB[buf][8 * c8 + 2 * b_][4 * rq]) = make_uint2(GM_BPAIR(l01), GM_BPAIR(l23)); \
+                *reinterpret_cast<uint2*>(&sB[buf][8 * c8 + 2 * b_ + 1][4 * rq]) = make_uint2(GM_BPAIR(h01), GM_BPAIR(h23)); \
+            } else {                                                                   \
+                *reinterpret_cast<uint32_t*>(&sB[buf][8 * c8 + 2 * b_][2 * rq]) = GM_BPAIR(l01); \
+                *reinterpret_cast<uint32_t*>(&sB[buf][8 * c8 + 2 * b_ + 1][2 * rq]) = GM_BPAIR(h01); \
+            }                                                                          \
         }                                                                              \
     } while (0)
 
