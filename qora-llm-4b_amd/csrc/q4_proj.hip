@@ -511,40 +511,48 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
 #undef GM_LSTORE
 #undef GM_BPAIR
 
-    // C fragment: lane (n = lane & 15, mg = lane >> 4) holds rows 4 mg .. +3
-    if constexpr (GU) {
+    // Epilogue through LDS.  A C fragment gives a lane 4 rows of one column
+    // (16 lanes: 32- or 64-byte pieces of a row), so each wave stages its
+    // tile 16 rows at a time in a private region of the idle W stages (the
+    // loop's last barrier ended every fragment read) and stores whole row
+    // segments, 16 bytes of fp32 per lane.  A wave reads back only what it
+    // wrote, and its LDS operations complete in order, so no barrier.  The
+    // row stride OC + 4 keeps the 64 lanes' stores in distinct banks.
+    constexpr int OC = GU ? 8 * NJ : 16 * NJ;              // output columns per wave
+    constexpr int EPS = OC + 4;
+    constexpr int LPR = OC / 4, RPI = 64 / LPR;            // lanes per staged row, rows per read
+    static_assert(WM * WN * 16 * EPS * 4 <= (int)sizeof(sB), "epilogue staging");
+    float* ep = reinterpret_cast<float*>(&sB[0][0][0]) + w * 16 * EPS;
+    const int oc0 = n0 + OC * wn;
 #pragma unroll
-        for (int j = 0; j < NJ; j += 2) {
-            const int col = n0 + 8 * NJ * wn + 8 * j + fr;
-            if (col >= A.n) continue;
+    for (int i = 0; i < MI; ++i) {
 #pragma unroll
-            for (int i = 0; i < MI; ++i)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int row = m0 + 16 * MI * wm + 16 * i + 4 * (lane >> 4) + e;
-                    if (row >= A.m) continue;
-                    const float g = acc[i][j][e], u = acc[i][j + 1][e];
-                    A.y_bf16[(size_t)row * A.n + col] = f32_to_bf16(g / (1.0f + expf(-g)) * u);
-                }
-        }
-        return;
-    }
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-        const int col = n0 + 16 * NJ * wn + 16 * j + fr;
-        if (col >= A.n) continue;
-#pragma unroll
-        for (int i = 0; i < MI; ++i)
+        for (int j = 0; j < NJ; j += (GU ? 2 : 1))
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int row = m0 + 16 * MI * wm + 16 * i + 4 * (lane >> 4) + e;
-                if (row >= A.m) continue;
-                const size_t o = (size_t)row * A.n + col;
-                float v = acc[i][j][e];
-                if (A.residual) v += A.residual[o];
-                if (A.y_bf16) A.y_bf16[o] = f32_to_bf16(v);
-                else A.y[o] = v;
+                // gate/up: fragments j, j + 1 are the gate and up values of the same outputs
+                const float v = GU ? silu_fast(acc[i][j][e]) * acc[i][j + 1][e] : acc[i][j][e];
+                ep[(4 * (lane >> 4) + e) * EPS + (GU ? 8 : 16) * j + fr] = v;
             }
+#pragma unroll
+        for (int r0 = 0; r0 < 16; r0 += RPI) {
+            const int r = r0 + lane / LPR, c = 4 * (lane % LPR);
+            const float4 v = *reinterpret_cast<const float4*>(&ep[r * EPS + c]);
+            const int row = m0 + 16 * MI * wm + 16 * i + r, col = oc0 + c;
+            if (row >= A.m || col >= A.n) continue;         // n % 32 == 0: the 4 columns are all in or all out
+            const size_t o = (size_t)row * A.n + col;
+            float4 y = v;
+            if (!GU && A.residual) {
+                const float4 rv = *reinterpret_cast<const float4*>(A.residual + o);
+                y = make_float4(v.x + rv.x, v.y + rv.y, v.z + rv.z, v.w + rv.w);
+            }
+            if (GU || A.y_bf16)
+                *reinterpret_cast<uint2*>(A.y_bf16 + o) =
+                    make_uint2((uint32_t)f32_to_bf16(y.x) | ((uint32_t)f32_to_bf16(y.y) << 16),
+                               (uint32_t)f32_to_bf16(y.z) | ((uint32_t)f32_to_bf16(y.w) << 16));
+            else
+                *reinterpret_cast<float4*>(A.y + o) = y;
+        }
     }
 }
 
