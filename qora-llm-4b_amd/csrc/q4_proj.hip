@@ -407,6 +407,11 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
     const uint16_t* bsc = (up ? A.gscales2 : A.gscales) + (size_t)(ncl / 32) * K + RQ * rq;
     const bool wthread = NTH * RQ == 4 * TN || tid < TN * 4 / RQ;
 
+    // the f16 exponent pattern 0x6400 (1024) of each half, held in a VGPR so
+    // that masking a nibble pair into it is one v_and_or_b32 (the mask is
+    // the instruction's one literal)
+    uint32_t vmagic;
+    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(vmagic));
     uint4 ra0, ra1;
     uint32_t rb[4];
     uint2 rs;                                            // RQ f16 scales of rows RQ rq .. +RQ-1
@@ -424,26 +429,31 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
     } while (0)
     // Columns 2b, 2b + 1 of a row pair come from byte b of each row's block.
     // v_perm_b32 puts the first row's byte at bits 0-7 and the second's at
-    // bits 16-23; masking a nibble pair into 0x6400 | q gives the f16 pair
+    // bits 16-23 (of the words, and of the words shifted down by 4 for the
+    // high nibbles); masking a nibble pair into 0x6400 | q gives the f16 pair
     // (1024 + q), and packed f16 ops make it s * (q - 8): exact, then one
     // rounding of the product (the same bits as rounding s * (q - 8) from
-    // fp32).  Column n's four rows are one 8-byte store.
+    // fp32).  Column n's four (two) rows are one 8-byte (4-byte) store.
 #define GM_BPAIR(v) (XBF16 ? f16x2_to_bf16x2(v) : __builtin_bit_cast(uint32_t, v))
 #define GM_LSTORE(buf)                                                                 \
     do {                                                                               \
         *reinterpret_cast<uint4*>(&sA[buf][ar][XH * ah]) = ra0;                        \
         if (XH == 16) *reinterpret_cast<uint4*>(&sA[buf][ar][XH * ah + 8]) = ra1;      \
         const half2 s01 = __builtin_bit_cast(half2, rs.x), s23 = __builtin_bit_cast(half2, rs.y); \
+        uint32_t rh[RQ];                                  /* high nibbles moved down once */ \
+        _Pragma("unroll") for (int i_ = 0; i_ < RQ; ++i_) rh[i_] = rb[i_] >> 4;       \
         if (wthread) _Pragma("unroll") for (int b_ = 0; b_ < 4; ++b_) {                \
             const uint32_t sel = 0x0c040c00u + 0x00010001u * b_;                       \
             const half2 k1032 = half2{1032.0f16, 1032.0f16};                           \
             const uint32_t p01 = __builtin_amdgcn_perm(rb[1], rb[0], sel);             \
-            const half2 l01 = (__builtin_bit_cast(half2, (p01 & 0x000f000fu) | 0x64006400u) - k1032) * s01; \
-            const half2 h01 = (__builtin_bit_cast(half2, ((p01 >> 4) & 0x000f000fu) | 0x64006400u) - k1032) * s01; \
+            const uint32_t q01 = __builtin_amdgcn_perm(rh[1], rh[0], sel);             \
+            const half2 l01 = (__builtin_bit_cast(half2, (p01 & 0x000f000fu) | vmagic) - k1032) * s01; \
+            const half2 h01 = (__builtin_bit_cast(half2, (q01 & 0x000f000fu) | vmagic) - k1032) * s01; \
             if constexpr (RQ == 4) {                                                   \
                 const uint32_t p23 = __builtin_amdgcn_perm(rb[3], rb[2], sel);         \
-                const half2 l23 = (__builtin_bit_cast(half2, (p23 & 0x000f000fu) | 0x64006400u) - k1032) * s23; \
-                const half2 h23 = (__builtin_bit_cast(half2, ((p23 >> 4) & 0x000f000fu) | 0x64006400u) - k1032) * s23; \
+                const uint32_t q23 = __builtin_amdgcn_perm(rh[3], rh[2], sel);         \
+                const half2 l23 = (__builtin_bit_cast(half2, (p23 & 0x000f000fu) | vmagic) - k1032) * s23; \
+                const half2 h23 = (__builtin_bit_cast(half2, (q23 & 0x000f000fu) | vmagic) - k1032) * s23; \
                 *reinterpret_cast<uint2*>(&sB[buf][8 * c8 + 2 * b_][4 * rq]) = make_uint2(GM_BPAIR(l01), GM_BPAIR(l23)); \
                 *reinterpret_cast<uint2*>(&sB[buf][8 * c8 + 2 * b_ + 1][4 * rq]) = make_uint2(GM_BPAIR(h01), GM_BPAIR(h23)); \
             } else {                                                                   \
