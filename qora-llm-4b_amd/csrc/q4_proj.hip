@@ -364,7 +364,7 @@ __device__ __forceinline__ uint32_t f16x2_to_bf16x2(half2 h) {
 // 16 MI WM x 16 NJ WN.  128 x 256 (2 x 2 waves of 64 x 128) where there are
 // tiles enough for two workgroups per CU; for narrow outputs that would
 // leave CUs idle, 128 x 128 (n = 2560: 10 column tiles of 256) or 64 x 128
-// (n = 1024), and 16 x 32 (one wave) for n = 32.  The W tile is staged by
+// (n = 1024); n = 32 has a kernel of its own below.  The W tile is staged by
 // threads 0 .. TN-1.  (64 x 256 tiles, four waves of 64 x 64 side by side,
 // measured 2% slower on the 4096-token prefill.)
 template <bool XBF16, bool GU, int WM, int WN, int MI, int NJ>
@@ -574,8 +574,82 @@ extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm_n128(Q4GemmArgs 
 extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm_xbf16_n128(Q4GemmArgs A) { q4_gemm_body<true, false, 2, 2, 4, 4>(A); }
 extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm_m64(Q4GemmArgs A) { q4_gemm_body<false, false, 2, 2, 2, 4>(A); }
 extern "C" __global__ __launch_bounds__(256, 2) void qm_q4_gemm_xbf16_m64(Q4GemmArgs A) { q4_gemm_body<true, false, 2, 2, 2, 4>(A); }
-extern "C" __global__ __launch_bounds__(64) void qm_q4_gemm_n32(Q4GemmArgs A) { q4_gemm_body<false, false, 1, 1, 1, 2>(A); }
-extern "C" __global__ __launch_bounds__(64) void qm_q4_gemm_xbf16_n32(Q4GemmArgs A) { q4_gemm_body<true, false, 1, 1, 1, 2>(A); }
+
+// n = 32 (the DeltaNet a/b projections, 8-column device tiles): 4096 x 2560
+// x 32 is too thin for LDS tiles, where each workgroup walks all k steps
+// behind one chain of loads.  Here a workgroup of four waves owns 16 rows
+// and deals the k steps to its waves round-robin.  Each wave builds its
+// MFMA operands straight from global memory: the x row piece (lane: row
+// lane & 15, k 8 (lane >> 4) .. +7) is the A operand as loaded; for the B
+// operand of column c the lane loads rows k .. k+7 of c's tile (32
+// contiguous bytes), takes nibble c & 7 of each and forms the f16 pairs
+// s * (q - 8) with the same magic-number arithmetic as the staged form (for
+// bf16 x, rounded on to bf16).  No LDS until the end, where the four
+// partial sums meet and are added in a fixed order.
+template <bool XBF16>
+__device__ __forceinline__ void q4_gemm_n32_body(const Q4GemmArgs& A) {
+    __shared__ floatx4 part[4][2][64];                   // [wave][column tile][lane]
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int m0 = (int)blockIdx.x * 16, K = A.k, nk = K / GM_TK;
+    const int fr = lane & 15, kg = lane >> 4;
+    const uint16_t* xr = A.x + (size_t)min(m0 + fr, A.m - 1) * K + 8 * kg;
+    const int sh = 4 * (fr & 7);                         // nibble of column 16 j + fr in its row word
+    const uint8_t* cb[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) cb[j] = A.codes + (size_t)(2 * j + (fr >> 3)) * K * 4 + 32 * kg;
+    const uint16_t* sb = A.gscales + 8 * kg;             // one 32-column group: scales [k]
+    uint32_t vmagic;
+    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(vmagic));
+    floatx4 acc[2] = {floatx4{0.0f, 0.0f, 0.0f, 0.0f}, floatx4{0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll 4
+    for (int kt = w; kt < nk; kt += 4) {
+        const int k0 = kt * GM_TK;
+        const half8 a = __builtin_bit_cast(half8, *reinterpret_cast<const uint4*>(xr + k0));
+        const uint4 sc = *reinterpret_cast<const uint4*>(sb + k0);
+        const uint32_t s4[4] = {sc.x, sc.y, sc.z, sc.w};
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint4 c0 = *reinterpret_cast<const uint4*>(cb[j] + (size_t)k0 * 4);
+            const uint4 c1 = *reinterpret_cast<const uint4*>(cb[j] + (size_t)k0 * 4 + 16);
+            const uint32_t wd[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+            uint32_t bw[4];
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const uint32_t q0 = (wd[2 * p] >> sh) & 0xfu, q1 = (wd[2 * p + 1] >> sh) & 0xfu;
+                const half2 v = (__builtin_bit_cast(half2, (q0 | (q1 << 16)) | vmagic) - half2{1032.0f16, 1032.0f16}) *
+                                __builtin_bit_cast(half2, s4[p]);
+                bw[p] = XBF16 ? f16x2_to_bf16x2(v) : __builtin_bit_cast(uint32_t, v);
+            }
+            const half8 bv = __builtin_bit_cast(half8, make_uint4(bw[0], bw[1], bw[2], bw[3]));
+            if constexpr (XBF16)
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, bv),
+                                                                 acc[j], 0, 0, 0);
+            else
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bv, acc[j], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) part[w][j][lane] = acc[j];
+    __syncthreads();
+    if (w != 0) return;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const floatx4 y = ((part[0][j][lane] + part[1][j][lane]) + part[2][j][lane]) + part[3][j][lane];
+        const int col = 16 * j + fr;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int row = m0 + 4 * kg + e;
+            if (row >= A.m) continue;
+            const size_t o = (size_t)row * A.n + col;
+            float v = y[e];
+            if (A.residual) v += A.residual[o];
+            if (A.y_bf16) A.y_bf16[o] = f32_to_bf16(v);
+            else A.y[o] = v;
+        }
+    }
+}
+extern "C" __global__ __launch_bounds__(256) void qm_q4_gemm_n32(Q4GemmArgs A) { q4_gemm_n32_body<false>(A); }
+extern "C" __global__ __launch_bounds__(256) void qm_q4_gemm_xbf16_n32(Q4GemmArgs A) { q4_gemm_n32_body<true>(A); }
 
 // rms_norm (1 + gamma, eps 1e-6; gemv.rs:571-579) of each of m rows of f32
 // x [m][k], written as the f16 input of qm_q4_gemm; without a norm weight,

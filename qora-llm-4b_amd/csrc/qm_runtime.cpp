@@ -53,7 +53,7 @@ struct qm_context {
     hipFunction_t f_q4_gemm[2][2] = {};  // [x bf16][gate/up form]
     hipFunction_t f_q4_gemm_n128[2] = {}; // [x bf16]: 128 x 128 tiles for narrow outputs
     hipFunction_t f_q4_gemm_m64[2] = {};  // [x bf16]: 64 x 128 tiles
-    hipFunction_t f_q4_gemm_n32[2] = {};  // [x bf16]: 16 x 32 tiles, one wave, for n = 32
+    hipFunction_t f_q4_gemm_n32[2] = {};  // [x bf16]: n = 32, 16 rows per 4-wave workgroup, k split over the waves
     hipFunction_t f_rms_f16 = nullptr;
     hipFunction_t f_lm_head = nullptr;
     hipFunction_t f_embed = nullptr;
@@ -1036,9 +1036,9 @@ int32_t qm_q4_gemm(qm_context* c, qm_stream stream, int32_t m, int32_t k, int32_
     auto tiles = [&](int64_t tm, int64_t tn) { return (m + tm - 1) / tm * ((n + tn - 1) / tn); };
     const int64_t two_per_cu = 2 * static_cast<int64_t>(c->num_cu);
     // the widest tile that still gives two workgroups per CU; n = 32 (the
-    // DeltaNet a/b projections) one wave per 16 rows
+    // DeltaNet a/b projections) a k-split kernel of 16 rows per workgroup
     if (n <= 32)
-        return launch(c, c->f_q4_gemm_n32[xb], static_cast<uint32_t>(tiles(16, 32)), 64, ga, pick(c, stream),
+        return launch(c, c->f_q4_gemm_n32[xb], static_cast<uint32_t>((m + 15) / 16), 256, ga, pick(c, stream),
                       "qm_q4_gemm");
     if (tiles(128, 256) >= two_per_cu)
         return launch(c, c->f_q4_gemm[xb][0], static_cast<uint32_t>(tiles(128, 256)), 256, ga, pick(c, stream),
