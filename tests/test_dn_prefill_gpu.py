@@ -116,6 +116,44 @@ def test_prefill_long_warm(ctx, T):
     assert np.array_equal(cb, rcb)
 
 
+@pytest.mark.parametrize("scale", [1e3, 1e4])
+def test_prefill_channel_outliers(ctx, scale):
+    """A few input channels scaled far past the rest (massive-activation
+    outliers): 4 v channels and 4 q/k channels times `scale` over 1024
+    tokens.  q and k are L2-normalised per head, so their outliers only
+    sharpen the direction; v's reach the f16 chunk operands and the state
+    (|S| to ~6e3 at 1e4).  Within the bar against the oracle's fp32."""
+    T = 1024
+    w = W.dn_prefill_workload(T, seed=11)
+    x = W.bf16_value(w["qkv"]).copy()
+    x[:, [4096 + 5, 4096 + 900, 4096 + 2100, 4096 + 4000]] *= np.float32(scale)
+    x[:, [7, 300, 2048 + 11, 2048 + 1500]] *= np.float32(scale)
+    w["qkv"] = W.bf16_bits(x)
+    print(f"case: dn prefill T={T} channel outliers x{scale:g}", flush=True)
+    o, S, cb = run_prefill(ctx, w, T)
+    ro, rS, rcb = run_oracle(w, T)
+    assert np.isfinite(o).all() and np.isfinite(S).all()
+    eo, es = rel(o, ro), rel(S, rS)
+    print(f"rel out {eo:.3e} rel state {es:.3e} max|S| {np.abs(rS).max():.3e}")
+    assert eo <= RTOL and es <= RTOL
+    assert np.array_equal(cb, rcb)
+
+
+def test_prefill_slow_decay(ctx):
+    """Decays near 1 (A_log = log 1e-4: alpha ~ 0.9999 per token) over 1024
+    tokens, so the chunk-local cumulative decays stay ~1 and the state keeps
+    every token's contribution."""
+    T = 1024
+    w = W.dn_prefill_workload(T, seed=13)
+    w["a_log"] = np.full(32, np.log(1e-4), np.float32)
+    print(f"case: dn prefill T={T} slow decay", flush=True)
+    o, S, cb = run_prefill(ctx, w, T)
+    ro, rS, rcb = run_oracle(w, T)
+    eo, es = rel(o, ro), rel(S, rS)
+    print(f"rel out {eo:.3e} rel state {es:.3e}")
+    assert eo <= RTOL and es <= RTOL
+
+
 def test_prefill_graph_replay_matches_eager(ctx):
     """The prefill captured in a graph replays to the eager result, bit for
     bit, three times (state and conv buffer reset between replays)."""

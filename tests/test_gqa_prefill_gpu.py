@@ -98,6 +98,27 @@ def test_prefill_score_jumps(ctx):
     check(o, K, V, ref, kc, vc, np.arange(S))
 
 
+@pytest.mark.parametrize("scale", [1e3, 3e4])
+def test_prefill_value_outliers(ctx, scale):
+    """v channels times `scale` / 4 (|v| up to ~3e4 at 3e4, inside f16's
+    range, which the configured f16 KV cache sets for the whole GQA path)
+    and q/k channels likewise (RMS-normalised per head, so they only sharpen
+    the scores)."""
+    S = 300
+    w = W.gqa_prefill_workload(S, seed=17)
+    v = W.bf16_value(w["v"]).reshape(S, 4, 256).copy()
+    v[:, :, [3, 100, 255]] *= np.float32(scale / 4)      # |v| up to ~3e4, below f16's 65504
+    k = W.bf16_value(w["k"]).reshape(S, 4, 256).copy()
+    k[:, :, [9, 200]] *= np.float32(scale)
+    w["v"] = W.bf16_bits(v.reshape(w["v"].shape))
+    w["k"] = W.bf16_bits(k.reshape(w["k"].shape))
+    print(f"case: gqa prefill S={S} value outliers x{scale:g}", flush=True)
+    o, K, V = run_gpu(ctx, w, S, S)
+    ref, kc, vc = run_oracle(w, S)
+    assert np.isfinite(o).all()
+    check(o, K, V, ref, kc, vc, np.arange(S))
+
+
 def test_prefill_graph_replay_matches_eager(ctx):
     """A captured prefill (K/V kernel, which resets the row-block queues, then
     the persistent attention) replayed several times, with eager prefills and
