@@ -5,8 +5,10 @@
 // cache replaced by the normed/roped K and V (f16), causal softmax attention
 // with kv head h/4, sigmoid output gate.
 //
-// qm_gqa_prefill_kv    K norm + RoPE -> f16 K cache; V -> f16 V cache and a
-//                      transposed f16 copy V^T (keys contiguous per dim).
+// qm_gqa_prefill_kv    K norm + RoPE -> f16 K cache; V -> f16 V cache; and
+//                      both again as 64-key tiles in the attention's MFMA
+//                      fragment order (K, and V transposed), so each tile
+//                      is one contiguous 64 KB block.
 // qm_gqa_prefill_attn  flash attention on MFMA.  A workgroup owns 48 query
 //                      tokens of all four query heads of one kv group (12
 //                      waves: head 4g + (w & 3), 16 rows each, three waves
@@ -21,8 +23,8 @@
 //                      permuted so that set is 8 consecutive keys).  No lane
 //                      shuffles between the two products.  Online softmax in
 //                      base 2, fp32, with a lazily moved reference max.  K / V
-//                      tiles are double-buffered in LDS and copied there by
-//                      LDS DMA one tile ahead of use.
+//                      tiles are double-buffered in LDS and copied there, 1 KB
+//                      per instruction, by LDS DMA one tile ahead of use.
 #include "qm_device.h"
 #include "qm_kernel_args.h"
 #include "qm_gqa_common.h"
@@ -49,10 +51,22 @@ QM_DEV uint2 f32x4_to_f16(float4 x) {
     return o;
 }
 
+// Key held by row i of S^T fragment kk: the four fragments of a 64-key tile
+// are arranged so that, for PV k-step ks = kk >> 1, a lane's pair of
+// fragments 2ks, 2ks+1 holds the 8 consecutive keys 32 ks + 8 lq .. + 7.
+QM_DEV int frag_key(int kk, int i) { return 32 * (kk >> 1) + 8 * (i >> 2) + 4 * (kk & 1) + (i & 3); }
+
 // ---------------------------------------------------------------------------
-// K / V cache write (gemv.rs:1387-1400).  Workgroup = 64 tokens of kv head g.
+// K / V cache write (gemv.rs:1387-1400).  Workgroup = 64 tokens (one tile) of
+// kv head g.  The tile copy kvf + (g * ntile + tile) * 64 KB is 64 blocks of
+// 1 KB, block entry l = the 16 bytes MFMA lane l = (lr, lq) = (l & 15, l >> 4)
+// reads:
+//   block b < 32, b = 8 kk + s:       K row frag_key(kk, lr), dims 32 s + 8 lq .. + 7
+//   block b >= 32, b - 32 = 2 dt + ks: V dim 16 dt + lr, keys 32 ks + 8 lq .. + 7
+// Keys past S are zero.
 // ---------------------------------------------------------------------------
 extern "C" __global__ __launch_bounds__(256) void qm_gqa_prefill_kv(GqaPrefillArgs A) {
+    __shared__ _Float16 ks[64][264];
     __shared__ _Float16 vs[64][264];
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int g = blockIdx.x % QM_GQA_KV_HEADS;
@@ -103,8 +117,12 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_prefill_kv(GqaPrefillAr
                 y.x = x.x * cr[jj].x + ps.x * sr[jj].x; y.y = x.y * cr[jj].y + ps.y * sr[jj].y;
                 y.z = x.z * cr[jj].z + ps.z * sr[jj].z; y.w = x.w * cr[jj].w + ps.w * sr[jj].w;
                 if (lane < 16) x = y;
-                if (t < A.S)                                      // wave-uniform
-                    *reinterpret_cast<uint2*>(A.k_cache + ((size_t)g * A.cap + t) * QM_GQA_HD + 4 * lane) = f32x4_to_f16(x);
+                uint2 h = make_uint2(0, 0);
+                if (t < A.S) {                                    // wave-uniform
+                    h = f32x4_to_f16(x);
+                    *reinterpret_cast<uint2*>(A.k_cache + ((size_t)g * A.cap + t) * QM_GQA_HD + 4 * lane) = h;
+                }
+                *reinterpret_cast<uint2*>(&ks[16 * w + jb + jj][4 * lane]) = h;
             }
         }
     }
@@ -126,15 +144,25 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_prefill_kv(GqaPrefillAr
         }
     }
     __syncthreads();
+    // the tile copy: entry p = tid + 256 i of 4096, consecutive threads on
+    // consecutive 16-byte entries
     {
-        const int d = tid;
-        uint16_t* dst = A.vt + ((size_t)g * QM_GQA_HD + d) * A.s_pad + t0;
+        uint16_t* dst = A.kvf + ((size_t)g * (A.s_pad / 64) + (t0 >> 6)) * (64 * 512);
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
+        for (int i = 0; i < 8; ++i) {
+            const int p = tid + 256 * i, b = p >> 6, l = p & 63, lr = l & 15, lq = l >> 4;
+            const int kk = b >> 3, s8 = b & 7;
+            *reinterpret_cast<half8*>(dst + 8 * p) =
+                *reinterpret_cast<const half8*>(&ks[frag_key(kk, lr)][32 * s8 + 8 * lq]);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int p = tid + 256 * i, b = p >> 6, l = p & 63, lr = l & 15, lq = l >> 4;
+            const int d = 16 * (b >> 1) + lr, k8 = 32 * (b & 1) + 8 * lq;
             half8 hv;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) hv[e] = vs[8 * q + e][d];
-            *reinterpret_cast<half8*>(dst + 8 * q) = hv;
+            for (int e = 0; e < 8; ++e) hv[e] = vs[k8 + e][d];
+            *reinterpret_cast<half8*>(dst + 32 * 512 + 8 * p) = hv;
         }
     }
 }
@@ -142,20 +170,14 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_prefill_kv(GqaPrefillAr
 // ---------------------------------------------------------------------------
 // Flash attention.  Lane (lr, lq) = (lane & 15, lane >> 4).
 // ---------------------------------------------------------------------------
-// LDS (bytes): K buffers 0, 1 then V^T buffers 0, 1 of 32 KB each.  A K
-// buffer holds a 64-key tile in MFMA fragment order as 32 blocks (kk, s) of
-// 1 KB, a V^T buffer as 32 blocks (dt, ks); block entry l is the 16 bytes
-// lane l reads for that product, so every fragment read is lane * 16 + an
-// immediate (no bank conflicts, no per-read address registers).  The gather
-// into that order is done by the per-lane source addresses of the LDS DMA.
-#define SM_K(b) ((b) * 32768)
-#define SM_V(b) (65536 + (b) * 32768)
+// LDS (bytes): tile buffers 0, 1 of 64 KB, each the 64 KB tile copy written
+// by qm_gqa_prefill_kv: K blocks (kk, s) then V^T blocks (dt, ks), block
+// entry l the 16 bytes lane l reads for that product, so every fragment read
+// is lane * 16 + an immediate (no bank conflicts, no per-read address
+// registers).
+#define SM_K(b) ((b) * 65536)
+#define SM_V(b) ((b) * 65536 + 32768)
 #define SM_BYTES 131072
-
-// Key held by row i of S^T fragment kk: the four fragments of a 64-key tile
-// are arranged so that, for PV k-step ks = kk >> 1, a lane's pair of
-// fragments 2ks, 2ks+1 holds the 8 consecutive keys 32 ks + 8 lq .. + 7.
-QM_DEV int frag_key(int kk, int i) { return 32 * (kk >> 1) + 8 * (i >> 2) + 4 * (kk & 1) + (i & 3); }
 
 // 16 bytes per lane from global memory straight into LDS: lane l writes
 // lds + 16 l.  Issued as inline asm so that no compiler-inserted wait ties
@@ -209,8 +231,7 @@ extern "C" __global__ __launch_bounds__(768) void qm_gqa_prefill_attn(GqaPrefill
     int item = item_s;
     while (item >= 0) {                     // workgroup-uniform
         const int g = item / nblk;
-        const uint16_t* kbase = A.k_cache + (size_t)g * A.cap * QM_GQA_HD;
-        const uint16_t* vbase = A.vt + (size_t)g * QM_GQA_HD * A.s_pad;
+        const uint16_t* tiles = A.kvf + (size_t)g * (A.s_pad / 64) * (64 * 512);
         // the next block is claimed three tiles before this one ends: late
         // enough to keep the longest-first order, early enough to hide the
         // atomic's latency
@@ -227,24 +248,18 @@ extern "C" __global__ __launch_bounds__(768) void qm_gqa_prefill_attn(GqaPrefill
         // tiles up to the block's last row, within the zero-padded V^T copy
         const int nkt = min((t0 + TQ3 + KT - 1) / KT, A.s_pad / KT);
 
-        // tile fetch: block b = w + 12 j of the tile's 64 (K blocks 0..31, V^T 32..63)
-        auto fetch = [&](int kt, int buf) {
-            const int k0 = kt * KT;
+        // tile fetch, K half (blocks 0..31) or V^T half (32..63): block
+        // h + w + 12 j, one contiguous 1 KB piece each
+        auto fetch = [&](int kt, int buf, int h) {
+            const uint16_t* src = tiles + (size_t)kt * (64 * 512) + 8 * lane;
 #pragma unroll
-            for (int j = 0; j < 6; ++j) {
-                const int b = w + 12 * j;
-                if (b < 32) {
-                    const int kk = b >> 3, s = b & 7;                  // K block: S^T fragment kk, k-step s
-                    const int key = min(k0 + frag_key(kk, lr), A.S - 1);  // rows past S feed masked scores only
-                    dma16(kbase + (size_t)key * QM_GQA_HD + 32 * s + 8 * lq, sm_lds + SM_K(buf) + 1024 * b);
-                } else if (b < 64) {
-                    const int dt = (b - 32) >> 1, ks = b & 1;          // V^T block: dims tile dt, keys step ks
-                    dma16(vbase + (size_t)(16 * dt + lr) * A.s_pad + k0 + 32 * ks + 8 * lq,
-                          sm_lds + SM_V(buf) + 1024 * (b - 32));
-                }
+            for (int j = 0; j < 3; ++j) {
+                const int b = h + w + 12 * j;
+                if (b < h + 32) dma16(src + 512 * b, sm_lds + SM_K(buf) + 1024 * b);
             }
         };
-        fetch(0, 0);                             // in flight during the q prep
+        fetch(0, 0, 0);                          // in flight during the q prep
+        fetch(0, 0, 32);
 
         // 1. q: RMSNorm (1+gamma, eps 1e-6; gemv.rs:586-597) and split-half RoPE
         //    (gemv.rs:604-627) straight into the B fragments: lane (lr, lq) holds
@@ -341,8 +356,9 @@ extern "C" __global__ __launch_bounds__(768) void qm_gqa_prefill_attn(GqaPrefill
             // behind the remaining tiles, and it is resolved at the end
             if (tid == 0 && kt == kt_claim) nxt = atomicAdd(A.queue + home, 1);
             const int k0 = kt * KT, b = kt & 1;
-            // the other buffer was last read before the previous barrier
-            if (kt + 1 < nkt) fetch(kt + 1, b ^ 1);
+            // the other buffer was last read before the previous barrier; the
+            // V^T half is requested after the scores
+            if (kt + 1 < nkt) fetch(kt + 1, b ^ 1, 0);
             const char* Kb = sm + SM_K(b);
             const char* Vb = sm + SM_V(b);
 
@@ -368,6 +384,7 @@ extern "C" __global__ __launch_bounds__(768) void qm_gqa_prefill_attn(GqaPrefill
                         sT[kk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[cur][j], qf[s0 + j], sT[kk], 0, 0, 0);
                 }
             }
+            if (kt + 1 < nkt) fetch(kt + 1, b ^ 1, 32);
             // online softmax (base 2); only tiles that reach past the wave's
             // first row need the causal mask
             float mx = -INFINITY;

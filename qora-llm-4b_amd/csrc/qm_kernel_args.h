@@ -98,9 +98,10 @@ struct DnPrefillArgs {
     int32_t nc;
 };
 
-// GQA causal prefill.  vt is a workspace copy of V transposed per kv head,
-// f16 [4][256][s_pad] (s_pad = S rounded up to 64, zero padded), so the PV
-// product can read consecutive keys per lane.
+// GQA causal prefill.  kvf is a workspace copy of the f16 K and V, per kv
+// head and 64-key tile (s_pad = S rounded up to 64, zero padded), in the
+// attention's MFMA fragment order: f16 [4][s_pad / 64][64 blocks][64 lanes][8],
+// blocks 0..31 K, 32..63 V transposed.
 struct GqaPrefillArgs {
     const uint16_t* q_gate;  // bf16 [S][16][512]
     const uint16_t* k;       // bf16 [S][4][256]
@@ -111,7 +112,7 @@ struct GqaPrefillArgs {
     const float* rope_sin;
     uint16_t* k_cache;       // f16 [4][cap][256]
     uint16_t* v_cache;
-    uint16_t* vt;            // f16 [4][256][s_pad]
+    uint16_t* kvf;           // f16 [4][s_pad / 64][64][64][8]
     uint16_t* out;           // bf16 [S][16][256]
     int32_t* queue;          // [4] next row block per kv head (zeroed by the kv kernel)
     int64_t cap;

@@ -195,9 +195,10 @@ struct DnPrefillLayout {
     size_t Wn, Qt, Ut, Y0t, Ktt, gC, Sc, total;
 };
 
-// GQA prefill workspace: the transposed V copy, then the row-block queue.
-size_t gqa_prefill_vt_bytes(size_t s_pad) {
-    return (static_cast<size_t>(QM_GQA_KV_HEADS) * QM_GQA_HD * s_pad * 2 + 255) & ~static_cast<size_t>(255);
+// GQA prefill workspace: the fragment-ordered K and V tile copy, then the
+// row-block queue.
+size_t gqa_prefill_kvf_bytes(size_t s_pad) {
+    return (static_cast<size_t>(QM_GQA_KV_HEADS) * QM_GQA_HD * s_pad * 2 * 2 + 255) & ~static_cast<size_t>(255);
 }
 
 DnPrefillLayout dn_prefill_layout(int64_t T) {
@@ -716,7 +717,7 @@ int32_t qm_reserve(qm_context* c, int32_t max_batch, int32_t max_kv_len, int32_t
     if (max_prefill_tokens > 0) {
         ws = std::max(ws, dn_prefill_layout(max_prefill_tokens).total);
         const size_t s_pad = (static_cast<size_t>(max_prefill_tokens) + 63) / 64 * 64;
-        ws = std::max(ws, gqa_prefill_vt_bytes(s_pad) + 256);
+        ws = std::max(ws, gqa_prefill_kvf_bytes(s_pad) + 256);
     }
     ws = std::max(ws, kSampleWsBytes);
     return ensure(c, c->stream, ws);
@@ -771,12 +772,12 @@ int32_t qm_gqa_prefill(qm_context* c, qm_stream stream, int32_t seq_len, const u
                     static_cast<long long>(cap));
     hipStream_t s = pick(c, stream);
     const int32_t s_pad = (seq_len + 63) / 64 * 64;
-    const size_t vt_bytes = gqa_prefill_vt_bytes(s_pad);
-    int32_t st = ensure(c, s, vt_bytes + 256);
+    const size_t kvf_bytes = gqa_prefill_kvf_bytes(s_pad);
+    int32_t st = ensure(c, s, kvf_bytes + 256);
     if (st != QM_OK) return st;
     GqaPrefillArgs ga{q_gate, k, v, q_norm, k_norm, rope_cos, rope_sin, k_cache, v_cache,
                       static_cast<uint16_t*>(c->ws), out,
-                      reinterpret_cast<int32_t*>(static_cast<char*>(c->ws) + vt_bytes), cap, seq_len, s_pad};
+                      reinterpret_cast<int32_t*>(static_cast<char*>(c->ws) + kvf_bytes), cap, seq_len, s_pad};
     st = launch(c, c->f_gqp_kv, static_cast<uint32_t>(s_pad / 64) * QM_GQA_KV_HEADS, 256, ga, s,
                 "qm_gqa_prefill_kv");
     if (st != QM_OK) return st;
