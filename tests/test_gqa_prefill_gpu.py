@@ -65,12 +65,18 @@ def test_prefill_small(ctx, S):
 
 
 def test_prefill_8192_rows(ctx):
+    """Rows checked: the first 40 and last 24, 40 evenly spaced, 256 drawn
+    at random over the whole triangle, and the rows on both sides of the
+    48-row block and 64-key tile edges around the middle (the K and V caches
+    are checked in full)."""
     S = 8192
     w = W.gqa_prefill_workload(S, seed=3)
     print("case: gqa prefill S=8192", flush=True)
     o, K, V = run_gpu(ctx, w, S, S)
+    mid = [e + d for e in (4080, 4128, 4096, 4160) for d in (-1, 0, 1)]
     rows = np.unique(np.concatenate([np.arange(0, 40), np.arange(S - 24, S),
-                                     np.linspace(0, S - 1, 40).astype(np.int64)]))
+                                     np.linspace(0, S - 1, 40).astype(np.int64),
+                                     np.random.default_rng(5).integers(0, S, 256), mid]))
     ref, kc, vc = run_oracle(w, S, rows=rows)
     check(o, K, V, ref, kc, vc, rows)
 
