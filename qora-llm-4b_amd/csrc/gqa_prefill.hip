@@ -206,6 +206,25 @@ QM_DEV void dma16(const void* gsrc, uint32_t lds) {
 // blocks of the other groups, which evens out the XCDs' speeds.
 #define TQ3 48
 
+// Fragment reads in flight per wave in the two products: with 32 reads of
+// 1 KB per product and three waves per SIMD, keeping 6 in flight (24 VGPRs)
+// hides the LDS latency; the compiler's own order kept one or two.
+#define LOOKAHEAD 6
+
+// Orders the preceding product's 32 LDS fragment reads and its 32 + EXTRA
+// MFMAs as: LOOKAHEAD reads, then (MFMA, read) pairs, then the remaining
+// MFMAs.  Only an ordering hint: the waits stay the compiler's.
+template <int EXTRA>
+QM_DEV void sched_reads_ahead() {
+    __builtin_amdgcn_sched_group_barrier(0x100, LOOKAHEAD, 0);      // DS reads
+#pragma unroll
+    for (int i = 0; i < 32 - LOOKAHEAD; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);          // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, LOOKAHEAD + EXTRA, 0);
+}
+
 extern "C" __global__ __launch_bounds__(768) void qm_gqa_prefill_attn(GqaPrefillArgs A) {
     __shared__ __attribute__((aligned(1024))) char sm[SM_BYTES];
     __shared__ int item_s;
@@ -362,27 +381,22 @@ extern "C" __global__ __launch_bounds__(768) void qm_gqa_prefill_attn(GqaPrefill
             const char* Kb = sm + SM_K(b);
             const char* Vb = sm + SM_V(b);
 
-            // S^T = K Q^T: fragment kk row i is key frag_key(kk, i) of the tile;
-            // K blocks read two at a time, one pair ahead of their MFMAs
+            // S^T = K Q^T: fragment kk row i is key frag_key(kk, i) of the tile.
+            // k-step major, so consecutive MFMAs feed four independent
+            // accumulators; the 32 K block reads are kept LOOKAHEAD ahead of
+            // their MFMAs (the compiler's own order kept one or two).
             floatx4 sT[4];
             {
-                half8 ka[2][2];
 #pragma unroll
-                for (int j = 0; j < 2; ++j) ka[0][j] = *reinterpret_cast<const half8*>(Kb + j * 1024 + 16 * lane);
+                for (int kk = 0; kk < 4; ++kk) sT[kk] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int grp = 0; grp < 16; ++grp) {         // pair = blocks 2grp, 2grp+1 = (kk, s)
-                    const int cur = grp & 1;
-                    if (grp + 1 < 16) {
+                for (int st = 0; st < 8; ++st)
 #pragma unroll
-                        for (int j = 0; j < 2; ++j)
-                            ka[cur ^ 1][j] = *reinterpret_cast<const half8*>(Kb + (2 * (grp + 1) + j) * 1024 + 16 * lane);
+                    for (int kk = 0; kk < 4; ++kk) {
+                        const half8 ka = *reinterpret_cast<const half8*>(Kb + (8 * kk + st) * 1024 + 16 * lane);
+                        sT[kk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qf[st], sT[kk], 0, 0, 0);
                     }
-                    const int kk = grp >> 2, s0 = 2 * (grp & 3);
-                    if ((grp & 3) == 0) sT[kk] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                    for (int j = 0; j < 2; ++j)
-                        sT[kk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[cur][j], qf[s0 + j], sT[kk], 0, 0, 0);
-                }
+                sched_reads_ahead<0>();
             }
             if (kt + 1 < nkt) fetch(kt + 1, b ^ 1, 32);
             // online softmax (base 2); only tiles that reach past the wave's
@@ -427,25 +441,18 @@ extern "C" __global__ __launch_bounds__(768) void qm_gqa_prefill_attn(GqaPrefill
                 }
             }
             // O += P V   (16x16x32; B lane (dim, lq) holds keys 32 ks + 8 lq .. + 7),
-            // V^T blocks read two at a time, one pair ahead of the MFMAs
+            // the V^T block reads LOOKAHEAD ahead of their MFMAs
             {
-                half8 vb[2][2];
 #pragma unroll
-                for (int j = 0; j < 2; ++j) vb[0][j] = *reinterpret_cast<const half8*>(Vb + j * 1024 + 16 * lane);
+                for (int dt = 0; dt < 16; ++dt)
 #pragma unroll
-                for (int dt = 0; dt < 16; ++dt) {            // pair = blocks (dt, 0), (dt, 1)
-                    const int cur = dt & 1;
-                    if (dt + 1 < 16) {
-#pragma unroll
-                        for (int j = 0; j < 2; ++j)
-                            vb[cur ^ 1][j] = *reinterpret_cast<const half8*>(Vb + (2 * (dt + 1) + j) * 1024 + 16 * lane);
+                    for (int ks = 0; ks < 2; ++ks) {
+                        const half8 vb = *reinterpret_cast<const half8*>(Vb + (2 * dt + ks) * 1024 + 16 * lane);
+                        O[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[ks], vb, O[dt], 0, 0, 0);
                     }
 #pragma unroll
-                    for (int ks = 0; ks < 2; ++ks)
-                        O[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[ks], vb[cur][ks], O[dt], 0, 0, 0);
-                }
-#pragma unroll
                 for (int ks = 0; ks < 2; ++ks) O[16] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[ks], ones, O[16], 0, 0, 0);
+                sched_reads_ahead<2>();
             }
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // next tile landed (this wave's part)
             __syncthreads();                    // ... for every wave; this tile fully consumed
