@@ -126,21 +126,27 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_prefill_kv(GqaPrefillAr
             }
         }
     }
-    // V: rows to the cache, and through LDS to V^T
+    // V: rows to the cache, and into LDS for the V^T tile copy.  The four
+    // threads of a token cover 32 consecutive dims per step (64-byte
+    // pieces), and all eight raw loads (at a clamped, valid row) are issued
+    // before any conversion.
     {
         const int i = tid >> 2, p = tid & 3, t = t0 + i;
+        const uint16_t* vrow = A.v + ((size_t)min(t, A.S - 1) * QM_GQA_KV_HEADS + g) * QM_GQA_HD + 8 * p;
+        uint4 raw[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) raw[q] = *reinterpret_cast<const uint4*>(vrow + 32 * q);
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
             uint4 h16 = make_uint4(0, 0, 0, 0);
             if (t < A.S) {
-                const uint4 raw = *reinterpret_cast<const uint4*>(A.v + ((size_t)t * QM_GQA_KV_HEADS + g) * QM_GQA_HD + 64 * p + 8 * q);
-                const float4 lo = bf16x4_to_f32(make_uint2(raw.x, raw.y));
-                const float4 hi = bf16x4_to_f32(make_uint2(raw.z, raw.w));
+                const float4 lo = bf16x4_to_f32(make_uint2(raw[q].x, raw[q].y));
+                const float4 hi = bf16x4_to_f32(make_uint2(raw[q].z, raw[q].w));
                 const uint2 a = f32x4_to_f16(lo), b = f32x4_to_f16(hi);
                 h16 = make_uint4(a.x, a.y, b.x, b.y);
-                *reinterpret_cast<uint4*>(A.v_cache + ((size_t)g * A.cap + t) * QM_GQA_HD + 64 * p + 8 * q) = h16;
+                *reinterpret_cast<uint4*>(A.v_cache + ((size_t)g * A.cap + t) * QM_GQA_HD + 32 * q + 8 * p) = h16;
             }
-            *reinterpret_cast<uint4*>(&vs[i][64 * p + 8 * q]) = h16;
+            *reinterpret_cast<uint4*>(&vs[i][32 * q + 8 * p]) = h16;
         }
     }
     __syncthreads();
