@@ -203,12 +203,13 @@ QM_DEV uint2 pack_f16x4(float a, float b, float c, float d) {
     return o;
 }
 
+template <int NW>
 struct SplitLds {
     // q columns in f16: rows 0..3 q_hi of heads 4g..4g+3, rows 4..7 q_lo,
     // row 8 zeros (the B operand's unused columns).
     __attribute__((aligned(16))) uint16_t qhl[9][QM_GQA_HD];
-    float wacc[4][4][QM_GQA_HD];                // per-wave partial PV
-    float wm[4][4], wl[4][4];
+    float wacc[NW][4][QM_GQA_HD];               // per-wave partial PV
+    float wm[NW][4], wl[NW][4];
     __attribute__((aligned(16))) uint16_t knew[QM_GQA_HD], vnew[QM_GQA_HD];   // appended rows
 };
 
@@ -216,8 +217,11 @@ struct SplitLds {
 // 1), so the RoPE rows and the append's inputs are known before any load and
 // are issued with the q row, ahead of the first round; otherwise they wait
 // for pos and follow the round.
-template <bool POS_ARG>
-QM_DEV void split_body(const GqaDecodeArgs& A, SplitLds& sh) {
+// NW: waves per workgroup (4 to 8).  Waves 0..3 also own the q prep and the
+// final merge of query heads 4g..4g+3; every wave streams rounds.  Short
+// splits (chunk = 16 NW keys, as at batch 1) thus take one round per wave.
+template <bool POS_ARG, int NW>
+QM_DEV void split_body(const GqaDecodeArgs& A, SplitLds<NW>& sh) {
     auto& qhl = sh.qhl;
     auto& wacc = sh.wacc;
     auto& wm = sh.wm;
@@ -243,7 +247,7 @@ QM_DEV void split_body(const GqaDecodeArgs& A, SplitLds& sh) {
     // loads complete in issue order, so the q norm starts while the round is
     // still in flight.
     int pos = POS_ARG ? A.max_pos : A.pos[b];
-    const float* qg = A.q_gate + ((size_t)b * QM_GQA_HEADS + 4 * g + w) * (2 * QM_GQA_HD);
+    const float* qg = A.q_gate + ((size_t)b * QM_GQA_HEADS + 4 * g + (w & 3)) * (2 * QM_GQA_HD);
     const float4 qx = ld4(qg + 4 * lane);
     const uint2 gq = *reinterpret_cast<const uint2*>(A.q_norm + 4 * lane);
     float4 rc, rs;
@@ -262,7 +266,7 @@ QM_DEV void split_body(const GqaDecodeArgs& A, SplitLds& sh) {
         pos_loads(pos, t_begin <= pos && pos < t_end);
     }
     __builtin_amdgcn_sched_barrier(0);
-    // 4a. Wave w takes rounds t_begin + 64*r + 16*w (r = 0 .. nr-1).
+    // 4a. Wave w takes rounds t_begin + 16*NW*r + 16*w (r = 0 .. nr-1).
     RoundBuf ra, rb;
     {
         const int t_end0 = min(t_begin + A.chunk, A.max_pos + 1);
@@ -274,15 +278,15 @@ QM_DEV void split_body(const GqaDecodeArgs& A, SplitLds& sh) {
     const int t_end = min(t_begin + A.chunk, L);
     const bool appends = (t_begin <= pos && pos < t_end);
     const int span = t_end - t_begin - 16 * w;
-    const int nr = __builtin_amdgcn_readfirstlane(span > 0 ? (span + 63) / 64 : 0);
+    const int nr = __builtin_amdgcn_readfirstlane(span > 0 ? (span + 16 * NW - 1) / (16 * NW) : 0);
     const int t_last = t_end - 1;
     if (!POS_ARG) pos_loads(pos, appends);
     float4 gv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (A.nsplit == 1) gv = gqa_gate(A, b, 4 * g + w, lane);
+    if (A.nsplit == 1) gv = gqa_gate(A, b, 4 * g + (w & 3), lane);
 
-    // 1. q prep: wave w handles query head 4g+w (gemv.rs:927-949), stored
-    //    as its f16 hi / lo parts.
-    {
+    // 1. q prep: wave w < 4 handles query head 4g+w (gemv.rs:927-949),
+    //    stored as its f16 hi / lo parts.
+    if (w < 4) {
         const float4 x = norm_rope_head(qx, gq, rc, rs, lane);
         const uint2 hi = pack_f16x4(x.x, x.y, x.z, x.w);
         const float4 xh = make_float4(f16_to_f32((uint16_t)(hi.x & 0xffffu)), f16_to_f32((uint16_t)(hi.x >> 16)),
@@ -328,14 +332,14 @@ QM_DEV void split_body(const GqaDecodeArgs& A, SplitLds& sh) {
 
     // 4b. Stream the rounds, next round's loads in flight during compute.
     for (int r = 0; r < nr; r += 2) {
-        const int t0 = t_begin + 64 * r + 16 * w;
-        if (r + 1 < nr) load_round(rb, kbase, vbase, t0 + 64, t_last, lane);
+        const int t0 = t_begin + 16 * NW * r + 16 * w;
+        if (r + 1 < nr) load_round(rb, kbase, vbase, t0 + 16 * NW, t_last, lane);
         __builtin_amdgcn_sched_barrier(0);
         compute_round(st, ra, qsrc, t0, t_end, lane, r == 0, ap, knew, vnew);
         if (r + 1 >= nr) break;
-        if (r + 2 < nr) load_round(ra, kbase, vbase, t0 + 128, t_last, lane);
+        if (r + 2 < nr) load_round(ra, kbase, vbase, t0 + 32 * NW, t_last, lane);
         __builtin_amdgcn_sched_barrier(0);
-        compute_round(st, rb, qsrc, t0 + 64, t_end, lane, false, ap, knew, vnew);
+        compute_round(st, rb, qsrc, t0 + 16 * NW, t_end, lane, false, ap, knew, vnew);
     }
 
     // 5. Join each head's hi and lo rows (lanes l and l^32: one row swap per
@@ -366,15 +370,15 @@ QM_DEV void split_body(const GqaDecodeArgs& A, SplitLds& sh) {
         }
     }
     __syncthreads();
-    {
+    if (w < 4) {
         const int h = w;                      // thread (h, lane): dims 4*lane..+3
         float M = -INFINITY;
 #pragma unroll
-        for (int ww = 0; ww < 4; ++ww) M = fmaxf(M, wm[ww][h]);
+        for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, wm[ww][h]);
         float Ls = 0.0f;
         float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-        for (int ww = 0; ww < 4; ++ww) {
+        for (int ww = 0; ww < NW; ++ww) {
             const float f = (wm[ww][h] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(wm[ww][h] - M);
             Ls += wl[ww][h] * f;
             const float4 a = *reinterpret_cast<const float4*>(&wacc[ww][h][4 * lane]);
@@ -390,11 +394,17 @@ QM_DEV void split_body(const GqaDecodeArgs& A, SplitLds& sh) {
     }
 }
 
-extern "C" __global__ __launch_bounds__(256) void qm_gqa_decode_split(GqaDecodeArgs A) {
-    __shared__ SplitLds sh;
-    if (A.pos) split_body<false>(A, sh);
-    else split_body<true>(A, sh);
+template <int NW>
+QM_DEV void split_kernel(const GqaDecodeArgs& A) {
+    __shared__ SplitLds<NW> sh;
+    if (A.pos) split_body<false, NW>(A, sh);
+    else split_body<true, NW>(A, sh);
 }
+extern "C" __global__ __launch_bounds__(256) void qm_gqa_decode_split(GqaDecodeArgs A) { split_kernel<4>(A); }
+extern "C" __global__ __launch_bounds__(320) void qm_gqa_decode_split_w5(GqaDecodeArgs A) { split_kernel<5>(A); }
+extern "C" __global__ __launch_bounds__(384) void qm_gqa_decode_split_w6(GqaDecodeArgs A) { split_kernel<6>(A); }
+extern "C" __global__ __launch_bounds__(448) void qm_gqa_decode_split_w7(GqaDecodeArgs A) { split_kernel<7>(A); }
+extern "C" __global__ __launch_bounds__(512) void qm_gqa_decode_split_w8(GqaDecodeArgs A) { split_kernel<8>(A); }
 
 // Merge the split partials of query head 4g+h of sequence b and apply the
 // gate.  One wave per (b, g, h, quarter of the dims): lane l owns dim

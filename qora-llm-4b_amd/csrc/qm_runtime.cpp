@@ -37,7 +37,7 @@ struct qm_context {
     std::vector<hipModule_t> modules;
     hipFunction_t f_conv = nullptr;
     hipFunction_t f_dn[3] = {nullptr, nullptr, nullptr};  // 256, 512, 1024 threads
-    hipFunction_t f_gqa_split = nullptr;
+    hipFunction_t f_gqa_split[5] = {};      // 4 .. 8 waves per workgroup
     hipFunction_t f_gqa_merge = nullptr;
     hipFunction_t f_fill = nullptr;
     hipFunction_t f_dnp_chunk = nullptr;
@@ -306,7 +306,11 @@ int32_t qm_create(qm_context** out, const qm_config* cfg, const char* code_objec
     const char* dn_names[3] = {"qm_dn_decode_t256", "qm_dn_decode_t512", "qm_dn_decode_t1024"};
     if (st == QM_OK) st = load_function(c, mods[0], "qm_dn_conv_silu", &c->f_conv);
     for (int i = 0; i < 3 && st == QM_OK; ++i) st = load_function(c, mods[0], dn_names[i], &c->f_dn[i]);
-    if (st == QM_OK) st = load_function(c, mods[1], "qm_gqa_decode_split", &c->f_gqa_split);
+    if (st == QM_OK) st = load_function(c, mods[1], "qm_gqa_decode_split", &c->f_gqa_split[0]);
+    if (st == QM_OK) st = load_function(c, mods[1], "qm_gqa_decode_split_w5", &c->f_gqa_split[1]);
+    if (st == QM_OK) st = load_function(c, mods[1], "qm_gqa_decode_split_w6", &c->f_gqa_split[2]);
+    if (st == QM_OK) st = load_function(c, mods[1], "qm_gqa_decode_split_w7", &c->f_gqa_split[3]);
+    if (st == QM_OK) st = load_function(c, mods[1], "qm_gqa_decode_split_w8", &c->f_gqa_split[4]);
     if (st == QM_OK) st = load_function(c, mods[1], "qm_gqa_decode_merge", &c->f_gqa_merge);
     if (st == QM_OK) st = load_function(c, mods[2], "qm_fill_normal", &c->f_fill);
     if (st == QM_OK) st = load_function(c, mods[3], "qm_dn_prefill_chunk", &c->f_dnp_chunk);
@@ -667,7 +671,11 @@ int32_t gqa_decode_impl(qm_context* c, qm_stream stream, int32_t batch, const fl
     GqaDecodeArgs ga{q_gate, k_new, v_new, q_norm, k_norm, rope_cos, rope_sin, pos, k_cache, v_cache,
                      out, partials, cap, max_pos,
                      static_cast<int32_t>(chunk), static_cast<int32_t>(nsplit), batch};
-    int32_t st = launch(c, c->f_gqa_split, static_cast<uint32_t>(grid), 256, ga, s, "qm_gqa_decode_split");
+    // a split of 80..128 keys gets one wave per 16-key round, so no wave
+    // runs two rounds one after the other; longer splits stream on 4 waves
+    const int nw = (chunk >= 80 && chunk <= 128) ? static_cast<int>(chunk / 16) : 4;
+    int32_t st = launch(c, c->f_gqa_split[nw - 4], static_cast<uint32_t>(grid), 64 * nw, ga, s,
+                        "qm_gqa_decode_split");
     if (st != QM_OK || nsplit == 1) return st;
     return launch(c, c->f_gqa_merge, static_cast<uint32_t>(batch) * QM_GQA_KV_HEADS * 16, 64, ga, s,
                   "qm_gqa_decode_merge");
