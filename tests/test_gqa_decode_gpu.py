@@ -20,12 +20,14 @@ W = load_workloads()
 TOL = 1e-3
 
 
-def run_gpu(ctx, w, positions, rope_rows, chunk=0):
+def run_gpu(ctx, w, positions, rope_rows, chunk=0, pos_array=True):
+    """pos_array=False passes no per-sequence positions (every sequence at
+    max(positions), the batch-1 form)."""
     B = w["q_gate"].shape[0]
     cos, sin = M.rope_table(rope_rows)
     d = {k: ctx.upload(w[k]) for k in ["q_gate", "k_new", "v_new", "q_norm", "k_norm", "k_cache", "v_cache"]}
     rc, rs = ctx.upload(cos), ctx.upload(sin)
-    pos_dev = ctx.upload(np.asarray(positions, np.int32))
+    pos_dev = ctx.upload(np.asarray(positions, np.int32)) if pos_array else None
     out = ctx.alloc(B * 16 * 256 * 4)
     ctx.set_option(M.QM_OPT_GQA_DECODE_CHUNK, chunk)
     try:
@@ -101,13 +103,37 @@ def test_decode_rows_past_the_end_never_reach_the_output(ctx, chunk):
     assert np.abs(got - ref).max() <= TOL
 
 
-@pytest.mark.parametrize("chunk", [64, 192, 1024, 4160])  # 4160: one split, no merge kernel
+@pytest.mark.parametrize("chunk", [64, 128, 192, 1024, 4160])  # 128: eight waves; 4160: one split, no merge kernel
 def test_decode_chunk_invariance(ctx, chunk):
     w = W.gqa_decode_workload(3000, 2, seed=3)
     print(f"case: gqa decode chunk={chunk}", flush=True)
     got, _, _ = run_gpu(ctx, w, [3000, 3000], 3001, chunk=chunk)
     ref, _, _ = run_oracle(w, [3000, 3000], 3001)
     assert np.abs(got - ref).max() <= TOL
+
+
+@pytest.mark.parametrize("max_pos", [5000, 6000, 7000, 8000])
+def test_decode_waves_per_split(ctx, max_pos):
+    """Automatic splits of 80, 96, 112 and 128 keys at these lengths run five
+    to eight waves per split workgroup (one 16-key round each).  The second
+    sequence ends inside a split, so some waves there have no round."""
+    positions = [max_pos, max_pos // 3 + 5]
+    w = W.gqa_decode_workload(max_pos, 2, seed=31 + max_pos)
+    print(f"case: gqa decode waves per split, positions {positions}", flush=True)
+    got, _, _ = run_gpu(ctx, w, positions, max_pos + 1)
+    ref, _, _ = run_oracle(w, positions, max_pos + 1)
+    print(f"max|dout|={np.abs(got - ref).max():.3e}")
+    assert np.abs(got - ref).max() <= TOL
+    # batch 1 without a position array (the RoPE rows and the appended row
+    # are loaded with the q row, ahead of the first round)
+    w1 = W.gqa_decode_workload(max_pos, 1, seed=41 + max_pos)
+    print(f"case: gqa decode waves per split, batch 1 at {max_pos}, no position array", flush=True)
+    got, kc, _ = run_gpu(ctx, w1, [max_pos], max_pos + 1, pos_array=False)
+    ref, krows, _ = run_oracle(w1, [max_pos], max_pos + 1)
+    print(f"max|dout|={np.abs(got - ref).max():.3e}")
+    assert np.abs(got - ref).max() <= TOL
+    kgot = W.f16_value(kc[0, :, max_pos])
+    assert np.all(np.abs(kgot - krows[0]) <= np.abs(krows[0]) * 2 ** -10 + 1e-7)
 
 
 def test_decode_many_splits_ragged(ctx):
