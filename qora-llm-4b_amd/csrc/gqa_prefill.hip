@@ -185,18 +185,6 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_prefill_kv(GqaPrefillAr
 #define SM_V(b) ((b) * 65536 + 32768)
 #define SM_BYTES 131072
 
-// 16 bytes per lane from global memory straight into LDS: lane l writes
-// lds + 16 l.  Issued as inline asm so that no compiler-inserted wait ties
-// later LDS reads to it; completion is awaited explicitly (vmcnt) before the
-// barrier that publishes the tile.  M0 has no other user in this kernel.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-QM_DEV void dma16(const void* gsrc, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-                 :: "v"(gsrc), "s"(lds) : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
 // A row block is 48 query rows of the four query heads of one kv group: 12
 // waves, wave w on head 4g + (w & 3) and rows 16 (w >> 2) .. +15, three
 // waves per SIMD, so one wave's LDS and softmax latency hides behind the

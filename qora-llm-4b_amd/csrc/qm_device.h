@@ -108,3 +108,16 @@ QM_DEV float sigmoid_fast(float x) {
 // ---- memory helpers ------------------------------------------------------
 QM_DEV float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 QM_DEV void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
+
+// 16 bytes per lane from global memory straight into LDS (LDS DMA): lane l
+// writes lds + 16 l.  Issued as inline asm so that no compiler-inserted wait
+// ties later LDS reads to it; the caller awaits completion explicitly
+// (vmcnt) before the barrier that publishes the data.  It sets M0, so a
+// kernel using it must have no other M0 user.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+QM_DEV void dma16(const void* gsrc, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :: "v"(gsrc), "s"(lds) : "memory", "m0");
+}
+#pragma clang diagnostic pop
