@@ -81,6 +81,20 @@ def test_prefill_8192_rows(ctx):
     check(o, K, V, ref, kc, vc, rows)
 
 
+def test_prefill_5000_rows(ctx):
+    """S = 5000, a multiple of neither the 48-row block nor the 64-key tile:
+    the last tile copy is zero padded past S, and the last row block is
+    partial.  Checked on the last 60 rows, 120 random rows and the first 20."""
+    S = 5000
+    w = W.gqa_prefill_workload(S, seed=23)
+    print("case: gqa prefill S=5000", flush=True)
+    o, K, V = run_gpu(ctx, w, S, S + 3)
+    rows = np.unique(np.concatenate([np.arange(0, 20), np.arange(S - 60, S),
+                                     np.random.default_rng(7).integers(0, S, 120)]))
+    ref, kc, vc = run_oracle(w, S, rows=rows)
+    check(o, K, V, ref, kc, vc, rows)
+
+
 def test_prefill_score_jumps(ctx):
     """Later keys that score far above the earlier ones: every query is one
     vector b; keys from position 150 lean 60% towards b (a jump of well over
