@@ -103,8 +103,8 @@ const char* qm_status_string(int32_t status);
 const char* qm_last_error(const qm_context* ctx);
 int32_t     qm_device_count(int32_t* count);
 /* Size the workspace for batches up to max_batch and KV lengths up to
- * max_kv_len (and DeltaNet prefill up to max_prefill_tokens) so that later
- * mixer calls do not allocate (e.g. under graph capture). */
+ * max_kv_len (and DeltaNet and GQA prefill up to max_prefill_tokens) so
+ * that later mixer calls do not allocate (e.g. under graph capture). */
 int32_t     qm_reserve(qm_context* ctx, int32_t max_batch, int32_t max_kv_len,
                        int32_t max_prefill_tokens);
 /* Launch-shape overrides for tests and tuning (0 = automatic).  Results do
