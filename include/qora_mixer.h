@@ -111,7 +111,10 @@ int32_t     qm_reserve(qm_context* ctx, int32_t max_batch, int32_t max_kv_len,
  * not depend on them beyond fp32 reassociation. */
 enum {
     QM_OPT_DN_DECODE_THREADS = 1,  /* threads per v-head workgroup: 256, 512, 1024 */
-    QM_OPT_GQA_DECODE_CHUNK = 2    /* keys per split-K workgroup (mult. 64)*/
+    QM_OPT_GQA_DECODE_CHUNK = 2,   /* keys per split-K workgroup (mult. 64)*/
+    QM_OPT_GQA_PREFILL_ORDER = 3   /* row-block order of the causal prefill:
+                                      1 longest first, 2 packed; results are
+                                      bit-identical */
 };
 int32_t     qm_set_option(qm_context* ctx, int32_t option, int64_t value);
 

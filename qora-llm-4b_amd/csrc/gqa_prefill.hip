@@ -193,11 +193,14 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_prefill_kv(GqaPrefillAr
 // the current tile's scores, softmax and P V.
 // The kernel is persistent: one workgroup per CU, workgroup b serving kv
 // group b & 3 (workgroups are dealt to the XCDs round-robin, so each XCD's L2
-// holds one group's K / V).  Row blocks are taken longest first from a
-// per-group atomic counter, so the causal triangle's unequal blocks balance
-// across CUs (a fixed assignment left some CUs with a third more tiles than
-// others).  A workgroup whose own queue is empty takes the remaining (short)
-// blocks of the other groups, which evens out the XCDs' speeds.
+// holds one group's K / V).  Row blocks are drawn from a per-group atomic
+// counter, so the causal triangle's unequal blocks balance across CUs (a
+// fixed assignment left some CUs with a third more tiles than others).  The
+// n-th draw takes block order[n] when the host passes an order (a packing of
+// the blocks into the workgroups, listed by planned start time), else the
+// n-th longest block.  A workgroup whose own queue is empty takes the
+// remaining (short) blocks of the other groups, which evens out the XCDs'
+// speeds.
 #define TQ3 48
 
 // Fragment reads in flight per wave in the two products: with 32 reads of
@@ -219,7 +222,8 @@ QM_DEV void sched_reads_ahead() {
     __builtin_amdgcn_sched_group_barrier(0x008, LOOKAHEAD + EXTRA, 0);
 }
 
-extern "C" __global__ __launch_bounds__(768) void qm_gqa_prefill_attn(GqaPrefillArgs A) {
+extern "C" __global__ __launch_bounds__(768) void qm_gqa_prefill_attn(GqaPrefillAttnArgs P) {
+    const GqaPrefillArgs& A = P.a;
     __shared__ __attribute__((aligned(1024))) char sm[SM_BYTES];
     __shared__ int item_s;
     const int tid = threadIdx.x;
@@ -246,15 +250,16 @@ extern "C" __global__ __launch_bounds__(768) void qm_gqa_prefill_attn(GqaPrefill
         const int g = item / nblk;
         const uint16_t* tiles = A.kvf + (size_t)g * (A.s_pad / 64) * (64 * 512);
         // the next block is claimed three tiles before this one ends: late
-        // enough to keep the longest-first order, early enough to hide the
-        // atomic's latency
+        // enough to keep the queue's order, early enough to hide the atomic's
+        // latency
         int nxt = 0;
         // lane-derived addresses are recomputed per row block (cheap)
         // rather than held across blocks, which would spill them
         int lane = tid & 63;
         asm volatile("" : "+v"(lane));
         const int lr = lane & 15, lq = lane >> 4;
-        const int tb = nblk - 1 - (item - g * nblk);   // longest rows first
+        const int draw = item - g * nblk;
+        const int tb = P.ordered ? (int)P.order[draw] : nblk - 1 - draw;
         const int t0 = tb * TQ3;
         const int qh = 4 * g + (w & 3);
         const int r0 = t0 + 16 * (w >> 2);

@@ -120,6 +120,16 @@ struct GqaPrefillArgs {
     int32_t s_pad;
 };
 
+// The attention kernel's arguments: the shared ones plus the order in which
+// each kv group's queue hands out its 48-row blocks (block 0 = rows 0..47).
+// ordered = 0: the n-th draw is the n-th longest block (nblk - 1 - n).
+#define QM_GQA_PREFILL_ORDER_MAX 1024
+struct GqaPrefillAttnArgs {
+    GqaPrefillArgs a;
+    int32_t ordered;
+    uint16_t order[QM_GQA_PREFILL_ORDER_MAX];
+};
+
 // Q4 GEMV (one input row) on the tile-major device layout, for up to
 // QM_Q4_MAX_OUT weights sharing x: one workgroup per column tile, weight p
 // taking workgroups wstart[p] .. wstart[p+1]-1 with tiles of tile[p]

@@ -28,7 +28,7 @@ STATUS_NAMES = {
 }
 QM_DN_POSTACT, QM_DN_PREACT = 0, 1
 QM_F32, QM_F16, QM_BF16 = 0, 1, 2
-QM_OPT_DN_DECODE_THREADS, QM_OPT_GQA_DECODE_CHUNK = 1, 2
+QM_OPT_DN_DECODE_THREADS, QM_OPT_GQA_DECODE_CHUNK, QM_OPT_GQA_PREFILL_ORDER = 1, 2, 3
 
 # Mixer shape (config.rs:42-97).
 DN_QK_HEADS, DN_V_HEADS, DN_HD, DN_CONV_K = 16, 32, 128, 4

@@ -49,6 +49,7 @@ pub mod raw {
 
     pub const QM_OPT_DN_DECODE_THREADS: i32 = 1;
     pub const QM_OPT_GQA_DECODE_CHUNK: i32 = 2;
+    pub const QM_OPT_GQA_PREFILL_ORDER: i32 = 3;
     pub const QM_F32: i32 = 0;
     pub const QM_F16: i32 = 1;
     pub const QM_BF16: i32 = 2;

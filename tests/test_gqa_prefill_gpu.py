@@ -95,6 +95,34 @@ def test_prefill_5000_rows(ctx):
     check(o, K, V, ref, kc, vc, rows)
 
 
+@pytest.mark.parametrize("S", [8192, 5000])
+def test_prefill_block_order(ctx, S):
+    """The packed row-block order (QM_OPT_GQA_PREFILL_ORDER = 2; at 8192
+    tokens also the automatic one) and longest first give bit-identical
+    outputs on every row: each block is computed once, by whichever
+    workgroup draws it.  The output starts as NaN, so a block left out
+    would show."""
+    w = W.gqa_prefill_workload(S, seed=41)
+    print(f"case: gqa prefill block order S={S}", flush=True)
+    cos, sin = M.rope_table(S)
+    d = {k: ctx.upload(w[k]) for k in ["q_gate", "k", "v", "q_norm", "k_norm"]}
+    rc, rs = ctx.upload(cos), ctx.upload(sin)
+    outs = []
+    try:
+        for mode in (1, 2, 0):
+            ctx.set_option(M.QM_OPT_GQA_PREFILL_ORDER, mode)
+            kc = ctx.alloc(4 * S * 256 * 2)
+            vc = ctx.alloc(4 * S * 256 * 2)
+            out = ctx.upload(np.full((S, 16, 256), 0x7FC0, np.uint16))
+            ctx.gqa_prefill(S, d["q_gate"], d["k"], d["v"], d["q_norm"], d["k_norm"], rc, rs, S, kc, vc, S, out)
+            outs.append(ctx.download(out, (S, 16, 256), np.uint16))
+    finally:
+        ctx.set_option(M.QM_OPT_GQA_PREFILL_ORDER, 0)
+    assert not np.isnan(W.bf16_value(outs[0])).any()
+    assert np.array_equal(outs[0], outs[1])
+    assert np.array_equal(outs[0], outs[2])
+
+
 def test_prefill_score_jumps(ctx):
     """Later keys that score far above the earlier ones: every query is one
     vector b; keys from position 150 lean 60% towards b (a jump of well over
