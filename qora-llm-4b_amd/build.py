@@ -94,10 +94,18 @@ def build_file_test() -> None:
           str(ROOT / "tests" / "cpp" / "qor4b_file_test.cpp"), "-o", str(LIB / "qor4b_file_test")])
 
 
+def build_plan_test() -> None:
+    """tests/cpp/gqa_plan_test.cpp: the GQA prefill row-block order on the CPU
+    (g++ only, no device code; test infrastructure)."""
+    _run(["g++", "-O2", "-std=c++17", "-Wall", "-Wextra", "-I", str(CSRC),
+          str(ROOT / "tests" / "cpp" / "gqa_plan_test.cpp"), "-o", str(LIB / "gqa_plan_test")])
+
+
 if __name__ == "__main__":
     build()
     if "--no-oracle" not in sys.argv:
         build_oracle()
         build_host_test()
         build_file_test()
+        build_plan_test()
     print("built:", ", ".join(sorted(p.name for p in LIB.iterdir())))

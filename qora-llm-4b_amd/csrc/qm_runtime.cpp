@@ -10,6 +10,7 @@
 // outside stream capture.
 #include "qora_mixer.h"
 #include "qm_kernel_args.h"
+#include "qm_gqa_plan.h"
 #include "qm_noalloc.h"
 
 #include <hip/hip_runtime_api.h>
@@ -773,98 +774,6 @@ int32_t qm_deltanet_prefill(qm_context* c, qm_stream stream, int32_t seq_len, co
 }
 
 // ---- GQA causal prefill ------------------------------------------------------------
-namespace {
-// Row-block order of the attention's per-group queues.  Each kv group's
-// blocks go to whichever of its `bins` workgroups draws next, so the order
-// decides how the causal triangle's unequal blocks pack.  Block tb (rows
-// 48 tb .. 48 tb + 47) costs its 64-key tiles plus about eight tiles' worth
-// of q preparation and epilogue (per-workgroup stamps at 8192 tokens: ~2.5 us
-// per tile, 14-20 us per block).  Longest first packs some lengths badly: at 8192 tokens
-// (171 blocks over 64 workgroups) the busiest workgroup gets 12% more than
-// the mean.  The plan packs the blocks by best-fit decreasing (each block
-// into the fullest workgroup it fits, under the smallest capacity, raised in
-// 0.25% steps from the mean, at which all fit) and lists them by planned
-// start time, longest first among equal starts: at equal speeds the queue
-// then reproduces the packing, and it still adapts when workgroups run at
-// different speeds.
-double gqp_block_cost(int32_t tb, int32_t S) {
-    const int32_t rows_end = std::min(48 * tb + 48, S);
-    return static_cast<double>((rows_end + 63) / 64) + 8.0;
-}
-
-// Finish time of the last of `bins` workgroups that draw the blocks in this
-// order, each drawing as it finishes (all at equal speed).
-double gqp_makespan(const std::vector<int32_t>& order, int32_t S, int32_t bins) {
-    std::vector<double> t(static_cast<size_t>(bins), 0.0);
-    for (int32_t tb : order) {
-        auto it = std::min_element(t.begin(), t.end());
-        *it += gqp_block_cost(tb, S);
-    }
-    return *std::max_element(t.begin(), t.end());
-}
-
-std::vector<int32_t> gqp_packed_order(int32_t S, int32_t bins) {
-    const int32_t nblk = (S + 47) / 48;
-    double total = 0.0;
-    for (int32_t tb = 0; tb < nblk; ++tb) total += gqp_block_cost(tb, S);
-    std::vector<std::vector<int32_t>> bin;
-    for (int step = 0;; ++step) {
-        const double cap = total / bins * (1.0 + 0.0025 * step) + 1e-9;
-        bin.assign(static_cast<size_t>(bins), {});
-        std::vector<double> load(static_cast<size_t>(bins), 0.0);
-        bool ok = true;
-        for (int32_t tb = nblk - 1; tb >= 0 && ok; --tb) {   // longest first
-            const double c = gqp_block_cost(tb, S);
-            int best = -1;
-            for (int i = 0; i < bins; ++i)
-                if (load[i] + c <= cap && (best < 0 || load[i] > load[best])) best = i;
-            if (best < 0) ok = false;
-            else { bin[best].push_back(tb); load[best] += c; }
-        }
-        if (ok) break;
-    }
-    struct Entry { double start, cost; int32_t tb; };
-    std::vector<Entry> e;
-    for (const auto& b : bin) {
-        double t = 0.0;
-        for (int32_t tb : b) {                  // already longest first
-            e.push_back({t, gqp_block_cost(tb, S), tb});
-            t += gqp_block_cost(tb, S);
-        }
-    }
-    std::stable_sort(e.begin(), e.end(), [](const Entry& x, const Entry& y) {
-        return x.start != y.start ? x.start < y.start : x.cost > y.cost;
-    });
-    std::vector<int32_t> order;
-    for (const auto& x : e) order.push_back(x.tb);
-    return order;
-}
-
-// Fill a.ordered / a.order for seq_len S over `bins` workgroups per group.
-// mode 0: the packed order where the queue simulation puts longest first at
-// least 5% behind it; 1: longest first; 2: the packed order whenever the
-// blocks outnumber the workgroups and fit the table.
-void gqp_set_order(GqaPrefillAttnArgs& a, int32_t S, int32_t bins, int64_t mode) {
-    a.ordered = 0;
-    const int32_t nblk = (S + 47) / 48;
-    if (mode == 1 || nblk <= bins || nblk > QM_GQA_PREFILL_ORDER_MAX) return;
-    const std::vector<int32_t> packed = gqp_packed_order(S, bins);
-    if (mode == 0) {
-        std::vector<int32_t> longest(static_cast<size_t>(nblk));
-        for (int32_t n = 0; n < nblk; ++n) longest[n] = nblk - 1 - n;
-        if (gqp_makespan(longest, S, bins) < 1.05 * gqp_makespan(packed, S, bins)) return;
-    }
-    // every block exactly once, or the longest-first order stays
-    std::vector<char> seen(static_cast<size_t>(nblk), 0);
-    if (static_cast<int32_t>(packed.size()) != nblk) return;
-    for (int32_t tb : packed) {
-        if (tb < 0 || tb >= nblk || seen[tb]) return;
-        seen[tb] = 1;
-    }
-    for (int32_t n = 0; n < nblk; ++n) a.order[n] = static_cast<uint16_t>(packed[n]);
-    a.ordered = 1;
-}
-}  // namespace
 
 int32_t qm_gqa_prefill(qm_context* c, qm_stream stream, int32_t seq_len, const uint16_t* q_gate,
                        const uint16_t* k, const uint16_t* v, const uint16_t* q_norm,
@@ -898,7 +807,7 @@ int32_t qm_gqa_prefill(qm_context* c, qm_stream stream, int32_t seq_len, const u
     const int32_t nblk = (seq_len + 47) / 48;
     const int32_t per_group = std::max(1, std::min(c->num_cu / QM_GQA_KV_HEADS, nblk));
     if (c->gqp_S != seq_len || c->gqp_bins != per_group || c->gqp_mode != c->opt_gqp_order) {
-        gqp_set_order(c->gqp_args, seq_len, per_group, c->opt_gqp_order);
+        c->gqp_args.ordered = qm_plan::gqp_set_order(c->gqp_args.order, seq_len, per_group, c->opt_gqp_order);
         c->gqp_S = seq_len;
         c->gqp_bins = per_group;
         c->gqp_mode = c->opt_gqp_order;
