@@ -95,10 +95,10 @@ def test_prefill_5000_rows(ctx):
     check(o, K, V, ref, kc, vc, rows)
 
 
-@pytest.mark.parametrize("S", [8192, 5000])
+@pytest.mark.parametrize("S", [8192, 10000, 5000])
 def test_prefill_block_order(ctx, S):
-    """The packed row-block order (QM_OPT_GQA_PREFILL_ORDER = 2; at 8192
-    tokens also the automatic one) and longest first give bit-identical
+    """The packed row-block order (QM_OPT_GQA_PREFILL_ORDER = 2; at 8192 and
+    10000 tokens also the automatic one) and longest first give bit-identical
     outputs on every row: each block is computed once, by whichever
     workgroup draws it.  The output starts as NaN, so a block left out
     would show."""
