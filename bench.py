@@ -268,11 +268,41 @@ def run_dn_decode(args, ctx):
         tm.wrap(lambda: step(Wm + t))
     ctx.sync()
     nbytes = dn_decode_bytes(1)
+    # Cold variant: the 2 MiB state stays in L2 / the 256 MB MALL across the
+    # steps above.  Here step t updates state t mod NS of NS = 256 distinct
+    # states (512 MiB), so each launch finds its state evicted by the 255
+    # launches since its last use.
+    NS = 256
+    states = ctx.alloc(NS * 32 * 128 * 128 * 4)
+    ctx.fill_normal(states, M.QM_F32, NS * 32 * 128 * 128, 0.0, 0.02, 40)
+
+    def step_cold(t, i):
+        ctx.deltanet_decode(1, M.QM_DN_POSTACT, qkv.offset(t * 8192 * 4), None, None,
+                            a.offset(t * 32 * 4), b.offset(t * 32 * 4), a_log, dt_bias,
+                            z.offset(t * 4096 * 4), norm_w, states.offset((i % NS) * 32 * 128 * 128 * 4),
+                            out.offset(t * 4096 * 4))
+
+    ctx.graph_begin()
+    for i in range(K):
+        step_cold(Wm + i, i)
+    gc_ = ctx.graph_end()
+    gc_.launch()                          # warm-up replay: every state touched once
+    ctx.sync()
+    c0, c1 = ctx.event(), ctx.event()
+    c0.record()
+    gc_.launch()
+    c1.record()
+    ctx.sync()
+    cold_ms = c0.elapsed_ms(c1) / K
+    gc_.close()
+    states.close()
     return {
         "tokens": K, "total_ms": total_ms, "wall_s": wall, "dominant": "qm_dn_decode_t512",
         "roofline": {"bound": "hbm", "achieved": nbytes / (k_ms * 1e-3), "peak": HBM_PEAK,
                      "unit": "GB/s", "kernel_ms": k_ms, "bytes_per_launch": nbytes},
         "eager_event_ms_per_launch": tm.mean_ms(),
+        "cold": {"ms_per_launch": cold_ms, "frac": nbytes / (cold_ms * 1e-3) / HBM_PEAK,
+                 "note": f"graph of {K} steps rotating over {NS} states ({NS * 2} MiB)"},
         "config": {"workload": "DeltaNet decode, 1 layer, batch 1, 16 qk / 32 v heads x 128, fp32 state",
                    "batch": 1, "seq_len": K, "global_batch": 1, "parallelism": "single GPU"},
     }
@@ -315,11 +345,43 @@ def run_gqa_decode(args, ctx):
         tm.wrap(step)
     ctx.sync()
     nbytes = gqa_decode_bytes(1, pos + 1)
+    # Cold variant: one 16 MiB cache stays resident in the 256 MB MALL across
+    # the steps above.  Here step i reads cache i mod NC of NC = 40 distinct
+    # caches (~670 MB), so each launch finds its cache evicted by the 39
+    # launches since its last use.
+    NC = 40
+    cache_elems = 4 * w["cap"] * 256
+    kcs, vcs = ctx.alloc(NC * cache_elems * 2), ctx.alloc(NC * cache_elems * 2)
+    ctx.fill_normal(kcs, M.QM_F16, NC * cache_elems, 0.0, 1.0, 41)
+    ctx.fill_normal(vcs, M.QM_F16, NC * cache_elems, 0.0, 1.0, 42)
+
+    def step_cold(i):
+        j = (i % NC) * cache_elems * 2
+        ctx.gqa_decode(1, d["q_gate"], d["k_new"], d["v_new"], d["q_norm"], d["k_norm"], rc, rs,
+                       pos + 1, None, pos, kcs.offset(j), vcs.offset(j), w["cap"], out)
+
+    ctx.graph_begin()
+    for i in range(K):
+        step_cold(i)
+    gc_ = ctx.graph_end()
+    gc_.launch()                          # warm-up replay
+    ctx.sync()
+    c0, c1 = ctx.event(), ctx.event()
+    c0.record()
+    gc_.launch()
+    c1.record()
+    ctx.sync()
+    cold_ms = c0.elapsed_ms(c1) / K
+    gc_.close()
+    kcs.close()
+    vcs.close()
     return {
         "tokens": K, "total_ms": total_ms, "wall_s": wall, "dominant": "qm_gqa_decode_split+merge",
         "roofline": {"bound": "hbm", "achieved": nbytes / (k_ms * 1e-3), "peak": HBM_PEAK,
                      "unit": "GB/s", "kernel_ms": k_ms, "bytes_per_launch": nbytes},
         "eager_event_ms_per_launch": tm.mean_ms(),
+        "cold": {"ms_per_launch": cold_ms, "frac": nbytes / (cold_ms * 1e-3) / HBM_PEAK,
+                 "note": f"graph of {K} steps rotating over {NC} caches ({NC * 2 * cache_elems * 2 / 2**20:.0f} MiB)"},
         "config": {"workload": "GQA decode, 1 layer, batch 1, 16q/4kv x 256, position 4096, f16 KV",
                    "batch": 1, "seq_len": pos + 1, "global_batch": 1, "parallelism": "single GPU"},
     }
@@ -922,8 +984,28 @@ def _repeat_for(fn, min_s=None, max_iters=10 ** 6):
             return n, dt
 
 
+def host_cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(workload: str) -> dict:
+    """The oracle on this host's cores, plus what the reference prints about
+    the host (simd.rs:18-27): the CPU model and its AVX-512 detection."""
     O = _load("qora_oracle_py", ROOT / "oracle" / "oracle.py")
+    r = _cpu_baseline(workload, O)
+    r["cpu_model"] = host_cpu_model()
+    r["avx512"] = bool(O.has_avx512())
+    r["host_cores"] = host_cores()
+    return r
+
+
+def _cpu_baseline(workload: str, O) -> dict:
     cores = host_cores()
     att_threads = min(16, cores)
     cfg = O.config()
@@ -938,8 +1020,24 @@ def cpu_baseline(workload: str) -> dict:
                 O.deltanet_decode_step(cfg, w["qkv"][t, 0], w["a"][t, 0], w["b"][t, 0], w["z"][t, 0],
                                        w["conv_w"], w["a_log"], w["dt_bias"], w["norm_w"], S)
         n, dt = _repeat_for(sample)
-        return {"value": n * steps / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
-                "sample": f"{n} x 256 decode steps, batch 1, {avx} head update, 1 thread ({dt:.1f} s)"}
+        res = {"value": n * steps / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
+               "sample": f"{n} x 256 decode steps, batch 1, {avx} head update, 1 thread ({dt:.1f} s)"}
+        # a stronger CPU figure than the reference's serial head loop
+        # (gemv.rs:817): the 32 v-heads of each step over all host cores
+        S2 = w["state0"][0].copy()
+
+        def sample_mt():
+            for t in range(steps):
+                O.deltanet_decode_step(cfg, w["qkv"][t, 0], w["a"][t, 0], w["b"][t, 0], w["z"][t, 0],
+                                       w["conv_w"], w["a_log"], w["dt_bias"], w["norm_w"], S2,
+                                       nthreads=att_threads)
+        n2, dt2 = _repeat_for(sample_mt, min_s=max(CPU_SAMPLE_S / 2, 2.0))
+        res["all_cores_heads_parallel"] = {
+            "value": n2 * steps / dt2, "unit": "tokens/s", "cores": att_threads,
+            "label": "stronger than the reference: its v-head loop (gemv.rs:817) is serial",
+            "sample": f"{n2} x 256 decode steps, v-heads over {att_threads} threads (the host's "
+                      f"CPU share for one GPU), {avx} head update ({dt2:.1f} s)"}
+        return res
     if workload == "dn_prefill":
         T = 1024
         w = W.dn_prefill_workload(T, seed=2)
@@ -1232,6 +1330,13 @@ def sub_config(name: str, workload: str, ctx, with_cpu: bool) -> dict:
     out = {"workload": r["config"]["workload"], "steps": ns.steps, "warmup": ns.warmup,
            "ms": rl["kernel_avg_ms"], "tokens_per_s": r["tokens"] / (r["total_ms"] * 1e-3),
            "roofline": {k: rl[k] for k in ("bound", "achieved", "peak", "unit", "frac", "kernel")}}
+    if "eager_event_ms_per_launch" in r:
+        # the per-launch variant: HIP events around single eager launches
+        # (at batch 1 this includes the host's submission gap between launches)
+        out["eager_ms_per_launch"] = r["eager_event_ms_per_launch"]
+        out["ms_note"] = "ms: graph-replayed steps (warm, working set in L2 / MALL)"
+    if "cold" in r:
+        out["cold"] = r["cold"]
     if with_cpu:
         global CPU_SAMPLE_S
         saved, CPU_SAMPLE_S = CPU_SAMPLE_S, SUB_CPU_SAMPLE_S

@@ -250,10 +250,12 @@ int32_t qm_gqa_decode(qm_context* ctx, qm_stream stream, int32_t batch,
  * a fixed 32 MiB scratch array each GPU holds for the life of the process
  * (batch x 4 x splits <= 8065, i.e. e.g. batch 64 up to ~63K positions at
  * the automatic split size), and a call that needs more is refused with
- * QM_ERR_WORKSPACE before anything is enqueued.  Every call on a GPU, from
- * any context, shares that GPU's array: calls that overlap in time on one
- * GPU (other streams, other contexts or threads) race and must be ordered
- * by the caller. */
+ * QM_ERR_WORKSPACE before anything is enqueued.  The first context that
+ * calls it on a GPU holds that GPU's array until qm_destroy; a call from
+ * any other context on the same GPU is refused with QM_ERR_WORKSPACE, since
+ * two contexts' calls could overlap on the device and race in the array.
+ * Calls from the holding context on different streams share it too: they
+ * must not overlap in time (order them by events or synchronisation). */
 int32_t qm_gqa_decode_noalloc(qm_context* ctx, qm_stream stream, int32_t batch,
                               const float* q_gate_dev, const float* k_new_dev,
                               const float* v_new_dev, const uint16_t* q_norm_dev,

@@ -53,6 +53,8 @@ _SIG = {
     "or_conv1d_step": ([_I32, _I32, _P, _P, _P, _P], None),
     "or_deltanet_decode_step": ([C.POINTER(OrConfig), _P, _I32, _P, _P, _P, _P, _P, _P, _P, _P,
                                  _P, _P, _I32], None),
+    "or_deltanet_decode_step_mt": ([C.POINTER(OrConfig), _P, _I32, _P, _P, _P, _P, _P, _P, _P, _P,
+                                    _P, _P, _I32, _I32], None),
     "or_deltanet_prefill": ([C.POINTER(OrConfig), _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                              _P], None),
     "or_attn_decode_step": ([C.POINTER(OrConfig), _P, _P, _P, _P, _P, _P, _P, _I32, _P, _P, _I32,
@@ -194,8 +196,10 @@ def conv1d_step(conv_buf, conv_w, x):
 
 # ---- layer slices --------------------------------------------------------------
 def deltanet_decode_step(cfg, qkv, a, b, z, conv_w, a_log, dt_bias, norm_w_f16, state,
-                         conv_buf=None, preact=False, kind=UPDATE_AUTO):
-    """gemv.rs:744-883.  state / conv_buf are updated in place; returns out."""
+                         conv_buf=None, preact=False, kind=UPDATE_AUTO, nthreads=1):
+    """gemv.rs:744-883.  state / conv_buf are updated in place; returns out.
+    nthreads > 1 runs the v-head loop in parallel (the reference's loop at
+    gemv.rs:817 is serial); the result does not depend on it."""
     qkv, a, b, z = _f32(qkv), _f32(a), _f32(b), _f32(z)
     conv_w, a_log, dt_bias = _f32(conv_w), _f32(a_log), _f32(dt_bias)
     nw = np.ascontiguousarray(norm_w_f16, np.uint16)
@@ -203,10 +207,11 @@ def deltanet_decode_step(cfg, qkv, a, b, z, conv_w, a_log, dt_bias, norm_w_f16, 
     if preact:
         assert conv_buf is not None and conv_buf.dtype == np.float32 and conv_buf.flags.c_contiguous
     out = np.empty(cfg.num_v_heads * cfg.dn_head_dim, np.float32)
-    lib().or_deltanet_decode_step(C.byref(cfg), qkv.ctypes.data, int(preact), _ptr(conv_buf),
-                                  conv_w.ctypes.data, a.ctypes.data, b.ctypes.data,
-                                  a_log.ctypes.data, dt_bias.ctypes.data, z.ctypes.data,
-                                  nw.ctypes.data, state.ctypes.data, out.ctypes.data, kind)
+    lib().or_deltanet_decode_step_mt(C.byref(cfg), qkv.ctypes.data, int(preact), _ptr(conv_buf),
+                                     conv_w.ctypes.data, a.ctypes.data, b.ctypes.data,
+                                     a_log.ctypes.data, dt_bias.ctypes.data, z.ctypes.data,
+                                     nw.ctypes.data, state.ctypes.data, out.ctypes.data, kind,
+                                     int(nthreads))
     return out
 
 

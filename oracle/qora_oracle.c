@@ -337,7 +337,8 @@ static void deltanet_token(const or_config* cfg, float* act /* [qkv_dim], mutate
                            const float* a, const float* b, const float* a_log,
                            const float* dt_bias, const float* z,
                            const uint16_t* norm_w, float* s, float* out,
-                           int32_t update_kind, float* y /* [v_dim] scratch */) {
+                           int32_t update_kind, float* y /* [v_dim] scratch */,
+                           int32_t nthreads) {
     int32_t num_qk = cfg->num_qk_heads, num_v = cfg->num_v_heads, hd = cfg->dn_head_dim;
     int32_t q_dim = num_qk * hd, k_dim = num_qk * hd;
     int32_t v_per_qk = num_v / num_qk;
@@ -351,6 +352,10 @@ static void deltanet_token(const or_config* cfg, float* act /* [qkv_dim], mutate
         or_l2_normalize(k + (size_t)h * hd, hd);
         for (int32_t j = 0; j < hd; ++j) q[(size_t)h * hd + j] *= scale;
     }
+    /* gemv.rs:817 runs the heads serially; nthreads > 1 runs them in
+     * parallel (each head's arithmetic is unchanged, so the result is too) */
+    if (nthreads < 1) nthreads = 1;
+    #pragma omp parallel for num_threads(nthreads) schedule(static) if(nthreads > 1)
     for (int32_t vh = 0; vh < num_v; ++vh) {
         /* gemv.rs:788-800: alpha = exp(-exp(A_log) * softplus(a + dt_bias)) */
         float a_exp = expf(a_log[vh]);
@@ -372,6 +377,17 @@ void or_deltanet_decode_step(const or_config* cfg, const float* qkv,
                              const float* dt_bias, const float* z,
                              const uint16_t* norm_w, float* s, float* out,
                              int32_t update_kind) {
+    or_deltanet_decode_step_mt(cfg, qkv, preact, conv_buf, conv_w, a, b, a_log, dt_bias, z,
+                               norm_w, s, out, update_kind, 1);
+}
+
+void or_deltanet_decode_step_mt(const or_config* cfg, const float* qkv,
+                                int32_t preact, float* conv_buf,
+                                const float* conv_w, const float* a,
+                                const float* b, const float* a_log,
+                                const float* dt_bias, const float* z,
+                                const uint16_t* norm_w, float* s, float* out,
+                                int32_t update_kind, int32_t nthreads) {
     int32_t hd = cfg->dn_head_dim;
     int32_t qkv_dim = (2 * cfg->num_qk_heads + cfg->num_v_heads) * hd;
     int32_t v_dim = cfg->num_v_heads * hd;
@@ -383,7 +399,7 @@ void or_deltanet_decode_step(const or_config* cfg, const float* qkv,
     } else {
         memcpy(act, qkv, sizeof(float) * (size_t)qkv_dim);
     }
-    deltanet_token(cfg, act, a, b, a_log, dt_bias, z, norm_w, s, out, update_kind, y);
+    deltanet_token(cfg, act, a, b, a_log, dt_bias, z, norm_w, s, out, update_kind, y, nthreads);
     free(act);
     free(y);
 }
@@ -407,7 +423,7 @@ void or_deltanet_prefill(const or_config* cfg, int32_t T,
         for (int32_t i = 0; i < qkv_dim; ++i) act[i] = or_silu(act[i]);
         deltanet_token(cfg, act, a_all + (size_t)t * num_v, b_all + (size_t)t * num_v,
                        a_log, dt_bias, z_all + (size_t)t * v_dim, norm_w, s,
-                       out_all + (size_t)t * v_dim, OR_UPDATE_SCALAR, y);
+                       out_all + (size_t)t * v_dim, OR_UPDATE_SCALAR, y, 1);
     }
     free(act);
     free(y);

@@ -107,6 +107,15 @@ void or_deltanet_decode_step(const or_config* cfg, const float* qkv,
                              const float* dt_bias, const float* z,
                              const uint16_t* norm_w, float* s, float* out,
                              int32_t update_kind);
+/* The same step with the v-head loop split over nthreads OpenMP threads
+ * (the reference runs it serially, gemv.rs:817); results are identical. */
+void or_deltanet_decode_step_mt(const or_config* cfg, const float* qkv,
+                                int32_t preact, float* conv_buf,
+                                const float* conv_w, const float* a,
+                                const float* b, const float* a_log,
+                                const float* dt_bias, const float* z,
+                                const uint16_t* norm_w, float* s, float* out,
+                                int32_t update_kind, int32_t nthreads);
 
 /* --- DeltaNet mixer slice: sequential prefill (gemv.rs:1119-1219) ----- */
 /* qkv_all [T][qkv_dim] raw projections, a_all/b_all [T][num_v],

@@ -17,6 +17,11 @@ extern "C" {
 // The device address of `device`'s copy of the scratch array, resolved once
 // per device with that device current and cached; returns a hipError_t.
 __attribute__((visibility("hidden"))) int qm_noalloc_scratch(int device, void** ptr);
+// Records `owner` (a context) as the one user of `device`'s scratch: 0 if it
+// is free or already owned by `owner`, nonzero if another context holds it.
+__attribute__((visibility("hidden"))) int qm_noalloc_claim(int device, const void* owner);
+// Releases `device`'s scratch if `owner` holds it.
+__attribute__((visibility("hidden"))) void qm_noalloc_release(int device, const void* owner);
 #ifdef __cplusplus
 }
 #endif

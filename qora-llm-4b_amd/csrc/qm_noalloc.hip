@@ -20,7 +20,22 @@ static __device__ __align__(256) unsigned char scratch[QM_NOALLOC_SCRATCH_BYTES]
 namespace {
 std::mutex g_mu;
 void* g_ptr[QM_NOALLOC_MAX_DEVICES] = {};
+const void* g_owner[QM_NOALLOC_MAX_DEVICES] = {};
 }  // namespace
+
+extern "C" int qm_noalloc_claim(int device, const void* owner) {
+    if (device < 0 || device >= QM_NOALLOC_MAX_DEVICES || !owner) return 1;
+    std::lock_guard<std::mutex> lock(g_mu);
+    if (g_owner[device] && g_owner[device] != owner) return 1;
+    g_owner[device] = owner;
+    return 0;
+}
+
+extern "C" void qm_noalloc_release(int device, const void* owner) {
+    if (device < 0 || device >= QM_NOALLOC_MAX_DEVICES) return;
+    std::lock_guard<std::mutex> lock(g_mu);
+    if (g_owner[device] == owner) g_owner[device] = nullptr;
+}
 
 extern "C" int qm_noalloc_scratch(int device, void** ptr) {
     if (!ptr || device < 0 || device >= QM_NOALLOC_MAX_DEVICES) return static_cast<int>(hipErrorInvalidValue);

@@ -68,19 +68,33 @@ struct qm_context {
     int q4_hidden_threads = 0, q4_inter_threads = 0;
     void* ws = nullptr;            // general workspace
     size_t ws_bytes = 0;
-    // Workspaces replaced by a larger one.  A graph captured earlier holds
-    // their addresses in its kernel arguments, so they stay allocated until
-    // qm_destroy.
+    // whether a call that used `ws` ran under stream capture: a graph may
+    // then hold its address in kernel arguments
+    bool ws_captured = false;
+    // Workspaces replaced by a larger one after a capture had used them.  A
+    // graph captured earlier holds their addresses in its kernel arguments,
+    // so they stay allocated until qm_destroy.
     std::vector<void*> retired_ws;
     std::string err;
     int64_t opt_dn_threads = 0;
     int64_t opt_gqa_chunk = 0;
     int64_t opt_gqp_order = 0;
-    // the GQA prefill attention's last queue order: for seq_len gqp_S over
-    // gqp_bins workgroups per kv group (ordered = 0: longest first)
-    int32_t gqp_S = -1, gqp_bins = -1;
-    int64_t gqp_mode = -1;
+    // the GQA prefill attention's queue orders of the last few sequence
+    // lengths (a plan costs 0.1-2.7 ms on the host), least recently used
+    // evicted; each entry is for seq_len S over `bins` workgroups per kv
+    // group under order option `mode` (ordered = 0: longest first)
+    struct GqpPlan {
+        int32_t S = -1, bins = -1;
+        int64_t mode = -1;
+        uint64_t used = 0;
+        int32_t ordered = 0;
+        uint16_t order[QM_GQA_PREFILL_ORDER_MAX];
+    };
+    static constexpr int kGqpPlans = 8;
+    GqpPlan gqp_plans[kGqpPlans];
+    uint64_t gqp_clock = 0;
     GqaPrefillAttnArgs gqp_args{};
+    bool noalloc_owner = false;    // this context holds its device's no-alloc scratch
     int num_cu = 0;                // compute units of the device
     // this device's copy of the fixed scratch array of the allocation-free
     // entry point (qm_noalloc.hip), resolved at qm_create; null if that failed
@@ -138,25 +152,38 @@ bool capturing(hipStream_t s) {
     return st != hipStreamCaptureStatusNone;
 }
 
-// Grow the workspace.  Growth is refused while the stream is being captured.
-// The old buffer is retired, not freed: graphs captured from earlier calls
-// keep its address in their kernel arguments and may be replayed later.
-// Growth is geometric (at least 1.5x) so that callers who never call
-// qm_reserve retire O(log) buffers, not one per KV-length step.
-int32_t ensure(qm_context* c, hipStream_t s, size_t ws_bytes) {
+// Grow the workspace (every call that uses it comes through here first).
+// Growth is refused while the stream is being captured.  If a capture has
+// used the old buffer, it is retired, not freed: the graph keeps its address
+// in kernel arguments and may be replayed later.  Otherwise it is freed once
+// the device has finished the work queued on it.  Growth on demand is
+// geometric (at least 1.5x) so that callers who never call qm_reserve grow
+// O(log) times, not once per KV-length step; qm_reserve asks for its exact
+// size.
+int32_t ensure(qm_context* c, hipStream_t s, size_t ws_bytes, bool exact = false) {
+    const bool cap = capturing(s);
+    if (cap) c->ws_captured = true;
     if (ws_bytes <= c->ws_bytes) return QM_OK;
-    if (capturing(s))
+    if (cap)
         return fail(c, QM_ERR_WORKSPACE,
                     "workspace must grow to %zu bytes during graph capture; "
                     "call qm_reserve() before capturing", ws_bytes);
     size_t want = ws_bytes;
-    if (c->ws_bytes > 0) want = std::max(want, c->ws_bytes + c->ws_bytes / 2);
+    if (c->ws_bytes > 0 && !exact) want = std::max(want, c->ws_bytes + c->ws_bytes / 2);
     want = (want + 4095) & ~static_cast<size_t>(4095);
+    if (c->ws && !c->ws_captured) {
+        // queued kernels on any stream may still read it
+        QM_HIP(c, hipDeviceSynchronize());
+        QM_HIP(c, hipFree(c->ws));
+        c->ws = nullptr;
+        c->ws_bytes = 0;
+    }
     void* fresh = nullptr;
     QM_HIP(c, hipMalloc(&fresh, want));
     if (c->ws) c->retired_ws.push_back(c->ws);
     c->ws = fresh;
     c->ws_bytes = want;
+    c->ws_captured = false;
     return QM_OK;
 }
 
@@ -382,6 +409,7 @@ int32_t qm_destroy(qm_context* c) {
     hipDeviceSynchronize();
     if (c->ws) hipFree(c->ws);
     for (void* p : c->retired_ws) hipFree(p);
+    if (c->noalloc_owner) qm_noalloc_release(c->device, c);
     if (c->stream) hipStreamDestroy(c->stream);
     for (hipModule_t m : c->modules) hipModuleUnload(m);
     delete c;
@@ -674,6 +702,16 @@ int32_t gqa_decode_impl(qm_context* c, qm_stream stream, int32_t batch, const fl
                         "partials; the fixed scratch holds %u (batch x 4 x splits <= %u)",
                         static_cast<long long>(nsplit), static_cast<long long>(chunk), batch, part_bytes,
                         QM_NOALLOC_SCRATCH_BYTES, QM_NOALLOC_SCRATCH_BYTES / (4 * 260 * 4));
+        if (!c->noalloc_owner) {
+            // one context per GPU may use the scratch: calls from two
+            // contexts could overlap on the device and race in it
+            const int e = qm_noalloc_claim(c->device, c);
+            if (e != 0)
+                return fail(c, QM_ERR_WORKSPACE,
+                            "qm_gqa_decode_noalloc: the fixed scratch of device %d is held by another context "
+                            "(calls from two contexts could overlap and race in it)", c->device);
+            c->noalloc_owner = true;
+        }
         partials = static_cast<float*>(c->noalloc_scratch);
     } else {
         const int32_t st = ensure(c, s, part_bytes);
@@ -740,7 +778,7 @@ int32_t qm_reserve(qm_context* c, int32_t max_batch, int32_t max_kv_len, int32_t
         ws = std::max(ws, gqa_prefill_kvf_bytes(s_pad) + 256);
     }
     ws = std::max(ws, kSampleWsBytes);
-    return ensure(c, c->stream, ws);
+    return ensure(c, c->stream, ws, true);
 }
 
 // ---- DeltaNet chunked prefill --------------------------------------------------------
@@ -806,12 +844,22 @@ int32_t qm_gqa_prefill(qm_context* c, qm_stream stream, int32_t seq_len, const u
     // more than there are 48-row blocks
     const int32_t nblk = (seq_len + 47) / 48;
     const int32_t per_group = std::max(1, std::min(c->num_cu / QM_GQA_KV_HEADS, nblk));
-    if (c->gqp_S != seq_len || c->gqp_bins != per_group || c->gqp_mode != c->opt_gqp_order) {
-        c->gqp_args.ordered = qm_plan::gqp_set_order(c->gqp_args.order, seq_len, per_group, c->opt_gqp_order);
-        c->gqp_S = seq_len;
-        c->gqp_bins = per_group;
-        c->gqp_mode = c->opt_gqp_order;
+    qm_context::GqpPlan* plan = nullptr;
+    for (auto& p : c->gqp_plans)
+        if (p.S == seq_len && p.bins == per_group && p.mode == c->opt_gqp_order) plan = &p;
+    if (!plan) {
+        plan = &c->gqp_plans[0];
+        for (auto& p : c->gqp_plans)
+            if (p.used < plan->used) plan = &p;
+        plan->ordered = qm_plan::gqp_set_order(plan->order, seq_len, per_group, c->opt_gqp_order);
+        plan->S = seq_len;
+        plan->bins = per_group;
+        plan->mode = c->opt_gqp_order;
     }
+    plan->used = ++c->gqp_clock;
+    c->gqp_args.ordered = plan->ordered;
+    if (plan->ordered)
+        std::memcpy(c->gqp_args.order, plan->order, sizeof(uint16_t) * static_cast<size_t>((seq_len + 47) / 48));
     c->gqp_args.a = ga;
     return launch(c, c->f_gqp_attn, static_cast<uint32_t>(per_group) * QM_GQA_KV_HEADS, 768, c->gqp_args,
                   s, "qm_gqa_prefill_attn");

@@ -365,18 +365,42 @@ pub struct AttnMixerDev {
     pub k_norm: *const u16,
 }
 
+/// A length or position that does not fit the C ABI's 32-bit integers
+/// becomes an error instead of wrapping.
+fn to_i32(what: &str, v: usize) -> Result<i32> {
+    i32::try_from(v).map_err(|_| MixerError {
+        code: raw::QM_ERR_INVALID_ARG,
+        message: format!("{} = {} does not fit in a 32-bit signed integer", what, v),
+    })
+}
+
+fn to_i64(what: &str, v: usize) -> Result<i64> {
+    i64::try_from(v).map_err(|_| MixerError {
+        code: raw::QM_ERR_INVALID_ARG,
+        message: format!("{} = {} does not fit in a 64-bit signed integer", what, v),
+    })
+}
+
 /// Mixer slice of `forward_deltanet_decode_gpu` (`gpu_inference.rs:149-227`):
 /// `qkv` is the raw in_proj_qkv output (conv1d + SiLU run here and the conv
 /// buffer shifts), `a`, `b`, `z` the other input projections; `out` [4096]
 /// receives the gated output, the out_proj input.  One sequence.
-pub fn deltanet_decode(ctx: &Context, stream: qm_stream, qkv: *const f32, a: *const f32, b: *const f32,
-                       z: *const f32, layer: &DeltaNetMixerDev, state: &mut DeltaNetStateDev,
-                       out: *mut f32) -> Result<()> {
-    ctx.check(unsafe {
-        raw::qm_deltanet_decode(ctx.raw, stream, 1, raw::QM_DN_PREACT, qkv, state.conv_buf, layer.conv1d_weight,
-                                a, b, layer.a_log, layer.dt_bias, z, layer.attn_norm_weight, state.s,
-                                32 * 128 * 128, out)
-    })?;
+///
+/// # Safety
+/// Every pointer (the arguments and the fields of `layer` and `state`) must
+/// be a device address of this context's GPU, 16-byte aligned, valid for the
+/// whole launch and sized as stated: `qkv` f32 [8192], `a` / `b` f32 [32],
+/// `z` f32 [4096], `out` f32 [4096], `state.s` f32 [32][128][128],
+/// `state.conv_buf` f32 [8192][3], and the layer parameters as
+/// `DeltaNetMixerDev` documents.  The kernels read and write through them
+/// without further checks; the library only rejects null and misaligned
+/// pointers.
+pub unsafe fn deltanet_decode(ctx: &Context, stream: qm_stream, qkv: *const f32, a: *const f32, b: *const f32,
+                              z: *const f32, layer: &DeltaNetMixerDev, state: &mut DeltaNetStateDev,
+                              out: *mut f32) -> Result<()> {
+    ctx.check(raw::qm_deltanet_decode(ctx.raw, stream, 1, raw::QM_DN_PREACT, qkv, state.conv_buf,
+                                      layer.conv1d_weight, a, b, layer.a_log, layer.dt_bias, z,
+                                      layer.attn_norm_weight, state.s, 32 * 128 * 128, out))?;
     state.conv_pos += 1;
     Ok(())
 }
@@ -384,13 +408,22 @@ pub fn deltanet_decode(ctx: &Context, stream: qm_stream, qkv: *const f32, a: *co
 /// Mixer slice of `forward_attn_decode_gpu` (`gpu_inference.rs:271-349`):
 /// q/gate interleaved per head [16][512], k and v [4][256] of the new
 /// token; appends at `kv.seq_len` and advances it (`gemv.rs:952-956`).
-pub fn attn_decode(ctx: &Context, stream: qm_stream, q_gate: *const f32, k_new: *const f32, v_new: *const f32,
-                   layer: &AttnMixerDev, kv: &mut KvCacheDev, rope_cos: *const f32, rope_sin: *const f32,
-                   rope_len: i32, out: *mut f32) -> Result<()> {
-    ctx.check(unsafe {
-        raw::qm_gqa_decode(ctx.raw, stream, 1, q_gate, k_new, v_new, layer.q_norm, layer.k_norm, rope_cos,
-                           rope_sin, rope_len, ptr::null(), kv.seq_len as i32, kv.k, kv.v, kv.capacity as i64, out)
-    })?;
+///
+/// # Safety
+/// Every pointer must be a device address of this context's GPU, 16-byte
+/// aligned and valid for the launch: `q_gate` f32 [16][512], `k_new` /
+/// `v_new` f32 [4][256], `out` f32 [16][256], `rope_cos` / `rope_sin` f32
+/// [rope_len][32], `layer`'s norms f16 [256], and `kv.k` / `kv.v` f16
+/// [4][kv.capacity][256].  The library checks `kv.seq_len < kv.capacity`
+/// and `kv.seq_len < rope_len`, not the sizes behind the pointers.
+pub unsafe fn attn_decode(ctx: &Context, stream: qm_stream, q_gate: *const f32, k_new: *const f32,
+                          v_new: *const f32, layer: &AttnMixerDev, kv: &mut KvCacheDev, rope_cos: *const f32,
+                          rope_sin: *const f32, rope_len: usize, out: *mut f32) -> Result<()> {
+    let pos = to_i32("kv.seq_len", kv.seq_len)?;
+    let cap = to_i64("kv.capacity", kv.capacity)?;
+    let rl = to_i32("rope_len", rope_len)?;
+    ctx.check(raw::qm_gqa_decode(ctx.raw, stream, 1, q_gate, k_new, v_new, layer.q_norm, layer.k_norm, rope_cos,
+                                 rope_sin, rl, ptr::null(), pos, kv.k, kv.v, cap, out))?;
     kv.seq_len += 1;
     Ok(())
 }
@@ -399,36 +432,55 @@ pub fn attn_decode(ctx: &Context, stream: qm_stream, q_gate: *const f32, k_new: 
 /// `seq_len` tokens of bf16 in_proj_qkv / in_proj_z outputs, f32 a / b, in
 /// chunks of 64; the state and conv buffer continue from where they are;
 /// `out` bf16 [seq_len][4096].
-pub fn deltanet_prefill(ctx: &Context, stream: qm_stream, seq_len: usize, qkv_bf16: *const u16, a: *const f32,
-                        b: *const f32, z_bf16: *const u16, layer: &DeltaNetMixerDev,
-                        state: &mut DeltaNetStateDev, out_bf16: *mut u16) -> Result<()> {
-    ctx.check(unsafe {
-        raw::qm_deltanet_prefill(ctx.raw, stream, seq_len as i32, qkv_bf16, state.conv_buf, layer.conv1d_weight,
-                                 a, b, layer.a_log, layer.dt_bias, z_bf16, layer.attn_norm_weight, state.s,
-                                 out_bf16)
-    })?;
+///
+/// # Safety
+/// Every pointer must be a device address of this context's GPU, 16-byte
+/// aligned and valid for the launch: `qkv_bf16` [seq_len][8192], `a` / `b`
+/// f32 [seq_len][32], `z_bf16` [seq_len][4096], `out_bf16` [seq_len][4096],
+/// and `state` / `layer` as for `deltanet_decode`.
+pub unsafe fn deltanet_prefill(ctx: &Context, stream: qm_stream, seq_len: usize, qkv_bf16: *const u16,
+                               a: *const f32, b: *const f32, z_bf16: *const u16, layer: &DeltaNetMixerDev,
+                               state: &mut DeltaNetStateDev, out_bf16: *mut u16) -> Result<()> {
+    let t = to_i32("seq_len", seq_len)?;
+    ctx.check(raw::qm_deltanet_prefill(ctx.raw, stream, t, qkv_bf16, state.conv_buf, layer.conv1d_weight, a, b,
+                                       layer.a_log, layer.dt_bias, z_bf16, layer.attn_norm_weight, state.s,
+                                       out_bf16))?;
     state.conv_pos += seq_len;
     Ok(())
 }
 
 /// Mixer slice of `prefill_attn_layer_gpu` (`gpu_inference.rs:679-766`): the
 /// cache is replaced by positions 0 .. seq_len-1 (`gemv.rs:1397-1400`).
-pub fn attn_prefill(ctx: &Context, stream: qm_stream, seq_len: usize, q_gate_bf16: *const u16, k_bf16: *const u16,
-                    v_bf16: *const u16, layer: &AttnMixerDev, kv: &mut KvCacheDev, rope_cos: *const f32,
-                    rope_sin: *const f32, rope_len: i32, out_bf16: *mut u16) -> Result<()> {
-    ctx.check(unsafe {
-        raw::qm_gqa_prefill(ctx.raw, stream, seq_len as i32, q_gate_bf16, k_bf16, v_bf16, layer.q_norm,
-                            layer.k_norm, rope_cos, rope_sin, rope_len, kv.k, kv.v, kv.capacity as i64, out_bf16)
-    })?;
+///
+/// # Safety
+/// Every pointer must be a device address of this context's GPU, 16-byte
+/// aligned and valid for the launch: `q_gate_bf16` [seq_len][16][512],
+/// `k_bf16` / `v_bf16` [seq_len][4][256], `out_bf16` [seq_len][16][256],
+/// `rope_cos` / `rope_sin` f32 [rope_len][32], `layer`'s norms f16 [256],
+/// and `kv.k` / `kv.v` f16 [4][kv.capacity][256].  The library checks
+/// `seq_len <= kv.capacity` and `seq_len <= rope_len`, not the sizes behind
+/// the pointers.
+pub unsafe fn attn_prefill(ctx: &Context, stream: qm_stream, seq_len: usize, q_gate_bf16: *const u16,
+                           k_bf16: *const u16, v_bf16: *const u16, layer: &AttnMixerDev, kv: &mut KvCacheDev,
+                           rope_cos: *const f32, rope_sin: *const f32, rope_len: usize, out_bf16: *mut u16)
+                           -> Result<()> {
+    let t = to_i32("seq_len", seq_len)?;
+    let cap = to_i64("kv.capacity", kv.capacity)?;
+    let rl = to_i32("rope_len", rope_len)?;
+    ctx.check(raw::qm_gqa_prefill(ctx.raw, stream, t, q_gate_bf16, k_bf16, v_bf16, layer.q_norm, layer.k_norm,
+                                  rope_cos, rope_sin, rl, kv.k, kv.v, cap, out_bf16))?;
     kv.seq_len = seq_len;
     Ok(())
 }
 
 /// RoPE tables [max_pos][32] with the formula of `convert.rs:161-176`.
-pub fn rope_table(max_pos: usize) -> (Vec<f32>, Vec<f32>) {
+pub fn rope_table(max_pos: usize) -> Result<(Vec<f32>, Vec<f32>)> {
+    let n = to_i32("max_pos", max_pos)?;
     let mut cos = vec![0.0f32; max_pos * 32];
     let mut sin = vec![0.0f32; max_pos * 32];
-    let st = unsafe { raw::qm_rope_table(1.0e7, 64, max_pos as i32, cos.as_mut_ptr(), sin.as_mut_ptr()) };
-    assert_eq!(st, raw::QM_OK, "qm_rope_table");
-    (cos, sin)
+    let st = unsafe { raw::qm_rope_table(1.0e7, 64, n, cos.as_mut_ptr(), sin.as_mut_ptr()) };
+    if st != raw::QM_OK {
+        return Err(MixerError { code: st, message: "qm_rope_table".to_string() });
+    }
+    Ok((cos, sin))
 }

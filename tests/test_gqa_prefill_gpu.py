@@ -167,12 +167,15 @@ def test_prefill_value_outliers(ctx, scale):
     check(o, K, V, ref, kc, vc, np.arange(S))
 
 
-def test_prefill_graph_replay_matches_eager(ctx):
+@pytest.mark.parametrize("S,order", [(2000, 0), (8192, 2)])
+def test_prefill_graph_replay_matches_eager(ctx, S, order):
     """A captured prefill (K/V kernel, which resets the row-block queues, then
     the persistent attention) replayed several times, with eager prefills and
     synchronisations in between, matches the eager output bit for bit: which
-    workgroup takes which row block does not change the arithmetic."""
-    S = 2000
+    workgroup takes which row block does not change the arithmetic.  At 8192
+    tokens the packed order travels in the captured kernel arguments, and
+    the eager prefills in between run another length (another plan), which
+    must not disturb the captured one."""
     w = W.gqa_prefill_workload(S, seed=17)
     cos, sin = M.rope_table(S)
     d = {k: ctx.upload(w[k]) for k in ["q_gate", "k", "v", "q_norm", "k_norm"]}
@@ -180,21 +183,27 @@ def test_prefill_graph_replay_matches_eager(ctx):
     kc, vc = ctx.alloc(4 * S * 256 * 2), ctx.alloc(4 * S * 256 * 2)
     out_e, out_g = ctx.alloc(S * 16 * 256 * 2), ctx.alloc(S * 16 * 256 * 2)
     ctx.reserve(max_batch=1, max_prefill_tokens=S)
+    other = S - 1000                      # the eager length run between replays
 
-    def run(out):
-        ctx.gqa_prefill(S, d["q_gate"], d["k"], d["v"], d["q_norm"], d["k_norm"], rc, rs, S, kc, vc, S, out)
+    def run(out, n=S):
+        ctx.gqa_prefill(n, d["q_gate"], d["k"], d["v"], d["q_norm"], d["k_norm"], rc, rs, S, kc, vc, S, out)
 
-    print("case: gqa prefill graph replay (eager reference)", flush=True)
-    run(out_e)
-    ref = ctx.download(out_e, (S, 16 * 256), np.uint16)
-    ctx.graph_begin()
-    run(out_g)
-    g = ctx.graph_end()
-    for rep in range(3):
-        print(f"case: gqa prefill graph replay {rep}", flush=True)
-        ctx.fill_normal(out_g, M.QM_BF16, S * 16 * 256, 0.0, 1.0, seed=rep)   # poison between replays
-        g.launch()
-        ctx.sync()
-        assert np.array_equal(ctx.download(out_g, (S, 16 * 256), np.uint16), ref)
-        run(out_e)                                                           # eager work in between
-        ctx.sync()
+    ctx.set_option(M.QM_OPT_GQA_PREFILL_ORDER, order)
+    try:
+        print(f"case: gqa prefill graph replay S={S} order={order} (eager reference)", flush=True)
+        run(out_e)
+        ref = ctx.download(out_e, (S, 16 * 256), np.uint16)
+        ctx.graph_begin()
+        run(out_g)
+        g = ctx.graph_end()
+        for rep in range(3):
+            print(f"case: gqa prefill graph replay S={S} order={order} rep {rep}", flush=True)
+            ctx.fill_normal(out_g, M.QM_BF16, S * 16 * 256, 0.0, 1.0, seed=rep)   # poison between replays
+            g.launch()
+            ctx.sync()
+            assert np.array_equal(ctx.download(out_g, (S, 16 * 256), np.uint16), ref)
+            run(out_e, other)                                                # eager work in between
+            ctx.sync()
+        g.close()
+    finally:
+        ctx.set_option(M.QM_OPT_GQA_PREFILL_ORDER, 0)

@@ -319,6 +319,31 @@ def test_deltanet_decode_gva_map_is_consecutive():
     assert np.all(o[2:] == 0.0) and np.all(np.abs(o[:2]).sum(1) > 0)
 
 
+def test_deltanet_decode_heads_parallel_equals_serial():
+    """The v-head loop split over threads (the CPU baseline's all-cores
+    variant) gives the serial loop's state and output bit for bit, at the
+    full dimensions with a conv step."""
+    cfg = O.config()
+    rng = np.random.default_rng(77)
+    qkv = rng.standard_normal(8192).astype(np.float32)
+    a, b = rng.standard_normal(32).astype(np.float32), rng.standard_normal(32).astype(np.float32)
+    z = rng.standard_normal(4096).astype(np.float32)
+    conv_w = (0.5 * rng.standard_normal((8192, 4))).astype(np.float32)
+    a_log = np.log(rng.uniform(0.01, 0.1, 32)).astype(np.float32)
+    dt_bias = np.zeros(32, np.float32)
+    nw = O.f16_bits(1.0 + 0.1 * rng.standard_normal(128))
+    S0 = (0.02 * rng.standard_normal((32, 128, 128))).astype(np.float32)
+    buf0 = rng.standard_normal((8192, 3)).astype(np.float32)
+    res = []
+    for nt in (1, 4):
+        S, buf = S0.copy(), buf0.copy()
+        out = O.deltanet_decode_step(cfg, qkv, a, b, z, conv_w, a_log, dt_bias, nw, S,
+                                     conv_buf=buf, preact=True, nthreads=nt)
+        res.append((out, S, buf))
+    for x, y in zip(res[0], res[1]):
+        assert np.array_equal(x, y)
+
+
 def test_deltanet_prefill_equals_decode_steps():
     """The sequential prefill (gemv.rs:1119-1219) is T scalar decode steps, bit for bit."""
     cfg = _tiny_cfg()

@@ -122,3 +122,18 @@ def test_build_script_follows_the_python_recipe():
         assert needed in rs, needed
     cargo = (CRATE / "Cargo.toml").read_text()
     assert 'links = "qora_mixer"' in cargo and 'build = "build.rs"' in cargo
+
+
+def test_layer_wrappers_are_unsafe_and_check_lengths():
+    """The layer-forward wrappers hand raw device pointers to kernels, so
+    they are `unsafe fn` with a `# Safety` section; lengths reach the C ABI
+    through checked conversions (an oversized usize is an error, not a
+    wrapped i32)."""
+    text = (CRATE / "src" / "lib.rs").read_text()
+    for fn in ("deltanet_decode", "attn_decode", "deltanet_prefill", "attn_prefill"):
+        m = re.search(r"((?:///[^\n]*\n)+)pub (unsafe )?fn " + fn + r"\(", text)
+        assert m and m.group(2), fn
+        assert "# Safety" in m.group(1), fn
+    body = text[text.index("pub use raw::"):]
+    assert not re.search(r"\bas i32\b", body), "narrowing cast outside the raw declarations"
+    assert "i32::try_from" in body and "i64::try_from" in body

@@ -87,3 +87,71 @@ def test_noalloc_refuses_partials_beyond_the_scratch():
             assert e.value.code == 9          # QM_ERR_WORKSPACE
         finally:
             c.set_option(M.QM_OPT_GQA_DECODE_CHUNK, 0)
+
+
+def test_noalloc_scratch_is_held_by_one_context_per_gpu():
+    """A second context on the same GPU is refused while the first holds the
+    scratch (their calls could overlap and race), and may use it once the
+    first is destroyed."""
+    w = W.gqa_decode_workload(300, 1, seed=24)
+    cos, sin = M.rope_table(301)
+
+    def call(c):
+        keys = ["q_gate", "k_new", "v_new", "q_norm", "k_norm", "k_cache", "v_cache"]
+        d = {k: c.upload(w[k]) for k in keys}
+        rc, rs = c.upload(cos), c.upload(sin)
+        out = c.alloc(16 * 256 * 4)
+        c.gqa_decode_noalloc(1, d["q_gate"], d["k_new"], d["v_new"], d["q_norm"], d["k_norm"], rc, rs, 301, None,
+                             300, d["k_cache"], d["v_cache"], w["cap"], out)
+        c.sync()
+        return c.download(out, (16, 256), np.float32)
+
+    print("case: gqa decode noalloc, two contexts on one GPU", flush=True)
+    a = M.Context(0)
+    b = M.Context(0)
+    try:
+        ra = call(a)
+        with pytest.raises(M.MixerError) as e:
+            call(b)
+        assert e.value.code == 9          # QM_ERR_WORKSPACE
+        ra2 = call(a)                     # the holder keeps working
+        assert np.array_equal(ra, ra2)
+    finally:
+        a.close()
+    try:
+        assert np.array_equal(call(b), ra)
+    finally:
+        b.close()
+
+
+def test_noalloc_captured_without_reserve_replays_like_eager():
+    """Captured into a HIP graph on a fresh context that never called
+    qm_reserve (the callers this entry is for), the replays equal the eager
+    call bit for bit, with eager work and synchronisation between them."""
+    with M.Context(0) as c:
+        print("case: gqa decode noalloc captured on an unreserved context, B=2 pos=2000", flush=True)
+        w = W.gqa_decode_workload(2000, 2, seed=25)
+        cos, sin = M.rope_table(2001)
+        keys = ["q_gate", "k_new", "v_new", "q_norm", "k_norm", "k_cache", "v_cache"]
+        d = {k: c.upload(w[k]) for k in keys}
+        rc, rs = c.upload(cos), c.upload(sin)
+        out = c.alloc(2 * 16 * 256 * 4)
+
+        def call():
+            c.gqa_decode_noalloc(2, d["q_gate"], d["k_new"], d["v_new"], d["q_norm"], d["k_norm"], rc, rs, 2001,
+                                 None, 2000, d["k_cache"], d["v_cache"], w["cap"], out)
+
+        c.graph_begin()
+        call()
+        g = c.graph_end()
+        call()
+        c.sync()
+        ref = c.download(out, (2, 16, 256), np.float32)
+        for rep in range(4):
+            c.fill_normal(out, M.QM_F32, 2 * 16 * 256, 0.0, 1.0, seed=rep)
+            c.upload(w["q_gate"], d["q_gate"])      # eager work between the replays
+            c.sync()
+            g.launch()
+            c.sync()
+            assert np.array_equal(c.download(out, (2, 16, 256), np.float32), ref), rep
+        g.close()
