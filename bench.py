@@ -1432,7 +1432,8 @@ def main():
     }
     if args.workload == "stack":
         line["roofline"].update(stored_traffic(GQA_DECODE_SOURCES))
-    for k in ("kernels", "step_frac_hbm", "graph_ms_per_step", "graph_step_frac_hbm", "eager_ms_per_step"):
+    for k in ("kernels", "step_frac_hbm", "graph_ms_per_step", "graph_step_frac_hbm", "eager_ms_per_step",
+              "eager_event_ms_per_launch", "cold"):
         if k in r:
             line[k] = r[k]
     if not args.no_cpu_baseline:
