@@ -43,6 +43,11 @@ QM_DEV half8 cat8(half4 a, half4 b) {
     return half8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
+// largest magnitude of four values (what an f16 conversion must hold)
+QM_DEV float max4abs(floatx4 v) {
+    return fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+}
+
 QM_DEV half4 to_half4(floatx4 v) {
     half4 r;
     r[0] = (_Float16)v[0]; r[1] = (_Float16)v[1]; r[2] = (_Float16)v[2]; r[3] = (_Float16)v[3];
@@ -76,6 +81,8 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
     __shared__ _Float16 Qs[CHK][136];              // q row-major (both v-heads)
     __shared__ _Float16 Ks[CHK][136];              // k row-major (both v-heads)
     __shared__ ChunkHeadLds hl[2];
+    __shared__ float vred[2][4][QM_DN_HD];         // per head and wave: max |v| per channel
+    __shared__ int vbad[2];                        // per head: an f16 operand would overflow
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int hh = tid >> 8;                       // v-head of the pair: waves 0-3 / 4-7
@@ -97,6 +104,10 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
     float (&Eg)[CHK] = H.Eg;
     float (&BG)[CHK] = H.BG;
     float (&Kd)[CHK] = H.Kd;
+    // largest magnitude this thread converts to an f16 operand on the v side
+    // or in the solve (q, k, A, P and K~ are bounded by the normalisation)
+    float om = 0.0f;
+    if (ht == 0) vbad[hh] = 0;
 
     // ---- 0. causal conv1d (gemv.rs:1132-1147), SiLU (:1149), per-head L2
     //      norm and q scale (:1151-1156) of this chunk's q, k (qk-head qkh,
@@ -134,6 +145,9 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
 #pragma unroll
         for (int e = 0; e < 8; ++e) wt[e] = ld4(A.conv_w + (size_t)(chb[0] + e) * 4);
         const bool tail = t0 + CHK > A.T;          // last chunk, partly past the sequence
+        float vm[8];                               // max |v| per channel over this thread's valid tokens
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vm[e] = 0.0f;
 #pragma unroll
         for (int part = 0; part < 2; ++part) {     // q or k, then v
             const int ch0 = chb[part];
@@ -180,6 +194,11 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
                     sacc = fmaf(x[j + 3][e], wt[e].w, sacc);
                     v[e] = silu_fast(sacc);
                 }
+                if (part == 1) {
+                    const bool ok = t0 + tok < A.T;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) vm[e] = fmaxf(vm[e], ok ? fabsf(v[e]) : 0.0f);
+                }
                 if (part == 0) {
                     // x /= ||x|| when ||x|| > 1e-12, q *= 1/sqrt(128)
                     float ss = 0.0f;
@@ -197,6 +216,16 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
             }
 #pragma unroll
             for (int e = 0; e < 8; ++e) wt[e] = wn[e];
+        }
+        // lanes cg, cg+16, cg+32, cg+48 of a wave hold the same channels
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            vm[e] = max_xor32(max_xor16(vm[e]));
+            om = fmaxf(om, vm[e]);
+        }
+        if ((lane >> 4) == 0) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) vred[hh][w][8 * cg + e] = vm[e];
         }
         if (tail) {
             // Tokens past the sequence read clamped rows above; their rows
@@ -285,6 +314,7 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
 #pragma unroll
             for (int j = 0; j < i; ++j) v -= (float)(j < 8 ? r0[j] : r1[j - 8]) * t[j];
             t[i] = v;
+            om = fmaxf(om, fabsf(v));
         }
 #pragma unroll
         for (int i = 0; i < 16; ++i) Td[w][i][m] = (_Float16)t[i];
@@ -314,6 +344,7 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
             }
             floatx4 x = {0.0f, 0.0f, 0.0f, 0.0f};
             x = __builtin_amdgcn_mfma_f32_16x16x16f16(tb, to_half4(r), x, 0, 0, 0);
+            om = fmaxf(om, fmaxf(max4abs(r), max4abs(x)));
             xh[b][cc] = to_half4(x);
             if (cc >= 2) cu[b][cc - 2] = x;
         }
@@ -347,6 +378,11 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
             }
         }
     }
+
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) om = fmaxf(om, fmaxf(max4abs(cq[i][cc]), max4abs(cy[i][cc])));
 
     // ---- 5. outputs, all in the scan's fragment order (16-byte pieces; see
     //      the scan kernel for the piece layouts)
@@ -416,6 +452,220 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
         }
     }
     if (ht == 0) A.gC[hc] = expf(Gs[CHK - 1]);
+
+    // ---- 6. precision guard statistics: each v channel's max |v| over the
+    //      chunk, and +inf in channel 0 if an f16 operand would overflow
+    if (!(om <= 65504.0f)) vbad[hh] = 1;
+    __syncthreads();
+    if (ht < QM_DN_HD) {
+        float m = fmaxf(fmaxf(vred[hh][0][ht], vred[hh][1][ht]), fmaxf(vred[hh][2][ht], vred[hh][3][ht]));
+        if (ht == 0 && vbad[hh]) m = __builtin_inff();
+        A.vstat[((size_t)h * (A.nc + 1) + c) * QM_DN_HD + ht] = m;
+    }
+    if (c == 0) {
+        // the entering state's row maxima (slot nc): two threads per row
+        const int r = ht >> 1, half = ht & 1;
+        const float* sp = A.state + (size_t)h * QM_DN_HEAD_ELEMS + (size_t)r * QM_DN_HD + 64 * half;
+        float4 sv[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) sv[j] = ld4(sp + 4 * j);
+        float m = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            m = fmaxf(m, fmaxf(fmaxf(fabsf(sv[j].x), fabsf(sv[j].y)), fmaxf(fabsf(sv[j].z), fabsf(sv[j].w))));
+        m = fmaxf(m, __shfl_xor(m, 1));
+        if (half == 0) A.vstat[((size_t)h * (A.nc + 1) + A.nc) * QM_DN_HD + r] = m;
+    }
+}
+
+// ============================================================================
+// Precision guard and the exact fallback
+// ============================================================================
+// The chunked path rounds its MFMA operands to f16 (11 bits).  That holds the
+// bf16-path bar while a head's v rows (and state rows) are of comparable size;
+// when a few rows are orders of magnitude larger than the rest, an output of
+// a large row at a token where it happens to be small carries an absolute
+// error of ~2^-11 of that row's scale, which the per-token RMSNorm then
+// divides by the small rows' scale.  Such heads, heads whose magnitudes
+// would approach f16's range, and any chunk whose f16 operands would
+// overflow, take the exact path below instead: the reference's per-token
+// recurrence in fp32.
+
+// LDS of the exact path, one 64-token block at a time.
+struct ExactLds {
+    float qn[CHK][QM_DN_HD];                     // q: conv + SiLU, then normalised and scaled
+    float kn[CHK][QM_DN_HD];                     // k: conv + SiLU, then normalised
+    float vv[CHK][16];                           // this slice's v channels
+    float4 gt[CHK];                              // alpha, beta, k^.q^, -
+    float yb[CHK][16];                           // pre-norm outputs of the slice's rows
+    float inv[2][CHK];                           // 1/||q||, 1/||k|| (1 where the norm is <= 1e-12)
+};
+
+// Whether head h takes the exact path: the rows' magnitudes (each v
+// channel's max |v| over the sequence, or the entering state row's max)
+// are spread so that fewer than half of the 128 rows lie within 1/16 of the
+// largest, or the largest exceeds 2^11, or a chunk flagged an f16 overflow
+// (+inf).  Uniform over the workgroup (every thread returns the same).
+QM_DEV bool dn_guard_exact(const DnPrefillArgs& A, int h, float* red /* 260 floats */) {
+    const int tid = threadIdx.x, lane = tid & 63, r = tid & 127, half = tid >> 7;
+    const float* vs = A.vstat + (size_t)h * (A.nc + 1) * QM_DN_HD + r;
+    float m = 0.0f;
+#pragma unroll 8
+    for (int c = half; c <= A.nc; c += 2) m = fmaxf(m, vs[(size_t)c * QM_DN_HD]);
+    red[tid] = m;
+    __syncthreads();
+    const float mr = tid < 128 ? fmaxf(red[tid], red[tid + 128]) : 0.0f;
+    const float wm = max_xor32(max_xor16(row_max16(mr)));
+    if (lane == 0 && tid < 128) red[256 + (tid >> 6)] = wm;
+    __syncthreads();
+    const float mmax = fmaxf(red[256], red[257]);
+    const uint64_t near = __ballot(tid < 128 && mr >= mmax * 0.0625f);
+    __syncthreads();
+    if (lane == 0 && tid < 128) red[258 + (tid >> 6)] = (float)__popcll(near);
+    __syncthreads();
+    const float count = red[258] + red[259];
+    __syncthreads();                             // red may be reused
+    return count < 64.0f || !(mmax <= 2048.0f);
+}
+
+// The exact path for one (v-head h, 16-row slice vt): gemv.rs:1119-1201 per
+// token in fp32 on this slice's state rows, from the raw inputs (conv1d +
+// SiLU, L2 norms, q scale and gates recomputed here, gemv.rs:1132-1172).
+// The update is evaluated in one sweep over the old row,
+//   p = alpha (S.k),  d = beta (v - p),  y = alpha (S.q) + d (k.q),
+//   S <- alpha S + d k^T,
+// which equals the reference's decay / retrieve / update / read order in
+// real arithmetic.  Each 64-token block's outputs go to the slice's 4 KB of
+// the (head, chunk) block of Sc as f32 [64 tokens][16 rows], where the out
+// kernel normalises them; the final rows go to the state.
+QM_DEV void dn_exact_rows(const DnPrefillArgs& A, int h, int vt, ExactLds& L) {
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int qkh = h >> 1;
+    // recurrence: lane (rr, m) holds columns 8m .. 8m+7 of slice row rr
+    const int rr = 4 * w + (lane >> 4), m = lane & 15;
+    float* srow = A.state + (size_t)h * QM_DN_HEAD_ELEMS + (size_t)(16 * vt + rr) * QM_DN_HD + 8 * m;
+    float sv[8];
+    {
+        const float4 a = ld4(srow), b = ld4(srow + 4);
+        sv[0] = a.x; sv[1] = a.y; sv[2] = a.z; sv[3] = a.w;
+        sv[4] = b.x; sv[5] = b.y; sv[6] = b.z; sv[7] = b.w;
+    }
+    const float ea = expf(A.a_log[h]), dtb = A.dt_bias[h];
+    const float qscale = 1.0f / sqrtf((float)QM_DN_HD);
+    // prep: thread (part, ci) owns q (part 0) or k (part 1) channel ci for
+    // all tokens of a block; thread (vq, vr) owns v channel vr of the slice
+    // for tokens 4vq .. 4vq+3
+    const int part = tid >> 7, ci = tid & 127;
+    const int chq = part * QM_DN_QK_DIM + qkh * QM_DN_HD + ci;
+    const float4 wq = ld4(A.conv_w + (size_t)chq * 4);
+    const int vr = tid & 15, vq = tid >> 4;
+    const int chv = 2 * QM_DN_QK_DIM + h * QM_DN_HD + 16 * vt + vr;
+    const float4 wv = ld4(A.conv_w + (size_t)chv * 4);
+    float (*dst)[QM_DN_HD] = part ? L.kn : L.qn;
+    // the three raw rows before the block (the conv buffer before token 0)
+    float xp0 = A.conv_buf[(size_t)chq * 3], xp1 = A.conv_buf[(size_t)chq * 3 + 1];
+    float xp2 = A.conv_buf[(size_t)chq * 3 + 2];
+
+    for (int blk = 0; blk < A.nc; ++blk) {
+        const int t0 = blk * CHK;
+        const int nb = min(CHK, A.T - t0);
+        // ---- q / k channel ci, 16 tokens per round of loads
+#pragma unroll 1
+        for (int g = 0; g < 4; ++g) {
+            float xr[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int t = min(t0 + 16 * g + j, A.T - 1);
+                xr[j] = bf16_to_f32(A.qkv[(size_t)t * QM_DN_QKV_DIM + chq]);
+            }
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                dst[16 * g + j][ci] = silu_f(conv_taps4(xp0, xp1, xp2, xr[j], wq));
+                xp0 = xp1; xp1 = xp2; xp2 = xr[j];
+            }
+        }
+        // ---- v channel vr, tokens 4vq .. 4vq+3
+        {
+            float xv[7];
+#pragma unroll
+            for (int j = 0; j < 7; ++j) {
+                const int t = t0 + 4 * vq - 3 + j;
+                xv[j] = bf16_to_f32(A.qkv[(size_t)min(max(t, 0), A.T - 1) * QM_DN_QKV_DIM + chv]);
+                if (t < 0) xv[j] = A.conv_buf[(size_t)chv * 3 + 3 + t];
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) L.vv[4 * vq + j][vr] = silu_f(conv_taps4(xv[j], xv[j + 1], xv[j + 2], xv[j + 3], wv));
+        }
+        __syncthreads();
+        // ---- per token: gates (gemv.rs:1171-1172), L2 norms (:1151-1156)
+        if (tid < CHK) {
+            const int t = t0 + tid;
+            float al = 1.0f, be = 0.0f;
+            if (t < A.T) {
+                al = expf(-ea * softplus_f(A.a[(size_t)t * QM_DN_V_HEADS + h] + dtb));
+                be = 1.0f / (1.0f + expf(-A.b[(size_t)t * QM_DN_V_HEADS + h]));
+            }
+            float sq = 0.0f, sk = 0.0f, qk = 0.0f;
+            for (int i = 0; i < QM_DN_HD; i += 4) {
+                const float4 a = *reinterpret_cast<const float4*>(&L.qn[tid][i]);
+                const float4 b = *reinterpret_cast<const float4*>(&L.kn[tid][i]);
+                sq += a.x * a.x; sq += a.y * a.y; sq += a.z * a.z; sq += a.w * a.w;
+                sk += b.x * b.x; sk += b.y * b.y; sk += b.z * b.z; sk += b.w * b.w;
+                qk += a.x * b.x; qk += a.y * b.y; qk += a.z * b.z; qk += a.w * b.w;
+            }
+            const float nq = sqrtf(sq), nk = sqrtf(sk);
+            const float iq = nq > 1e-12f ? 1.0f / nq : 1.0f, ik = nk > 1e-12f ? 1.0f / nk : 1.0f;
+            L.inv[0][tid] = iq;
+            L.inv[1][tid] = ik;
+            L.gt[tid] = make_float4(al, be, qk * iq * ik * qscale, 0.0f);
+        }
+        __syncthreads();
+        {
+            const float* iv = L.inv[part];
+#pragma unroll 8
+            for (int j = 0; j < CHK; ++j) {
+                float x = dst[j][ci] * iv[j];
+                if (part == 0) x *= qscale;
+                dst[j][ci] = x;
+            }
+        }
+        __syncthreads();
+        // ---- the recurrence over the block's tokens
+#pragma unroll 2
+        for (int j = 0; j < nb; ++j) {
+            const float4 g = L.gt[j];
+            const float4 k0 = *reinterpret_cast<const float4*>(&L.kn[j][8 * m]);
+            const float4 k1 = *reinterpret_cast<const float4*>(&L.kn[j][8 * m + 4]);
+            const float4 q0 = *reinterpret_cast<const float4*>(&L.qn[j][8 * m]);
+            const float4 q1 = *reinterpret_cast<const float4*>(&L.qn[j][8 * m + 4]);
+            const float v = L.vv[j][rr];
+            const float kk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+            const float qq[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+            float sk = 0.0f, sq = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                sk = fmaf(sv[e], kk[e], sk);
+                sq = fmaf(sv[e], qq[e], sq);
+            }
+            sk = row_sum16(sk);
+            sq = row_sum16(sq);
+            const float dl = g.y * (v - g.x * sk);
+            const float y = fmaf(g.x, sq, dl * g.z);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sv[e] = fmaf(dl, kk[e], g.x * sv[e]);
+            if (m == 0) L.yb[j][rr] = y;
+        }
+        __syncthreads();
+        {
+            // f32 [64 tokens][16 rows] into the slice's 4 KB of block (h, blk)
+            float* yo = reinterpret_cast<float*>(reinterpret_cast<char*>(A.Sc) +
+                                                 ((size_t)h * A.nc + blk) * (QM_DN_HD * QM_DN_HD * 2) + 4096 * vt);
+            st4(yo + 4 * tid, *reinterpret_cast<const float4*>(&L.yb[tid >> 2][4 * (tid & 3)]));
+        }
+        __syncthreads();
+    }
+    st4(srow, make_float4(sv[0], sv[1], sv[2], sv[3]));
+    st4(srow + 4, make_float4(sv[4], sv[5], sv[6], sv[7]));
 }
 
 // ============================================================================
@@ -455,6 +705,8 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
 extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillArgs A) {
     __shared__ half8 Sx[4][64];                  // S^T piece p (k-tiles 2p, 2p+1), f16
     __shared__ half4 Ux[4][64];                  // U token tile i, f16
+    __shared__ ExactLds XL;                      // the exact path's block buffers
+    __shared__ float gred[260];                  // guard reductions
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     // blocks are dealt to the 8 XCDs round-robin: keep a head's 8 row slices
     // on one XCD so its chunk operands are fetched into one L2
@@ -462,6 +714,13 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillAr
     const int h = xcd + 8 * (idx >> 3), vt = idx & 7;
     const int nc = A.nc;
     const size_t hbase = (size_t)h * nc;
+
+    if (dn_guard_exact(A, h, gred)) {
+        dn_exact_rows(A, h, vt, XL);
+        if (tid == 0) A.mode[h * 8 + vt] = 1;
+        return;
+    }
+    float om = 0.0f;                             // largest |U|, |S| converted to f16
 
     float* Srow = A.state + (size_t)h * QM_DN_HEAD_ELEMS + (size_t)(16 * vt + (lane & 15)) * QM_DN_HD + 4 * (lane >> 4);
     floatx4 S[2];                                // S^T k-tiles 2w, 2w+1 (fp32)
@@ -520,7 +779,9 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillAr
         __builtin_amdgcn_sched_barrier(0);
         load_w(o, cn);
         __builtin_amdgcn_sched_barrier(0);
-        Ux[w][lane] = to_half4(u0 + u1);
+        const floatx4 us = u0 + u1;
+        om = fmaxf(om, max4abs(us));
+        Ux[w][lane] = to_half4(us);
         __syncthreads();
         half8 ub[2];
 #pragma unroll
@@ -533,6 +794,7 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillAr
                 S[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.k[2 * t + p], ub[p], S[t], 0, 0, 0);
         }
         const half8 mine = cat8(to_half4(S[0]), to_half4(S[1]));
+        om = fmaxf(om, fmaxf(max4abs(S[0]), max4abs(S[1])));
         __builtin_amdgcn_sched_barrier(0);
         load_uk(o, cn);
         __builtin_amdgcn_sched_barrier(0);
@@ -551,6 +813,7 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillAr
     }
     {
         const half8 mine = cat8(to_half4(S[0]), to_half4(S[1]));
+        om = fmaxf(om, fmaxf(max4abs(S[0]), max4abs(S[1])));
         Sx[w][lane] = mine;
         sc_store(0, mine);
     }
@@ -563,8 +826,19 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillAr
 #pragma unroll
     for (int i = 0; i < 3; ++i)
         if (c + i < nc) step(c + i, ops[i]);
+    // if an f16 copy of U or S overflowed, redo this slice exactly (the
+    // entering state is still in place: the state is written only here)
+    const float ow = max_xor32(max_xor16(row_max16(om)));
+    if (lane == 0) gred[w] = ow;
+    __syncthreads();
+    if (!(fmaxf(fmaxf(gred[0], gred[1]), fmaxf(gred[2], gred[3])) <= 65504.0f)) {
+        dn_exact_rows(A, h, vt, XL);
+        if (tid == 0) A.mode[h * 8 + vt] = 1;
+        return;
+    }
 #pragma unroll
     for (int t = 0; t < 2; ++t) st4(Srow + 16 * (2 * w + t), make_float4(S[t][0], S[t][1], S[t][2], S[t][3]));
+    if (tid == 0) A.mode[h * 8 + vt] = 0;
 }
 
 // ============================================================================
@@ -619,16 +893,27 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_out(DnPrefillArg
         }
 #pragma unroll
         for (int j = 0; j < 16; ++j) qf[j] = *reinterpret_cast<const half8*>(qsrc + j * 512);
+        // slices the scan ran exactly left f32 [64 tokens][16 rows] in
+        // their 4 KB of this block instead of S_c pieces
+        const bool ex[2] = {A.mode[h * 8 + 2 * w] != 0, A.mode[h * 8 + 2 * w + 1] != 0};
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc) {
-                const half8 src = yf[cc][i >> 1];
-                const int o = 4 * (i & 1);
-                floatx4 y = {(float)src[o], (float)src[o + 1], (float)src[o + 2], (float)src[o + 3]};
+                floatx4 y;
+                if (ex[cc]) {
+                    const float* yx = reinterpret_cast<const float*>(
+                        reinterpret_cast<const char*>(A.Sc) + hc * (QM_DN_HD * QM_DN_HD * 2) + 4096 * (2 * w + cc));
 #pragma unroll
-                for (int p = 0; p < 4; ++p)
-                    y = __builtin_amdgcn_mfma_f32_16x16x32_f16(qf[4 * i + p], sf[cc][p], y, 0, 0, 0);
+                    for (int e = 0; e < 4; ++e) y[e] = yx[(16 * i + 4 * (lane >> 4) + e) * 16 + (lane & 15)];
+                } else {
+                    const half8 src = yf[cc][i >> 1];
+                    const int o = 4 * (i & 1);
+                    y = floatx4{(float)src[o], (float)src[o + 1], (float)src[o + 2], (float)src[o + 3]};
+#pragma unroll
+                    for (int p = 0; p < 4; ++p)
+                        y = __builtin_amdgcn_mfma_f32_16x16x32_f16(qf[4 * i + p], sf[cc][p], y, 0, 0, 0);
+                }
                 const int col = 16 * (2 * w + cc) + (lane & 15);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) ys[16 * i + 4 * (lane >> 4) + e][col] = y[e];

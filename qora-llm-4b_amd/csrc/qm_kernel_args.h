@@ -94,6 +94,14 @@ struct DnPrefillArgs {
     uint16_t* Ktt;
     float* gC;
     uint16_t* Sc;
+    // Precision guard: vstat f32 [32][nc + 1][128] holds, per (v-head,
+    // chunk), each v channel's max |v| after conv1d + SiLU (+inf in entry 0
+    // if any f16 operand of that chunk would overflow); slot nc holds the
+    // entering state's row maxima.  mode int32 [32][8]: per (v-head, 16-row
+    // slice) 0 = chunked f16 path, 1 = exact fp32 recurrence (its pre-norm
+    // outputs then sit in the slice's part of Sc as f32 [64 tokens][16]).
+    float* vstat;
+    int32_t* mode;
     int32_t T;
     int32_t nc;
 };

@@ -116,19 +116,39 @@ def test_prefill_long_warm(ctx, T):
     assert np.array_equal(cb, rcb)
 
 
+# v channels 5, 900, 2100, 4000 lie in v-heads 0, 7, 16 and 31
+OUTLIER_V = [4096 + 5, 4096 + 900, 4096 + 2100, 4096 + 4000]
+OUTLIER_HEADS = [0, 7, 16, 31]
+
+
+def outlier_workload(T, seed, v_scale=None, qk_scale=None, slow=False):
+    w = W.dn_prefill_workload(T, seed=seed)
+    x = W.bf16_value(w["qkv"]).copy()
+    if v_scale:
+        x[:, OUTLIER_V] *= np.float32(v_scale)
+    if qk_scale:
+        x[:, [7, 300, 2048 + 11, 2048 + 1500]] *= np.float32(qk_scale)
+    w["qkv"] = W.bf16_bits(x)
+    if slow:
+        w["a_log"] = np.full(32, np.log(1e-4), np.float32)    # alpha ~ 0.9999 per token
+    return w
+
+
+def head_rel(o, ro, h):
+    """||d||_inf / ||ref||_inf over one v-head's outputs."""
+    return rel(o.reshape(o.shape[0], 32, 128)[:, h], ro.reshape(ro.shape[0], 32, 128)[:, h])
+
+
 @pytest.mark.parametrize("scale", [1e3, 1e4])
 def test_prefill_channel_outliers(ctx, scale):
     """A few input channels scaled far past the rest (massive-activation
     outliers): 4 v channels and 4 q/k channels times `scale` over 1024
-    tokens.  q and k are L2-normalised per head, so their outliers only
-    sharpen the direction; v's reach the f16 chunk operands and the state
-    (|S| to ~6e3 at 1e4).  Within the bar against the oracle's fp32."""
+    tokens.  The four heads holding a v outlier have rows 1e3-1e4 times
+    their others, so they take the exact fp32 path (their outputs match the
+    oracle's to fp32 rounding, which the f16 operands could not); the other
+    28 heads stay on the chunked path.  Within the bar against the oracle."""
     T = 1024
-    w = W.dn_prefill_workload(T, seed=11)
-    x = W.bf16_value(w["qkv"]).copy()
-    x[:, [4096 + 5, 4096 + 900, 4096 + 2100, 4096 + 4000]] *= np.float32(scale)
-    x[:, [7, 300, 2048 + 11, 2048 + 1500]] *= np.float32(scale)
-    w["qkv"] = W.bf16_bits(x)
+    w = outlier_workload(T, 11, v_scale=scale, qk_scale=scale)
     print(f"case: dn prefill T={T} channel outliers x{scale:g}", flush=True)
     o, S, cb = run_prefill(ctx, w, T)
     ro, rS, rcb = run_oracle(w, T)
@@ -136,6 +156,82 @@ def test_prefill_channel_outliers(ctx, scale):
     eo, es = rel(o, ro), rel(S, rS)
     print(f"rel out {eo:.3e} rel state {es:.3e} max|S| {np.abs(rS).max():.3e}")
     assert eo <= RTOL and es <= RTOL
+    assert np.array_equal(cb, rcb)
+    # the outlier heads ran exactly: fp32-level agreement (the bf16 output
+    # rounding, 2^-9, is the only large term left)
+    for h in OUTLIER_HEADS:
+        assert head_rel(o, ro, h) <= 4e-3, h
+        assert rel(S[h], rS[h]) <= 1e-4, h
+
+
+@pytest.mark.parametrize("scale", [3e4, 1e5])
+def test_prefill_v_outliers_past_f16_range(ctx, scale):
+    """v channels 3e4 and 1e5 times the rest: |v| past f16's range (65504),
+    where f16 chunk operands would overflow to inf/NaN.  The guard sends
+    those heads to the exact path: finite and within the bar."""
+    T = 1024
+    w = outlier_workload(T, 12, v_scale=scale)
+    print(f"case: dn prefill T={T} v outliers x{scale:g}", flush=True)
+    o, S, cb = run_prefill(ctx, w, T)
+    ro, rS, rcb = run_oracle(w, T)
+    assert np.isfinite(o).all() and np.isfinite(S).all()
+    eo, es = rel(o, ro), rel(S, rS)
+    print(f"rel out {eo:.3e} rel state {es:.3e} max|S| {np.abs(rS).max():.3e}")
+    assert eo <= RTOL and es <= RTOL
+    assert np.array_equal(cb, rcb)
+
+
+@pytest.mark.parametrize("scale", [1e3, 1e4])
+def test_prefill_slow_decay_with_v_outliers(ctx, scale):
+    """Decays of ~0.9999 per token together with v channels 1e3 / 1e4 times
+    the rest, over 1024 tokens: the state keeps every token's contribution,
+    the outlier rows grow to ~1e3-1e4 times the others, and an output of
+    such a row where it is near zero needs ~16 bits in every product (the
+    f16 path reached 2.3e-2 and 7.3e-2 here).  Within the bar."""
+    T = 1024
+    w = outlier_workload(T, 11, v_scale=scale, slow=True)
+    print(f"case: dn prefill T={T} slow decay + v outliers x{scale:g}", flush=True)
+    o, S, cb = run_prefill(ctx, w, T)
+    ro, rS, rcb = run_oracle(w, T)
+    assert np.isfinite(o).all() and np.isfinite(S).all()
+    eo, es = rel(o, ro), rel(S, rS)
+    print(f"rel out {eo:.3e} rel state {es:.3e} max|S| {np.abs(rS).max():.3e}")
+    assert eo <= RTOL and es <= RTOL
+
+
+def test_prefill_moderate_spread_stays_chunked(ctx):
+    """v channels 6x the rest (inside the guard's 16x) with slow decay: the
+    chunked f16 path runs and holds the bar with a wide margin."""
+    T = 1024
+    w = outlier_workload(T, 14, v_scale=6.0, slow=True)
+    print(f"case: dn prefill T={T} slow decay + v outliers x6 (chunked path)", flush=True)
+    o, S, cb = run_prefill(ctx, w, T)
+    ro, rS, rcb = run_oracle(w, T)
+    eo, es = rel(o, ro), rel(S, rS)
+    print(f"rel out {eo:.3e} rel state {es:.3e}")
+    assert eo <= 5e-3 and es <= RTOL
+
+
+def test_prefill_large_uniform_magnitude_is_exact(ctx):
+    """Every v channel 2000 times N(0,1) (|v| past 2^11 on every row, no
+    spread): the guard's magnitude bound sends all heads to the exact path;
+    finite and within the bar, from a warm state and conv buffer over a
+    partial last chunk."""
+    T = 700
+    w = W.dn_prefill_workload(T, seed=15)
+    x = W.bf16_value(w["qkv"]).copy()
+    x[:, 4096:] *= np.float32(2000.0)
+    w["qkv"] = W.bf16_bits(x)
+    r = np.random.default_rng(15)
+    w["state0"] = (0.02 * r.standard_normal((32, 128, 128))).astype(np.float32)
+    w["conv_buf0"] = r.standard_normal((8192, 3)).astype(np.float32)
+    print(f"case: dn prefill T={T} all v x2000 (exact path, warm)", flush=True)
+    o, S, cb = run_prefill(ctx, w, T)
+    ro, rS, rcb = run_oracle(w, T)
+    assert np.isfinite(o).all() and np.isfinite(S).all()
+    eo, es = rel(o, ro), rel(S, rS)
+    print(f"rel out {eo:.3e} rel state {es:.3e}")
+    assert eo <= 4e-3 and es <= 1e-4
     assert np.array_equal(cb, rcb)
 
 
