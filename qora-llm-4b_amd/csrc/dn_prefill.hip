@@ -25,11 +25,12 @@
 //   qm_dn_prefill_scan   the sequential part: one 4-wave workgroup per
 //                        (v-head, 16 state rows) with its rows of the fp32
 //                        state in registers, two f16 MFMA GEMMs per chunk
-//                        split over the waves; stores each chunk's entry
-//                        state in f16;
-//   qm_dn_prefill_out    Y = Y0 + Q~ S_c^T on MFMA, fully parallel over
-//                        (chunk, v-head), fused with the gated RMSNorm and
-//                        the conv buffer update.
+//                        split over the waves, and the slice's outputs
+//                        Y = Y0 + Q~ S_c^T from each chunk's entry state
+//                        S_c (or the exact fp32 path, see the guard);
+//   qm_dn_prefill_out    the gated RMSNorm over the head's 128 rows of Y,
+//                        fully parallel over (chunk, v-head), and the conv
+//                        buffer update.
 #include "qm_device.h"
 #include "qm_kernel_args.h"
 
@@ -536,7 +537,7 @@ QM_DEV bool dn_guard_exact(const DnPrefillArgs& A, int h, float* red /* 260 floa
 //   S <- alpha S + d k^T,
 // which equals the reference's decay / retrieve / update / read order in
 // real arithmetic.  Each 64-token block's outputs go to the slice's 4 KB of
-// the (head, chunk) block of Sc as f32 [64 tokens][16 rows], where the out
+// the (head, chunk) block of Yx as f32 [64 tokens][16 rows], where the out
 // kernel normalises them; the final rows go to the state.
 QM_DEV void dn_exact_rows(const DnPrefillArgs& A, int h, int vt, ExactLds& L) {
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
@@ -658,7 +659,7 @@ QM_DEV void dn_exact_rows(const DnPrefillArgs& A, int h, int vt, ExactLds& L) {
         __syncthreads();
         {
             // f32 [64 tokens][16 rows] into the slice's 4 KB of block (h, blk)
-            float* yo = reinterpret_cast<float*>(reinterpret_cast<char*>(A.Sc) +
+            float* yo = reinterpret_cast<float*>(reinterpret_cast<char*>(A.Yx) +
                                                  ((size_t)h * A.nc + blk) * (QM_DN_HD * QM_DN_HD * 2) + 4096 * vt);
             st4(yo + 4 * tid, *reinterpret_cast<const float4*>(&L.yb[tid >> 2][4 * (tid & 3)]));
         }
@@ -674,9 +675,10 @@ QM_DEV void dn_exact_rows(const DnPrefillArgs& A, int h, int vt, ExactLds& L) {
 // Under the chunked delta rule every state row evolves on its own:
 //   U_r = U~_r - W S_r^T,  S_r <- gamma_C S_r + U_r^T K~
 // so a v-head's 128 rows split over 8 independent slices (grid 256).  The
-// output Y_r = Y0_r + Q~ S_r^T only reads the chunk-entry state, so the scan
-// stores that state (in f16, the precision the product consumes it in) and
-// the out kernel forms Y fully in parallel.
+// output Y_r = Y0_r + Q~ S_r^T of a chunk reads only its entry state, in the
+// same f16 pieces the U product takes, so each wave forms its token tile of
+// Y beside U, off the chain, and stores it in f16; the per-token norm over
+// all 128 rows is left to the out kernel.
 // S_r^T (k-cols x 16 rows, fp32) is held as eight C fragments; for k tile
 // t, lane (r, q) = (lane & 15, lane >> 4) holds S[16 vt + r][16 t + 4q .. +3].
 // All chunk operands arrive in fragment order as 16-byte pieces, piece
@@ -686,22 +688,20 @@ QM_DEV void dn_exact_rows(const DnPrefillArgs& A, int h, int vt, ExactLds& L) {
 //   K~^T     j = 2 kt + p: k-col 16 kt + (lane & 15), tokens 32 p + 4 (lane >> 4)
 //            + {0..3} and + 16 + {0..3};
 //   U~, Y0   j = 2 vt + p: row 16 vt + (lane & 15), tokens 32 p + 4 (lane >> 4)
-//            + {0..3} and + 16 + {0..3};
-//   S_c      j = 4 vt + p: row 16 vt + (lane & 15), k-cols 32 p + 4 (lane >> 4)
-//            + {0..3} and + 16 + {0..3} (written here).
+//            + {0..3} and + 16 + {0..3}.
 // A 16-byte piece is the A operand of one v_mfma_f32_16x16x32_f16: a product
 // only needs A and B to agree on which k each (lane, element) holds, and the
 // two C fragments of S^T k tiles 2p, 2p+1 (or of U token tiles 2p, 2p+1)
 // concatenated hold exactly the k (token) set of piece p.
 // A workgroup of four waves (one per SIMD) owns one (v-head, 16 rows) slice,
 // so the per-chunk chain is split four ways: wave w forms U's token tile w
-// (4 MFMAs) and updates S^T k-tiles 2w, 2w+1 (4 MFMAs).  The f16 U tiles and
-// S pieces are exchanged through LDS, two barriers per chunk; a wave writes
-// S piece w, which is also what the out kernel reads for S_c.
+// (4 MFMAs) and Y's token tile w (4 MFMAs, same S pieces), and updates S^T
+// k-tiles 2w, 2w+1 (4 MFMAs).  The f16 U tiles and S pieces are exchanged
+// through LDS, two barriers per chunk.
 // Single buffers suffice: a wave writes Sx (Ux) only after passing the
 // barrier that every wave reaches after its last read of the previous
-// contents.  Each wave's operands for chunk c + 4 are loaded right after
-// their last use in chunk c.
+// contents.  Each wave's chain operands for chunk c + 4 (Y's for c + 2)
+// are loaded right after their last use in chunk c.
 extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillArgs A) {
     __shared__ half8 Sx[4][64];                  // S^T piece p (k-tiles 2p, 2p+1), f16
     __shared__ half4 Ux[4][64];                  // U token tile i, f16
@@ -749,17 +749,31 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillAr
 #pragma unroll
         for (int j = 0; j < 4; ++j) o.k[j] = *reinterpret_cast<const half8*>(ks + j * 512);
     };
-    auto sc_store = [&](int c, half8 v) {
-        *reinterpret_cast<half8*>(A.Sc + (hbase + c) * (QM_DN_HD * QM_DN_HD) + (size_t)((4 * vt + w) * 64 + lane) * 8) = v;
+    // Q~ pieces 4w .. 4w+3 (token block w) and the Y0 tile w, two chunks ahead
+    struct OpsY {
+        half8 q[4];
+        half4 y;
+    };
+    auto load_qy = [&](OpsY& o, int c) {
+        const uint16_t* qs = blk(A.Qt, c) + 4 * w * 512;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) o.q[p] = *reinterpret_cast<const half8*>(qs + p * 512);
+        o.y = *reinterpret_cast<const half4*>(blk(A.Y0t, c) + (2 * vt + (w >> 1)) * 512 + 4 * (w & 1));
+    };
+    // Y tile w of this slice: lane (r, q) holds tokens 16 w + 4 q .. +3 of
+    // row 16 vt + r, as one 8-byte piece per lane
+    auto y_store = [&](int c, half4 v) {
+        *reinterpret_cast<half4*>(A.Yt + ((((hbase + c) * 8 + vt) * 4 + w) * 64 + lane) * 4) = v;
     };
     // gamma_C of 64 chunks at a time, one per lane (a vector load, so LDS
     // waits never wait on it), the next 64 fetched half way through
     auto load_g = [&](int c0) { return A.gC[hbase + min(c0 + lane, nc - 1)]; };
     float gv = load_g(0), gn = 0.0f;
 
-    // One chunk: U tile w = U~ + (-W) S^T; exchange U; S^T tiles <- gamma_C
-    // S^T + K~^T U; exchange S and store it as the next chunk's entry state.
-    auto step = [&](int c, Ops& o) {
+    // One chunk: U tile w = U~ + (-W) S^T; Y tile w = Y0 + Q~ S^T (the
+    // chunk's outputs, off the chain); exchange U; S^T tiles <- gamma_C S^T +
+    // K~^T U; exchange S.
+    auto step = [&](int c, Ops& o, OpsY& oy) {
         if ((c & 63) == 32) gn = load_g(c + 32);
         if ((c & 63) == 0 && c) gv = gn;
         const float g = readlane_f32(gv, c & 63);
@@ -782,6 +796,12 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillAr
         const floatx4 us = u0 + u1;
         om = fmaxf(om, max4abs(us));
         Ux[w][lane] = to_half4(us);
+        floatx4 y0 = {(float)oy.y[0], (float)oy.y[1], (float)oy.y[2], (float)oy.y[3]};
+        floatx4 y1 = {0.0f, 0.0f, 0.0f, 0.0f};
+        y0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(oy.q[0], sb[0], y0, 0, 0, 0);
+        y1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(oy.q[1], sb[1], y1, 0, 0, 0);
+        y0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(oy.q[2], sb[2], y0, 0, 0, 0);
+        y1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(oy.q[3], sb[3], y1, 0, 0, 0);
         __syncthreads();
         half8 ub[2];
 #pragma unroll
@@ -795,37 +815,42 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillAr
         }
         const half8 mine = cat8(to_half4(S[0]), to_half4(S[1]));
         om = fmaxf(om, fmaxf(max4abs(S[0]), max4abs(S[1])));
+        const floatx4 ys = y0 + y1;
+        om = fmaxf(om, max4abs(ys));
+        y_store(c, to_half4(ys));
         __builtin_amdgcn_sched_barrier(0);
         load_uk(o, cn);
+        load_qy(oy, min(c + 2, nc - 1));
         __builtin_amdgcn_sched_barrier(0);
         Sx[w][lane] = mine;
-        if (c + 1 < nc) sc_store(c + 1, mine);
         __syncthreads();
     };
 
-    // four chunks of operands in flight (a wave has a SIMD to itself)
+    // four chunks of the chain's operands and two of the outputs' operands
+    // in flight (a wave has a SIMD to itself)
     Ops ops[4];
+    OpsY opy[2];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         load_w(ops[i], min(i, nc - 1));
         load_uk(ops[i], min(i, nc - 1));
+        if (i < 2) load_qy(opy[i], min(i, nc - 1));
         __builtin_amdgcn_sched_barrier(0);
     }
     {
         const half8 mine = cat8(to_half4(S[0]), to_half4(S[1]));
         om = fmaxf(om, fmaxf(max4abs(S[0]), max4abs(S[1])));
         Sx[w][lane] = mine;
-        sc_store(0, mine);
     }
     __syncthreads();
     int c = 0;
     for (; c + 3 < nc; c += 4) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) step(c + i, ops[i]);
+        for (int i = 0; i < 4; ++i) step(c + i, ops[i], opy[i & 1]);
     }
 #pragma unroll
     for (int i = 0; i < 3; ++i)
-        if (c + i < nc) step(c + i, ops[i]);
+        if (c + i < nc) step(c + i, ops[i], opy[i & 1]);
     // if an f16 copy of U or S overflowed, redo this slice exactly (the
     // entering state is still in place: the state is written only here)
     const float ow = max_xor32(max_xor16(row_max16(om)));
@@ -842,12 +867,13 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillAr
 }
 
 // ============================================================================
-// 4. out: Y = Y0 + Q~ S_c^T and the gated RMSNorm (gemv.rs:1205-1219), plus
+// 4. out: the gated RMSNorm (gemv.rs:1205-1219) of the scan's outputs, plus
 //    the conv buffer update
 // ============================================================================
-// One workgroup per (chunk, v-head).  Wave w forms the 64 x 32 block of Y for
-// rows 32w .. 32w+31 on 16x16x32 f16 MFMA from the fragment-order pieces,
-// stages it in LDS, and the norm then runs 32 lanes per token with 4
+// One workgroup per (chunk, v-head).  The head's 128 rows of Y for the
+// chunk's 64 tokens come from the eight slices, in the scan's fragment order
+// (f16) or, for a slice that ran exactly, as f32 [64 tokens][16 rows]; they
+// are staged in LDS, and the norm then runs 32 lanes per token with 4
 // consecutive values each, so z and the output move 512 contiguous bytes per
 // token pair.
 extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_out(DnPrefillArgs A) {
@@ -880,44 +906,36 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_out(DnPrefillArg
         zr[q] = *reinterpret_cast<const uint2*>(A.z + ((size_t)t * QM_DN_V_HEADS + h) * QM_DN_HD + col);
     }
     {
-        const uint16_t* qsrc = A.Qt + hc * (CHK * QM_DN_HD) + (size_t)lane * 8;
-        const uint16_t* ssrc = A.Sc + hc * (QM_DN_HD * QM_DN_HD) + (size_t)lane * 8;
-        const uint16_t* ysrc = A.Y0t + hc * (CHK * QM_DN_HD) + (size_t)lane * 8;
-        half8 qf[16], sf[2][4], yf[2][2];
+        // fragment-order f16 tiles: item i = ((vt * 4 + wt) * 64 + l) holds
+        // tokens 16 wt + 4 (l >> 4) .. +3 of row 16 vt + (l & 15)
+        const half4* ysrc = reinterpret_cast<const half4*>(A.Yt) + hc * (8 * 4 * 64);
+        half4 yv[8];
 #pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
+        for (int k = 0; k < 8; ++k) yv[k] = ysrc[tid + 256 * k];
+        bool ex[8];
 #pragma unroll
-            for (int p = 0; p < 4; ++p) sf[cc][p] = *reinterpret_cast<const half8*>(ssrc + (4 * (2 * w + cc) + p) * 512);
+        for (int vt = 0; vt < 8; ++vt) ex[vt] = A.mode[h * 8 + vt] != 0;
 #pragma unroll
-            for (int p = 0; p < 2; ++p) yf[cc][p] = *reinterpret_cast<const half8*>(ysrc + (2 * (2 * w + cc) + p) * 512);
-        }
+        for (int k = 0; k < 8; ++k) {
+            const int i = tid + 256 * k, vt = i >> 8, wt = (i >> 6) & 3, l = i & 63;
+            if (!ex[vt]) {
 #pragma unroll
-        for (int j = 0; j < 16; ++j) qf[j] = *reinterpret_cast<const half8*>(qsrc + j * 512);
-        // slices the scan ran exactly left f32 [64 tokens][16 rows] in
-        // their 4 KB of this block instead of S_c pieces
-        const bool ex[2] = {A.mode[h * 8 + 2 * w] != 0, A.mode[h * 8 + 2 * w + 1] != 0};
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int cc = 0; cc < 2; ++cc) {
-                floatx4 y;
-                if (ex[cc]) {
-                    const float* yx = reinterpret_cast<const float*>(
-                        reinterpret_cast<const char*>(A.Sc) + hc * (QM_DN_HD * QM_DN_HD * 2) + 4096 * (2 * w + cc));
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) y[e] = yx[(16 * i + 4 * (lane >> 4) + e) * 16 + (lane & 15)];
-                } else {
-                    const half8 src = yf[cc][i >> 1];
-                    const int o = 4 * (i & 1);
-                    y = floatx4{(float)src[o], (float)src[o + 1], (float)src[o + 2], (float)src[o + 3]};
-#pragma unroll
-                    for (int p = 0; p < 4; ++p)
-                        y = __builtin_amdgcn_mfma_f32_16x16x32_f16(qf[4 * i + p], sf[cc][p], y, 0, 0, 0);
-                }
-                const int col = 16 * (2 * w + cc) + (lane & 15);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) ys[16 * i + 4 * (lane >> 4) + e][col] = y[e];
+                for (int e = 0; e < 4; ++e) ys[16 * wt + 4 * (l >> 4) + e][16 * vt + (l & 15)] = (float)yv[k][e];
             }
+        }
+        // slices the scan ran exactly: f32 [64 tokens][16 rows] in their
+        // 4 KB of this (head, chunk) block
+        const float4* xsrc = reinterpret_cast<const float4*>(
+            reinterpret_cast<const char*>(A.Yx) + hc * (QM_DN_HD * QM_DN_HD * 2));
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int i = tid + 256 * k, vt = i >> 8;            // float4 i: slice vt, token (i >> 2) & 63
+            if (ex[vt]) {
+                const float4 v = xsrc[i];
+                const int tok = (i >> 2) & 63, r0 = 16 * vt + 4 * (i & 3);
+                ys[tok][r0] = v.x; ys[tok][r0 + 1] = v.y; ys[tok][r0 + 2] = v.z; ys[tok][r0 + 3] = v.w;
+            }
+        }
     }
     __syncthreads();
 

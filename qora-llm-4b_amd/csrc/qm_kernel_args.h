@@ -93,13 +93,18 @@ struct DnPrefillArgs {
     uint16_t* Y0t;
     uint16_t* Ktt;
     float* gC;
-    uint16_t* Sc;
+    // the scan's outputs Y (pre-norm) in f16, per (v-head, chunk) 8 slices x
+    // 4 token tiles x 64 lanes x 4 tokens (fragment order)
+    uint16_t* Yt;
+    // pre-norm outputs of slices run exactly: per (v-head, chunk) 32 KB, the
+    // 4 KB at 4096 * slice holding f32 [64 tokens][16 rows]
+    float* Yx;
     // Precision guard: vstat f32 [32][nc + 1][128] holds, per (v-head,
     // chunk), each v channel's max |v| after conv1d + SiLU (+inf in entry 0
     // if any f16 operand of that chunk would overflow); slot nc holds the
     // entering state's row maxima.  mode int32 [32][8]: per (v-head, 16-row
-    // slice) 0 = chunked f16 path, 1 = exact fp32 recurrence (its pre-norm
-    // outputs then sit in the slice's part of Sc as f32 [64 tokens][16]).
+    // slice) 0 = chunked f16 path (outputs in Yt), 1 = exact fp32 recurrence
+    // (outputs in Yx).
     float* vstat;
     int32_t* mode;
     int32_t T;
