@@ -427,14 +427,12 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
             *reinterpret_cast<half8*>(qdst + o) = cat8(q0, q1);
         }
     }
-    // K~^T = (gamma_C / gamma_j) K^T: piece 2kt + p, kt = 2w, 2w+1, holds
-    // token blocks 2p, 2p+1 of k-col tile kt; the A operand of a K tile is a
-    // row read (token 16 tau + lr, cols 16 kt + 4 lq .. +3)
-    {
-        uint16_t* dst = A.Ktt + hc * CHK * QM_DN_HD;
-        float4 kd[4];
-#pragma unroll
-        for (int tau = 0; tau < 4; ++tau) kd[tau] = *reinterpret_cast<const float4*>(&Kd[16 * tau + 4 * lq]);
+    // K^T of the qk-head, once for both v-heads (the scan applies each
+    // head's decays gamma_C / gamma_j to U instead): piece 2kt + p, kt = 2w,
+    // 2w+1, holds token blocks 2p, 2p+1 of k-col tile kt; the A operand of a
+    // K tile is a row read (token 16 tau + lr, cols 16 kt + 4 lq .. +3)
+    if (hh == 0) {
+        uint16_t* dst = A.Ktt + ((size_t)qkh * A.nc + c) * CHK * QM_DN_HD;
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             const int kt = 2 * w + t;
@@ -445,13 +443,13 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
                 for (int hb = 0; hb < 2; ++hb) {
                     const int tau = 2 * p + hb;
                     const half4 a = *reinterpret_cast<const half4*>(&Ks[16 * tau + lr][16 * kt + 4 * lq]);
-                    const floatx4 kc = __builtin_amdgcn_mfma_f32_16x16x16f16(a, idm, floatx4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-                    hv[hb] = to_half4(floatx4{kc[0] * kd[tau].x, kc[1] * kd[tau].y, kc[2] * kd[tau].z, kc[3] * kd[tau].w});
+                    hv[hb] = transpose(a);
                 }
                 *reinterpret_cast<half8*>(dst + (size_t)((2 * kt + p) * 64 + lane) * 8) = cat8(hv[0], hv[1]);
             }
         }
     }
+    if (ht < CHK) A.Dt[hc * CHK + ht] = Kd[ht];
     if (ht == 0) A.gC[hc] = expf(Gs[CHK - 1]);
 
     // ---- 6. precision guard statistics: each v channel's max |v| over the
@@ -673,7 +671,8 @@ QM_DEV void dn_exact_rows(const DnPrefillArgs& A, int h, int vt, ExactLds& L) {
 // 3. scan: sequential over chunks, one workgroup per (v-head, 16 state rows)
 // ============================================================================
 // Under the chunked delta rule every state row evolves on its own:
-//   U_r = U~_r - W S_r^T,  S_r <- gamma_C S_r + U_r^T K~
+//   U_r = U~_r - W S_r^T,  S_r <- gamma_C S_r + (D U_r)^T K,
+// D = diag(gamma_C / gamma), K the qk-head's keys (shared by its two v-heads)
 // so a v-head's 128 rows split over 8 independent slices (grid 256).  The
 // output Y_r = Y0_r + Q~ S_r^T of a chunk reads only its entry state, in the
 // same f16 pieces the U product takes, so each wave forms its token tile of
@@ -685,8 +684,8 @@ QM_DEV void dn_exact_rows(const DnPrefillArgs& A, int h, int vt, ExactLds& L) {
 // (j, lane) at byte offset 16 (64 j + lane) of the (head, chunk) block:
 //   -W, Q~   j = 4 i + p: tokens 16 i + (lane & 15), k-cols 32 p + 4 (lane >> 4)
 //            + {0..3} (k step 2p) and + 16 + {0..3} (k step 2p+1);
-//   K~^T     j = 2 kt + p: k-col 16 kt + (lane & 15), tokens 32 p + 4 (lane >> 4)
-//            + {0..3} and + 16 + {0..3};
+//   K^T      j = 2 kt + p: k-col 16 kt + (lane & 15), tokens 32 p + 4 (lane >> 4)
+//            + {0..3} and + 16 + {0..3} (per qk-head and chunk);
 //   U~, Y0   j = 2 vt + p: row 16 vt + (lane & 15), tokens 32 p + 4 (lane >> 4)
 //            + {0..3} and + 16 + {0..3}.
 // A 16-byte piece is the A operand of one v_mfma_f32_16x16x32_f16: a product
@@ -696,7 +695,7 @@ QM_DEV void dn_exact_rows(const DnPrefillArgs& A, int h, int vt, ExactLds& L) {
 // A workgroup of four waves (one per SIMD) owns one (v-head, 16 rows) slice,
 // so the per-chunk chain is split four ways: wave w forms U's token tile w
 // (4 MFMAs) and Y's token tile w (4 MFMAs, same S pieces), and updates S^T
-// k-tiles 2w, 2w+1 (4 MFMAs).  The f16 U tiles and S pieces are exchanged
+// k-tiles 2w, 2w+1 (4 MFMAs).  The f16 (D U) tiles and S pieces are exchanged
 // through LDS, two barriers per chunk.
 // Single buffers suffice: a wave writes Sx (Ux) only after passing the
 // barrier that every wave reaches after its last read of the previous
@@ -710,10 +709,12 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillAr
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     // blocks are dealt to the 8 XCDs round-robin: keep a head's 8 row slices
     // on one XCD so its chunk operands are fetched into one L2
+    // (XCD x takes v-heads 4x .. 4x+3, i.e. both v-heads of two qk-heads,
+    // which read the same K^T pieces)
     const int b = blockIdx.x, xcd = b & 7, idx = b >> 3;
-    const int h = xcd + 8 * (idx >> 3), vt = idx & 7;
+    const int h = 4 * xcd + (idx >> 3), vt = idx & 7;
     const int nc = A.nc;
-    const size_t hbase = (size_t)h * nc;
+    const size_t hbase = (size_t)h * nc, kbase = (size_t)(h >> 1) * nc;
 
     if (dn_guard_exact(A, h, gred)) {
         dn_exact_rows(A, h, vt, XL);
@@ -745,7 +746,7 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillAr
     };
     auto load_uk = [&](Ops& o, int c) {
         o.u = *reinterpret_cast<const half4*>(blk(A.Ut, c) + (2 * vt + (w >> 1)) * 512 + 4 * (w & 1));
-        const uint16_t* ks = blk(A.Ktt, c) + 4 * w * 512;
+        const uint16_t* ks = A.Ktt + (kbase + c) * (CHK * QM_DN_HD) + (size_t)lane * 8 + 4 * w * 512;
 #pragma unroll
         for (int j = 0; j < 4; ++j) o.k[j] = *reinterpret_cast<const half8*>(ks + j * 512);
     };
@@ -753,12 +754,14 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillAr
     struct OpsY {
         half8 q[4];
         half4 y;
+        float4 d;                                // gamma_C / gamma_t of this lane's 4 tokens of tile w
     };
     auto load_qy = [&](OpsY& o, int c) {
         const uint16_t* qs = blk(A.Qt, c) + 4 * w * 512;
 #pragma unroll
         for (int p = 0; p < 4; ++p) o.q[p] = *reinterpret_cast<const half8*>(qs + p * 512);
         o.y = *reinterpret_cast<const half4*>(blk(A.Y0t, c) + (2 * vt + (w >> 1)) * 512 + 4 * (w & 1));
+        o.d = ld4(A.Dt + (hbase + c) * CHK + 16 * w + 4 * (lane >> 4));
     };
     // Y tile w of this slice: lane (r, q) holds tokens 16 w + 4 q .. +3 of
     // row 16 vt + r, as one 8-byte piece per lane
@@ -771,8 +774,8 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillAr
     float gv = load_g(0), gn = 0.0f;
 
     // One chunk: U tile w = U~ + (-W) S^T; Y tile w = Y0 + Q~ S^T (the
-    // chunk's outputs, off the chain); exchange U; S^T tiles <- gamma_C S^T +
-    // K~^T U; exchange S.
+    // chunk's outputs, off the chain); exchange D U; S^T tiles <- gamma_C S^T
+    // + K^T (D U); exchange S.
     auto step = [&](int c, Ops& o, OpsY& oy) {
         if ((c & 63) == 32) gn = load_g(c + 32);
         if ((c & 63) == 0 && c) gv = gn;
@@ -793,7 +796,9 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillAr
         __builtin_amdgcn_sched_barrier(0);
         load_w(o, cn);
         __builtin_amdgcn_sched_barrier(0);
-        const floatx4 us = u0 + u1;
+        // U's rows (tokens) scaled by gamma_C / gamma_t: the S update
+        // takes diag(gamma_C / gamma) U against the qk-head's K
+        const floatx4 us = (u0 + u1) * floatx4{oy.d.x, oy.d.y, oy.d.z, oy.d.w};
         om = fmaxf(om, max4abs(us));
         Ux[w][lane] = to_half4(us);
         floatx4 y0 = {(float)oy.y[0], (float)oy.y[1], (float)oy.y[2], (float)oy.y[3]};

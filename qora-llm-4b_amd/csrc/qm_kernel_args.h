@@ -69,9 +69,10 @@ struct GqaDecodeArgs {
 //   Wn, Qt  f16 [32][nc][8192]     -W = -T diag(beta*gamma) K and
 //                                   Q~ = diag(gamma) Q - P W
 //   Ut, Y0t f16 [32][nc][8192]     U~ = T diag(beta) V and Y0 = P U~
-//   Ktt     f16 [32][nc][8192]     K~^T = (diag(gamma_C / gamma) K)^T
+//   Ktt     f16 [16][nc][8192]     K^T per qk-head (normalised keys)
+//   Dt      f32 [32][nc][64]       gamma_C / gamma_t per token
 //   gC      f32 [32][nc]           gamma_C = prod of the chunk's decays
-//   Sc      f16 [32][nc][16384]    state entering each chunk
+//   Yt      f16 [32][nc][8192]     pre-norm outputs of the chunked path
 // The per-(head, chunk) blocks are stored in the MFMA fragment order the
 // scan and out kernels load them in (described at the scan kernel).
 #define QM_DN_CHUNK 64
@@ -92,6 +93,7 @@ struct DnPrefillArgs {
     uint16_t* Ut;
     uint16_t* Y0t;
     uint16_t* Ktt;
+    float* Dt;
     float* gC;
     // the scan's outputs Y (pre-norm) in f16, per (v-head, chunk) 8 slices x
     // 4 token tiles x 64 lanes x 4 tokens (fragment order)

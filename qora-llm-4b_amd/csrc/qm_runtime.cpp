@@ -226,7 +226,7 @@ int32_t load_function(qm_context* c, hipModule_t m, const char* name, hipFunctio
 
 namespace {
 struct DnPrefillLayout {
-    size_t Wn, Qt, Ut, Y0t, Ktt, gC, Yt, Yx, vstat, mode, total;
+    size_t Wn, Qt, Ut, Y0t, Ktt, Dt, gC, Yt, Yx, vstat, mode, total;
 };
 
 // GQA prefill workspace: the fragment-ordered K and V tile copy, then the
@@ -245,7 +245,8 @@ DnPrefillLayout dn_prefill_layout(int64_t T) {
     L.Qt = o; o += al(blk);
     L.Ut = o; o += al(blk);
     L.Y0t = o; o += al(blk);
-    L.Ktt = o; o += al(blk);
+    L.Ktt = o; o += al(blk / 2);
+    L.Dt = o; o += al(static_cast<size_t>(QM_DN_V_HEADS) * nc * QM_DN_CHUNK * 4);
     L.gC = o; o += al(static_cast<size_t>(QM_DN_V_HEADS) * nc * 4);
     L.Yt = o; o += al(blk);
     L.Yx = o; o += al(2 * blk);
@@ -806,6 +807,7 @@ int32_t qm_deltanet_prefill(qm_context* c, qm_stream stream, int32_t seq_len, co
                      reinterpret_cast<uint16_t*>(ws + L.Wn),
                      reinterpret_cast<uint16_t*>(ws + L.Qt), reinterpret_cast<uint16_t*>(ws + L.Ut),
                      reinterpret_cast<uint16_t*>(ws + L.Y0t), reinterpret_cast<uint16_t*>(ws + L.Ktt),
+                     reinterpret_cast<float*>(ws + L.Dt),
                      reinterpret_cast<float*>(ws + L.gC), reinterpret_cast<uint16_t*>(ws + L.Yt),
                      reinterpret_cast<float*>(ws + L.Yx),
                      reinterpret_cast<float*>(ws + L.vstat), reinterpret_cast<int32_t*>(ws + L.mode), seq_len, nc};
