@@ -72,27 +72,31 @@ QM_DEV void q4_accumulate(float (&acc)[8], uint32_t c, float sx) { q4_word(acc, 
 QM_DEV float xor_swz4(float x) {            // the value of lane l ^ 4 (ds_swizzle bit mode)
     return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x101F));
 }
-QM_DEV void halve32(float* v, int n) {      // n values -> n/2: lanes < 32 keep 0..n/2-1
+// (n is a template parameter: as a runtime argument the compiler did not
+// unroll these loops and indexed v through 16-way compare/select chains)
+template <int N>
+QM_DEV void halve32(float* v) {             // N values -> N/2: lanes < 32 keep 0..N/2-1
 #pragma unroll
-    for (int j = 0; j < n / 2; ++j) {
-        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[j]), __float_as_uint(v[j + n / 2]), false, false);
+    for (int j = 0; j < N / 2; ++j) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[j]), __float_as_uint(v[j + N / 2]), false, false);
         v[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
     }
 }
-QM_DEV void halve16(float* v, int n) {      // even 16-lane rows keep 0..n/2-1
+template <int N>
+QM_DEV void halve16(float* v) {             // even 16-lane rows keep 0..N/2-1
 #pragma unroll
-    for (int j = 0; j < n / 2; ++j) {
-        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[j]), __float_as_uint(v[j + n / 2]), false, false);
+    for (int j = 0; j < N / 2; ++j) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[j]), __float_as_uint(v[j + N / 2]), false, false);
         v[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
     }
 }
-template <int BIT>
-QM_DEV void halve_dpp(float* v, int n, int lane) {   // lanes with bit BIT clear keep 0..n/2-1
+template <int BIT, int N>
+QM_DEV void halve_dpp(float* v, int lane) {  // lanes with bit BIT clear keep 0..N/2-1
     const bool hi = (lane >> BIT) & 1;
 #pragma unroll
-    for (int j = 0; j < n / 2; ++j) {
-        const float keep = hi ? v[j + n / 2] : v[j];
-        const float send = hi ? v[j] : v[j + n / 2];
+    for (int j = 0; j < N / 2; ++j) {
+        const float keep = hi ? v[j + N / 2] : v[j];
+        const float send = hi ? v[j] : v[j + N / 2];
         const float got = BIT == 3 ? dpp_f32<0x128>(send) : xor_swz4(send);   // row_ror:8 = lane ^ 8
         v[j] = keep + got;
     }
@@ -103,12 +107,12 @@ template <int T> QM_DEV int q4_col(int lane) {
 }
 template <int T>
 QM_DEV float q4_wave_reduce(float (&v)[T], int lane) {
-    halve32(v, T);
-    halve16(v, T / 2);
-    halve_dpp<3>(v, T / 4, lane);
+    halve32<T>(v);
+    halve16<T / 2>(v);
+    halve_dpp<3, T / 4>(v, lane);
     float x;
     if (T == 16) {
-        halve_dpp<2>(v, 2, lane);
+        halve_dpp<2, 2>(v, lane);
         x = v[0];
     } else {
         x = v[0];
@@ -117,6 +121,14 @@ QM_DEV float q4_wave_reduce(float (&v)[T], int lane) {
     x += dpp_f32<0x4E>(x);                  // lane ^ 2
     x += dpp_f32<0xB1>(x);                  // lane ^ 1
     return x;
+}
+
+// base[idx] with a 32-bit byte offset from a wave-uniform base, so the load
+// takes the scalar-base + 32-bit vector-offset form (no 64-bit address
+// arithmetic per lane)
+template <class V>
+QM_DEV V ld_off(const V* base, uint32_t idx) {
+    return *reinterpret_cast<const V*>(reinterpret_cast<const char*>(base) + (size_t)(idx * (uint32_t)sizeof(V)));
 }
 
 template <bool GATE_UP, int T, int STEPS, int THREADS>
@@ -146,15 +158,15 @@ QM_DEV void q4_tile(const Q4GemvArgs& A, int p, int tile, float (*red)[33]) {
         float xv[STEPS];
 #pragma unroll
         for (int s = 0; s < STEPS; ++s) {
-            const int k = min(k0 + tid + THREADS * s, K - 1);
-            pk[s] = codes[k];
-            sc[s] = gsc[k];
+            const uint32_t k = min((uint32_t)(k0 + tid + THREADS * s), (uint32_t)(K - 1));
+            pk[s] = ld_off(codes, k);
+            sc[s] = ld_off(gsc, k);
             if (GATE_UP) {
-                pu[s] = codes_u[k];
-                su[s] = gsc_u[k];
+                pu[s] = ld_off(codes_u, k);
+                su[s] = ld_off(gsc_u, k);
             }
-            xv[s] = A.x[k];
-            nw[s] = nwp[k];
+            xv[s] = ld_off(A.x, k);
+            nw[s] = ld_off(nwp, k);
         }
 #pragma unroll
         for (int s = 0; s < STEPS; ++s) {
