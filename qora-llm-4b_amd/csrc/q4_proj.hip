@@ -168,11 +168,12 @@ QM_DEV void q4_tile(const Q4GemvArgs& A, int p, int tile, float (*red)[33]) {
             xv[s] = ld_off(A.x, k);
             nw[s] = ld_off(nwp, k);
         }
+        const bool full = k0 + THREADS * STEPS <= K;    // workgroup-uniform: every row valid
 #pragma unroll
         for (int s = 0; s < STEPS; ++s) {
             // rows past k (wave-uniform except in the last wave) add nothing
-            if (k0 + THREADS * s + (tid & ~63) >= K) break;
-            const float xl = k0 + tid + THREADS * s < K ? xv[s] : 0.0f;
+            if (!full && k0 + THREADS * s + (tid & ~63) >= K) break;
+            const float xl = full || k0 + tid + THREADS * s < K ? xv[s] : 0.0f;
             ss = fmaf(xl, xl, ss);
             const float xn = A.norm_w ? xl * (1.0f + f16_to_f32(nw[s])) : xl;   // gemv.rs:575 but inv_rms
             const float sx = f16_to_f32(sc[s]) * xn;                           // gemv.rs:429: scale * x_k
