@@ -744,8 +744,10 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillAr
 #pragma unroll
         for (int p = 0; p < 4; ++p) o.w[p] = *reinterpret_cast<const half8*>(ws + p * 512);
     };
-    auto load_uk = [&](Ops& o, int c) {
+    auto load_u = [&](Ops& o, int c) {
         o.u = *reinterpret_cast<const half4*>(blk(A.Ut, c) + (2 * vt + (w >> 1)) * 512 + 4 * (w & 1));
+    };
+    auto load_k = [&](Ops& o, int c) {
         const uint16_t* ks = A.Ktt + (kbase + c) * (CHK * QM_DN_HD) + (size_t)lane * 8 + 4 * w * 512;
 #pragma unroll
         for (int j = 0; j < 4; ++j) o.k[j] = *reinterpret_cast<const half8*>(ks + j * 512);
@@ -761,6 +763,8 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillAr
 #pragma unroll
         for (int p = 0; p < 4; ++p) o.q[p] = *reinterpret_cast<const half8*>(qs + p * 512);
         o.y = *reinterpret_cast<const half4*>(blk(A.Y0t, c) + (2 * vt + (w >> 1)) * 512 + 4 * (w & 1));
+    };
+    auto load_d = [&](OpsY& o, int c) {
         o.d = ld4(A.Dt + (hbase + c) * CHK + 16 * w + 4 * (lane >> 4));
     };
     // Y tile w of this slice: lane (r, q) holds tokens 16 w + 4 q .. +3 of
@@ -776,37 +780,47 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillAr
     // One chunk: U tile w = U~ + (-W) S^T; Y tile w = Y0 + Q~ S^T (the
     // chunk's outputs, off the chain); exchange D U; S^T tiles <- gamma_C S^T
     // + K^T (D U); exchange S.
+    // A wave's ~15 operand loads per chunk (1 KB each) take the CU's
+    // address unit ~16 cycles apiece, ~960 cycles per chunk for the four
+    // waves.  Each register set's next load is issued right after the
+    // instruction that consumes it, so the loads drain while the wave waits
+    // on MFMA and LDS latency (issued together after the state update they
+    // held every wave ~700 cycles per chunk).
     auto step = [&](int c, Ops& o, OpsY& oy) {
         if ((c & 63) == 32) gn = load_g(c + 32);
         if ((c & 63) == 0 && c) gv = gn;
         const float g = readlane_f32(gv, c & 63);
+        const int cn = min(c + 4, nc - 1), cy = min(c + 2, nc - 1);
         half8 sb[4];
 #pragma unroll
         for (int p = 0; p < 4; ++p) sb[p] = Sx[p][lane];
         floatx4 u0 = {(float)o.u[0], (float)o.u[1], (float)o.u[2], (float)o.u[3]};
         floatx4 u1 = {0.0f, 0.0f, 0.0f, 0.0f};
+        __builtin_amdgcn_sched_barrier(0);
+        load_u(o, cn);
+        __builtin_amdgcn_sched_barrier(0);
         u0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.w[0], sb[0], u0, 0, 0, 0);
         u1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.w[1], sb[1], u1, 0, 0, 0);
         u0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.w[2], sb[2], u0, 0, 0, 0);
         u1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.w[3], sb[3], u1, 0, 0, 0);
-        // this chunk's -W is consumed: fetch chunk c + 4's now, the rest of
-        // its operands after the state update, so the loads are spread over
-        // the chunk
-        const int cn = min(c + 4, nc - 1);
         __builtin_amdgcn_sched_barrier(0);
         load_w(o, cn);
         __builtin_amdgcn_sched_barrier(0);
-        // U's rows (tokens) scaled by gamma_C / gamma_t: the S update
-        // takes diag(gamma_C / gamma) U against the qk-head's K
-        const floatx4 us = (u0 + u1) * floatx4{oy.d.x, oy.d.y, oy.d.z, oy.d.w};
-        om = fmaxf(om, max4abs(us));
-        Ux[w][lane] = to_half4(us);
         floatx4 y0 = {(float)oy.y[0], (float)oy.y[1], (float)oy.y[2], (float)oy.y[3]};
         floatx4 y1 = {0.0f, 0.0f, 0.0f, 0.0f};
         y0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(oy.q[0], sb[0], y0, 0, 0, 0);
         y1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(oy.q[1], sb[1], y1, 0, 0, 0);
         y0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(oy.q[2], sb[2], y0, 0, 0, 0);
         y1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(oy.q[3], sb[3], y1, 0, 0, 0);
+        // U's rows (tokens) scaled by gamma_C / gamma_t: the S update
+        // takes diag(gamma_C / gamma) U against the qk-head's K
+        const floatx4 us = (u0 + u1) * floatx4{oy.d.x, oy.d.y, oy.d.z, oy.d.w};
+        Ux[w][lane] = to_half4(us);
+        __builtin_amdgcn_sched_barrier(0);
+        load_qy(oy, cy);
+        load_d(oy, cy);
+        __builtin_amdgcn_sched_barrier(0);
+        om = fmaxf(om, max4abs(us));
         __syncthreads();
         half8 ub[2];
 #pragma unroll
@@ -818,16 +832,14 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillAr
             for (int p = 0; p < 2; ++p)
                 S[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.k[2 * t + p], ub[p], S[t], 0, 0, 0);
         }
+        __builtin_amdgcn_sched_barrier(0);
+        load_k(o, cn);
+        __builtin_amdgcn_sched_barrier(0);
         const half8 mine = cat8(to_half4(S[0]), to_half4(S[1]));
-        om = fmaxf(om, fmaxf(max4abs(S[0]), max4abs(S[1])));
-        const floatx4 ys = y0 + y1;
-        om = fmaxf(om, max4abs(ys));
-        y_store(c, to_half4(ys));
-        __builtin_amdgcn_sched_barrier(0);
-        load_uk(o, cn);
-        load_qy(oy, min(c + 2, nc - 1));
-        __builtin_amdgcn_sched_barrier(0);
         Sx[w][lane] = mine;
+        const floatx4 ys = y0 + y1;
+        y_store(c, to_half4(ys));
+        om = fmaxf(om, fmaxf(fmaxf(max4abs(S[0]), max4abs(S[1])), max4abs(ys)));
         __syncthreads();
     };
 
@@ -838,8 +850,9 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillAr
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         load_w(ops[i], min(i, nc - 1));
-        load_uk(ops[i], min(i, nc - 1));
-        if (i < 2) load_qy(opy[i], min(i, nc - 1));
+        load_u(ops[i], min(i, nc - 1));
+        load_k(ops[i], min(i, nc - 1));
+        if (i < 2) { load_qy(opy[i], min(i, nc - 1)); load_d(opy[i], min(i, nc - 1)); }
         __builtin_amdgcn_sched_barrier(0);
     }
     {
