@@ -571,8 +571,7 @@ __device__ __forceinline__ void q4_gemm_body(const Q4GemmArgs& A) {
             }
             if (GU || A.y_bf16)
                 *reinterpret_cast<uint2*>(A.y_bf16 + o) =
-                    make_uint2((uint32_t)f32_to_bf16(y.x) | ((uint32_t)f32_to_bf16(y.y) << 16),
-                               (uint32_t)f32_to_bf16(y.z) | ((uint32_t)f32_to_bf16(y.w) << 16));
+                    make_uint2(pack_bf16x2(y.x, y.y), pack_bf16x2(y.z, y.w));
             else
                 *reinterpret_cast<float4*>(A.y + o) = y;
         }

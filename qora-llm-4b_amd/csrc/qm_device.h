@@ -69,11 +69,14 @@ QM_DEV float wave_sum64(float x) {
 QM_DEV float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 QM_DEV uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 QM_DEV float bf16_to_f32(uint16_t h) { return __builtin_bit_cast(float, (uint32_t)h << 16); }
-QM_DEV uint16_t f32_to_bf16(float f) {   // round to nearest even
-    uint32_t x = __builtin_bit_cast(uint32_t, f);
-    if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
-    x += 0x7fffu + ((x >> 16) & 1u);
-    return (uint16_t)(x >> 16);
+// f32 -> bf16, round to nearest even: one v_cvt_pk_bf16_f32 (gfx950) per
+// pair of values, where the integer form (NaN test, bias, carry) took ~6
+// VALU ops per value.  NaN stays NaN.
+QM_DEV uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+QM_DEV uint32_t pack_bf16x2(float lo, float hi) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
 }
 
 // ---- scalar math (gemv.rs:631-659 semantics) -----------------------------
