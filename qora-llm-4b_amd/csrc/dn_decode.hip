@@ -85,9 +85,17 @@ QM_DEV void dn_decode_body(const DnDecodeArgs& A) {
     const float* act = A.act + (size_t)b * QM_DN_QKV_DIM;
     float* S = A.state + (size_t)b * A.state_stride + (size_t)vh * QM_DN_HEAD_ELEMS;
 
-    // Issue the state loads first: they are the HBM stream.  Group g owns
-    // rows g, g + GROUPS, ...; at each i the groups of a wave cover
-    // consecutive rows, so every wave instruction reads contiguous 2 KB.
+    // q and k first: a wave's loads return in issue order, so their norms
+    // (and the gates, from scalar loads) run while the state rows are in
+    // flight.  Then the state, the HBM stream: group g owns rows g,
+    // g + GROUPS, ...; at each i the groups of a wave cover consecutive
+    // rows, so every wave instruction reads contiguous 2 KB.
+    float4 q0 = ld4(act + qkh * QM_DN_HD + 4 * l), q1 = ld4(act + qkh * QM_DN_HD + 64 + 4 * l);
+    float4 k0 = ld4(act + 2048 + qkh * QM_DN_HD + 4 * l), k1 = ld4(act + 2048 + qkh * QM_DN_HD + 64 + 4 * l);
+    float vr[RPG];
+#pragma unroll
+    for (int i = 0; i < RPG; ++i) vr[i] = act[2 * 2048 + vh * QM_DN_HD + g + GROUPS * i];
+    __builtin_amdgcn_sched_barrier(0);           // keep these loads ahead of the state's
     float4 s0[RPG], s1[RPG];
 #pragma unroll
     for (int i = 0; i < RPG; ++i) {
@@ -95,21 +103,17 @@ QM_DEV void dn_decode_body(const DnDecodeArgs& A) {
         s0[i] = ld4(row + 4 * l);
         s1[i] = ld4(row + 64 + 4 * l);
     }
-    float vr[RPG];
-#pragma unroll
-    for (int i = 0; i < RPG; ++i) vr[i] = act[2 * 2048 + vh * QM_DN_HD + g + GROUPS * i];
     // The epilogue's inputs (norm weight, z gate) do not depend on the
     // update: fetch them with the state so the norm costs no extra round trip.
-    float zz = 0.0f, nw = 0.0f;
+    float zz = 0.0f;
+    uint32_t nw_bits = 0;                        // converted where it is used, after the update
     if (tid < QM_DN_HD) {
         zz = A.z[(size_t)b * QM_DN_V_DIM + vh * QM_DN_HD + tid];
-        nw = f16_to_f32(A.norm_w[tid]);
+        nw_bits = A.norm_w[tid];
     }
     const float a_in = A.a[b * QM_DN_V_HEADS + vh], b_in = A.b[b * QM_DN_V_HEADS + vh];
     const float a_log = A.a_log[vh], dt_bias = A.dt_bias[vh];
 
-    float4 q0 = ld4(act + qkh * QM_DN_HD + 4 * l), q1 = ld4(act + qkh * QM_DN_HD + 64 + 4 * l);
-    float4 k0 = ld4(act + 2048 + qkh * QM_DN_HD + 4 * l), k1 = ld4(act + 2048 + qkh * QM_DN_HD + 64 + 4 * l);
     l2norm_row(q0, q1, 0.08838834764831845f);    // q *= 1/sqrt(128)
     l2norm_row(k0, k1, 1.0f);
 
@@ -143,6 +147,8 @@ QM_DEV void dn_decode_body(const DnDecodeArgs& A) {
         const float y0 = ys[ln], y1 = ys[64 + ln];
         const float ss = wave_sum64(fmaf(y1, y1, y0 * y0));
         const float inv_rms = __builtin_amdgcn_rsqf(ss * (1.0f / (float)QM_DN_HD) + 1e-6f);
+        asm volatile("" : "+v"(nw_bits));
+        const float nw = f16_to_f32((uint16_t)nw_bits);
         A.out[(size_t)b * QM_DN_V_DIM + vh * QM_DN_HD + tid] = ys[tid] * inv_rms * (nw * silu_fast(zz));
     }
 }
