@@ -59,16 +59,13 @@ QM_DEV void l2norm_row(float4& x0, float4& x1, float scale) {
     x1 = scale4(x1, inv);
 }
 
-// The gates on the hardware transcendentals (v_exp_f32 / v_log_f32 / v_rcp_f32,
-// a few ulp from libm): every thread of a workgroup evaluates them, and on a
-// 16-lane SIMD each wave64 VALU instruction takes 4 cycles, so libm's
-// expansions were a large part of a batch-1 step.  gemv.rs:788-800:
-// alpha = exp(-exp(A_log) softplus(a + dt_bias)), softplus(x) = x above 20,
-// else ln(1 + e^x); beta = sigmoid(b).
-QM_DEV float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
-QM_DEV float softplus_fast(float x) {
-    return x > 20.0f ? x : __builtin_amdgcn_logf(1.0f + exp_fast(x)) * 0.6931471805599453f;
-}
+// The gates on the hardware transcendentals (exp_fast, softplus_fast,
+// sigmoid_fast: v_exp_f32 / v_log_f32 / v_rcp_f32, a few ulp from libm):
+// every thread of a workgroup evaluates them, and on a 16-lane SIMD each
+// wave64 VALU instruction takes 4 cycles, so libm's expansions were a large
+// part of a batch-1 step.  gemv.rs:788-800: alpha = exp(-exp(A_log)
+// softplus(a + dt_bias)), softplus(x) = x above 20, else ln(1 + e^x);
+// beta = sigmoid(b).
 
 template <int RPG>
 QM_DEV void dn_decode_body(const DnDecodeArgs& A) {

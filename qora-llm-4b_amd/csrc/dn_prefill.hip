@@ -123,14 +123,6 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
         int chb[2];                                // first channel of this thread, per part
         chb[0] = hh * QM_DN_QK_DIM + qkh * QM_DN_HD + 8 * cg;          // q or k
         chb[1] = 2 * QM_DN_QK_DIM + h * QM_DN_HD + 8 * cg;             // v of head h
-        // gate inputs (wave 0 of each head) first: they are consumed last
-        float ga = 0.0f, gb = 0.0f;
-        if (ht < CHK) {
-            const int t = min(t0 + ht, A.T - 1);
-            ga = A.a[(size_t)t * QM_DN_V_HEADS + h];
-            gb = A.b[(size_t)t * QM_DN_V_HEADS + h];
-        }
-        const float a_log_h = A.a_log[h], dt_bias_h = A.dt_bias[h];
         // all 14 raw rows the thread needs (7 per part), loaded at clamped,
         // always valid rows before any arithmetic; rows before the sequence
         // come from the conv buffer, and the tokens past it are zeroed below
@@ -145,6 +137,17 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
         float4 wt[8], wn[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) wt[e] = ld4(A.conv_w + (size_t)(chb[0] + e) * 4);
+        // gate inputs (wave 0 of each head), consumed last: requested here,
+        // after the rows (a wave's loads return in issue order, and these
+        // 4-byte loads touch one cache line per token), but before the
+        // arithmetic, so that they are not a round trip of their own
+        float ga = 0.0f, gb = 0.0f;
+        if (ht < CHK) {
+            const int t = min(t0 + ht, A.T - 1);
+            ga = A.a[(size_t)t * QM_DN_V_HEADS + h];
+            gb = A.b[(size_t)t * QM_DN_V_HEADS + h];
+        }
+        const float a_log_h = A.a_log[h], dt_bias_h = A.dt_bias[h];
         const bool tail = t0 + CHK > A.T;          // last chunk, partly past the sequence
         float vm[8];                               // max |v| per channel over this thread's valid tokens
 #pragma unroll
@@ -176,9 +179,16 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         const float cbv = A.conv_buf[(size_t)(ch0 + e) * 3 + 3 + tb];
-                        if (t < 0) x[r][e] = cbv;
+                        x[r][e] = t < 0 ? cbv : x[r][e];
                     }
                 }
+                // the selects complete here, inside the branch: no load of it
+                // is then pending where the paths join, and other chunks'
+                // arithmetic waits only for the rows it uses
+#pragma unroll
+                for (int r = 0; r < 3; ++r)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(x[r][e]));
             }
             _Float16 (*dst)[136] = part == 1 ? Vs : (hh == 0 ? Qs : Ks);
             const float scale = (part == 0 && hh == 0) ? 1.0f / sqrtf((float)QM_DN_HD) : 1.0f;
@@ -244,32 +254,42 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
             // log alpha = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b);
             // padded tokens get alpha = 1, beta = 0 (no effect on the state);
             // then the inclusive prefix sum over the chunk (one wave)
+            // (the hardware transcendentals, a few ulp from libm: with libm
+            // these two waves' gates delayed the workgroup barrier by ~2K cycles)
             float g = 0.0f, be = 0.0f;
+            // opaque here, so that the compiler does not start this
+            // arithmetic next to the loads (a wait for every earlier load)
+            asm volatile("" : "+v"(ga), "+v"(gb));
             if (t0 + ht < A.T) {
-                g = -expf(a_log_h) * softplus_f(ga + dt_bias_h);
-                be = 1.0f / (1.0f + expf(-gb));
+                g = -exp_fast(a_log_h) * softplus_fast(ga + dt_bias_h);
+                be = sigmoid_fast(gb);
             }
 #pragma unroll
             for (int off = 1; off < 64; off <<= 1) {
                 const float o = __shfl_up(g, off);
                 if (ht >= off) g += o;
             }
+            const float eg = exp_fast(g);
             Gs[ht] = g;
             Bs[ht] = be;
-            Eg[ht] = expf(g);                   // gamma_i
-            BG[ht] = be * expf(g);              // beta_i gamma_i
+            Eg[ht] = eg;                        // gamma_i
+            BG[ht] = be * eg;                   // beta_i gamma_i
         }
     }
     __syncthreads();
-    if (ht < CHK) Kd[ht] = expf(Gs[CHK - 1] - Gs[ht]);       // gamma_C / gamma_i
+    if (ht < CHK) Kd[ht] = exp_fast(Gs[CHK - 1] - Gs[ht]);   // gamma_C / gamma_i
 
     // ---- 1. KK^T and QK^T (16x16x32 f16), masked and decayed -> A, P (f16).
     //      Computed transposed, C = K_j K_i^T and K_j Q_i^T: lane (lr, lq)
     //      then holds row i = 16w + lr, columns 16j + 4lq .. +3, one 8-byte
     //      store per matrix and tile.  Decays exp(G_i - G_jj) on v_exp_f32
     //      with the exponent clamped at 0 (the masked upper part).
+    //      Row tile w of head 0 has w + 1 column tiles; head 1 takes its
+    //      row tiles in the opposite order, so that the two waves sharing a
+    //      SIMD (w and w + 4) have five tiles between them.
     {
-        const int i = 16 * w + lr;
+        const int rt = hh ? 3 - w : w;
+        const int i = 16 * rt + lr;
         const float gi = Gs[i], bi = Bs[i];
         half8 bk[4], bq[4];                        // B operands: row i's k, q
 #pragma unroll
@@ -279,7 +299,7 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
         }
         for (int j = 0; j < 4; ++j) {
             half4 ha = {}, hp = {};
-            if (j <= w) {                          // wave-uniform
+            if (j <= rt) {                         // wave-uniform
                 floatx4 ckk = {0.0f, 0.0f, 0.0f, 0.0f}, cqk = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
@@ -450,7 +470,7 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
         }
     }
     if (ht < CHK) A.Dt[hc * CHK + ht] = Kd[ht];
-    if (ht == 0) A.gC[hc] = expf(Gs[CHK - 1]);
+    if (ht == 0) A.gC[hc] = exp_fast(Gs[CHK - 1]);
 
     // ---- 6. precision guard statistics: each v channel's max |v| over the
     //      chunk, and +inf in channel 0 if an f16 operand would overflow

@@ -102,6 +102,11 @@ QM_DEV float silu_fast(float x) {
     return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
 }
 QM_DEV float softplus_f(float x) { return x > 20.0f ? x : logf(1.0f + expf(x)); }
+// e^x and ln(1 + e^x) on v_exp_f32 / v_log_f32 (a few ulp from libm)
+QM_DEV float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+QM_DEV float softplus_fast(float x) {
+    return x > 20.0f ? x : __builtin_amdgcn_logf(1.0f + exp_fast(x)) * 0.6931471805599453f;
+}
 QM_DEV float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
 // 1 / (1 + 2^(-x log2 e)) on v_exp_f32 / v_rcp_f32 (about 1 ulp each)
 QM_DEV float sigmoid_fast(float x) {
