@@ -76,6 +76,10 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_prefill_kv(GqaPrefillAr
     // K: wave w normalises and rotates tokens t0+16w .. t0+16w+15.  All 16
     // rows are loaded (at clamped, valid rows) before any arithmetic, so the
     // wave waits for one memory round trip, not one per token.
+    // V's rows are requested right after K's (their conversion waits until
+    // K is done, and a wave's loads return in issue order).
+    const int vi = tid >> 2, vp = tid & 3, vt = t0 + vi;
+    uint4 vraw[8];
     {
         uint2 raw[16];
 #pragma unroll
@@ -84,19 +88,34 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_prefill_kv(GqaPrefillAr
             raw[j] = *reinterpret_cast<const uint2*>(A.k + ((size_t)t * QM_GQA_KV_HEADS + g) * QM_GQA_HD + 4 * lane);
         }
         const uint2 gw = *reinterpret_cast<const uint2*>(A.k_norm + 4 * lane);
+        // RoPE rows four tokens at a time, loaded by every lane (lanes 0..15
+        // use them) so no per-token branch serializes the loads; each group's
+        // rows are requested one group ahead
+        const int i0 = (lane & 7) * 4;
+        float4 cr[2][4], sr[2][4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            const int tc = min(t0 + 16 * w + jj, A.S - 1);
+            cr[0][jj] = ld4(A.rope_cos + (size_t)tc * 32 + i0);
+            sr[0][jj] = ld4(A.rope_sin + (size_t)tc * 32 + i0);
+        }
+        {
+            const uint16_t* vrow = A.v + ((size_t)min(vt, A.S - 1) * QM_GQA_KV_HEADS + g) * QM_GQA_HD + 8 * vp;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) vraw[q] = *reinterpret_cast<const uint4*>(vrow + 32 * q);
+        }
         const float g1[4] = {1.0f + f16_to_f32((uint16_t)(gw.x & 0xffffu)), 1.0f + f16_to_f32((uint16_t)(gw.x >> 16)),
                              1.0f + f16_to_f32((uint16_t)(gw.y & 0xffffu)), 1.0f + f16_to_f32((uint16_t)(gw.y >> 16))};
-        // RoPE rows four tokens at a time, loaded by every lane (lanes 0..15
-        // use them) so no per-token branch serializes the loads
-        const int i0 = (lane & 7) * 4;
 #pragma unroll
         for (int jb = 0; jb < 16; jb += 4) {
-            float4 cr[4], sr[4];
+            const int cb = (jb >> 2) & 1;
+            if (jb + 4 < 16) {
 #pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-                const int tc = min(t0 + 16 * w + jb + jj, A.S - 1);
-                cr[jj] = ld4(A.rope_cos + (size_t)tc * 32 + i0);
-                sr[jj] = ld4(A.rope_sin + (size_t)tc * 32 + i0);
+                for (int jj = 0; jj < 4; ++jj) {
+                    const int tc = min(t0 + 16 * w + jb + 4 + jj, A.S - 1);
+                    cr[cb ^ 1][jj] = ld4(A.rope_cos + (size_t)tc * 32 + i0);
+                    sr[cb ^ 1][jj] = ld4(A.rope_sin + (size_t)tc * 32 + i0);
+                }
             }
 #pragma unroll
             for (int jj = 0; jj < 4; ++jj) {
@@ -114,8 +133,8 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_prefill_kv(GqaPrefillAr
                 // x1 c - x2 s (lanes 0..7), x2 c + x1 s (lanes 8..15)
                 const float4 ps = lane < 8 ? make_float4(-pr.x, -pr.y, -pr.z, -pr.w) : pr;
                 float4 y;
-                y.x = x.x * cr[jj].x + ps.x * sr[jj].x; y.y = x.y * cr[jj].y + ps.y * sr[jj].y;
-                y.z = x.z * cr[jj].z + ps.z * sr[jj].z; y.w = x.w * cr[jj].w + ps.w * sr[jj].w;
+                y.x = x.x * cr[cb][jj].x + ps.x * sr[cb][jj].x; y.y = x.y * cr[cb][jj].y + ps.y * sr[cb][jj].y;
+                y.z = x.z * cr[cb][jj].z + ps.z * sr[cb][jj].z; y.w = x.w * cr[cb][jj].w + ps.w * sr[cb][jj].w;
                 if (lane < 16) x = y;
                 uint2 h = make_uint2(0, 0);
                 if (t < A.S) {                                    // wave-uniform
@@ -128,14 +147,11 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_prefill_kv(GqaPrefillAr
     }
     // V: rows to the cache, and into LDS for the V^T tile copy.  The four
     // threads of a token cover 32 consecutive dims per step (64-byte
-    // pieces), and all eight raw loads (at a clamped, valid row) are issued
-    // before any conversion.
+    // pieces); all eight raw loads (at a clamped, valid row) were issued
+    // with K's.
     {
-        const int i = tid >> 2, p = tid & 3, t = t0 + i;
-        const uint16_t* vrow = A.v + ((size_t)min(t, A.S - 1) * QM_GQA_KV_HEADS + g) * QM_GQA_HD + 8 * p;
-        uint4 raw[8];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) raw[q] = *reinterpret_cast<const uint4*>(vrow + 32 * q);
+        const int i = vi, p = vp, t = vt;
+        const uint4 (&raw)[8] = vraw;
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
             uint4 h16 = make_uint4(0, 0, 0, 0);
