@@ -44,9 +44,13 @@ QM_DEV half8 cat8(half4 a, half4 b) {
     return half8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
-// largest magnitude of four values (what an f16 conversion must hold)
-QM_DEV float max4abs(floatx4 v) {
-    return fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+// max(m, |v0|, .., |v3|): the running largest magnitude that an f16
+// conversion must hold.  IEEE maximum (NaN-propagating, so a NaN also fails
+// the f16 range check) compiles to two v_maximum3_f32 with abs modifiers;
+// fmaxf's maxNum needs a canonicalising max per MFMA result first.
+QM_DEV float max_abs(float m, float a) { return __builtin_elementwise_maximum(m, fabsf(a)); }
+QM_DEV float max_abs4(float m, floatx4 v) {
+    return max_abs(max_abs(max_abs(max_abs(m, v[0]), v[1]), v[2]), v[3]);
 }
 
 QM_DEV half4 to_half4(floatx4 v) {
@@ -205,10 +209,10 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
                     sacc = fmaf(x[j + 3][e], wt[e].w, sacc);
                     v[e] = silu_fast(sacc);
                 }
-                if (part == 1) {
-                    const bool ok = t0 + tok < A.T;
+                // (tail is wave-uniform: interior chunks take every token)
+                if (part == 1 && (!tail || t0 + tok < A.T)) {
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) vm[e] = fmaxf(vm[e], ok ? fabsf(v[e]) : 0.0f);
+                    for (int e = 0; e < 8; ++e) vm[e] = max_abs(vm[e], v[e]);
                 }
                 if (part == 0) {
                     // x /= ||x|| when ||x|| > 1e-12, q *= 1/sqrt(128)
@@ -231,8 +235,11 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
         // lanes cg, cg+16, cg+32, cg+48 of a wave hold the same channels
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            vm[e] = max_xor32(max_xor16(vm[e]));
-            om = fmaxf(om, vm[e]);
+            const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(vm[e]), __float_as_uint(vm[e]), false, false);
+            const float m16 = __builtin_elementwise_maximum(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+            const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(m16), __float_as_uint(m16), false, false);
+            vm[e] = __builtin_elementwise_maximum(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+            om = __builtin_elementwise_maximum(om, vm[e]);
         }
         if ((lane >> 4) == 0) {
 #pragma unroll
@@ -335,7 +342,7 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
 #pragma unroll
             for (int j = 0; j < i; ++j) v -= (float)(j < 8 ? r0[j] : r1[j - 8]) * t[j];
             t[i] = v;
-            om = fmaxf(om, fabsf(v));
+            om = max_abs(om, v);
         }
 #pragma unroll
         for (int i = 0; i < 16; ++i) Td[w][i][m] = (_Float16)t[i];
@@ -365,7 +372,7 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
             }
             floatx4 x = {0.0f, 0.0f, 0.0f, 0.0f};
             x = __builtin_amdgcn_mfma_f32_16x16x16f16(tb, to_half4(r), x, 0, 0, 0);
-            om = fmaxf(om, fmaxf(max4abs(r), max4abs(x)));
+            om = max_abs4(max_abs4(om, r), x);
             xh[b][cc] = to_half4(x);
             if (cc >= 2) cu[b][cc - 2] = x;
         }
@@ -403,7 +410,7 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int cc = 0; cc < 2; ++cc) om = fmaxf(om, fmaxf(max4abs(cq[i][cc]), max4abs(cy[i][cc])));
+        for (int cc = 0; cc < 2; ++cc) om = max_abs4(max_abs4(om, cq[i][cc]), cy[i][cc]);
 
     // ---- 5. outputs, all in the scan's fragment order (16-byte pieces; see
     //      the scan kernel for the piece layouts)
@@ -858,8 +865,9 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillAr
         load_qy(oy, cy);
         load_d(oy, cy);
         __builtin_amdgcn_sched_barrier(0);
-        om = fmaxf(om, max4abs(us));
         __syncthreads();
+        // the range checks come after the barriers, off the chain's path
+        om = max_abs4(om, us);
         half8 ub[2];
 #pragma unroll
         for (int p = 0; p < 2; ++p) ub[p] = cat8(Ux[2 * p][lane], Ux[2 * p + 1][lane]);
@@ -877,8 +885,8 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillAr
         Sx[w][lane] = mine;
         const floatx4 ys = y0 + y1;
         y_store(c, to_half4(ys));
-        om = fmaxf(om, fmaxf(fmaxf(max4abs(S[0]), max4abs(S[1])), max4abs(ys)));
         __syncthreads();
+        om = max_abs4(max_abs4(max_abs4(om, S[0]), S[1]), ys);
     };
 
     // four chunks of the chain's operands and two of the outputs' operands
@@ -895,7 +903,7 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillAr
     }
     {
         const half8 mine = cat8(to_half4(S[0]), to_half4(S[1]));
-        om = fmaxf(om, fmaxf(max4abs(S[0]), max4abs(S[1])));
+        om = max_abs4(max_abs4(om, S[0]), S[1]);
         Sx[w][lane] = mine;
     }
     __syncthreads();
