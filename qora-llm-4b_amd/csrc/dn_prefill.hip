@@ -63,7 +63,7 @@ QM_DEV half4 to_half4(floatx4 v) {
 struct ChunkHeadLds {
     _Float16 Vs[CHK][136];                         // v row-major
     _Float16 pm[CHK][72];                          // P (lower, incl. diagonal)
-    _Float16 am[CHK][72];                          // A (strictly lower)
+    _Float16 am[CHK][72];                          // -A (strictly lower), the sign the solve uses
     _Float16 Td[4][16][24];                        // (I + A_bb)^-1
     __attribute__((aligned(16))) float Gs[CHK];
     float Bs[CHK], Eg[CHK], BG[CHK];
@@ -286,7 +286,7 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
     __syncthreads();
     if (ht < CHK) Kd[ht] = exp_fast(Gs[CHK - 1] - Gs[ht]);   // gamma_C / gamma_i
 
-    // ---- 1. KK^T and QK^T (16x16x32 f16), masked and decayed -> A, P (f16).
+    // ---- 1. KK^T and QK^T (16x16x32 f16), masked and decayed -> -A, P (f16).
     //      Computed transposed, C = K_j K_i^T and K_j Q_i^T: lane (lr, lq)
     //      then holds row i = 16w + lr, columns 16j + 4lq .. +3, one 8-byte
     //      store per matrix and tile.  Decays exp(G_i - G_jj) on v_exp_f32
@@ -320,7 +320,7 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
                 for (int e = 0; e < 4; ++e) {
                     const int jj = 16 * j + 4 * lq + e;
                     const float dec = __builtin_amdgcn_exp2f(fminf(gi - gjv[e], 0.0f) * 1.4426950408889634f);
-                    ha[e] = (_Float16)(jj < i ? bi * dec * ckk[e] : 0.0f);
+                    ha[e] = (_Float16)(jj < i ? -(bi * dec) * ckk[e] : 0.0f);
                     hp[e] = (_Float16)(jj <= i ? dec * cqk[e] : 0.0f);
                 }
             }
@@ -340,7 +340,7 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
             const half8 r1 = *reinterpret_cast<const half8*>(&Am[b0 + i][b0 + 8]);
             float v = (i == m) ? 1.0f : 0.0f;
 #pragma unroll
-            for (int j = 0; j < i; ++j) v -= (float)(j < 8 ? r0[j] : r1[j - 8]) * t[j];
+            for (int j = 0; j < i; ++j) v += (float)(j < 8 ? r0[j] : r1[j - 8]) * t[j];
             t[i] = v;
             om = max_abs(om, v);
         }
@@ -363,11 +363,14 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int tk = 16 * b + 4 * lq + e;
-                r[e] = cc < 2 ? BG[tk] * (float)Ks[tk][col] : Bs[tk] * (float)Vs[tk][col];
+                // fma(h, s, 0) is the product, as one v_fma_mix_f32 that
+                // also widens the f16 operand
+                r[e] = cc < 2 ? __builtin_fmaf((float)Ks[tk][col], BG[tk], 0.0f)
+                              : __builtin_fmaf((float)Vs[tk][col], Bs[tk], 0.0f);
             }
 #pragma unroll
             for (int k = 0; k < b; ++k) {
-                const half4 an = -*reinterpret_cast<const half4*>(&Am[16 * b + lr][16 * k + 4 * lq]);
+                const half4 an = *reinterpret_cast<const half4*>(&Am[16 * b + lr][16 * k + 4 * lq]);
                 r = __builtin_amdgcn_mfma_f32_16x16x16f16(an, xh[k][cc], r, 0, 0, 0);
             }
             floatx4 x = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -389,19 +392,23 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int tk = 16 * i + 4 * lq + e;
-                cq[i][cc][e] = Eg[tk] * (float)Qs[tk][col];
+                cq[i][cc][e] = __builtin_fmaf((float)Qs[tk][col], Eg[tk], 0.0f);
             }
             cy[i][cc] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
         }
+    // -W fragments: the B operands of Q~ and, transposed, the -W output
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) xh[i][cc] = -xh[i][cc];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
         for (int kt = 0; kt <= i; ++kt) {
             const half4 ap = *reinterpret_cast<const half4*>(&Pm[16 * i + lr][16 * kt + 4 * lq]);
-            const half4 an = -ap;
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc) {
-                cq[i][cc] = __builtin_amdgcn_mfma_f32_16x16x16f16(an, xh[kt][cc], cq[i][cc], 0, 0, 0);
+                cq[i][cc] = __builtin_amdgcn_mfma_f32_16x16x16f16(ap, xh[kt][cc], cq[i][cc], 0, 0, 0);
                 cy[i][cc] = __builtin_amdgcn_mfma_f32_16x16x16f16(ap, xh[kt][cc + 2], cy[i][cc], 0, 0, 0);
             }
         }
@@ -447,7 +454,7 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
         uint16_t* qdst = A.Qt + hc * CHK * QM_DN_HD;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const half4 w0 = transpose(-xh[i][0]), w1 = transpose(-xh[i][1]);
+            const half4 w0 = transpose(xh[i][0]), w1 = transpose(xh[i][1]);
             const half4 q0 = transpose(to_half4(cq[i][0])), q1 = transpose(to_half4(cq[i][1]));
             const size_t o = (size_t)((4 * i + w) * 64 + lane) * 8;
             *reinterpret_cast<half8*>(wdst + o) = cat8(w0, w1);
