@@ -409,7 +409,10 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc) {
                 cq[i][cc] = __builtin_amdgcn_mfma_f32_16x16x16f16(ap, xh[kt][cc], cq[i][cc], 0, 0, 0);
-                cy[i][cc] = __builtin_amdgcn_mfma_f32_16x16x16f16(ap, xh[kt][cc + 2], cy[i][cc], 0, 0, 0);
+                // Y0^T = U~^T P^T, transposed by swapping the operands: the U~
+                // fragment as A and the P fragment as B (lane (r, q) then
+                // holds v-cols 16 vt + 4q .. +3 of token 16 i + r)
+                cy[i][cc] = __builtin_amdgcn_mfma_f32_16x16x16f16(xh[kt][cc + 2], ap, cy[i][cc], 0, 0, 0);
             }
         }
     }
@@ -421,7 +424,8 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
 
     // ---- 5. outputs, all in the scan's fragment order (16-byte pieces; see
     //      the scan kernel for the piece layouts)
-    // U~ and Y0: this wave's C fragments are the scan's fragments as they stand
+    // U~ and Y0^T: this wave's C fragments are the scan's fragments as they
+    // stand (Y0^T is the accumulator layout of the scan's Y^T = S Q~^T)
     {
         const size_t base = hc * CHK * QM_DN_HD;
 #pragma unroll
@@ -804,7 +808,7 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillAr
 #pragma unroll
         for (int j = 0; j < 4; ++j) o.k[j] = *reinterpret_cast<const half8*>(ks + j * 512);
     };
-    // Q~ pieces 4w .. 4w+3 (token block w) and the Y0 tile w, two chunks ahead
+    // Q~ pieces 4w .. 4w+3 (token block w) and the Y0^T tile w, two chunks ahead
     struct OpsY {
         half8 q[4];
         half4 y;
@@ -819,17 +823,21 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillAr
     auto load_d = [&](OpsY& o, int c) {
         o.d = ld4(A.Dt + (hbase + c) * CHK + 16 * w + 4 * (lane >> 4));
     };
-    // Y tile w of this slice: lane (r, q) holds tokens 16 w + 4 q .. +3 of
-    // row 16 vt + r, as one 8-byte piece per lane
+    // Y^T tile w of this slice: lane (r, q) holds rows 16 vt + 4 q .. +3 of
+    // token 16 w + r.  The slice's outputs are stored token-major, [64
+    // tokens][16 rows] f16 per (head, chunk, slice), so that this store is
+    // 512 contiguous bytes per wave (a store scattered over 16 token rows of
+    // 256 bytes cost the scan ~6 us: its memory path is what bounds it).
     auto y_store = [&](int c, half4 v) {
-        *reinterpret_cast<half4*>(A.Yt + ((((hbase + c) * 8 + vt) * 4 + w) * 64 + lane) * 4) = v;
+        *reinterpret_cast<half4*>(A.Yt + (((hbase + c) * 8 + vt) * CHK + 16 * w + (lane & 15)) * 16
+                                  + 4 * (lane >> 4)) = v;
     };
     // gamma_C of 64 chunks at a time, one per lane (a vector load, so LDS
     // waits never wait on it), the next 64 fetched half way through
     auto load_g = [&](int c0) { return A.gC[hbase + min(c0 + lane, nc - 1)]; };
     float gv = load_g(0), gn = 0.0f;
 
-    // One chunk: U tile w = U~ + (-W) S^T; Y tile w = Y0 + Q~ S^T (the
+    // One chunk: U tile w = U~ + (-W) S^T; Y^T tile w = Y0^T + S Q~^T (the
     // chunk's outputs, off the chain); exchange D U; S^T tiles <- gamma_C S^T
     // + K^T (D U); exchange S.
     // A wave's ~15 operand loads per chunk (1 KB each) take the CU's
@@ -860,10 +868,13 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillAr
         __builtin_amdgcn_sched_barrier(0);
         floatx4 y0 = {(float)oy.y[0], (float)oy.y[1], (float)oy.y[2], (float)oy.y[3]};
         floatx4 y1 = {0.0f, 0.0f, 0.0f, 0.0f};
-        y0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(oy.q[0], sb[0], y0, 0, 0, 0);
-        y1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(oy.q[1], sb[1], y1, 0, 0, 0);
-        y0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(oy.q[2], sb[2], y0, 0, 0, 0);
-        y1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(oy.q[3], sb[3], y1, 0, 0, 0);
+        // Y^T = S Q~^T + Y0^T: the S piece as the A operand and the Q~ piece
+        // as B (both hold the same k set per lane and register), so each
+        // lane gets four consecutive rows of one token
+        y0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(sb[0], oy.q[0], y0, 0, 0, 0);
+        y1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(sb[1], oy.q[1], y1, 0, 0, 0);
+        y0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(sb[2], oy.q[2], y0, 0, 0, 0);
+        y1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(sb[3], oy.q[3], y1, 0, 0, 0);
         // U's rows (tokens) scaled by gamma_C / gamma_t: the S update
         // takes diag(gamma_C / gamma) U against the qk-head's K
         const floatx4 us = (u0 + u1) * floatx4{oy.d.x, oy.d.y, oy.d.z, oy.d.w};
@@ -942,13 +953,14 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillAr
 //    the conv buffer update
 // ============================================================================
 // One workgroup per (chunk, v-head).  The head's 128 rows of Y for the
-// chunk's 64 tokens come from the eight slices, in the scan's fragment order
-// (f16) or, for a slice that ran exactly, as f32 [64 tokens][16 rows]; they
-// are staged in LDS, and the norm then runs 32 lanes per token with 4
-// consecutive values each, so z and the output move 512 contiguous bytes per
-// token pair.
-extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_out(DnPrefillArgs A) {
-    __shared__ float ys[CHK][132];
+// chunk's 64 tokens come from the eight slices, each [64 tokens][16 rows],
+// f16 (the scan stores Y^T fragments) or, for a slice that ran exactly,
+// f32.  The norm runs 32 lanes per token with 4 consecutive values each, so
+// z and the output move 512 contiguous bytes per token pair, with no
+// staging through LDS.  At most 64 VGPRs, so that all of a 4096-token
+// layer's 2048 workgroups (8 per CU) are resident at once.
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8)))
+void qm_dn_prefill_out(DnPrefillArgs A) {
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int c = blockIdx.x / QM_DN_V_HEADS, h = blockIdx.x % QM_DN_V_HEADS;
     const size_t hc = (size_t)h * A.nc + c;
@@ -967,69 +979,46 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_out(DnPrefillArg
         for (int j = 0; j < 3; ++j) A.conv_buf[(size_t)ch * 3 + j] = nb[j];
     }
 
-    // z for this thread's tokens first: it does not depend on anything
+    // Lane (col, token) = (4 (lane & 31), 16 w + (lane >> 5) + 2 q): rows
+    // col .. col+3 of 8 tokens; z and the output are whole 256-byte token
+    // rows per 32 lanes.
     const int col = 4 * (lane & 31);
     const int tk0 = 16 * w + (lane >> 5);
-    uint2 zr[8];
+    uint2 zr[8], yr[8];
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
         const int t = min(c * CHK + tk0 + 2 * q, A.T - 1);      // rows past T are not written
         zr[q] = *reinterpret_cast<const uint2*>(A.z + ((size_t)t * QM_DN_V_HEADS + h) * QM_DN_HD + col);
     }
-    {
-        // fragment-order f16 tiles: item i = ((vt * 4 + wt) * 64 + l) holds
-        // tokens 16 wt + 4 (l >> 4) .. +3 of row 16 vt + (l & 15)
-        const half4* ysrc = reinterpret_cast<const half4*>(A.Yt) + hc * (8 * 4 * 64);
-        half4 yv[8];
+    const uint16_t* ysrc = A.Yt + (hc * 8 + (col >> 4)) * (CHK * 16) + (col & 15);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) yv[k] = ysrc[tid + 256 * k];
-        bool ex[8];
-#pragma unroll
-        for (int vt = 0; vt < 8; ++vt) ex[vt] = A.mode[h * 8 + vt] != 0;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int i = tid + 256 * k, vt = i >> 8, wt = (i >> 6) & 3, l = i & 63;
-            if (!ex[vt]) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) ys[16 * wt + 4 * (l >> 4) + e][16 * vt + (l & 15)] = (float)yv[k][e];
-            }
-        }
-        // slices the scan ran exactly: f32 [64 tokens][16 rows] in their
-        // 4 KB of this (head, chunk) block
-        const float4* xsrc = reinterpret_cast<const float4*>(
-            reinterpret_cast<const char*>(A.Yx) + hc * (QM_DN_HD * QM_DN_HD * 2));
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int i = tid + 256 * k, vt = i >> 8;            // float4 i: slice vt, token (i >> 2) & 63
-            if (ex[vt]) {
-                const float4 v = xsrc[i];
-                const int tok = (i >> 2) & 63, r0 = 16 * vt + 4 * (i & 3);
-                ys[tok][r0] = v.x; ys[tok][r0 + 1] = v.y; ys[tok][r0 + 2] = v.z; ys[tok][r0 + 3] = v.w;
-            }
-        }
-    }
-    __syncthreads();
-
-    float4 y[8];
-#pragma unroll
-    for (int q = 0; q < 8; ++q) y[q] = *reinterpret_cast<const float4*>(&ys[tk0 + 2 * q][col]);
+    for (int q = 0; q < 8; ++q) yr[q] = *reinterpret_cast<const uint2*>(ysrc + (tk0 + 2 * q) * 16);
+    // a slice the scan ran exactly has its rows as f32 [64 tokens][16 rows]
+    // in its 4 KB of this (head, chunk) block instead
+    const bool exl = A.mode[h * 8 + (col >> 4)] != 0;
+    const float* xsrc = A.Yx + hc * (QM_DN_HD * QM_DN_HD / 2) + (col >> 4) * (CHK * 16) + (col & 15);
     const uint2 gw = *reinterpret_cast<const uint2*>(A.norm_w + col);
     const float g0 = f16_to_f32((uint16_t)(gw.x & 0xffffu)), g1 = f16_to_f32((uint16_t)(gw.x >> 16));
     const float g2 = f16_to_f32((uint16_t)(gw.y & 0xffffu)), g3 = f16_to_f32((uint16_t)(gw.y >> 16));
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
-        float ss = y[q].x * y[q].x;
-        ss = fmaf(y[q].y, y[q].y, ss);
-        ss = fmaf(y[q].z, y[q].z, ss);
-        ss = fmaf(y[q].w, y[q].w, ss);
+        float4 yq = make_float4(f16_to_f32((uint16_t)(yr[q].x & 0xffffu)), f16_to_f32((uint16_t)(yr[q].x >> 16)),
+                                f16_to_f32((uint16_t)(yr[q].y & 0xffffu)), f16_to_f32((uint16_t)(yr[q].y >> 16)));
+        if (exl) yq = ld4(xsrc + (tk0 + 2 * q) * 16);
+        float ss = yq.x * yq.x;
+        ss = fmaf(yq.y, yq.y, ss);
+        ss = fmaf(yq.z, yq.z, ss);
+        ss = fmaf(yq.w, yq.w, ss);
         ss = sum_xor16(row_sum16(ss));
         const int t = c * CHK + tk0 + 2 * q;
         if (t < A.T) {
-            const float inv_rms = 1.0f / sqrtf(ss / (float)QM_DN_HD + 1e-6f);
+            // 1/sqrt(mean + eps) as v_rsq_f32 (1 ulp), as the decode step
+            // computes it; the exact sqrt and divide cost ~30 instructions
+            const float inv_rms = __builtin_amdgcn_rsqf(ss * (1.0f / (float)QM_DN_HD) + 1e-6f);
             const float z0 = bf16_to_f32((uint16_t)(zr[q].x & 0xffffu)), z1 = bf16_to_f32((uint16_t)(zr[q].x >> 16));
             const float z2 = bf16_to_f32((uint16_t)(zr[q].y & 0xffffu)), z3 = bf16_to_f32((uint16_t)(zr[q].y >> 16));
-            const uint32_t o01 = pack_bf16x2(y[q].x * inv_rms * g0 * silu_fast(z0), y[q].y * inv_rms * g1 * silu_fast(z1));
-            const uint32_t o23 = pack_bf16x2(y[q].z * inv_rms * g2 * silu_fast(z2), y[q].w * inv_rms * g3 * silu_fast(z3));
+            const uint32_t o01 = pack_bf16x2(yq.x * inv_rms * g0 * silu_fast(z0), yq.y * inv_rms * g1 * silu_fast(z1));
+            const uint32_t o23 = pack_bf16x2(yq.z * inv_rms * g2 * silu_fast(z2), yq.w * inv_rms * g3 * silu_fast(z3));
             *reinterpret_cast<uint2*>(A.out + ((size_t)t * QM_DN_V_HEADS + h) * QM_DN_HD + col) = make_uint2(o01, o23);
         }
     }

@@ -72,9 +72,10 @@ struct GqaDecodeArgs {
 //   Ktt     f16 [16][nc][8192]     K^T per qk-head (normalised keys)
 //   Dt      f32 [32][nc][64]       gamma_C / gamma_t per token
 //   gC      f32 [32][nc]           gamma_C = prod of the chunk's decays
-//   Yt      f16 [32][nc][8192]     pre-norm outputs of the chunked path
-// The per-(head, chunk) blocks are stored in the MFMA fragment order the
-// scan and out kernels load them in (described at the scan kernel).
+//   Yt      f16 [32][nc][8][64][16] pre-norm outputs of the chunked path,
+//                                   per 16-row slice, token-major
+// The other per-(head, chunk) blocks are stored in the MFMA fragment order
+// the scan kernel loads them in (described there).
 #define QM_DN_CHUNK 64
 struct DnPrefillArgs {
     const uint16_t* qkv;     // bf16 [T][8192]
