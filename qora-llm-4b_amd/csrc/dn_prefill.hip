@@ -327,25 +327,28 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
             *reinterpret_cast<half4*>(&Am[i][16 * j + 4 * lq]) = ha;
             *reinterpret_cast<half4*>(&Pm[i][16 * j + 4 * lq]) = hp;
         }
-    }
-    __syncthreads();
 
-    // ---- 2. diagonal blocks T_bb = (I + A_bb)^-1 by substitution (lane m owns column m)
-    if (lane < 16) {
-        const int b0 = 16 * w, m = lane;
-        float t[16];
+        // ---- 2. the diagonal block T_bb = (I + A_bb)^-1 of this wave's row
+        //      tile b = rt, by substitution (lane m owns column m).  The wave
+        //      has just written that A tile itself (a wave's LDS accesses
+        //      complete in order), so no workgroup barrier comes between, and
+        //      one wave's inverse overlaps the other wave's KK/QK tiles.
+        if (lane < 16) {
+            const int b0 = 16 * rt, m = lane;
+            float t[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const half8 r0 = *reinterpret_cast<const half8*>(&Am[b0 + i][b0]);
-            const half8 r1 = *reinterpret_cast<const half8*>(&Am[b0 + i][b0 + 8]);
-            float v = (i == m) ? 1.0f : 0.0f;
+            for (int i = 0; i < 16; ++i) {
+                const half8 r0 = *reinterpret_cast<const half8*>(&Am[b0 + i][b0]);
+                const half8 r1 = *reinterpret_cast<const half8*>(&Am[b0 + i][b0 + 8]);
+                float v = (i == m) ? 1.0f : 0.0f;
 #pragma unroll
-            for (int j = 0; j < i; ++j) v += (float)(j < 8 ? r0[j] : r1[j - 8]) * t[j];
-            t[i] = v;
-            om = max_abs(om, v);
+                for (int j = 0; j < i; ++j) v += (float)(j < 8 ? r0[j] : r1[j - 8]) * t[j];
+                t[i] = v;
+                om = max_abs(om, v);
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) Td[rt][i][m] = (_Float16)t[i];
         }
-#pragma unroll
-        for (int i = 0; i < 16; ++i) Td[w][i][m] = (_Float16)t[i];
     }
     __syncthreads();
 
