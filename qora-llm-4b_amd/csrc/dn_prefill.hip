@@ -333,21 +333,29 @@ extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillA
         //      has just written that A tile itself (a wave's LDS accesses
         //      complete in order), so no workgroup barrier comes between, and
         //      one wave's inverse overlaps the other wave's KK/QK tiles.
+        //      Row i is v_i = e_i + sum_{j<i} (-A)_ij t_j, accumulated in
+        //      order of j; written column by column (t_j, then its term in
+        //      every later row), so the dependent chain is 16 steps long, not
+        //      the 120 of the row-by-row order.
         if (lane < 16) {
             const int b0 = 16 * rt, m = lane;
-            float t[16];
+            half8 ar[16][2];                       // rows 1..15 of -A_bb (columns 0-7, 8-15)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const half8 r0 = *reinterpret_cast<const half8*>(&Am[b0 + i][b0]);
-                const half8 r1 = *reinterpret_cast<const half8*>(&Am[b0 + i][b0 + 8]);
-                float v = (i == m) ? 1.0f : 0.0f;
-#pragma unroll
-                for (int j = 0; j < i; ++j) v += (float)(j < 8 ? r0[j] : r1[j - 8]) * t[j];
-                t[i] = v;
-                om = max_abs(om, v);
+            for (int i = 1; i < 16; ++i) {
+                ar[i][0] = *reinterpret_cast<const half8*>(&Am[b0 + i][b0]);
+                if (i > 8) ar[i][1] = *reinterpret_cast<const half8*>(&Am[b0 + i][b0 + 8]);
             }
+            float v[16];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) Td[rt][i][m] = (_Float16)t[i];
+            for (int i = 0; i < 16; ++i) v[i] = (i == m) ? 1.0f : 0.0f;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const float tj = v[j];
+                om = max_abs(om, tj);
+                Td[rt][j][m] = (_Float16)tj;
+#pragma unroll
+                for (int i = j + 1; i < 16; ++i) v[i] += (float)ar[i][j >> 3][j & 7] * tj;
+            }
         }
     }
     __syncthreads();
