@@ -823,7 +823,7 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillAr
     struct OpsY {
         half8 q[4];
         half4 y;
-        float4 d;                                // gamma_C / gamma_t of this lane's 4 tokens of tile w
+        float d;                                 // gamma_C / gamma_t of token 16 w + 4 (lane >> 4) + (lane & 3)
     };
     auto load_qy = [&](OpsY& o, int c) {
         const uint16_t* qs = blk(A.Qt, c) + 4 * w * 512;
@@ -832,7 +832,10 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillAr
         o.y = *reinterpret_cast<const half4*>(blk(A.Y0t, c) + (2 * vt + (w >> 1)) * 512 + 4 * (w & 1));
     };
     auto load_d = [&](OpsY& o, int c) {
-        o.d = ld4(A.Dt + (hbase + c) * CHK + 16 * w + 4 * (lane >> 4));
+        // one float per lane: a 256-byte load rather than a 16-byte one per
+        // lane of 64 distinct bytes (the CU's load path bounds this kernel);
+        // each lane's four tokens come from its quad by DPP
+        o.d = A.Dt[(hbase + c) * CHK + 16 * w + 4 * (lane >> 4) + (lane & 3)];
     };
     // Y^T tile w of this slice: lane (r, q) holds rows 16 vt + 4 q .. +3 of
     // token 16 w + r.  The slice's outputs are stored token-major, [64
@@ -888,7 +891,8 @@ extern "C" __global__ __launch_bounds__(256) void qm_dn_prefill_scan(DnPrefillAr
         y1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(sb[3], oy.q[3], y1, 0, 0, 0);
         // U's rows (tokens) scaled by gamma_C / gamma_t: the S update
         // takes diag(gamma_C / gamma) U against the qk-head's K
-        const floatx4 us = (u0 + u1) * floatx4{oy.d.x, oy.d.y, oy.d.z, oy.d.w};
+        const floatx4 us = (u0 + u1) * floatx4{dpp_f32<0x00>(oy.d), dpp_f32<0x55>(oy.d),
+                                               dpp_f32<0xAA>(oy.d), dpp_f32<0xFF>(oy.d)};
         Ux[w][lane] = to_half4(us);
         __builtin_amdgcn_sched_barrier(0);
         load_qy(oy, cy);
