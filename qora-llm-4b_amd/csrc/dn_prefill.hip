@@ -15,7 +15,8 @@
 //
 // Three kernels:
 //   qm_dn_prefill_chunk  everything that does not depend on S0, fully
-//                        parallel over (chunk, v-head): the conv1d + SiLU +
+//                        parallel over (chunk, qk-head; its two v-heads in
+//                        turn, two workgroups per CU): the conv1d + SiLU +
 //                        L2 norm of the chunk's q, k, v and the gates into
 //                        LDS, KK^T / QK^T on MFMA, [W | U~] by block forward
 //                        substitution (16x16 diagonal inverses by
@@ -59,20 +60,172 @@ QM_DEV half4 to_half4(floatx4 v) {
     return r;
 }
 
-// Per-v-head LDS of the chunk kernel.
+// LDS of the chunk kernel for the v-head it is working on (the two v-heads
+// of a qk-head take it in turn).
 struct ChunkHeadLds {
     _Float16 Vs[CHK][136];                         // v row-major
     _Float16 pm[CHK][72];                          // P (lower, incl. diagonal)
     _Float16 am[CHK][72];                          // -A (strictly lower), the sign the solve uses
     _Float16 Td[4][16][24];                        // (I + A_bb)^-1
-    __attribute__((aligned(16))) float Gs[CHK];
-    float Bs[CHK], Eg[CHK], BG[CHK];
-    __attribute__((aligned(16))) float Kd[CHK];
 };
 
+// Per-v-head gates of the chunk (both heads' are formed in the first phase).
+struct ChunkGates {
+    __attribute__((aligned(16))) float Gs[CHK];    // in-chunk cumulative log decay G_i
+    float Bs[CHK], Eg[CHK], BG[CHK];               // beta_i, gamma_i, beta_i gamma_i
+    __attribute__((aligned(16))) float Kd[CHK];    // gamma_C / gamma_i
+};
+
+// Phase 0 of the chunk kernel for NP parts of 128 channels: causal conv1d
+// (gemv.rs:1132-1147), SiLU (:1149) and, for the first NQK parts (q, then k),
+// the per-head L2 norm and q scale (:1151-1156), f16 into dst[part].  Thread
+// (cg, tg) = (tid & 15, tid >> 4) owns channels chb[part] .. +7 for tokens
+// 4tg .. 4tg+3: the 16 lanes of a DPP row share the tokens, so the L2 norm is
+// a row reduction.  All 7 NP raw rows the thread needs are loaded at
+// clamped, always valid rows before any arithmetic; rows before the sequence
+// come from the conv buffer, and the tokens past it are zeroed at the end.
+// The gate inputs of both v-heads (waves 0 and 1) are requested after the
+// rows when `gates` is set (a wave's loads return in issue order, and these
+// 4-byte loads touch one cache line per token).  vm gets each v channel's
+// max |v| over the valid tokens.
+template <int NP, int NQK>
+QM_DEV void chunk_prep(const DnPrefillArgs& A, const int (&chb)[NP], _Float16 (*const (&dst)[NP])[136],
+                       int qkh, int t0, int c, bool tail, bool gates, float& ga, float& gb, float (&vm)[8]) {
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));                 // no row addresses shared with another call's
+    const int cg = tid & 15, tg = tid >> 4;
+    uint4 u[NP][7];
+#pragma unroll
+    for (int part = 0; part < NP; ++part)
+#pragma unroll
+        for (int r = 0; r < 7; ++r) {
+            const int t = min(max(t0 + 4 * tg - 3 + r, 0), A.T - 1);
+            u[part][r] = *reinterpret_cast<const uint4*>(A.qkv + (size_t)t * QM_DN_QKV_DIM + chb[part]);
+        }
+    float4 wt[8], wn[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) wt[e] = ld4(A.conv_w + (size_t)(chb[0] + e) * 4);
+    if (gates && tid < 2 * CHK) {
+        const int t = min(t0 + (tid & (CHK - 1)), A.T - 1);
+        const int h = 2 * qkh + (tid >> 6);
+        ga = A.a[(size_t)t * QM_DN_V_HEADS + h];
+        gb = A.b[(size_t)t * QM_DN_V_HEADS + h];
+    }
+#pragma unroll
+    for (int part = 0; part < NP; ++part) {
+        const int ch0 = chb[part];
+        if (part + 1 < NP) {                       // next part's taps while this one computes
+#pragma unroll
+            for (int e = 0; e < 8; ++e) wn[e] = ld4(A.conv_w + (size_t)(chb[part + 1] + e) * 4);
+        }
+        float x[7][8];
+#pragma unroll
+        for (int r = 0; r < 7; ++r) {
+            const uint32_t wv[4] = {u[part][r].x, u[part][r].y, u[part][r].z, u[part][r].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                x[r][2 * e] = bf16_to_f32((uint16_t)(wv[e] & 0xffffu));
+                x[r][2 * e + 1] = bf16_to_f32((uint16_t)(wv[e] >> 16));
+            }
+        }
+        // the masks are wave-uniform branches: interior chunks skip them
+        if (c == 0) {                              // x_{-3..-1} from the conv buffer
+            asm volatile("" ::: "memory");        // keep these loads inside the branch
+#pragma unroll
+            for (int r = 0; r < 3; ++r) {
+                const int t = 4 * tg - 3 + r;
+                const int tb = min(t, -1);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float cbv = A.conv_buf[(size_t)(ch0 + e) * 3 + 3 + tb];
+                    x[r][e] = t < 0 ? cbv : x[r][e];
+                }
+            }
+            // the selects complete here, inside the branch: no load of it
+            // is then pending where the paths join, and other chunks'
+            // arithmetic waits only for the rows it uses
+#pragma unroll
+            for (int r = 0; r < 3; ++r)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(x[r][e]));
+        }
+        const float scale = part == 0 ? 1.0f / sqrtf((float)QM_DN_HD) : 1.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int tok = 4 * tg + j;
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                // gemv.rs:1134-1139: taps oldest first, then the new token
+                float sacc = x[j][e] * wt[e].x;
+                sacc = fmaf(x[j + 1][e], wt[e].y, sacc);
+                sacc = fmaf(x[j + 2][e], wt[e].z, sacc);
+                sacc = fmaf(x[j + 3][e], wt[e].w, sacc);
+                v[e] = silu_fast(sacc);
+            }
+            // (tail is wave-uniform: interior chunks take every token)
+            if (part >= NQK && (!tail || t0 + tok < A.T)) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) vm[e] = max_abs(vm[e], v[e]);
+            }
+            if (part < NQK) {
+                // x /= ||x|| when ||x|| > 1e-12, q *= 1/sqrt(128)
+                float ss = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
+                ss = row_sum16(ss);
+                const float f = (ss > 1e-24f ? __builtin_amdgcn_rsqf(ss) : 1.0f) * scale;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] *= f;
+            }
+            half8 hv;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) hv[e] = (_Float16)v[e];
+            *reinterpret_cast<half8*>(&dst[part][tok][8 * cg]) = hv;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) wt[e] = wn[e];
+    }
+    if (tail) {
+        // Tokens past the sequence read clamped rows above; their rows are
+        // zeroed here (a token's conv and norm involve only itself and
+        // earlier rows, so no valid token saw them).
+#pragma unroll
+        for (int part = 0; part < NP; ++part)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (t0 + 4 * tg + j >= A.T) *reinterpret_cast<half8*>(&dst[part][4 * tg + j][8 * cg]) = half8{};
+    }
+}
+
+// The v-channel maxima of one v part, reduced over the wave's 64 tokens:
+// lanes cg, cg+16, cg+32, cg+48 hold the same channels.  Wave w's result
+// goes to red[w][channel]; om gets the largest.
+QM_DEV void chunk_vmax(float (&vm)[8], float (*red)[QM_DN_HD], float& om) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, cg = threadIdx.x & 15;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(vm[e]), __float_as_uint(vm[e]), false, false);
+        const float m16 = __builtin_elementwise_maximum(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+        const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(m16), __float_as_uint(m16), false, false);
+        vm[e] = __builtin_elementwise_maximum(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+        om = __builtin_elementwise_maximum(om, vm[e]);
+    }
+    if ((lane >> 4) == 0) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) red[w][8 * cg + e] = vm[e];
+    }
+}
+
 // ============================================================================
-// 2. chunk: per (chunk, pair of v-heads sharing a qk-head), everything independent of the entering state
+// 2. chunk: per (chunk, qk-head), everything independent of the entering state
 // ============================================================================
+// One 4-wave workgroup takes the qk-head's two v-heads 2 qkh and 2 qkh + 1
+// in turn: q and k (shared by both), v of the first head and both heads'
+// gates are formed first, the second head's v once the first head is done
+// with the per-head LDS.  At ~79 KB of LDS two workgroups share a CU, and
+// one's VALU-heavy input preparation runs beside the other's MFMA phases and
+// stores.
 // [W | U~] = (I + A)^-1 [diag(beta gamma) K | diag(beta) V] is solved by block
 // forward substitution over the four 16-token blocks b:
 //   R_b = B_b - sum_{k<b} A_bk X_k,  X_b = T_bb R_b,  T_bb = (I + A_bb)^-1,
@@ -82,447 +235,345 @@ struct ChunkHeadLds {
 // an X_k fragment (4 consecutive tokens of one column per lane) is already
 // the B operand of the next block's correction, so the solve needs no
 // workgroup barrier.
-extern "C" __global__ __launch_bounds__(512) void qm_dn_prefill_chunk(DnPrefillArgs A) {
-    __shared__ _Float16 Qs[CHK][136];              // q row-major (both v-heads)
-    __shared__ _Float16 Ks[CHK][136];              // k row-major (both v-heads)
-    __shared__ ChunkHeadLds hl[2];
+extern "C" __global__ __launch_bounds__(QM_DN_CHUNK_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void qm_dn_prefill_chunk(DnPrefillArgs A) {
+    __shared__ _Float16 Qs[CHK][136];              // q row-major
+    __shared__ _Float16 Ks[CHK][136];              // k row-major
+    __shared__ ChunkHeadLds H;                     // the v-head being worked on
+    __shared__ ChunkGates gts[2];
     __shared__ float vred[2][4][QM_DN_HD];         // per head and wave: max |v| per channel
     __shared__ int vbad[2];                        // per head: an f16 operand would overflow
 
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int hh = tid >> 8;                       // v-head of the pair: waves 0-3 / 4-7
-    const int w = (tid >> 6) & 3;                  // wave within its head's group
-    const int ht = tid & 255;                      // thread within its head's group
+    const int tid = threadIdx.x;
     // GVA: v-heads 2 qkh and 2 qkh + 1 read qk-head qkh (gemv.rs:1160)
     const int c = blockIdx.x / QM_DN_QK_HEADS, qkh = blockIdx.x % QM_DN_QK_HEADS;
-    const int h = 2 * qkh + hh;
     const int t0 = c * CHK;
-    const size_t hc = (size_t)h * A.nc + c;
-    const int lr = lane & 15, lq = lane >> 4;
-    ChunkHeadLds& H = hl[hh];
+    const bool tail = t0 + CHK > A.T;              // last chunk, partly past the sequence
     _Float16 (&Vs)[CHK][136] = H.Vs;
     _Float16 (&Pm)[CHK][72] = H.pm;
     _Float16 (&Am)[CHK][72] = H.am;
     _Float16 (&Td)[4][16][24] = H.Td;
-    float (&Gs)[CHK] = H.Gs;
-    float (&Bs)[CHK] = H.Bs;
-    float (&Eg)[CHK] = H.Eg;
-    float (&BG)[CHK] = H.BG;
-    float (&Kd)[CHK] = H.Kd;
-    // largest magnitude this thread converts to an f16 operand on the v side
-    // or in the solve (q, k, A, P and K~ are bounded by the normalisation)
-    float om = 0.0f;
-    if (ht == 0) vbad[hh] = 0;
+    if (tid < 2) vbad[tid] = 0;
+    // the gate parameters of the v-head whose gates this wave forms (waves 0, 1)
+    const int hg = 2 * qkh + ((tid >> 6) & 1);
+    const float a_log_g = A.a_log[hg], dt_bias_g = A.dt_bias[hg];
+    float om_v0 = 0.0f;                            // the first head's largest |v|
 
-    // ---- 0. causal conv1d (gemv.rs:1132-1147), SiLU (:1149), per-head L2
-    //      norm and q scale (:1151-1156) of this chunk's q, k (qk-head qkh,
-    //      once for both v-heads) and the two v-heads' v, straight into LDS;
-    //      gates (:1171-1172).  Threads 0-255 do q and v of head 2qkh,
-    //      threads 256-511 k and v of head 2qkh+1.  Thread (cg, tg) =
-    //      (ht & 15, ht >> 4) owns channels 8cg .. 8cg+7 for tokens 4tg ..
-    //      4tg+3: the 16 lanes of a DPP row share the tokens, so the L2 norm
-    //      is a row reduction.
+    // ---- 0. q, k and the first head's v, and both heads' gates (gemv.rs:1171-1172)
     {
-        const int cg = ht & 15, tg = ht >> 4;
-        int chb[2];                                // first channel of this thread, per part
-        chb[0] = hh * QM_DN_QK_DIM + qkh * QM_DN_HD + 8 * cg;          // q or k
-        chb[1] = 2 * QM_DN_QK_DIM + h * QM_DN_HD + 8 * cg;             // v of head h
-        // all 14 raw rows the thread needs (7 per part), loaded at clamped,
-        // always valid rows before any arithmetic; rows before the sequence
-        // come from the conv buffer, and the tokens past it are zeroed below
-        uint4 u[2][7];
-#pragma unroll
-        for (int part = 0; part < 2; ++part)
-#pragma unroll
-            for (int r = 0; r < 7; ++r) {
-                const int t = min(max(t0 + 4 * tg - 3 + r, 0), A.T - 1);
-                u[part][r] = *reinterpret_cast<const uint4*>(A.qkv + (size_t)t * QM_DN_QKV_DIM + chb[part]);
-            }
-        float4 wt[8], wn[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) wt[e] = ld4(A.conv_w + (size_t)(chb[0] + e) * 4);
-        // gate inputs (wave 0 of each head), consumed last: requested here,
-        // after the rows (a wave's loads return in issue order, and these
-        // 4-byte loads touch one cache line per token), but before the
-        // arithmetic, so that they are not a round trip of their own
-        float ga = 0.0f, gb = 0.0f;
-        if (ht < CHK) {
-            const int t = min(t0 + ht, A.T - 1);
-            ga = A.a[(size_t)t * QM_DN_V_HEADS + h];
-            gb = A.b[(size_t)t * QM_DN_V_HEADS + h];
-        }
-        const float a_log_h = A.a_log[h], dt_bias_h = A.dt_bias[h];
-        const bool tail = t0 + CHK > A.T;          // last chunk, partly past the sequence
-        float vm[8];                               // max |v| per channel over this thread's valid tokens
+        const int cg = tid & 15;
+        const int chb[2] = {qkh * QM_DN_HD + 8 * cg, QM_DN_QK_DIM + qkh * QM_DN_HD + 8 * cg};
+        _Float16 (*const dst[2])[136] = {Qs, Ks};
+        const int chv[1] = {2 * QM_DN_QK_DIM + (2 * qkh) * QM_DN_HD + 8 * cg};
+        _Float16 (*const dsv[1])[136] = {Vs};
+        float ga = 0.0f, gb = 0.0f, vm[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) vm[e] = 0.0f;
-#pragma unroll
-        for (int part = 0; part < 2; ++part) {     // q or k, then v
-            const int ch0 = chb[part];
-            if (part < 1) {                        // next part's taps while this one computes
-#pragma unroll
-                for (int e = 0; e < 8; ++e) wn[e] = ld4(A.conv_w + (size_t)(chb[part + 1] + e) * 4);
-            }
-            float x[7][8];
-#pragma unroll
-            for (int r = 0; r < 7; ++r) {
-                const uint32_t wv[4] = {u[part][r].x, u[part][r].y, u[part][r].z, u[part][r].w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    x[r][2 * e] = bf16_to_f32((uint16_t)(wv[e] & 0xffffu));
-                    x[r][2 * e + 1] = bf16_to_f32((uint16_t)(wv[e] >> 16));
-                }
-            }
-            // the masks are wave-uniform branches: interior chunks skip them
-            if (c == 0) {                          // x_{-3..-1} from the conv buffer
-                asm volatile("" ::: "memory");    // keep these loads inside the branch
-#pragma unroll
-                for (int r = 0; r < 3; ++r) {
-                    const int t = 4 * tg - 3 + r;
-                    const int tb = min(t, -1);
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const float cbv = A.conv_buf[(size_t)(ch0 + e) * 3 + 3 + tb];
-                        x[r][e] = t < 0 ? cbv : x[r][e];
-                    }
-                }
-                // the selects complete here, inside the branch: no load of it
-                // is then pending where the paths join, and other chunks'
-                // arithmetic waits only for the rows it uses
-#pragma unroll
-                for (int r = 0; r < 3; ++r)
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(x[r][e]));
-            }
-            _Float16 (*dst)[136] = part == 1 ? Vs : (hh == 0 ? Qs : Ks);
-            const float scale = (part == 0 && hh == 0) ? 1.0f / sqrtf((float)QM_DN_HD) : 1.0f;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int tok = 4 * tg + j;
-                float v[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    // gemv.rs:1134-1139: taps oldest first, then the new token
-                    float sacc = x[j][e] * wt[e].x;
-                    sacc = fmaf(x[j + 1][e], wt[e].y, sacc);
-                    sacc = fmaf(x[j + 2][e], wt[e].z, sacc);
-                    sacc = fmaf(x[j + 3][e], wt[e].w, sacc);
-                    v[e] = silu_fast(sacc);
-                }
-                // (tail is wave-uniform: interior chunks take every token)
-                if (part == 1 && (!tail || t0 + tok < A.T)) {
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) vm[e] = max_abs(vm[e], v[e]);
-                }
-                if (part == 0) {
-                    // x /= ||x|| when ||x|| > 1e-12, q *= 1/sqrt(128)
-                    float ss = 0.0f;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
-                    ss = row_sum16(ss);
-                    const float f = (ss > 1e-24f ? __builtin_amdgcn_rsqf(ss) : 1.0f) * scale;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) v[e] *= f;
-                }
-                half8 hv;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) hv[e] = (_Float16)v[e];
-                *reinterpret_cast<half8*>(&dst[tok][8 * cg]) = hv;
-            }
-#pragma unroll
-            for (int e = 0; e < 8; ++e) wt[e] = wn[e];
-        }
-        // lanes cg, cg+16, cg+32, cg+48 of a wave hold the same channels
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(vm[e]), __float_as_uint(vm[e]), false, false);
-            const float m16 = __builtin_elementwise_maximum(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
-            const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(m16), __float_as_uint(m16), false, false);
-            vm[e] = __builtin_elementwise_maximum(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
-            om = __builtin_elementwise_maximum(om, vm[e]);
-        }
-        if ((lane >> 4) == 0) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) vred[hh][w][8 * cg + e] = vm[e];
-        }
-        if (tail) {
-            // Tokens past the sequence read clamped rows above; their rows
-            // are zeroed here (a token's conv and norm involve only itself
-            // and earlier rows, so no valid token saw them).
-#pragma unroll
-            for (int part = 0; part < 2; ++part) {
-                _Float16 (*dst)[136] = part == 1 ? Vs : (hh == 0 ? Qs : Ks);
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    if (t0 + 4 * tg + j >= A.T) *reinterpret_cast<half8*>(&dst[4 * tg + j][8 * cg]) = half8{};
-            }
-        }
-        if (ht < CHK) {
+        chunk_prep<2, 2>(A, chb, dst, qkh, t0, c, tail, true, ga, gb, vm);
+        chunk_prep<1, 0>(A, chv, dsv, qkh, t0, c, tail, false, ga, gb, vm);
+        chunk_vmax(vm, vred[0], om_v0);
+        if (tid < 2 * CHK) {
             // log alpha = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b);
             // padded tokens get alpha = 1, beta = 0 (no effect on the state);
-            // then the inclusive prefix sum over the chunk (one wave)
-            // (the hardware transcendentals, a few ulp from libm: with libm
-            // these two waves' gates delayed the workgroup barrier by ~2K cycles)
+            // then the inclusive prefix sum over the chunk (one wave per head)
+            // (the hardware transcendentals, a few ulp from libm)
+            const int hh = tid >> 6, i = tid & (CHK - 1);
+            ChunkGates& G = gts[hh];
             float g = 0.0f, be = 0.0f;
             // opaque here, so that the compiler does not start this
             // arithmetic next to the loads (a wait for every earlier load)
             asm volatile("" : "+v"(ga), "+v"(gb));
-            if (t0 + ht < A.T) {
-                g = -exp_fast(a_log_h) * softplus_fast(ga + dt_bias_h);
+            if (t0 + i < A.T) {
+                g = -exp_fast(a_log_g) * softplus_fast(ga + dt_bias_g);
                 be = sigmoid_fast(gb);
             }
 #pragma unroll
             for (int off = 1; off < 64; off <<= 1) {
                 const float o = __shfl_up(g, off);
-                if (ht >= off) g += o;
+                if (i >= off) g += o;
             }
             const float eg = exp_fast(g);
-            Gs[ht] = g;
-            Bs[ht] = be;
-            Eg[ht] = eg;                        // gamma_i
-            BG[ht] = be * eg;                   // beta_i gamma_i
+            G.Gs[i] = g;
+            G.Bs[i] = be;
+            G.Eg[i] = eg;                          // gamma_i
+            G.BG[i] = be * eg;                     // beta_i gamma_i
         }
     }
     __syncthreads();
-    if (ht < CHK) Kd[ht] = exp_fast(Gs[CHK - 1] - Gs[ht]);   // gamma_C / gamma_i
+    if (tid < 2 * CHK) {
+        ChunkGates& G = gts[tid >> 6];
+        const int i = tid & (CHK - 1);
+        G.Kd[i] = exp_fast(G.Gs[CHK - 1] - G.Gs[i]);   // gamma_C / gamma_i
+    }
 
-    // ---- 1. KK^T and QK^T (16x16x32 f16), masked and decayed -> -A, P (f16).
-    //      Computed transposed, C = K_j K_i^T and K_j Q_i^T: lane (lr, lq)
-    //      then holds row i = 16w + lr, columns 16j + 4lq .. +3, one 8-byte
-    //      store per matrix and tile.  Decays exp(G_i - G_jj) on v_exp_f32
-    //      with the exponent clamped at 0 (the masked upper part).
-    //      Row tile w of head 0 has w + 1 column tiles; head 1 takes its
-    //      row tiles in the opposite order, so that the two waves sharing a
-    //      SIMD (w and w + 4) have five tiles between them.
-    {
-        const int rt = hh ? 3 - w : w;
-        const int i = 16 * rt + lr;
-        const float gi = Gs[i], bi = Bs[i];
-        half8 bk[4], bq[4];                        // B operands: row i's k, q
+#pragma unroll 1
+    for (int hh = 0; hh < 2; ++hh) {
+        // The thread's indices, re-derived from an opaque copy in each pass:
+        // otherwise the compiler computes every lane-dependent address and
+        // constant of the body once, ahead of the loop, and keeps them all
+        // live across both passes (it spilled them).
+        int tid = threadIdx.x;
+        asm volatile("" : "+v"(tid));
+        const int lane = tid & 63, lr = lane & 15, lq = lane >> 4;
+        const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave
+        const int h = 2 * qkh + hh;
+        const size_t hc = (size_t)h * A.nc + c;
+        const ChunkGates& G = gts[hh];
+        // largest magnitude this thread converts to an f16 operand in the
+        // solve (q, k, A, P and K~ are bounded by the normalisation)
+        float om = hh == 0 ? om_v0 : 0.0f;
+        if (hh == 1) {
+            // the second head's v, into the per-head LDS the first head has
+            // finished with (the barrier after its statistics)
+            const int cg = tid & 15;
+            const int chb[1] = {2 * QM_DN_QK_DIM + h * QM_DN_HD + 8 * cg};
+            _Float16 (*const dst[1])[136] = {Vs};
+            float ga = 0.0f, gb = 0.0f, vm[8];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            bk[s] = *reinterpret_cast<const half8*>(&Ks[i][32 * s + 8 * lq]);
-            bq[s] = *reinterpret_cast<const half8*>(&Qs[i][32 * s + 8 * lq]);
+            for (int e = 0; e < 8; ++e) vm[e] = 0.0f;
+            chunk_prep<1, 0>(A, chb, dst, qkh, t0, c, tail, false, ga, gb, vm);
+            chunk_vmax(vm, vred[1], om);
+            __syncthreads();
         }
-        for (int j = 0; j < 4; ++j) {
-            half4 ha = {}, hp = {};
-            if (j <= rt) {                         // wave-uniform
-                floatx4 ckk = {0.0f, 0.0f, 0.0f, 0.0f}, cqk = {0.0f, 0.0f, 0.0f, 0.0f};
+
+        // ---- 1. KK^T and QK^T (16x16x32 f16), masked and decayed -> -A, P (f16).
+        //      Computed transposed, C = K_j K_i^T and K_j Q_i^T: lane (lr, lq)
+        //      then holds row i = 16 rt + lr, columns 16j + 4lq .. +3, one
+        //      8-byte store per matrix and tile.  Decays exp(G_i - G_jj) on
+        //      v_exp_f32 with the exponent clamped at 0 (the masked upper
+        //      part).  Row tile rt has rt + 1 column tiles; the second head
+        //      takes its row tiles in the opposite order, so that every wave
+        //      has five tiles over the two heads.
+        {
+            const int rt = hh ? 3 - w : w;
+            const int i = 16 * rt + lr;
+            const float gi = G.Gs[i], bi = G.Bs[i];
+            half8 bk[4], bq[4];                    // B operands: row i's k, q
 #pragma unroll
-                for (int s = 0; s < 4; ++s) {
-                    const half8 ak = *reinterpret_cast<const half8*>(&Ks[16 * j + lr][32 * s + 8 * lq]);
-                    ckk = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak, bk[s], ckk, 0, 0, 0);
-                    cqk = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak, bq[s], cqk, 0, 0, 0);
+            for (int s = 0; s < 4; ++s) {
+                bk[s] = *reinterpret_cast<const half8*>(&Ks[i][32 * s + 8 * lq]);
+                bq[s] = *reinterpret_cast<const half8*>(&Qs[i][32 * s + 8 * lq]);
+            }
+            for (int j = 0; j < 4; ++j) {
+                half4 ha = {}, hp = {};
+                if (j <= rt) {                     // wave-uniform
+                    floatx4 ckk = {0.0f, 0.0f, 0.0f, 0.0f}, cqk = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) {
+                        const half8 ak = *reinterpret_cast<const half8*>(&Ks[16 * j + lr][32 * s + 8 * lq]);
+                        ckk = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak, bk[s], ckk, 0, 0, 0);
+                        cqk = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak, bq[s], cqk, 0, 0, 0);
+                    }
+                    const float4 gj = *reinterpret_cast<const float4*>(&G.Gs[16 * j + 4 * lq]);
+                    const float gjv[4] = {gj.x, gj.y, gj.z, gj.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int jj = 16 * j + 4 * lq + e;
+                        const float dec = __builtin_amdgcn_exp2f(fminf(gi - gjv[e], 0.0f) * 1.4426950408889634f);
+                        ha[e] = (_Float16)(jj < i ? -(bi * dec) * ckk[e] : 0.0f);
+                        hp[e] = (_Float16)(jj <= i ? dec * cqk[e] : 0.0f);
+                    }
                 }
-                const float4 gj = *reinterpret_cast<const float4*>(&Gs[16 * j + 4 * lq]);
-                const float gjv[4] = {gj.x, gj.y, gj.z, gj.w};
+                *reinterpret_cast<half4*>(&Am[i][16 * j + 4 * lq]) = ha;
+                *reinterpret_cast<half4*>(&Pm[i][16 * j + 4 * lq]) = hp;
+            }
+
+            // ---- 2. the diagonal block T_bb = (I + A_bb)^-1 of this wave's
+            //      row tile b = rt, by substitution (lane m owns column m).
+            //      The wave has just written that A tile itself (a wave's LDS
+            //      accesses complete in order), so no workgroup barrier comes
+            //      between.  Row i is v_i = e_i + sum_{j<i} (-A)_ij t_j,
+            //      accumulated in order of j; written column by column (t_j,
+            //      then its term in every later row), so the dependent chain
+            //      is 16 steps long, not the 120 of the row-by-row order.
+            if (lane < 16) {
+                const int b0 = 16 * rt, m = lane;
+                half8 ar[16][2];                   // rows 1..15 of -A_bb (columns 0-7, 8-15)
+#pragma unroll
+                for (int i2 = 1; i2 < 16; ++i2) {
+                    ar[i2][0] = *reinterpret_cast<const half8*>(&Am[b0 + i2][b0]);
+                    if (i2 > 8) ar[i2][1] = *reinterpret_cast<const half8*>(&Am[b0 + i2][b0 + 8]);
+                }
+                float v[16];
+#pragma unroll
+                for (int i2 = 0; i2 < 16; ++i2) v[i2] = (i2 == m) ? 1.0f : 0.0f;
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const float tj = v[j];
+                    om = max_abs(om, tj);
+                    Td[rt][j][m] = (_Float16)tj;
+#pragma unroll
+                    for (int i2 = j + 1; i2 < 16; ++i2) v[i2] += (float)ar[i2][j >> 3][j & 7] * tj;
+                }
+            }
+        }
+        __syncthreads();
+
+        // ---- 3. [W | U~] by block forward substitution (16x16x16 f16)
+        //      tiles: cc = 0,1 -> W k-col tiles 2w+cc; cc = 2,3 -> U~ v-col tiles 2w+cc-2
+        floatx4 cu[4][2];
+        half4 xh[4][4];                            // X_b fragments as f16 B operands
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const half4 tb = *reinterpret_cast<const half4*>(&Td[b][lr][4 * lq]);
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) {
+                const int col = 16 * (2 * w + (cc & 1)) + lr;
+                floatx4 r;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const int jj = 16 * j + 4 * lq + e;
-                    const float dec = __builtin_amdgcn_exp2f(fminf(gi - gjv[e], 0.0f) * 1.4426950408889634f);
-                    ha[e] = (_Float16)(jj < i ? -(bi * dec) * ckk[e] : 0.0f);
-                    hp[e] = (_Float16)(jj <= i ? dec * cqk[e] : 0.0f);
+                    const int tk = 16 * b + 4 * lq + e;
+                    // fma(h, s, 0) is the product, as one v_fma_mix_f32 that
+                    // also widens the f16 operand
+                    r[e] = cc < 2 ? __builtin_fmaf((float)Ks[tk][col], G.BG[tk], 0.0f)
+                                  : __builtin_fmaf((float)Vs[tk][col], G.Bs[tk], 0.0f);
                 }
+#pragma unroll
+                for (int k = 0; k < b; ++k) {
+                    const half4 an = *reinterpret_cast<const half4*>(&Am[16 * b + lr][16 * k + 4 * lq]);
+                    r = __builtin_amdgcn_mfma_f32_16x16x16f16(an, xh[k][cc], r, 0, 0, 0);
+                }
+                floatx4 x = {0.0f, 0.0f, 0.0f, 0.0f};
+                x = __builtin_amdgcn_mfma_f32_16x16x16f16(tb, to_half4(r), x, 0, 0, 0);
+                om = max_abs4(max_abs4(om, r), x);
+                xh[b][cc] = to_half4(x);
+                if (cc >= 2) cu[b][cc - 2] = x;
             }
-            *reinterpret_cast<half4*>(&Am[i][16 * j + 4 * lq]) = ha;
-            *reinterpret_cast<half4*>(&Pm[i][16 * j + 4 * lq]) = hp;
         }
 
-        // ---- 2. the diagonal block T_bb = (I + A_bb)^-1 of this wave's row
-        //      tile b = rt, by substitution (lane m owns column m).  The wave
-        //      has just written that A tile itself (a wave's LDS accesses
-        //      complete in order), so no workgroup barrier comes between, and
-        //      one wave's inverse overlaps the other wave's KK/QK tiles.
-        //      Row i is v_i = e_i + sum_{j<i} (-A)_ij t_j, accumulated in
-        //      order of j; written column by column (t_j, then its term in
-        //      every later row), so the dependent chain is 16 steps long, not
-        //      the 120 of the row-by-row order.
-        if (lane < 16) {
-            const int b0 = 16 * rt, m = lane;
-            half8 ar[16][2];                       // rows 1..15 of -A_bb (columns 0-7, 8-15)
+        // ---- 4. Q~ = diag(gamma) Q - P W and Y0 = P U~ (16x16x16 f16; the
+        //      W / U~ fragments are the B operands as they stand)
+        floatx4 cq[4][2], cy[4][2];
 #pragma unroll
-            for (int i = 1; i < 16; ++i) {
-                ar[i][0] = *reinterpret_cast<const half8*>(&Am[b0 + i][b0]);
-                if (i > 8) ar[i][1] = *reinterpret_cast<const half8*>(&Am[b0 + i][b0 + 8]);
-            }
-            float v[16];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) v[i] = (i == m) ? 1.0f : 0.0f;
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const float tj = v[j];
-                om = max_abs(om, tj);
-                Td[rt][j][m] = (_Float16)tj;
-#pragma unroll
-                for (int i = j + 1; i < 16; ++i) v[i] += (float)ar[i][j >> 3][j & 7] * tj;
-            }
-        }
-    }
-    __syncthreads();
-
-    // ---- 3. [W | U~] by block forward substitution (16x16x16 f16)
-    //      tiles: cc = 0,1 -> W k-col tiles 2w+cc; cc = 2,3 -> U~ v-col tiles 2w+cc-2
-    floatx4 cu[4][2];
-    half4 xh[4][4];                                   // X_b fragments as f16 B operands
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-        const half4 tb = *reinterpret_cast<const half4*>(&Td[b][lr][4 * lq]);
-#pragma unroll
-        for (int cc = 0; cc < 4; ++cc) {
-            const int col = 16 * (2 * w + (cc & 1)) + lr;
-            floatx4 r;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int tk = 16 * b + 4 * lq + e;
-                // fma(h, s, 0) is the product, as one v_fma_mix_f32 that
-                // also widens the f16 operand
-                r[e] = cc < 2 ? __builtin_fmaf((float)Ks[tk][col], BG[tk], 0.0f)
-                              : __builtin_fmaf((float)Vs[tk][col], Bs[tk], 0.0f);
-            }
-#pragma unroll
-            for (int k = 0; k < b; ++k) {
-                const half4 an = *reinterpret_cast<const half4*>(&Am[16 * b + lr][16 * k + 4 * lq]);
-                r = __builtin_amdgcn_mfma_f32_16x16x16f16(an, xh[k][cc], r, 0, 0, 0);
-            }
-            floatx4 x = {0.0f, 0.0f, 0.0f, 0.0f};
-            x = __builtin_amdgcn_mfma_f32_16x16x16f16(tb, to_half4(r), x, 0, 0, 0);
-            om = max_abs4(max_abs4(om, r), x);
-            xh[b][cc] = to_half4(x);
-            if (cc >= 2) cu[b][cc - 2] = x;
-        }
-    }
-
-    // ---- 4. Q~ = diag(gamma) Q - P W and Y0 = P U~ (16x16x16 f16; the W / U~
-    //      fragments are the B operands as they stand)
-    floatx4 cq[4][2], cy[4][2];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
-            const int col = 16 * (2 * w + cc) + lr;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int tk = 16 * i + 4 * lq + e;
-                cq[i][cc][e] = __builtin_fmaf((float)Qs[tk][col], Eg[tk], 0.0f);
-            }
-            cy[i][cc] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-        }
-    // -W fragments: the B operands of Q~ and, transposed, the -W output
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int cc = 0; cc < 2; ++cc) xh[i][cc] = -xh[i][cc];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int kt = 0; kt <= i; ++kt) {
-            const half4 ap = *reinterpret_cast<const half4*>(&Pm[16 * i + lr][16 * kt + 4 * lq]);
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc) {
-                cq[i][cc] = __builtin_amdgcn_mfma_f32_16x16x16f16(ap, xh[kt][cc], cq[i][cc], 0, 0, 0);
-                // Y0^T = U~^T P^T, transposed by swapping the operands: the U~
-                // fragment as A and the P fragment as B (lane (r, q) then
-                // holds v-cols 16 vt + 4q .. +3 of token 16 i + r)
-                cy[i][cc] = __builtin_amdgcn_mfma_f32_16x16x16f16(xh[kt][cc + 2], ap, cy[i][cc], 0, 0, 0);
+                const int col = 16 * (2 * w + cc) + lr;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int tk = 16 * i + 4 * lq + e;
+                    cq[i][cc][e] = __builtin_fmaf((float)Qs[tk][col], G.Eg[tk], 0.0f);
+                }
+                cy[i][cc] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
             }
-        }
-    }
-
+        // -W fragments: the B operands of Q~ and, transposed, the -W output
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int cc = 0; cc < 2; ++cc) om = max_abs4(max_abs4(om, cq[i][cc]), cy[i][cc]);
-
-    // ---- 5. outputs, all in the scan's fragment order (16-byte pieces; see
-    //      the scan kernel for the piece layouts)
-    // U~ and Y0^T: this wave's C fragments are the scan's fragments as they
-    // stand (Y0^T is the accumulator layout of the scan's Y^T = S Q~^T)
-    {
-        const size_t base = hc * CHK * QM_DN_HD;
-#pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
-            const int vt = 2 * w + cc;
-#pragma unroll
-            for (int p = 0; p < 2; ++p) {
-                const size_t o = base + (size_t)((vt * 2 + p) * 64 + lane) * 8;
-                const half4 u0 = to_half4(cu[2 * p][cc]), u1 = to_half4(cu[2 * p + 1][cc]);
-                const half4 y0 = to_half4(cy[2 * p][cc]), y1 = to_half4(cy[2 * p + 1][cc]);
-                *reinterpret_cast<half8*>(A.Ut + o) = half8{u0[0], u0[1], u0[2], u0[3], u1[0], u1[1], u1[2], u1[3]};
-                *reinterpret_cast<half8*>(A.Y0t + o) = half8{y0[0], y0[1], y0[2], y0[3], y1[0], y1[1], y1[2], y1[3]};
-            }
-        }
-    }
-    // -W, Q~ and K~^T want four consecutive columns of one token (or tokens
-    // of one column) per lane, the transpose of a C fragment.  A C fragment
-    // read as an A operand is the transposed tile, so one 16x16x16 product
-    // with an identity B operand transposes it in registers (exactly: every
-    // product is x * 1 or x * 0 in fp32).
-    half4 idm;                                    // B[k][n] = (k == n): lane (n, kq) holds k = 4kq .. +3
-#pragma unroll
-    for (int e = 0; e < 4; ++e) idm[e] = (_Float16)(4 * lq + e == lr ? 1.0f : 0.0f);
-    auto transpose = [&](half4 a) {
-        return to_half4(__builtin_amdgcn_mfma_f32_16x16x16f16(a, idm, floatx4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0));
-    };
-    // -W and Q~: piece 4i + w holds col tiles 2w, 2w+1 of token block i
-    {
-        uint16_t* wdst = A.Wn + hc * CHK * QM_DN_HD;
-        uint16_t* qdst = A.Qt + hc * CHK * QM_DN_HD;
+            for (int cc = 0; cc < 2; ++cc) xh[i][cc] = -xh[i][cc];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const half4 w0 = transpose(xh[i][0]), w1 = transpose(xh[i][1]);
-            const half4 q0 = transpose(to_half4(cq[i][0])), q1 = transpose(to_half4(cq[i][1]));
-            const size_t o = (size_t)((4 * i + w) * 64 + lane) * 8;
-            *reinterpret_cast<half8*>(wdst + o) = cat8(w0, w1);
-            *reinterpret_cast<half8*>(qdst + o) = cat8(q0, q1);
-        }
-    }
-    // K^T of the qk-head, once for both v-heads (the scan applies each
-    // head's decays gamma_C / gamma_j to U instead): piece 2kt + p, kt = 2w,
-    // 2w+1, holds token blocks 2p, 2p+1 of k-col tile kt; the A operand of a
-    // K tile is a row read (token 16 tau + lr, cols 16 kt + 4 lq .. +3)
-    if (hh == 0) {
-        uint16_t* dst = A.Ktt + ((size_t)qkh * A.nc + c) * CHK * QM_DN_HD;
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const int kt = 2 * w + t;
+            for (int kt = 0; kt <= i; ++kt) {
+                const half4 ap = *reinterpret_cast<const half4*>(&Pm[16 * i + lr][16 * kt + 4 * lq]);
 #pragma unroll
-            for (int p = 0; p < 2; ++p) {
-                half4 hv[2];
-#pragma unroll
-                for (int hb = 0; hb < 2; ++hb) {
-                    const int tau = 2 * p + hb;
-                    const half4 a = *reinterpret_cast<const half4*>(&Ks[16 * tau + lr][16 * kt + 4 * lq]);
-                    hv[hb] = transpose(a);
+                for (int cc = 0; cc < 2; ++cc) {
+                    cq[i][cc] = __builtin_amdgcn_mfma_f32_16x16x16f16(ap, xh[kt][cc], cq[i][cc], 0, 0, 0);
+                    // Y0^T = U~^T P^T, transposed by swapping the operands: the
+                    // U~ fragment as A and the P fragment as B (lane (r, q)
+                    // then holds v-cols 16 vt + 4q .. +3 of token 16 i + r)
+                    cy[i][cc] = __builtin_amdgcn_mfma_f32_16x16x16f16(xh[kt][cc + 2], ap, cy[i][cc], 0, 0, 0);
                 }
-                *reinterpret_cast<half8*>(dst + (size_t)((2 * kt + p) * 64 + lane) * 8) = cat8(hv[0], hv[1]);
             }
         }
-    }
-    if (ht < CHK) A.Dt[hc * CHK + ht] = Kd[ht];
-    if (ht == 0) A.gC[hc] = exp_fast(Gs[CHK - 1]);
 
-    // ---- 6. precision guard statistics: each v channel's max |v| over the
-    //      chunk, and +inf in channel 0 if an f16 operand would overflow
-    if (!(om <= 65504.0f)) vbad[hh] = 1;
-    __syncthreads();
-    if (ht < QM_DN_HD) {
-        float m = fmaxf(fmaxf(vred[hh][0][ht], vred[hh][1][ht]), fmaxf(vred[hh][2][ht], vred[hh][3][ht]));
-        if (ht == 0 && vbad[hh]) m = __builtin_inff();
-        A.vstat[((size_t)h * (A.nc + 1) + c) * QM_DN_HD + ht] = m;
-    }
-    if (c == 0) {
-        // the entering state's row maxima (slot nc): two threads per row
-        const int r = ht >> 1, half = ht & 1;
-        const float* sp = A.state + (size_t)h * QM_DN_HEAD_ELEMS + (size_t)r * QM_DN_HD + 64 * half;
-        float4 sv[16];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) sv[j] = ld4(sp + 4 * j);
-        float m = 0.0f;
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 16; ++j)
-            m = fmaxf(m, fmaxf(fmaxf(fabsf(sv[j].x), fabsf(sv[j].y)), fmaxf(fabsf(sv[j].z), fabsf(sv[j].w))));
-        m = fmaxf(m, __shfl_xor(m, 1));
-        if (half == 0) A.vstat[((size_t)h * (A.nc + 1) + A.nc) * QM_DN_HD + r] = m;
+            for (int cc = 0; cc < 2; ++cc) om = max_abs4(max_abs4(om, cq[i][cc]), cy[i][cc]);
+
+        // ---- 5. outputs, all in the scan's fragment order (16-byte pieces;
+        //      see the scan kernel for the piece layouts)
+        // U~ and Y0^T: this wave's C fragments are the scan's fragments as
+        // they stand (Y0^T is the accumulator layout of the scan's Y^T = S Q~^T)
+        {
+            const size_t base = hc * CHK * QM_DN_HD;
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc) {
+                const int vt = 2 * w + cc;
+#pragma unroll
+                for (int p = 0; p < 2; ++p) {
+                    const size_t o = base + (size_t)((vt * 2 + p) * 64 + lane) * 8;
+                    const half4 u0 = to_half4(cu[2 * p][cc]), u1 = to_half4(cu[2 * p + 1][cc]);
+                    const half4 y0 = to_half4(cy[2 * p][cc]), y1 = to_half4(cy[2 * p + 1][cc]);
+                    *reinterpret_cast<half8*>(A.Ut + o) = half8{u0[0], u0[1], u0[2], u0[3], u1[0], u1[1], u1[2], u1[3]};
+                    *reinterpret_cast<half8*>(A.Y0t + o) = half8{y0[0], y0[1], y0[2], y0[3], y1[0], y1[1], y1[2], y1[3]};
+                }
+            }
+        }
+        // -W, Q~ and K~^T want four consecutive columns of one token (or
+        // tokens of one column) per lane, the transpose of a C fragment.  A C
+        // fragment read as an A operand is the transposed tile, so one
+        // 16x16x16 product with an identity B operand transposes it in
+        // registers (exactly: every product is x * 1 or x * 0 in fp32).
+        half4 idm;                                // B[k][n] = (k == n): lane (n, kq) holds k = 4kq .. +3
+#pragma unroll
+        for (int e = 0; e < 4; ++e) idm[e] = (_Float16)(4 * lq + e == lr ? 1.0f : 0.0f);
+        auto transpose = [&](half4 a) {
+            return to_half4(__builtin_amdgcn_mfma_f32_16x16x16f16(a, idm, floatx4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0));
+        };
+        // -W and Q~: piece 4i + w holds col tiles 2w, 2w+1 of token block i
+        {
+            uint16_t* wdst = A.Wn + hc * CHK * QM_DN_HD;
+            uint16_t* qdst = A.Qt + hc * CHK * QM_DN_HD;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const half4 w0 = transpose(xh[i][0]), w1 = transpose(xh[i][1]);
+                const half4 q0 = transpose(to_half4(cq[i][0])), q1 = transpose(to_half4(cq[i][1]));
+                const size_t o = (size_t)((4 * i + w) * 64 + lane) * 8;
+                *reinterpret_cast<half8*>(wdst + o) = cat8(w0, w1);
+                *reinterpret_cast<half8*>(qdst + o) = cat8(q0, q1);
+            }
+        }
+        // K^T of the qk-head, once for both v-heads (the scan applies each
+        // head's decays gamma_C / gamma_j to U instead): piece 2kt + p, kt =
+        // 2w, 2w+1, holds token blocks 2p, 2p+1 of k-col tile kt; the A
+        // operand of a K tile is a row read (token 16 tau + lr, cols 16 kt +
+        // 4 lq .. +3)
+        if (hh == 0) {
+            uint16_t* dst = A.Ktt + ((size_t)qkh * A.nc + c) * CHK * QM_DN_HD;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const int kt = 2 * w + t;
+#pragma unroll
+                for (int p = 0; p < 2; ++p) {
+                    half4 hv[2];
+#pragma unroll
+                    for (int hb = 0; hb < 2; ++hb) {
+                        const int tau = 2 * p + hb;
+                        const half4 a = *reinterpret_cast<const half4*>(&Ks[16 * tau + lr][16 * kt + 4 * lq]);
+                        hv[hb] = transpose(a);
+                    }
+                    *reinterpret_cast<half8*>(dst + (size_t)((2 * kt + p) * 64 + lane) * 8) = cat8(hv[0], hv[1]);
+                }
+            }
+        }
+        if (tid < CHK) A.Dt[hc * CHK + tid] = G.Kd[tid];
+        if (tid == 0) A.gC[hc] = exp_fast(G.Gs[CHK - 1]);
+
+        // ---- 6. precision guard statistics: each v channel's max |v| over
+        //      the chunk, and +inf in channel 0 if an f16 operand would overflow
+        if (!(om <= 65504.0f)) vbad[hh] = 1;
+        __syncthreads();
+        if (tid < QM_DN_HD) {
+            float m = fmaxf(fmaxf(vred[hh][0][tid], vred[hh][1][tid]), fmaxf(vred[hh][2][tid], vred[hh][3][tid]));
+            if (tid == 0 && vbad[hh]) m = __builtin_inff();
+            A.vstat[((size_t)h * (A.nc + 1) + c) * QM_DN_HD + tid] = m;
+        }
+        if (c == 0) {
+            // the entering state's row maxima (slot nc): two threads per row
+            const int r = tid >> 1, half = tid & 1;
+            const float* sp = A.state + (size_t)h * QM_DN_HEAD_ELEMS + (size_t)r * QM_DN_HD + 64 * half;
+            float4 sv[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) sv[j] = ld4(sp + 4 * j);
+            float m = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                m = fmaxf(m, fmaxf(fmaxf(fabsf(sv[j].x), fabsf(sv[j].y)), fmaxf(fabsf(sv[j].z), fabsf(sv[j].w))));
+            m = fmaxf(m, __shfl_xor(m, 1));
+            if (half == 0) A.vstat[((size_t)h * (A.nc + 1) + A.nc) * QM_DN_HD + r] = m;
+        }
     }
 }
 

@@ -77,6 +77,7 @@ struct GqaDecodeArgs {
 // The other per-(head, chunk) blocks are stored in the MFMA fragment order
 // the scan kernel loads them in (described there).
 #define QM_DN_CHUNK 64
+#define QM_DN_CHUNK_THREADS 256   // chunk kernel: one 4-wave workgroup per (chunk, qk-head)
 struct DnPrefillArgs {
     const uint16_t* qkv;     // bf16 [T][8192]
     float* conv_buf;         // [8192][3]

@@ -63,6 +63,7 @@ struct qm_context {
     hipFunction_t f_sample_select = nullptr;
     int lm_head_hidden = 0;              // the hidden size lm_head_wg_per_cu was computed for
     int lm_head_wg_per_cu = 1;
+    int dnp_chunk_threads = 0;     // the DeltaNet prefill chunk kernel's workgroup size (its launch bounds)
     int q4_threads = 0;            // the Q4 kernels' workgroup sizes (their launch bounds)
     int q4_gu_threads = 0;
     int q4_hidden_threads = 0, q4_inter_threads = 0;
@@ -386,6 +387,9 @@ int32_t qm_create(qm_context** out, const qm_config* cfg, const char* code_objec
          hipFuncGetAttribute(&c->q4_inter_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, c->f_q4_gemv_inter) !=
              hipSuccess))
         st = fail(c, QM_ERR_CODE_OBJECT, "qm_q4_gemv: cannot read its workgroup size");
+    if (st == QM_OK && hipFuncGetAttribute(&c->dnp_chunk_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK,
+                                           c->f_dnp_chunk) != hipSuccess)
+        st = fail(c, QM_ERR_CODE_OBJECT, "qm_dn_prefill_chunk: cannot read its workgroup size");
     if (st == QM_OK && hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess)
         st = fail(c, QM_ERR_HIP, "hipStreamCreate failed");
     if (st == QM_OK) {
@@ -811,7 +815,8 @@ int32_t qm_deltanet_prefill(qm_context* c, qm_stream stream, int32_t seq_len, co
                      reinterpret_cast<float*>(ws + L.gC), reinterpret_cast<uint16_t*>(ws + L.Yt),
                      reinterpret_cast<float*>(ws + L.Yx),
                      reinterpret_cast<float*>(ws + L.vstat), reinterpret_cast<int32_t*>(ws + L.mode), seq_len, nc};
-    st = launch(c, c->f_dnp_chunk, static_cast<uint32_t>(nc) * QM_DN_QK_HEADS, 512, pa, s, "qm_dn_prefill_chunk");
+    st = launch(c, c->f_dnp_chunk, static_cast<uint32_t>(nc) * QM_DN_QK_HEADS, c->dnp_chunk_threads, pa, s,
+                "qm_dn_prefill_chunk");
     if (st != QM_OK) return st;
     st = launch(c, c->f_dnp_scan, QM_DN_V_HEADS * 8, 256, pa, s, "qm_dn_prefill_scan");
     if (st != QM_OK) return st;
