@@ -148,6 +148,23 @@ def test_decode_many_splits_ragged(ctx):
     assert np.abs(got - ref).max() <= TOL
 
 
+@pytest.mark.parametrize("positions", [[5000, 70, 4351, 640], [63, 64, 4095, 1000]])
+def test_decode_multi_round_splits_ragged(ctx, positions):
+    """192-key splits (three 64-key rounds of the four waves each): ragged
+    lengths whose ends fall in different splits and rounds, appends at round
+    edges (63, 64, 4095), and sequences so short that most splits are empty."""
+    w = W.gqa_decode_workload(5000, len(positions), seed=13)
+    print("case: gqa decode chunk=192 ragged", positions, flush=True)
+    got, kc, vc = run_gpu(ctx, w, positions, 5001, chunk=192)
+    ref, krows, vrows = run_oracle(w, positions, 5001)
+    print(f"max|dout|={np.abs(got - ref).max():.3e}")
+    assert np.abs(got - ref).max() <= TOL
+    for b, p in enumerate(positions):              # each sequence's row appended by the split that owns it
+        kgot, vgot = W.f16_value(kc[b, :, p]), W.f16_value(vc[b, :, p])
+        assert np.all(np.abs(kgot - krows[b]) <= np.abs(krows[b]) * 2 ** -10 + 1e-7)
+        assert np.array_equal(vgot, vrows[b])
+
+
 def test_decode_range_errors(ctx):
     w = W.gqa_decode_workload(16, 1, cap=17, seed=4)
     cos, sin = M.rope_table(16)
