@@ -223,9 +223,10 @@ QM_DEV void chunk_vmax(float (&vm)[8], float (*red)[QM_DN_HD], float& om) {
 // One 4-wave workgroup takes the qk-head's two v-heads 2 qkh and 2 qkh + 1
 // in turn: q and k (shared by both), v of the first head and both heads'
 // gates are formed first, the second head's v once the first head is done
-// with the per-head LDS.  At ~79 KB of LDS two workgroups share a CU, and
-// one's VALU-heavy input preparation runs beside the other's MFMA phases and
-// stores.
+// with the per-head LDS.  At ~79 KB of LDS two workgroups share a CU, so
+// one's stalls (loads, barriers, MFMA and LDS latency) can be filled by the
+// other's work; an 8-wave workgroup doing both heads at once (119 KB, one per
+// CU) measured 74.5 us against 71 us for a 4096-token layer.
 // [W | U~] = (I + A)^-1 [diag(beta gamma) K | diag(beta) V] is solved by block
 // forward substitution over the four 16-token blocks b:
 //   R_b = B_b - sum_{k<b} A_bk X_k,  X_b = T_bb R_b,  T_bb = (I + A_bb)^-1,
