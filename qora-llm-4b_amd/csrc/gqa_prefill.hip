@@ -65,7 +65,7 @@ QM_DEV int frag_key(int kk, int i) { return 32 * (kk >> 1) + 8 * (i >> 2) + 4 * 
 //   block b >= 32, b - 32 = 2 dt + ks: V dim 16 dt + lr, keys 32 ks + 8 lq .. + 7
 // Keys past S are zero.
 // ---------------------------------------------------------------------------
-extern "C" __global__ __launch_bounds__(256) void qm_gqa_prefill_kv(GqaPrefillArgs A) {
+extern "C" __global__ __launch_bounds__(512) void qm_gqa_prefill_kv(GqaPrefillArgs A) {
     __shared__ _Float16 ks[64][264];
     __shared__ _Float16 vs[64][264];
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
@@ -73,18 +73,18 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_prefill_kv(GqaPrefillAr
     const int t0 = (blockIdx.x / QM_GQA_KV_HEADS) * 64;
     // the attention kernel that follows takes its row blocks from these
     if (blockIdx.x == 0 && tid < QM_GQA_KV_HEADS) A.queue[tid] = 0;
-    // K: wave w normalises and rotates tokens t0+16w .. t0+16w+15.  All 16
-    // rows are loaded (at clamped, valid rows) before any arithmetic, so the
-    // wave waits for one memory round trip, not one per token.
+    // K: wave w (of 8) normalises and rotates tokens t0+8w .. t0+8w+7.  All
+    // 8 rows are loaded (at clamped, valid rows) before any arithmetic, so
+    // the wave waits for one memory round trip, not one per token.
     // V's rows are requested right after K's (their conversion waits until
     // K is done, and a wave's loads return in issue order).
-    const int vi = tid >> 2, vp = tid & 3, vt = t0 + vi;
-    uint4 vraw[8];
+    const int vi = tid >> 3, vp = tid & 7, vt = t0 + vi;
+    uint4 vraw[4];
     {
-        uint2 raw[16];
+        uint2 raw[8];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const int t = min(t0 + 16 * w + j, A.S - 1);
+        for (int j = 0; j < 8; ++j) {
+            const int t = min(t0 + 8 * w + j, A.S - 1);
             raw[j] = *reinterpret_cast<const uint2*>(A.k + ((size_t)t * QM_GQA_KV_HEADS + g) * QM_GQA_HD + 4 * lane);
         }
         const uint2 gw = *reinterpret_cast<const uint2*>(A.k_norm + 4 * lane);
@@ -95,31 +95,31 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_prefill_kv(GqaPrefillAr
         float4 cr[2][4], sr[2][4];
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-            const int tc = min(t0 + 16 * w + jj, A.S - 1);
+            const int tc = min(t0 + 8 * w + jj, A.S - 1);
             cr[0][jj] = ld4(A.rope_cos + (size_t)tc * 32 + i0);
             sr[0][jj] = ld4(A.rope_sin + (size_t)tc * 32 + i0);
         }
         {
             const uint16_t* vrow = A.v + ((size_t)min(vt, A.S - 1) * QM_GQA_KV_HEADS + g) * QM_GQA_HD + 8 * vp;
 #pragma unroll
-            for (int q = 0; q < 8; ++q) vraw[q] = *reinterpret_cast<const uint4*>(vrow + 32 * q);
+            for (int q = 0; q < 4; ++q) vraw[q] = *reinterpret_cast<const uint4*>(vrow + 64 * q);
         }
         const float g1[4] = {1.0f + f16_to_f32((uint16_t)(gw.x & 0xffffu)), 1.0f + f16_to_f32((uint16_t)(gw.x >> 16)),
                              1.0f + f16_to_f32((uint16_t)(gw.y & 0xffffu)), 1.0f + f16_to_f32((uint16_t)(gw.y >> 16))};
 #pragma unroll
-        for (int jb = 0; jb < 16; jb += 4) {
+        for (int jb = 0; jb < 8; jb += 4) {
             const int cb = (jb >> 2) & 1;
-            if (jb + 4 < 16) {
+            if (jb + 4 < 8) {
 #pragma unroll
                 for (int jj = 0; jj < 4; ++jj) {
-                    const int tc = min(t0 + 16 * w + jb + 4 + jj, A.S - 1);
+                    const int tc = min(t0 + 8 * w + jb + 4 + jj, A.S - 1);
                     cr[cb ^ 1][jj] = ld4(A.rope_cos + (size_t)tc * 32 + i0);
                     sr[cb ^ 1][jj] = ld4(A.rope_sin + (size_t)tc * 32 + i0);
                 }
             }
 #pragma unroll
             for (int jj = 0; jj < 4; ++jj) {
-                const int t = t0 + 16 * w + jb + jj;
+                const int t = t0 + 8 * w + jb + jj;
                 // gemv.rs:586-597 (RMSNorm, 1 + gamma) and :604-627 (split-half RoPE)
                 float4 x = bf16x4_to_f32(raw[jb + jj]);
                 float ss = x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
@@ -141,45 +141,45 @@ extern "C" __global__ __launch_bounds__(256) void qm_gqa_prefill_kv(GqaPrefillAr
                     h = f32x4_to_f16(x);
                     *reinterpret_cast<uint2*>(A.k_cache + ((size_t)g * A.cap + t) * QM_GQA_HD + 4 * lane) = h;
                 }
-                *reinterpret_cast<uint2*>(&ks[16 * w + jb + jj][4 * lane]) = h;
+                *reinterpret_cast<uint2*>(&ks[8 * w + jb + jj][4 * lane]) = h;
             }
         }
     }
-    // V: rows to the cache, and into LDS for the V^T tile copy.  The four
-    // threads of a token cover 32 consecutive dims per step (64-byte
-    // pieces); all eight raw loads (at a clamped, valid row) were issued
+    // V: rows to the cache, and into LDS for the V^T tile copy.  The eight
+    // threads of a token cover 64 consecutive dims per step (128-byte
+    // pieces); all four raw loads (at a clamped, valid row) were issued
     // with K's.
     {
         const int i = vi, p = vp, t = vt;
-        const uint4 (&raw)[8] = vraw;
+        const uint4 (&raw)[4] = vraw;
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
+        for (int q = 0; q < 4; ++q) {
             uint4 h16 = make_uint4(0, 0, 0, 0);
             if (t < A.S) {
                 const float4 lo = bf16x4_to_f32(make_uint2(raw[q].x, raw[q].y));
                 const float4 hi = bf16x4_to_f32(make_uint2(raw[q].z, raw[q].w));
                 const uint2 a = f32x4_to_f16(lo), b = f32x4_to_f16(hi);
                 h16 = make_uint4(a.x, a.y, b.x, b.y);
-                *reinterpret_cast<uint4*>(A.v_cache + ((size_t)g * A.cap + t) * QM_GQA_HD + 32 * q + 8 * p) = h16;
+                *reinterpret_cast<uint4*>(A.v_cache + ((size_t)g * A.cap + t) * QM_GQA_HD + 64 * q + 8 * p) = h16;
             }
-            *reinterpret_cast<uint4*>(&vs[i][32 * q + 8 * p]) = h16;
+            *reinterpret_cast<uint4*>(&vs[i][64 * q + 8 * p]) = h16;
         }
     }
     __syncthreads();
-    // the tile copy: entry p = tid + 256 i of 4096, consecutive threads on
+    // the tile copy: entry p = tid + 512 i of 4096, consecutive threads on
     // consecutive 16-byte entries
     {
         uint16_t* dst = A.kvf + ((size_t)g * (A.s_pad / 64) + (t0 >> 6)) * (64 * 512);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int p = tid + 256 * i, b = p >> 6, l = p & 63, lr = l & 15, lq = l >> 4;
+        for (int i = 0; i < 4; ++i) {
+            const int p = tid + 512 * i, b = p >> 6, l = p & 63, lr = l & 15, lq = l >> 4;
             const int kk = b >> 3, s8 = b & 7;
             *reinterpret_cast<half8*>(dst + 8 * p) =
                 *reinterpret_cast<const half8*>(&ks[frag_key(kk, lr)][32 * s8 + 8 * lq]);
         }
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int p = tid + 256 * i, b = p >> 6, l = p & 63, lr = l & 15, lq = l >> 4;
+        for (int i = 0; i < 4; ++i) {
+            const int p = tid + 512 * i, b = p >> 6, l = p & 63, lr = l & 15, lq = l >> 4;
             const int d = 16 * (b >> 1) + lr, k8 = 32 * (b & 1) + 8 * lq;
             half8 hv;
 #pragma unroll

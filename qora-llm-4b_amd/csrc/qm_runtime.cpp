@@ -64,6 +64,7 @@ struct qm_context {
     int lm_head_hidden = 0;              // the hidden size lm_head_wg_per_cu was computed for
     int lm_head_wg_per_cu = 1;
     int dnp_chunk_threads = 0;     // the DeltaNet prefill chunk kernel's workgroup size (its launch bounds)
+    int gqp_kv_threads = 0;        // the GQA prefill K/V kernel's workgroup size (its launch bounds)
     int q4_threads = 0;            // the Q4 kernels' workgroup sizes (their launch bounds)
     int q4_gu_threads = 0;
     int q4_hidden_threads = 0, q4_inter_threads = 0;
@@ -390,6 +391,9 @@ int32_t qm_create(qm_context** out, const qm_config* cfg, const char* code_objec
     if (st == QM_OK && hipFuncGetAttribute(&c->dnp_chunk_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK,
                                            c->f_dnp_chunk) != hipSuccess)
         st = fail(c, QM_ERR_CODE_OBJECT, "qm_dn_prefill_chunk: cannot read its workgroup size");
+    if (st == QM_OK && hipFuncGetAttribute(&c->gqp_kv_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK,
+                                           c->f_gqp_kv) != hipSuccess)
+        st = fail(c, QM_ERR_CODE_OBJECT, "qm_gqa_prefill_kv: cannot read its workgroup size");
     if (st == QM_OK && hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess)
         st = fail(c, QM_ERR_HIP, "hipStreamCreate failed");
     if (st == QM_OK) {
@@ -849,7 +853,7 @@ int32_t qm_gqa_prefill(qm_context* c, qm_stream stream, int32_t seq_len, const u
     GqaPrefillArgs ga{q_gate, k, v, q_norm, k_norm, rope_cos, rope_sin, k_cache, v_cache,
                       static_cast<uint16_t*>(c->ws), out,
                       reinterpret_cast<int32_t*>(static_cast<char*>(c->ws) + kvf_bytes), cap, seq_len, s_pad};
-    st = launch(c, c->f_gqp_kv, static_cast<uint32_t>(s_pad / 64) * QM_GQA_KV_HEADS, 256, ga, s,
+    st = launch(c, c->f_gqp_kv, static_cast<uint32_t>(s_pad / 64) * QM_GQA_KV_HEADS, c->gqp_kv_threads, ga, s,
                 "qm_gqa_prefill_kv");
     if (st != QM_OK) return st;
     // persistent: one workgroup per CU (a multiple of the 4 kv groups), no
