@@ -1046,47 +1046,66 @@ void qm_dn_prefill_out(DnPrefillArgs A) {
         for (int j = 0; j < 3; ++j) A.conv_buf[(size_t)ch * 3 + j] = nb[j];
     }
 
-    // Lane (col, token) = (4 (lane & 31), 16 w + (lane >> 5) + 2 q): rows
-    // col .. col+3 of 8 tokens; z and the output are whole 256-byte token
-    // rows per 32 lanes.
-    const int col = 4 * (lane & 31);
-    const int tk0 = 16 * w + (lane >> 5);
-    uint2 zr[8], yr[8];
+    // Lane (col, token) = (8 (lane & 15), 16 w + (lane >> 4) + 4 q): rows
+    // col .. col+7 of 4 tokens; z and the output are whole 256-byte token
+    // rows per 16 lanes (16-byte accesses), and a token's 128 rows are one
+    // DPP row, so the sum of squares is one row reduction.
+    const int col = 8 * (lane & 15);
+    const int tk0 = 16 * w + (lane >> 4);
+    uint4 zr[4], yr[4];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-        const int t = min(c * CHK + tk0 + 2 * q, A.T - 1);      // rows past T are not written
-        zr[q] = *reinterpret_cast<const uint2*>(A.z + ((size_t)t * QM_DN_V_HEADS + h) * QM_DN_HD + col);
+    for (int q = 0; q < 4; ++q) {
+        const int t = min(c * CHK + tk0 + 4 * q, A.T - 1);      // rows past T are not written
+        zr[q] = *reinterpret_cast<const uint4*>(A.z + ((size_t)t * QM_DN_V_HEADS + h) * QM_DN_HD + col);
     }
     const uint16_t* ysrc = A.Yt + (hc * 8 + (col >> 4)) * (CHK * 16) + (col & 15);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) yr[q] = *reinterpret_cast<const uint2*>(ysrc + (tk0 + 2 * q) * 16);
+    for (int q = 0; q < 4; ++q) yr[q] = *reinterpret_cast<const uint4*>(ysrc + (tk0 + 4 * q) * 16);
     // a slice the scan ran exactly has its rows as f32 [64 tokens][16 rows]
     // in its 4 KB of this (head, chunk) block instead
     const bool exl = A.mode[h * 8 + (col >> 4)] != 0;
     const float* xsrc = A.Yx + hc * (QM_DN_HD * QM_DN_HD / 2) + (col >> 4) * (CHK * 16) + (col & 15);
-    const uint2 gw = *reinterpret_cast<const uint2*>(A.norm_w + col);
-    const float g0 = f16_to_f32((uint16_t)(gw.x & 0xffffu)), g1 = f16_to_f32((uint16_t)(gw.x >> 16));
-    const float g2 = f16_to_f32((uint16_t)(gw.y & 0xffffu)), g3 = f16_to_f32((uint16_t)(gw.y >> 16));
+    const uint4 gw = *reinterpret_cast<const uint4*>(A.norm_w + col);
+    const uint32_t gwv[4] = {gw.x, gw.y, gw.z, gw.w};
+    float gg[8];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-        float4 yq = make_float4(f16_to_f32((uint16_t)(yr[q].x & 0xffffu)), f16_to_f32((uint16_t)(yr[q].x >> 16)),
-                                f16_to_f32((uint16_t)(yr[q].y & 0xffffu)), f16_to_f32((uint16_t)(yr[q].y >> 16)));
-        if (exl) yq = ld4(xsrc + (tk0 + 2 * q) * 16);
-        float ss = yq.x * yq.x;
-        ss = fmaf(yq.y, yq.y, ss);
-        ss = fmaf(yq.z, yq.z, ss);
-        ss = fmaf(yq.w, yq.w, ss);
-        ss = sum_xor16(row_sum16(ss));
-        const int t = c * CHK + tk0 + 2 * q;
+    for (int e = 0; e < 4; ++e) {
+        gg[2 * e] = f16_to_f32((uint16_t)(gwv[e] & 0xffffu));
+        gg[2 * e + 1] = f16_to_f32((uint16_t)(gwv[e] >> 16));
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t yv[4] = {yr[q].x, yr[q].y, yr[q].z, yr[q].w};
+        float yq[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            yq[2 * e] = f16_to_f32((uint16_t)(yv[e] & 0xffffu));
+            yq[2 * e + 1] = f16_to_f32((uint16_t)(yv[e] >> 16));
+        }
+        if (exl) {
+            const float4 a = ld4(xsrc + (tk0 + 4 * q) * 16), b = ld4(xsrc + (tk0 + 4 * q) * 16 + 4);
+            yq[0] = a.x; yq[1] = a.y; yq[2] = a.z; yq[3] = a.w;
+            yq[4] = b.x; yq[5] = b.y; yq[6] = b.z; yq[7] = b.w;
+        }
+        float ss = yq[0] * yq[0];
+#pragma unroll
+        for (int e = 1; e < 8; ++e) ss = fmaf(yq[e], yq[e], ss);
+        ss = row_sum16(ss);
+        const int t = c * CHK + tk0 + 4 * q;
         if (t < A.T) {
             // 1/sqrt(mean + eps) as v_rsq_f32 (1 ulp), as the decode step
             // computes it; the exact sqrt and divide cost ~30 instructions
             const float inv_rms = __builtin_amdgcn_rsqf(ss * (1.0f / (float)QM_DN_HD) + 1e-6f);
-            const float z0 = bf16_to_f32((uint16_t)(zr[q].x & 0xffffu)), z1 = bf16_to_f32((uint16_t)(zr[q].x >> 16));
-            const float z2 = bf16_to_f32((uint16_t)(zr[q].y & 0xffffu)), z3 = bf16_to_f32((uint16_t)(zr[q].y >> 16));
-            const uint32_t o01 = pack_bf16x2(yq.x * inv_rms * g0 * silu_fast(z0), yq.y * inv_rms * g1 * silu_fast(z1));
-            const uint32_t o23 = pack_bf16x2(yq.z * inv_rms * g2 * silu_fast(z2), yq.w * inv_rms * g3 * silu_fast(z3));
-            *reinterpret_cast<uint2*>(A.out + ((size_t)t * QM_DN_V_HEADS + h) * QM_DN_HD + col) = make_uint2(o01, o23);
+            const uint32_t zv[4] = {zr[q].x, zr[q].y, zr[q].z, zr[q].w};
+            uint32_t o[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float z0 = bf16_to_f32((uint16_t)(zv[e] & 0xffffu)), z1 = bf16_to_f32((uint16_t)(zv[e] >> 16));
+                o[e] = pack_bf16x2(yq[2 * e] * inv_rms * gg[2 * e] * silu_fast(z0),
+                                   yq[2 * e + 1] * inv_rms * gg[2 * e + 1] * silu_fast(z1));
+            }
+            *reinterpret_cast<uint4*>(A.out + ((size_t)t * QM_DN_V_HEADS + h) * QM_DN_HD + col) =
+                make_uint4(o[0], o[1], o[2], o[3]);
         }
     }
 }
