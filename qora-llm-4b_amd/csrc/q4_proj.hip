@@ -47,6 +47,15 @@
 template <int T> struct Q4Codes;                          // T/2 bytes of codes
 template <> struct Q4Codes<16> { typedef uint2 type; };
 template <> struct Q4Codes<8> { typedef uint32_t type; };
+template <int T> struct Q4Pair;                           // two consecutive rows' codes
+template <> struct Q4Pair<16> {
+    typedef uint4 type;
+    static QM_DEV uint2 half(uint4 v, int h) { return h ? make_uint2(v.z, v.w) : make_uint2(v.x, v.y); }
+};
+template <> struct Q4Pair<8> {
+    typedef uint2 type;
+    static QM_DEV uint32_t half(uint2 v, int h) { return h ? v.y : v.x; }
+};
 
 QM_DEV void q4_word(float* acc, uint32_t w, float sx) {  // 8 codes: columns 0..7 of acc
     uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
@@ -131,7 +140,7 @@ QM_DEV V ld_off(const V* base, uint32_t idx) {
     return *reinterpret_cast<const V*>(reinterpret_cast<const char*>(base) + (size_t)(idx * (uint32_t)sizeof(V)));
 }
 
-template <bool GATE_UP, int T, int STEPS, int THREADS>
+template <bool GATE_UP, bool PAIR, int T, int STEPS, int THREADS>
 QM_DEV void q4_tile(const Q4GemvArgs& A, int p, int tile, float (*red)[33]) {
     typedef typename Q4Codes<T>::type CodeT;
     const int tid = threadIdx.x;
@@ -152,37 +161,89 @@ QM_DEV void q4_tile(const Q4GemvArgs& A, int p, int tile, float (*red)[33]) {
 #pragma unroll
     for (int j = 0; j < (GATE_UP ? T : 1); ++j) acc_u[j] = 0.0f;
     float bsum = 0.0f, bsum_u = 0.0f, ss = 0.0f;
-    for (int k0 = 0; k0 < K; k0 += THREADS * STEPS) {
-        CodeT pk[STEPS], pu[GATE_UP ? STEPS : 1];
-        uint16_t sc[STEPS], su[GATE_UP ? STEPS : 1], nw[STEPS];
-        float xv[STEPS];
+    if (PAIR) {
+        // two consecutive rows per load: their codes (2 x T/2 bytes), scales,
+        // x values and norm weights are adjacent, so one load instruction of
+        // twice the width takes both (k is even on this path)
+        typedef typename Q4Pair<T>::type PairT;
+        const int KP = K >> 1;
+        const PairT* codes2 = reinterpret_cast<const PairT*>(codes);
+        const PairT* codes2_u = reinterpret_cast<const PairT*>(codes_u);
+        const uint32_t* gsc2 = reinterpret_cast<const uint32_t*>(gsc);
+        const uint32_t* gsc2_u = reinterpret_cast<const uint32_t*>(gsc_u);
+        const uint32_t* nwp2 = reinterpret_cast<const uint32_t*>(nwp);
+        const float2* x2 = reinterpret_cast<const float2*>(A.x);
+        constexpr int PS = STEPS / 2;
+        for (int k0 = 0; k0 < KP; k0 += THREADS * PS) {
+            PairT pk[PS], pu[GATE_UP ? PS : 1];
+            uint32_t sc[PS], su[GATE_UP ? PS : 1], nw[PS];
+            float2 xv[PS];
 #pragma unroll
-        for (int s = 0; s < STEPS; ++s) {
-            const uint32_t k = min((uint32_t)(k0 + tid + THREADS * s), (uint32_t)(K - 1));
-            pk[s] = ld_off(codes, k);
-            sc[s] = ld_off(gsc, k);
-            if (GATE_UP) {
-                pu[s] = ld_off(codes_u, k);
-                su[s] = ld_off(gsc_u, k);
+            for (int s = 0; s < PS; ++s) {
+                const uint32_t kp = min((uint32_t)(k0 + tid + THREADS * s), (uint32_t)(KP - 1));
+                pk[s] = ld_off(codes2, kp);
+                sc[s] = ld_off(gsc2, kp);
+                if (GATE_UP) {
+                    pu[s] = ld_off(codes2_u, kp);
+                    su[s] = ld_off(gsc2_u, kp);
+                }
+                xv[s] = ld_off(x2, kp);
+                nw[s] = ld_off(nwp2, kp);
             }
-            xv[s] = ld_off(A.x, k);
-            nw[s] = ld_off(nwp, k);
-        }
-        const bool full = k0 + THREADS * STEPS <= K;    // workgroup-uniform: every row valid
+            const bool full = k0 + THREADS * PS <= KP;
 #pragma unroll
-        for (int s = 0; s < STEPS; ++s) {
-            // rows past k (wave-uniform except in the last wave) add nothing
-            if (!full && k0 + THREADS * s + (tid & ~63) >= K) break;
-            const float xl = full || k0 + tid + THREADS * s < K ? xv[s] : 0.0f;
-            ss = fmaf(xl, xl, ss);
-            const float xn = A.norm_w ? xl * (1.0f + f16_to_f32(nw[s])) : xl;   // gemv.rs:575 but inv_rms
-            const float sx = f16_to_f32(sc[s]) * xn;                           // gemv.rs:429: scale * x_k
-            bsum += sx;
-            q4_accumulate(acc, pk[s], sx);
-            if (GATE_UP) {
-                const float sxu = f16_to_f32(su[s]) * xn;
-                bsum_u += sxu;
-                q4_accumulate(reinterpret_cast<float(&)[T]>(acc_u), pu[s], sxu);
+            for (int s = 0; s < PS; ++s) {
+                if (!full && k0 + THREADS * s + (tid & ~63) >= KP) break;
+                const bool ok = full || k0 + tid + THREADS * s < KP;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const float xl = ok ? (h ? xv[s].y : xv[s].x) : 0.0f;
+                    ss = fmaf(xl, xl, ss);
+                    const float xn = A.norm_w ? xl * (1.0f + f16_to_f32((uint16_t)(nw[s] >> (16 * h)))) : xl;
+                    const float sx = f16_to_f32((uint16_t)(sc[s] >> (16 * h))) * xn;
+                    bsum += sx;
+                    q4_accumulate(acc, Q4Pair<T>::half(pk[s], h), sx);
+                    if (GATE_UP) {
+                        const float sxu = f16_to_f32((uint16_t)(su[s] >> (16 * h))) * xn;
+                        bsum_u += sxu;
+                        q4_accumulate(reinterpret_cast<float(&)[T]>(acc_u), Q4Pair<T>::half(pu[s], h), sxu);
+                    }
+                }
+            }
+        }
+    } else {
+        for (int k0 = 0; k0 < K; k0 += THREADS * STEPS) {
+            CodeT pk[STEPS], pu[GATE_UP ? STEPS : 1];
+            uint16_t sc[STEPS], su[GATE_UP ? STEPS : 1], nw[STEPS];
+            float xv[STEPS];
+    #pragma unroll
+            for (int s = 0; s < STEPS; ++s) {
+                const uint32_t k = min((uint32_t)(k0 + tid + THREADS * s), (uint32_t)(K - 1));
+                pk[s] = ld_off(codes, k);
+                sc[s] = ld_off(gsc, k);
+                if (GATE_UP) {
+                    pu[s] = ld_off(codes_u, k);
+                    su[s] = ld_off(gsc_u, k);
+                }
+                xv[s] = ld_off(A.x, k);
+                nw[s] = ld_off(nwp, k);
+            }
+            const bool full = k0 + THREADS * STEPS <= K;    // workgroup-uniform: every row valid
+    #pragma unroll
+            for (int s = 0; s < STEPS; ++s) {
+                // rows past k (wave-uniform except in the last wave) add nothing
+                if (!full && k0 + THREADS * s + (tid & ~63) >= K) break;
+                const float xl = full || k0 + tid + THREADS * s < K ? xv[s] : 0.0f;
+                ss = fmaf(xl, xl, ss);
+                const float xn = A.norm_w ? xl * (1.0f + f16_to_f32(nw[s])) : xl;   // gemv.rs:575 but inv_rms
+                const float sx = f16_to_f32(sc[s]) * xn;                           // gemv.rs:429: scale * x_k
+                bsum += sx;
+                q4_accumulate(acc, pk[s], sx);
+                if (GATE_UP) {
+                    const float sxu = f16_to_f32(su[s]) * xn;
+                    bsum_u += sxu;
+                    q4_accumulate(reinterpret_cast<float(&)[T]>(acc_u), pu[s], sxu);
+                }
             }
         }
     }
@@ -256,8 +317,13 @@ QM_DEV void q4_gemv_body(const Q4GemvArgs& A) {
             if (q < A.count && (int)blockIdx.x >= A.wstart[q]) p = q;
     }
     const int tile = (int)blockIdx.x - A.wstart[p];
-    if (A.tile[p] == 16) q4_tile<GATE_UP, 16, STEPS, THREADS>(A, p, tile, red);
-    else q4_tile<GATE_UP, 8, STEPS, THREADS>(A, p, tile, red);
+    if (A.k & 1) {
+        if (A.tile[p] == 16) q4_tile<GATE_UP, false, 16, STEPS, THREADS>(A, p, tile, red);
+        else q4_tile<GATE_UP, false, 8, STEPS, THREADS>(A, p, tile, red);
+    } else {
+        if (A.tile[p] == 16) q4_tile<GATE_UP, true, 16, STEPS, THREADS>(A, p, tile, red);
+        else q4_tile<GATE_UP, true, 8, STEPS, THREADS>(A, p, tile, red);
+    }
 }
 
 extern "C" __global__ __launch_bounds__(Q4_THREADS) void qm_q4_gemv(Q4GemvArgs A) {
@@ -289,7 +355,7 @@ void qm_q4_gemv_hidden(Q4GemvArgs A) {
 }
 extern "C" __global__ __launch_bounds__(Q4_THREADS) __attribute__((amdgpu_waves_per_eu(4)))
 void qm_q4_gemv_inter(Q4GemvArgs A) {
-    q4_gemv_body<false, 9, Q4_THREADS>(A);
+    q4_gemv_body<false, 10, Q4_THREADS>(A);
 }
 
 // Reference layout -> tile-major.  Workgroup = 64 rows x 16 groups: each
