@@ -140,7 +140,7 @@ QM_DEV V ld_off(const V* base, uint32_t idx) {
     return *reinterpret_cast<const V*>(reinterpret_cast<const char*>(base) + (size_t)(idx * (uint32_t)sizeof(V)));
 }
 
-template <bool GATE_UP, bool PAIR, int T, int STEPS, int THREADS>
+template <bool GATE_UP, bool PAIR, bool NORM, int T, int STEPS, int THREADS>
 QM_DEV void q4_tile(const Q4GemvArgs& A, int p, int tile, float (*red)[33]) {
     typedef typename Q4Codes<T>::type CodeT;
     const int tid = threadIdx.x;
@@ -150,10 +150,10 @@ QM_DEV void q4_tile(const Q4GemvArgs& A, int p, int tile, float (*red)[33]) {
     const uint16_t* gsc = A.gscales[p] + (size_t)g * K;
     const CodeT* codes_u = GATE_UP ? reinterpret_cast<const CodeT*>(A.codes[1]) + (size_t)tile * K : nullptr;
     const uint16_t* gsc_u = GATE_UP ? A.gscales[1] + (size_t)g * K : nullptr;
-    // the norm weights are read from a valid array either way (without a
-    // norm, the weight's own scales, value unused): a conditional load would
-    // wait for its data before the next step's loads issue
-    const uint16_t* nwp = A.norm_w ? A.norm_w : gsc;
+    // NORM (A.norm_w set, uniform over the launch) is a template parameter: a
+    // load under a condition would wait for its data before the next step's
+    // loads issue
+    const uint16_t* nwp = A.norm_w;
 
     float acc[T], acc_u[GATE_UP ? T : 1];
 #pragma unroll
@@ -188,7 +188,7 @@ QM_DEV void q4_tile(const Q4GemvArgs& A, int p, int tile, float (*red)[33]) {
                     su[s] = ld_off(gsc2_u, kp);
                 }
                 xv[s] = ld_off(x2, kp);
-                nw[s] = ld_off(nwp2, kp);
+                if (NORM) nw[s] = ld_off(nwp2, kp);
             }
             const bool full = k0 + THREADS * PS <= KP;
 #pragma unroll
@@ -199,7 +199,7 @@ QM_DEV void q4_tile(const Q4GemvArgs& A, int p, int tile, float (*red)[33]) {
                 for (int h = 0; h < 2; ++h) {
                     const float xl = ok ? (h ? xv[s].y : xv[s].x) : 0.0f;
                     ss = fmaf(xl, xl, ss);
-                    const float xn = A.norm_w ? xl * (1.0f + f16_to_f32((uint16_t)(nw[s] >> (16 * h)))) : xl;
+                    const float xn = NORM ? xl * (1.0f + f16_to_f32((uint16_t)(nw[s] >> (16 * h)))) : xl;
                     const float sx = f16_to_f32((uint16_t)(sc[s] >> (16 * h))) * xn;
                     bsum += sx;
                     q4_accumulate(acc, Q4Pair<T>::half(pk[s], h), sx);
@@ -226,7 +226,7 @@ QM_DEV void q4_tile(const Q4GemvArgs& A, int p, int tile, float (*red)[33]) {
                     su[s] = ld_off(gsc_u, k);
                 }
                 xv[s] = ld_off(A.x, k);
-                nw[s] = ld_off(nwp, k);
+                if (NORM) nw[s] = ld_off(nwp, k);
             }
             const bool full = k0 + THREADS * STEPS <= K;    // workgroup-uniform: every row valid
     #pragma unroll
@@ -235,7 +235,7 @@ QM_DEV void q4_tile(const Q4GemvArgs& A, int p, int tile, float (*red)[33]) {
                 if (!full && k0 + THREADS * s + (tid & ~63) >= K) break;
                 const float xl = full || k0 + tid + THREADS * s < K ? xv[s] : 0.0f;
                 ss = fmaf(xl, xl, ss);
-                const float xn = A.norm_w ? xl * (1.0f + f16_to_f32(nw[s])) : xl;   // gemv.rs:575 but inv_rms
+                const float xn = NORM ? xl * (1.0f + f16_to_f32(nw[s])) : xl;   // gemv.rs:575 but inv_rms
                 const float sx = f16_to_f32(sc[s]) * xn;                           // gemv.rs:429: scale * x_k
                 bsum += sx;
                 q4_accumulate(acc, pk[s], sx);
@@ -262,7 +262,7 @@ QM_DEV void q4_tile(const Q4GemvArgs& A, int p, int tile, float (*red)[33]) {
         for (int j = 0; j < T; ++j) acc_u[j] = fmaf(-8.0f, bsum_u, acc_u[j]);
         cs_u = q4_wave_reduce<T>(reinterpret_cast<float(&)[T]>(acc_u), lane);
     }
-    const float ssw = A.norm_w ? wave_sum64(ss) : 0.0f;
+    const float ssw = NORM ? wave_sum64(ss) : 0.0f;
     if ((lane & (64 / T - 1)) == 0) {
         red[wv][q4_col<T>(lane)] = cs;
         if (GATE_UP) red[wv][16 + q4_col<T>(lane)] = cs_u;
@@ -279,7 +279,7 @@ QM_DEV void q4_tile(const Q4GemvArgs& A, int p, int tile, float (*red)[33]) {
         }
     }
     // gemv.rs:573: 1 / sqrt(mean(x^2) + 1e-6)
-    const float inv = A.norm_w ? 1.0f / sqrtf(sst / (float)K + 1e-6f) : 1.0f;
+    const float inv = NORM ? 1.0f / sqrtf(sst / (float)K + 1e-6f) : 1.0f;
     y *= inv;
     if (GATE_UP) {
         u *= inv;
@@ -305,7 +305,18 @@ QM_DEV void q4_tile(const Q4GemvArgs& A, int p, int tile, float (*red)[33]) {
     }
 }
 
-template <bool GATE_UP, int STEPS, int THREADS>
+template <bool GATE_UP, bool NORM, int STEPS, int THREADS>
+QM_DEV void q4_tile_pick(const Q4GemvArgs& A, int p, int tile, float (*red)[33]) {
+    if (A.k & 1) {
+        if (A.tile[p] == 16) q4_tile<GATE_UP, false, NORM, 16, STEPS, THREADS>(A, p, tile, red);
+        else q4_tile<GATE_UP, false, NORM, 8, STEPS, THREADS>(A, p, tile, red);
+    } else {
+        if (A.tile[p] == 16) q4_tile<GATE_UP, true, NORM, 16, STEPS, THREADS>(A, p, tile, red);
+        else q4_tile<GATE_UP, true, NORM, 8, STEPS, THREADS>(A, p, tile, red);
+    }
+}
+
+template <bool GATE_UP, int STEPS, int THREADS, bool WITH_NORM = true>
 QM_DEV void q4_gemv_body(const Q4GemvArgs& A) {
     __shared__ float red[THREADS / 64][33];   // per wave: column sums (gate, up), x's sum of squares
     // which weight: workgroups wstart[p] .. wstart[p+1]-1 are weight p's
@@ -317,13 +328,8 @@ QM_DEV void q4_gemv_body(const Q4GemvArgs& A) {
             if (q < A.count && (int)blockIdx.x >= A.wstart[q]) p = q;
     }
     const int tile = (int)blockIdx.x - A.wstart[p];
-    if (A.k & 1) {
-        if (A.tile[p] == 16) q4_tile<GATE_UP, false, 16, STEPS, THREADS>(A, p, tile, red);
-        else q4_tile<GATE_UP, false, 8, STEPS, THREADS>(A, p, tile, red);
-    } else {
-        if (A.tile[p] == 16) q4_tile<GATE_UP, true, 16, STEPS, THREADS>(A, p, tile, red);
-        else q4_tile<GATE_UP, true, 8, STEPS, THREADS>(A, p, tile, red);
-    }
+    if (WITH_NORM && A.norm_w) q4_tile_pick<GATE_UP, WITH_NORM, STEPS, THREADS>(A, p, tile, red);
+    else q4_tile_pick<GATE_UP, false, STEPS, THREADS>(A, p, tile, red);
 }
 
 extern "C" __global__ __launch_bounds__(Q4_THREADS) void qm_q4_gemv(Q4GemvArgs A) {
@@ -341,11 +347,12 @@ extern "C" __global__ __launch_bounds__(256) void qm_q4_gate_up(Q4GemvArgs A) {
 // Shape-fitted forms.  A launch's workgroups should all be resident at once
 // (a second dispatch round repeats the whole load -> reduce latency), and a
 // lane's rows should come in as few load rounds as possible:
-//   k <= 2560 (the hidden size): 256 threads of 10 rows, one load round, 91
+//   k <= 2560 (the hidden size): 256 threads of 10 rows, one load round, 84
 //     VGPRs (five workgroups per CU, 1280 slots for the 776 tiles of the
 //     fused DeltaNet input projections);
-//   k <= 9216 (the MLP's down_proj): 9 rows per lane, two rounds instead of
-//     three, at <= 128 VGPRs (two workgroups per CU, 512 slots for 320 tiles).
+//   k <= 9216 without a norm (the MLP's down_proj): 18 rows per lane, one
+//     load round, 115 VGPRs (two workgroups per CU, 512 slots for 320
+//     tiles); the host sends a launch with a norm to the general form.
 // (512-thread forms of 5 rows for k <= 2560, of 18 or 12 rows at 256 threads
 // for down_proj, and of 16 at 256 threads for the general case all measured
 // slower over a model token.)
@@ -355,7 +362,7 @@ void qm_q4_gemv_hidden(Q4GemvArgs A) {
 }
 extern "C" __global__ __launch_bounds__(Q4_THREADS) __attribute__((amdgpu_waves_per_eu(4)))
 void qm_q4_gemv_inter(Q4GemvArgs A) {
-    q4_gemv_body<false, 10, Q4_THREADS>(A);
+    q4_gemv_body<false, 18, Q4_THREADS, false>(A);
 }
 
 // Reference layout -> tile-major.  Workgroup = 64 rows x 16 groups: each

@@ -948,7 +948,7 @@ int32_t q4_gemv_multi_impl(qm_context* c, qm_stream stream, int32_t k, const flo
     if (k <= 2560) {
         f = c->f_q4_gemv_hidden;
         threads = c->q4_hidden_threads;
-    } else if (k > 4096 && k <= 9216) {
+    } else if (k > 4096 && k <= 9216 && !norm_w) {
         f = c->f_q4_gemv_inter;
         threads = c->q4_inter_threads;
     }
