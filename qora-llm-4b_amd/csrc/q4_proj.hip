@@ -336,10 +336,10 @@ extern "C" __global__ __launch_bounds__(Q4_THREADS) void qm_q4_gemv(Q4GemvArgs A
     q4_gemv_body<false, Q4_STEPS, Q4_THREADS>(A);
 }
 
-// 256 threads, 10 rows per lane: one load round at k = 2560, and at 134
-// VGPRs three workgroups per CU, so the 576 tiles of the 2560 x 9216 gate /
-// up pair are resident in one dispatch round (the 512-thread form fitted two
-// per CU and ran 3% slower per model token).
+// 256 threads, 10 rows (5 row pairs) per lane: one load round at k = 2560,
+// and at 132 VGPRs three workgroups per CU, so the 576 tiles of the 2560 x
+// 9216 gate / up pair are resident in one dispatch round (the 512-thread form
+// fitted two per CU and ran 3% slower per model token).
 extern "C" __global__ __launch_bounds__(256) void qm_q4_gate_up(Q4GemvArgs A) {
     q4_gemv_body<true, 10, 256>(A);
 }
